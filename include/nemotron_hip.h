@@ -1,0 +1,221 @@
+/*
+ * nemotron_hip.h -- C ABI of the MI355X (gfx950) int8 quantized-linear path.
+ *
+ * Drop-in boundary for nemotron-rs's nemotron-kernels wrappers: a Rust FFI
+ * crate (nemotron-hip-sys) binds these declarations 1:1 and the existing
+ * wrapper signatures keep their host-fallback contract by calling the *_host
+ * twin whenever an nh_supports_* predicate says the device envelope does not
+ * cover a shape (gemm.rs:290-299 backend_for_shape pattern).
+ *
+ * Conventions
+ *   - Device entry points take caller-owned DEVICE pointers and an explicit
+ *     stream; they only enqueue work (no allocation, no synchronisation).
+ *     Every argument is validated on the host BEFORE anything is launched,
+ *     as the reference validates before upload (gemm.rs:323, quantize.rs:286).
+ *   - *_host entry points take HOST pointers and run the library's own CPU
+ *     implementation (the reference's *_host functions).
+ *   - Lengths are element counts.  Status codes mirror the reference error
+ *     enums; nh_error (optional, may be NULL) carries their payload.
+ *   - int8 weights are [N][K] row-major (K contiguous) with one f32 scale per
+ *     output row N.  The reference stores f32 linear weights [K][N]
+ *     (linear.rs:324); quantization transposes once, offline.
+ *   - Functions never abort the process.
+ */
+#ifndef NEMOTRON_HIP_H
+#define NEMOTRON_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error variants of QuantizeError (quantize.rs:211-225), GemmError
+ * (gemm.rs:175-184), MoeRoutingError (moe_routing.rs:422-430) and LinearError
+ * (linear.rs:369-385). */
+typedef enum nh_status {
+    NH_OK = 0,
+    NH_INVALID_SHAPE = 1,     /* *Error::InvalidShape */
+    NH_LENGTH_MISMATCH = 2,   /* *Error::LengthMismatch{argument, expected, actual} */
+    NH_INVALID_PARAMS = 3,    /* QuantizeError::InvalidParams */
+    NH_NON_FINITE_INPUT = 4,  /* QuantizeError::NonFiniteInput{index, value} */
+    NH_OUT_OF_RANGE = 5,      /* QuantizeError::Int4OutOfRange(u8) */
+    NH_INVALID_ROW_COUNT = 6, /* LinearError::InvalidRowCount */
+    NH_UNSUPPORTED = 7,       /* shape outside the device envelope: use the *_host twin */
+    NH_DEVICE_ERROR = 8       /* *Error::DeviceError(String) */
+} nh_status;
+
+typedef struct nh_error {
+    const char *argument; /* static string naming the offending argument */
+    uint64_t expected;
+    uint64_t actual;
+    uint64_t index;       /* NonFiniteInput.index (flat, row-major) */
+    float value;          /* NonFiniteInput.value */
+    uint32_t byte;        /* Int4OutOfRange payload */
+    char message[256];    /* human-readable detail (DeviceError text) */
+} nh_error;
+
+typedef enum nh_dtype { NH_F32 = 0, NH_BF16 = 1 } nh_dtype;
+
+typedef struct nh_context nh_context;
+typedef void *nh_stream; /* hipStream_t; NULL = the device's null stream */
+
+/* ---- D0: device, context, buffers (GpuDevice / GpuTensor, device.rs:117-153,
+ *      tensor.rs:259-446) ------------------------------------------------- */
+int nh_device_count(void);
+/* Loads the gfx950 code object (embedded in the library when path is NULL)
+ * with hipModuleLoadData and resolves every kernel once; the context is
+ * immutable afterwards and safe to share across threads (device.rs:33-42). */
+nh_status nh_context_create(int device, const char *code_object_path, nh_context **out, nh_error *err);
+void nh_context_destroy(nh_context *ctx);
+int nh_context_device(const nh_context *ctx);
+nh_status nh_malloc(nh_context *ctx, size_t bytes, void **ptr, nh_error *err);
+nh_status nh_free(nh_context *ctx, void *ptr, nh_error *err);
+nh_status nh_memcpy_htod(nh_context *ctx, void *dst, const void *src, size_t bytes, nh_error *err);
+nh_status nh_memcpy_dtoh(nh_context *ctx, void *dst, const void *src, size_t bytes, nh_error *err);
+nh_status nh_memset_d8(nh_context *ctx, void *dst, int value, size_t bytes, nh_error *err);
+nh_status nh_stream_create(nh_context *ctx, nh_stream *out, nh_error *err);
+nh_status nh_stream_destroy(nh_context *ctx, nh_stream stream, nh_error *err);
+nh_status nh_stream_synchronize(nh_context *ctx, nh_stream stream, nh_error *err);
+
+/* ---- Kernel registry (supported_*_kernels(), gemm.rs:80-82,
+ *      quantize.rs:45-47, moe_routing.rs:71-73) --------------------------- */
+int nh_kernel_count(void);
+/* name of kernel i and its backend tag: 0 = host fallback, 1 = gfx950 device */
+const char *nh_kernel_name(int i, int *backend);
+
+/* ---- Q0: affine INT4 (quantize.rs:49-204) ----------------------------- */
+size_t nh_packed_int4_len(size_t value_count);                                           /* :49-51 */
+nh_status nh_pack_int4_host(const uint8_t *values, size_t n, uint8_t *packed, size_t packed_len,
+                            nh_error *err);                                               /* :59-81 */
+nh_status nh_unpack_int4_host(const uint8_t *packed, size_t packed_len, size_t value_count,
+                              uint8_t *out, size_t out_len, nh_error *err);               /* :89-120 */
+nh_status nh_quantize_int4_host(const float *values, size_t n, float scale, uint32_t zero_point,
+                                uint8_t *packed, size_t packed_len, nh_error *err);       /* :131-144 */
+nh_status nh_dequantize_int4_host(const uint8_t *packed, size_t packed_len, size_t value_count,
+                                  float scale, uint32_t zero_point, float *out, size_t out_len,
+                                  nh_error *err);                                         /* :156-178 */
+/* Q0d, replaces dequantize_int4 (quantize.rs:332-349): unpack + dequantize
+ * on the device from the packed bytes (any value_count, not only powers of
+ * two as :207-209). */
+nh_status nh_dequantize_int4(nh_context *ctx, const uint8_t *packed, size_t packed_len, size_t value_count,
+                             float scale, uint32_t zero_point, float *out, size_t out_len, nh_stream stream,
+                             nh_error *err);
+
+/* ---- Q1/Q2/Q3: symmetric int8, one f32 scale per row (new; numerics of
+ *      quantize_scalar quantize.rs:188-200 with zero point 0) ------------- */
+/* s[r] = max|x[r,:]| / 127 (RN); q = clamp(roundf(x / s), -127, 127);
+ * s == 0 -> codes 0.  Used for weights (Q1, offline) and per-token
+ * activations (Q2).  row_status (optional, [rows]) receives -1 or the first
+ * non-finite column of the row; codes of such a row are unspecified. */
+nh_status nh_quantize_rows_i8(nh_context *ctx, const void *x, nh_dtype dtype, size_t rows, size_t cols,
+                              int8_t *q, float *scales, int32_t *row_status, nh_stream stream, nh_error *err);
+nh_status nh_quantize_rows_i8_host(const void *x, nh_dtype dtype, size_t rows, size_t cols, int8_t *q,
+                                   float *scales, nh_error *err); /* NonFiniteInput on the first bad element */
+/* Q3: out = (float)q * s (dequantize_scalar, quantize.rs:202-204). */
+nh_status nh_dequantize_i8(nh_context *ctx, const int8_t *q, const float *scales, size_t rows, size_t cols,
+                           float *out, nh_stream stream, nh_error *err);
+nh_status nh_dequantize_i8_host(const int8_t *q, const float *scales, size_t rows, size_t cols, float *out,
+                                nh_error *err);
+
+/* ---- G0/G1/G2/G3: GEMM family (gemm.rs, linear.rs:283-342) ------------- */
+/* G0: gemm_into_host restated (gemm.rs:91-147): f32 in, f64 accumulation. */
+nh_status nh_gemm_f32_host(const float *lhs, size_t lhs_len, const float *rhs, size_t rhs_len, size_t m,
+                           size_t k, size_t n, float *out, size_t out_len, nh_error *err);
+/* Device envelope of the W8A8 GEMM family (supports_shape, gemm.rs:247-254). */
+int nh_supports_gemm_w8a8(size_t m, size_t n, size_t k);
+/* G1/G3: out[m,n] = ((float)sum_k xq[m,k]*wq[n,k] * sx[m]) * sw[n] (+ bias[n])
+ * in f32 or bf16 (RNE).  int32 accumulation is exact.  M <= 16 runs the
+ * HBM-bound GEMV, larger M the MFMA GEMM. */
+nh_status nh_gemm_w8a8(nh_context *ctx, const int8_t *xq, const float *sx, const int8_t *wq, const float *sw,
+                       const float *bias, size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype,
+                       nh_stream stream, nh_error *err);
+nh_status nh_gemm_w8a8_host(const int8_t *xq, const float *sx, const int8_t *wq, const float *sw,
+                            const float *bias, size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype,
+                            nh_error *err);
+/* Quantized linear layer, the drop-in for LinearProjection::project_into
+ * with int8 per-row weights (linear.rs:283-342): dynamic per-token
+ * quantization of x (f32 or bf16) then G1/G3 + bias.  For m <= 4 the
+ * quantization is fused into the GEMV (one launch, no workspace); otherwise
+ * it needs a workspace of nh_linear_w8a8_workspace_size(m, k) bytes.
+ * xq_out/sx_out (optional) receive the quantized activations. */
+size_t nh_linear_w8a8_workspace_size(size_t m, size_t k);
+nh_status nh_linear_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const int8_t *wq, const float *sw,
+                         const float *bias, size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype,
+                         void *workspace, size_t workspace_bytes, int8_t *xq_out, float *sx_out,
+                         nh_stream stream, nh_error *err);
+/* G2: W8A32 dequant GEMV, y = x * ((float)q * s)^T with f64 accumulation,
+ * the arithmetic of materialize_dense + gemm_into_host (linear.rs:126-131). */
+nh_status nh_gemv_w8a32(nh_context *ctx, const float *x, const int8_t *wq, const float *sw, size_t m, size_t n,
+                        size_t k, float *y, nh_stream stream, nh_error *err);
+nh_status nh_gemv_w8a32_host(const float *x, const int8_t *wq, const float *sw, size_t m, size_t n, size_t k,
+                             float *y, nh_error *err);
+
+/* ---- R1..R4: MoE routing, permutation, grouped GEMM, combine ---------- */
+float nh_sigmoid_f32_host(float x); /* sigmoid_scalar, activations.rs:73-81 */
+/* R1: moe_route_into_host / moe_route (moe_routing.rs:118-141, :499-523):
+ * sigmoid scores, top-k by (weight desc, expert asc).  renormalize divides
+ * the selected weights by their sum (route order); scaling multiplies after.
+ * Indices are int32 (usize in the reference). */
+nh_status nh_moe_route_sigmoid_topk(nh_context *ctx, const float *scores, size_t tokens, size_t experts,
+                                    size_t top_k, int renormalize, float scaling, int32_t *indices,
+                                    float *weights, nh_stream stream, nh_error *err);
+nh_status nh_moe_route_sigmoid_topk_host(const float *scores, size_t scores_len, size_t tokens, size_t experts,
+                                         size_t top_k, int renormalize, float scaling, int32_t *indices,
+                                         size_t indices_len, float *weights, size_t weights_len, nh_error *err);
+/* R1s: moe_route_softmax_into_host (moe_routing.rs:143-166, :188-216). */
+nh_status nh_moe_route_softmax_topk_host(const float *scores, size_t scores_len, size_t tokens, size_t experts,
+                                         size_t top_k, int32_t *indices, size_t indices_len, float *weights,
+                                         size_t weights_len, nh_error *err);
+/* R2: counts -> offsets[E+1] (exclusive scan), perm (slot -> route, stable
+ * by route id inside an expert), pos (route -> slot). */
+nh_status nh_moe_permute(nh_context *ctx, const int32_t *indices, size_t tokens, size_t top_k, size_t experts,
+                         int32_t *offsets, int32_t *perm, int32_t *pos, nh_stream stream, nh_error *err);
+nh_status nh_moe_permute_host(const int32_t *indices, size_t tokens, size_t top_k, size_t experts,
+                              int32_t *offsets, int32_t *perm, int32_t *pos, nh_error *err);
+/* R3: grouped W8A8 GEMM over the expert segments of offsets.  gather != 0:
+ * the A row of slot i is token perm[i] / top_k (up projection); otherwise
+ * the A row is slot i (down projection).  out is f32 [routes][n]; relu2
+ * applies ReLU^2 after the epilogue (mlp.rs:205). */
+nh_status nh_moe_grouped_gemm_w8a8(nh_context *ctx, const int8_t *aq, const float *sa, int gather,
+                                   size_t top_k, const int32_t *offsets, const int32_t *perm, size_t routes,
+                                   size_t a_rows, size_t experts, const int8_t *w, const float *sw, size_t n,
+                                   size_t k, int relu2, float *out, nh_stream stream, nh_error *err);
+nh_status nh_moe_grouped_gemm_w8a8_host(const int8_t *aq, const float *sa, int gather, size_t top_k,
+                                        const int32_t *offsets, const int32_t *perm, size_t routes,
+                                        size_t a_rows, size_t experts, const int8_t *w, const float *sw, size_t n,
+                                        size_t k, int relu2, float *out, nh_error *err);
+/* R4: out[t] = sum_j w[t,j] * slot_out[pos[t*k+j]] in route order (f32),
+ * the combine of MoeLayer::forward_into (moe.rs:195, :221-244). */
+nh_status nh_moe_combine(nh_context *ctx, const float *slot_out, const int32_t *pos, const float *weights,
+                         size_t tokens, size_t top_k, size_t hidden, void *out, nh_dtype out_dtype,
+                         nh_stream stream, nh_error *err);
+nh_status nh_moe_combine_host(const float *slot_out, const int32_t *pos, const float *weights, size_t tokens,
+                              size_t top_k, size_t hidden, void *out, nh_dtype out_dtype, nh_error *err);
+/* Whole int8 MoE layer on the device: Q2(x) -> R1 -> R2 -> up (R3, gather,
+ * ReLU^2) -> Q2 -> down (R3) -> R4.  Replaces MoeLayer::forward_into
+ * (moe.rs:154-249) for routed experts with int8 per-row weights
+ * w_up [E][inter][hidden], w_down [E][hidden][inter].  The routing stages
+ * leave indices, weights, offsets, perm and pos in the workspace at the byte
+ * offsets reported by nh_moe_workspace_layout. */
+size_t nh_moe_forward_w8a8_workspace_size(size_t tokens, size_t hidden, size_t inter, size_t experts,
+                                          size_t top_k);
+/* byte offsets in the workspace of: [0] indices i32[T*k], [1] weights
+ * f32[T*k], [2] offsets i32[E+1], [3] perm i32[T*k], [4] pos i32[T*k]. */
+void nh_moe_workspace_layout(size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
+                             size_t offsets_out[5]);
+nh_status nh_moe_forward_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const float *logits,
+                              size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
+                              int renormalize, float scaling, const int8_t *w_up, const float *s_up,
+                              const int8_t *w_down, const float *s_down, void *out, nh_dtype out_dtype,
+                              void *workspace, size_t workspace_bytes, nh_stream stream, nh_error *err);
+
+/* ---- synthetic inputs (build-defined seeded generator; the reference has
+ *      no RNG): splitmix64 -> Box-Muller (f64) -> f32 ------------------- */
+void nh_fill_normal_f32_host(uint64_t seed, float mean, float stddev, float *out, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NEMOTRON_HIP_H */

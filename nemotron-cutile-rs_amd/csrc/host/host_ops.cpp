@@ -1,0 +1,350 @@
+// Host twins: the library's CPU implementation of every op, used by callers
+// outside the device envelope (the reference's host-fallback contract,
+// gemm.rs:290-310).  They share nh_numerics.h with the kernels, so a twin and
+// its kernel round identically.  Built with -ffp-contract=off.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "../kernels/nh_numerics.h"
+#include "../runtime/nh_runtime.h"
+
+using namespace nh;
+
+namespace {
+
+bool int4_params_ok(float scale, uint32_t zp) { return std::isfinite(scale) && scale > 0.0f && zp <= 0x0F; }
+
+float load_f32(const void* x, size_t i, nh_dtype d) {
+    return d == NH_BF16 ? bf16_to_f32(((const uint16_t*)x)[i]) : ((const float*)x)[i];
+}
+
+void store_f32(void* out, size_t i, float v, nh_dtype d) {
+    if (d == NH_BF16)
+        ((uint16_t*)out)[i] = f32_to_bf16(v);
+    else
+        ((float*)out)[i] = v;
+}
+
+nh_status route_shape(size_t scores_len, size_t tokens, size_t experts, size_t top_k, size_t indices_len,
+                      size_t weights_len, nh_error* err) {
+    if (experts == 0 || top_k == 0 || top_k > experts)
+        return set_error(err, NH_INVALID_SHAPE, "invalid routing shape tokens=%zu experts=%zu top_k=%zu", tokens,
+                         experts, top_k);
+    size_t sl, rl;
+    if (!mul_ok(tokens, experts, &sl) || !mul_ok(tokens, top_k, &rl))
+        return set_error(err, NH_INVALID_SHAPE, "routing shape overflows");
+    if (scores_len != sl) return mismatch(err, "scores", sl, scores_len);
+    if (indices_len != rl) return mismatch(err, "indices", rl, indices_len);
+    if (weights_len != rl) return mismatch(err, "weights", rl, weights_len);
+    return NH_OK;
+}
+
+// Top-k of one token's weights by (total_cmp desc, expert asc).
+void top_k_of(const std::vector<float>& w, size_t top_k, int32_t* idx, float* out) {
+    std::vector<int32_t> order(w.size());
+    for (size_t e = 0; e < w.size(); ++e) order[e] = (int32_t)e;
+    std::partial_sort(order.begin(), order.begin() + top_k, order.end(), [&](int32_t a, int32_t b) {
+        const int32_t ka = total_cmp_key(w[a]), kb = total_cmp_key(w[b]);
+        return ka != kb ? ka > kb : a < b;
+    });
+    for (size_t j = 0; j < top_k; ++j) {
+        idx[j] = order[j];
+        out[j] = w[order[j]];
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t nh_packed_int4_len(size_t value_count) { return value_count / 2 + value_count % 2; }
+
+nh_status nh_pack_int4_host(const uint8_t* values, size_t n, uint8_t* packed, size_t packed_len, nh_error* err) {
+    clear_error(err);
+    if (packed_len != nh_packed_int4_len(n)) return mismatch(err, "packed", nh_packed_int4_len(n), packed_len);
+    if (packed_len) std::memset(packed, 0, packed_len);
+    for (size_t i = 0; i < n; ++i) {
+        if (values[i] > 0x0F) {
+            if (err) err->byte = values[i];
+            return set_error(err, NH_OUT_OF_RANGE, "INT4 value %u out of range", (unsigned)values[i]);
+        }
+        packed[i >> 1] |= (i & 1) ? (uint8_t)(values[i] << 4) : values[i];
+    }
+    return NH_OK;
+}
+
+nh_status nh_unpack_int4_host(const uint8_t* packed, size_t packed_len, size_t value_count, uint8_t* out,
+                              size_t out_len, nh_error* err) {
+    clear_error(err);
+    if (packed_len != nh_packed_int4_len(value_count))
+        return mismatch(err, "packed", nh_packed_int4_len(value_count), packed_len);
+    if (out_len != value_count) return mismatch(err, "output", value_count, out_len);
+    for (size_t i = 0; i < value_count; ++i) out[i] = (i & 1) ? (packed[i >> 1] >> 4) & 0x0F : packed[i >> 1] & 0x0F;
+    return NH_OK;
+}
+
+nh_status nh_quantize_int4_host(const float* values, size_t n, float scale, uint32_t zero_point, uint8_t* packed,
+                                size_t packed_len, nh_error* err) {
+    clear_error(err);
+    if (!int4_params_ok(scale, zero_point)) return set_error(err, NH_INVALID_PARAMS, "invalid INT4 params");
+    std::vector<uint8_t> codes(n);
+    for (size_t i = 0; i < n; ++i) {
+        const float v = values[i];
+        if (!std::isfinite(v)) {
+            if (err) {
+                err->index = i;
+                err->value = v;
+            }
+            return set_error(err, NH_NON_FINITE_INPUT, "non-finite input at %zu", i);
+        }
+        float q = std::round(v / scale + (float)zero_point);
+        q = std::min(std::max(q, 0.0f), 15.0f);
+        codes[i] = (uint8_t)q;
+    }
+    return nh_pack_int4_host(codes.data(), n, packed, packed_len, err);
+}
+
+nh_status nh_dequantize_int4_host(const uint8_t* packed, size_t packed_len, size_t value_count, float scale,
+                                  uint32_t zero_point, float* out, size_t out_len, nh_error* err) {
+    clear_error(err);
+    if (!int4_params_ok(scale, zero_point)) return set_error(err, NH_INVALID_PARAMS, "invalid INT4 params");
+    if (out_len != value_count) return mismatch(err, "output", value_count, out_len);
+    std::vector<uint8_t> codes(value_count);
+    nh_status st = nh_unpack_int4_host(packed, packed_len, value_count, codes.data(), value_count, err);
+    if (st) return st;
+    for (size_t i = 0; i < value_count; ++i) out[i] = ((float)codes[i] - (float)zero_point) * scale;
+    return NH_OK;
+}
+
+nh_status nh_quantize_rows_i8_host(const void* x, nh_dtype dtype, size_t rows, size_t cols, int8_t* q,
+                                   float* scales, nh_error* err) {
+    clear_error(err);
+    if (dtype != NH_F32 && dtype != NH_BF16) return set_error(err, NH_INVALID_PARAMS, "unknown dtype");
+    size_t total;
+    if (!mul_ok(rows, cols, &total)) return set_error(err, NH_INVALID_SHAPE, "rows*cols overflows");
+    for (size_t i = 0; i < total; ++i) {
+        const float v = load_f32(x, i, dtype);
+        if (!std::isfinite(v)) {
+            if (err) {
+                err->index = i;
+                err->value = v;
+            }
+            return set_error(err, NH_NON_FINITE_INPUT, "non-finite input at %zu", i);
+        }
+    }
+    for (size_t r = 0; r < rows; ++r) {
+        float amax = 0.0f;
+        for (size_t c = 0; c < cols; ++c) amax = std::max(amax, std::fabs(load_f32(x, r * cols + c, dtype)));
+        const float s = scale_from_amax(amax);
+        scales[r] = s;
+        for (size_t c = 0; c < cols; ++c) q[r * cols + c] = quantize_i8(load_f32(x, r * cols + c, dtype), s);
+    }
+    return NH_OK;
+}
+
+nh_status nh_dequantize_i8_host(const int8_t* q, const float* scales, size_t rows, size_t cols, float* out,
+                                nh_error* err) {
+    clear_error(err);
+    size_t total;
+    if (!mul_ok(rows, cols, &total)) return set_error(err, NH_INVALID_SHAPE, "rows*cols overflows");
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t c = 0; c < cols; ++c) out[r * cols + c] = (float)q[r * cols + c] * scales[r];
+    return NH_OK;
+}
+
+nh_status nh_gemm_f32_host(const float* lhs, size_t lhs_len, const float* rhs, size_t rhs_len, size_t m, size_t k,
+                           size_t n, float* out, size_t out_len, nh_error* err) {
+    clear_error(err);
+    size_t ll, rl, ol;
+    if (m == 0 || k == 0 || n == 0 || !mul_ok(m, k, &ll) || !mul_ok(k, n, &rl) || !mul_ok(m, n, &ol))
+        return set_error(err, NH_INVALID_SHAPE, "invalid GEMM shape m=%zu k=%zu n=%zu", m, k, n);
+    if (lhs_len != ll) return mismatch(err, "lhs", ll, lhs_len);
+    if (rhs_len != rl) return mismatch(err, "rhs", rl, rhs_len);
+    if (out_len != ol) return mismatch(err, "output", ol, out_len);
+    for (size_t r = 0; r < m; ++r)
+        for (size_t c = 0; c < n; ++c) {
+            double acc = 0.0;
+            for (size_t d = 0; d < k; ++d) acc += (double)lhs[r * k + d] * (double)rhs[d * n + c];
+            out[r * n + c] = (float)acc;
+        }
+    return NH_OK;
+}
+
+nh_status nh_gemm_w8a8_host(const int8_t* xq, const float* sx, const int8_t* wq, const float* sw, const float* bias,
+                            size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype, nh_error* err) {
+    clear_error(err);
+    size_t t;
+    if (m == 0 || n == 0 || k == 0 || !mul_ok(m, k, &t) || !mul_ok(n, k, &t) || !mul_ok(m, n, &t))
+        return set_error(err, NH_INVALID_SHAPE, "invalid GEMM shape");
+    if (out_dtype != NH_F32 && out_dtype != NH_BF16) return set_error(err, NH_INVALID_PARAMS, "unknown dtype");
+    for (size_t r = 0; r < m; ++r)
+        for (size_t c = 0; c < n; ++c) {
+            int32_t acc = 0;
+            for (size_t d = 0; d < k; ++d) acc += (int32_t)xq[r * k + d] * (int32_t)wq[c * k + d];
+            float y = epilogue_w8a8(acc, sx[r], sw[c]);
+            if (bias) y = y + bias[c];
+            store_f32(out, r * n + c, y, out_dtype);
+        }
+    return NH_OK;
+}
+
+nh_status nh_gemv_w8a32_host(const float* x, const int8_t* wq, const float* sw, size_t m, size_t n, size_t k,
+                             float* y, nh_error* err) {
+    clear_error(err);
+    size_t t;
+    if (m == 0 || n == 0 || k == 0 || !mul_ok(m, k, &t) || !mul_ok(n, k, &t))
+        return set_error(err, NH_INVALID_SHAPE, "invalid GEMV shape");
+    for (size_t r = 0; r < m; ++r)
+        for (size_t c = 0; c < n; ++c) {
+            double acc = 0.0;
+            for (size_t d = 0; d < k; ++d) acc += (double)x[r * k + d] * (double)((float)wq[c * k + d] * sw[c]);
+            y[r * n + c] = (float)acc;
+        }
+    return NH_OK;
+}
+
+float nh_sigmoid_f32_host(float x) { return sigmoid_f32(x); }
+
+nh_status nh_moe_route_sigmoid_topk_host(const float* scores, size_t scores_len, size_t tokens, size_t experts,
+                                         size_t top_k, int renormalize, float scaling, int32_t* indices,
+                                         size_t indices_len, float* weights, size_t weights_len, nh_error* err) {
+    clear_error(err);
+    nh_status st = route_shape(scores_len, tokens, experts, top_k, indices_len, weights_len, err);
+    if (st) return st;
+    std::vector<float> w(experts);
+    for (size_t t = 0; t < tokens; ++t) {
+        for (size_t e = 0; e < experts; ++e) w[e] = sigmoid_f32(scores[t * experts + e]);
+        int32_t* idx = indices + t * top_k;
+        float* out = weights + t * top_k;
+        top_k_of(w, top_k, idx, out);
+        if (renormalize) {
+            float total = 0.0f;
+            for (size_t j = 0; j < top_k; ++j) total = total + out[j];
+            for (size_t j = 0; j < top_k; ++j) out[j] = out[j] / total;
+        }
+        if (scaling != 1.0f)
+            for (size_t j = 0; j < top_k; ++j) out[j] = out[j] * scaling;
+    }
+    return NH_OK;
+}
+
+nh_status nh_moe_route_softmax_topk_host(const float* scores, size_t scores_len, size_t tokens, size_t experts,
+                                         size_t top_k, int32_t* indices, size_t indices_len, float* weights,
+                                         size_t weights_len, nh_error* err) {
+    clear_error(err);
+    nh_status st = route_shape(scores_len, tokens, experts, top_k, indices_len, weights_len, err);
+    if (st) return st;
+    std::vector<float> p(experts);
+    for (size_t t = 0; t < tokens; ++t) {
+        const float* row = scores + t * experts;
+        float mx = -INFINITY;
+        for (size_t e = 0; e < experts; ++e) mx = std::fmax(mx, row[e]);
+        float total = 0.0f;
+        for (size_t e = 0; e < experts; ++e) {
+            p[e] = expf_rn(row[e] - mx);
+            total = total + p[e];
+        }
+        for (size_t e = 0; e < experts; ++e) p[e] = p[e] / total;
+        int32_t* idx = indices + t * top_k;
+        float* out = weights + t * top_k;
+        top_k_of(p, top_k, idx, out);
+        float sel = 0.0f;
+        for (size_t j = 0; j < top_k; ++j) sel = sel + out[j];
+        for (size_t j = 0; j < top_k; ++j) out[j] = out[j] / sel;
+    }
+    return NH_OK;
+}
+
+nh_status nh_moe_permute_host(const int32_t* indices, size_t tokens, size_t top_k, size_t experts, int32_t* offsets,
+                              int32_t* perm, int32_t* pos, nh_error* err) {
+    clear_error(err);
+    if (experts == 0 || top_k == 0) return set_error(err, NH_INVALID_SHAPE, "experts and top_k must be non-zero");
+    const size_t routes = tokens * top_k;
+    std::vector<int32_t> count(experts, 0);
+    for (size_t r = 0; r < routes; ++r) {
+        if (indices[r] < 0 || (size_t)indices[r] >= experts)
+            return set_error(err, NH_OUT_OF_RANGE, "route %zu names expert %d of %zu", r, indices[r], experts);
+        ++count[indices[r]];
+    }
+    offsets[0] = 0;
+    for (size_t e = 0; e < experts; ++e) offsets[e + 1] = offsets[e] + count[e];
+    std::vector<int32_t> next(offsets, offsets + experts);
+    for (size_t r = 0; r < routes; ++r) {
+        const int32_t slot = next[indices[r]]++;
+        perm[slot] = (int32_t)r;
+        pos[r] = slot;
+    }
+    return NH_OK;
+}
+
+nh_status nh_moe_grouped_gemm_w8a8_host(const int8_t* aq, const float* sa, int gather, size_t top_k,
+                                        const int32_t* offsets, const int32_t* perm, size_t routes, size_t a_rows,
+                                        size_t experts, const int8_t* w, const float* sw, size_t n, size_t k,
+                                        int relu2_flag, float* out, nh_error* err) {
+    clear_error(err);
+    (void)routes;
+    (void)a_rows;
+    if (experts == 0 || top_k == 0 || n == 0 || k == 0) return set_error(err, NH_INVALID_SHAPE, "invalid shape");
+    for (size_t e = 0; e < experts; ++e) {
+        const int8_t* we = w + e * n * k;
+        for (int32_t slot = offsets[e]; slot < offsets[e + 1]; ++slot) {
+            const size_t row = gather ? (size_t)perm[slot] / top_k : (size_t)slot;
+            const int8_t* a = aq + row * k;
+            for (size_t c = 0; c < n; ++c) {
+                int32_t acc = 0;
+                for (size_t d = 0; d < k; ++d) acc += (int32_t)a[d] * (int32_t)we[c * k + d];
+                float y = epilogue_w8a8(acc, sa[row], sw[e * n + c]);
+                if (relu2_flag) y = relu2(y);
+                out[(size_t)slot * n + c] = y;
+            }
+        }
+    }
+    return NH_OK;
+}
+
+nh_status nh_moe_combine_host(const float* slot_out, const int32_t* pos, const float* weights, size_t tokens,
+                              size_t top_k, size_t hidden, void* out, nh_dtype out_dtype, nh_error* err) {
+    clear_error(err);
+    if (out_dtype != NH_F32 && out_dtype != NH_BF16) return set_error(err, NH_INVALID_PARAMS, "unknown dtype");
+    for (size_t t = 0; t < tokens; ++t)
+        for (size_t h = 0; h < hidden; ++h) {
+            float v = 0.0f;
+            for (size_t j = 0; j < top_k; ++j) {
+                const size_t r = t * top_k + j;
+                const float p = weights[r] * slot_out[(size_t)pos[r] * hidden + h];
+                v = v + p;
+            }
+            store_f32(out, t * hidden + h, v, out_dtype);
+        }
+    return NH_OK;
+}
+
+// splitmix64 -> two 53-bit uniforms in (0, 1) -> Box-Muller in f64 ->
+// mean + std * z rounded to f32; (cos, sin) fill consecutive elements.
+void nh_fill_normal_f32_host(uint64_t seed, float mean, float stddev, float* out, size_t n) {
+    uint64_t state = seed;
+    auto next = [&state]() {
+        uint64_t z = (state += 0x9E3779B97F4A7C15ull);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    };
+    auto uniform = [&]() {
+        double u;
+        do u = (double)(next() >> 11) * 0x1.0p-53;
+        while (u == 0.0);
+        return u;
+    };
+    const double two_pi = 6.283185307179586476925286766559;
+    for (size_t i = 0; i < n; i += 2) {
+        const double u1 = uniform(), u2 = uniform();
+        const double r = std::sqrt(-2.0 * std::log(u1));
+        const double t = two_pi * u2;
+        out[i] = (float)((double)mean + (double)stddev * (r * std::cos(t)));
+        if (i + 1 < n) out[i + 1] = (float)((double)mean + (double)stddev * (r * std::sin(t)));
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,233 @@
+// R1..R4: MoE routing, token permutation, grouped expert GEMM, combine.
+//
+// The reference runs every selected expert densely over ALL rows and combines
+// on the host (moe.rs:207-246).  Here the routes are sorted by expert on the
+// device (counting sort, deterministic, no global atomics), each expert's
+// weights are streamed once against only the rows routed to it, and the
+// weighted combine reads each route's row back through pos[].
+#include "nh_device.h"
+
+using namespace nh;
+
+namespace {
+
+// total_cmp key of the weight in the high word, ~expert in the low word: the
+// maximum is the highest weight and, among equal weights, the lowest expert
+// (moe_routing.rs:176-180).
+__device__ __forceinline__ int64_t route_key(float w, int e) {
+    return ((int64_t)total_cmp_key(w) << 32) | (int64_t)(uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+}
+
+__device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const int64_t o = __shfl_xor(v, off, kWave);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
+
+}  // namespace
+
+// R1: one wave per token.  Expert e lives in lane e % 64, slot e / 64.
+extern "C" __global__ __launch_bounds__(256) void nh_moe_route_sigmoid_kernel(RouteArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int token = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (token >= a.tokens) return;
+    const int E = a.experts;
+    const float* s = a.scores + (int64_t)token * E;
+    int64_t key[kMaxExpertsPerLane];
+#pragma unroll
+    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
+        const int e = lane + 64 * i;
+        key[i] = e < E ? route_key(sigmoid_f32(s[e]), e) : INT64_MIN;
+    }
+    float wsel = 0.0f;  // lane j keeps the j-th selected weight (top_k <= 64)
+    int esel = 0;
+    for (int j = 0; j < a.top_k; ++j) {
+        int64_t best = INT64_MIN;
+#pragma unroll
+        for (int i = 0; i < kMaxExpertsPerLane; ++i) best = key[i] > best ? key[i] : best;
+        best = wave_max_i64(best);
+        const int e = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFF));
+        const int32_t k32 = (int32_t)(best >> 32);
+        const float w = f32_from_bits((uint32_t)total_cmp_key(f32_from_bits((uint32_t)k32)));
+#pragma unroll
+        for (int i = 0; i < kMaxExpertsPerLane; ++i)  // the owner drops it
+            if (lane + 64 * i == e) key[i] = INT64_MIN;
+        if (lane == j) {
+            wsel = w;
+            esel = e;
+        }
+    }
+    if (a.renormalize) {
+        // sum in route order, as selected_total (moe_routing.rs:207-211)
+        float total = 0.0f;
+        for (int j = 0; j < a.top_k; ++j) total = total + __shfl(wsel, j, kWave);
+        wsel = wsel / total;
+    }
+    if (a.scaling != 1.0f) wsel = wsel * a.scaling;
+    if (lane < a.top_k) {
+        a.indices[(int64_t)token * a.top_k + lane] = esel;
+        a.weights[(int64_t)token * a.top_k + lane] = wsel;
+    }
+}
+
+// R2: one workgroup of 1024 threads.  Phase 1 histograms the experts (LDS
+// atomics: counts do not depend on order), phase 2 scans them into offsets,
+// phase 3 walks the routes in order in rounds of 1024 and gives every route
+// its stable rank: inside a wave by ballot-matching equal experts, across
+// waves by handing a running per-expert base from wave to wave in order.
+extern "C" __global__ __launch_bounds__(1024) void nh_moe_permute_kernel(PermuteArgs a) {
+    extern __shared__ int sm[];  // counts[E], base[E]
+    const int E = a.experts, R = a.routes;
+    int* counts = sm;
+    int* running = sm + E;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    for (int e = tid; e < E; e += blockDim.x) {
+        counts[e] = 0;
+        running[e] = 0;
+    }
+    __syncthreads();
+    // an expert id outside [0, E) is not placed (pos = -1), so no slot can
+    // ever leave [0, routes)
+    for (int r = tid; r < R; r += blockDim.x) {
+        const int e = a.indices[r];
+        if (e >= 0 && e < E) atomicAdd(&counts[e], 1);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int carry = 0;
+        for (int base = 0; base < E; base += 64) {
+            const int e = base + lane;
+            int v = e < E ? counts[e] : 0;
+            // inclusive scan across the wave
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const int o = __shfl_up(v, off, kWave);
+                if (lane >= off) v += o;
+            }
+            if (e < E) {
+                const int excl = carry + v - (e < E ? counts[e] : 0);
+                a.offsets[e] = excl;
+                running[e] = excl;
+            }
+            carry += __shfl(v, 63, kWave);
+        }
+        if (lane == 0) a.offsets[E] = carry;
+    }
+    __syncthreads();
+    int nbits = 0;
+    while ((1 << nbits) < E) ++nbits;
+    for (int round = 0; round < R; round += blockDim.x) {
+        const int r = round + tid;
+        const int ein = r < R ? a.indices[r] : -1;
+        const bool valid = ein >= 0 && ein < E;
+        const int e = valid ? ein : -1;
+        if (r < R && !valid) a.pos[r] = -1;
+        uint64_t mask = __ballot(valid);
+        for (int b = 0; b < nbits; ++b) {
+            const uint64_t bal = __ballot(valid && ((e >> b) & 1));
+            mask &= ((e >> b) & 1) ? bal : ~bal;
+        }
+        const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        const int rank = __popcll(mask & lt);
+        const int cnt = __popcll(mask);
+        const int leader = valid ? (__ffsll((long long)mask) - 1) : 0;
+        for (int w = 0; w < nw; ++w) {
+            int base = 0;
+            if (wave == w && valid && lane == leader) {
+                base = running[e];
+                running[e] = base + cnt;
+            }
+            if (wave == w) {
+                base = __shfl(base, leader, kWave);
+                if (valid) {
+                    const int slot = base + rank;
+                    a.perm[slot] = r;
+                    a.pos[r] = slot;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// R3: grouped W8A8 GEMM.  grid.x = N tiles of 16 rows, grid.y = experts.
+// The workgroup streams its [16 x K] weight tile of expert e once per 16-row
+// block of the expert's segment (one block for a typical ~24-row segment;
+// later blocks hit L2) with K split across its waves, as the GEMV does.
+extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(GroupedGemmArgs a) {
+    __shared__ v4i red[8 * 64];
+    const int e = blockIdx.y;
+    const int tile = blockIdx.x;
+    const int seg0 = a.offsets[e], seg1 = a.offsets[e + 1];
+    if (seg0 >= seg1) return;  // no routes: this expert's weights are never read
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int N = a.N, K = a.K;
+    const int kslice = ((K + nw * 64 - 1) / (nw * 64)) * 64;
+    const int kbeg = wave * kslice;
+    const int kend = min(K, kbeg + kslice);
+    const int n = tile * 16 + r16;
+    const bool nok = n < N;
+    const int8_t* wrow = a.w + ((int64_t)e * N + (nok ? n : 0)) * K;
+    for (int m0 = seg0; m0 < seg1; m0 += 16) {
+        const int slot = m0 + r16;
+        const bool mok = slot < seg1;
+        const int arow = mok ? (a.gather ? a.perm[slot] / a.top_k : slot) : 0;
+        const int8_t* xrow = a.aq + (int64_t)arow * K;
+        v4i acc = {0, 0, 0, 0};
+        for (int k0 = kbeg; k0 < kend; k0 += 64 * 8) {
+            v4i b[8], x[8];
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const int k = k0 + s * 64 + g * 16;
+                const bool kok = k < kend;
+                b[s] = (nok && kok) ? *(const v4i*)(wrow + k) : v4i{0, 0, 0, 0};
+                x[s] = (mok && kok) ? *(const v4i*)(xrow + k) : v4i{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[s], b[s], acc, 0, 0, 0);
+        }
+        if (nw > 1) {
+            red[wave * 64 + lane] = acc;
+            __syncthreads();
+            if (wave == 0)
+                for (int w = 1; w < nw; ++w) acc += red[w * 64 + lane];
+        }
+        if (wave == 0 && nok) {
+            const float swn = a.sw[(int64_t)e * N + n];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int srow = m0 + 4 * g + r;
+                if (srow < seg1) {
+                    const int ar = a.gather ? a.perm[srow] / a.top_k : srow;
+                    float y = epilogue_w8a8(acc[r], a.sa[ar], swn);
+                    if (a.relu2) y = relu2(y);
+                    a.out[(int64_t)srow * N + n] = y;
+                }
+            }
+        }
+        if (nw > 1) __syncthreads();
+    }
+}
+
+// R4: out[t][h] = sum_j w[t,j] * slot_out[pos[t*k+j]][h], j ascending, f32
+// multiply then add (moe.rs:239-244).  grid = (ceil(H/256), T).
+extern "C" __global__ __launch_bounds__(256) void nh_moe_combine_kernel(CombineArgs a) {
+    const int t = blockIdx.y;
+    const int h = blockIdx.x * blockDim.x + threadIdx.x;
+    if (h >= a.hidden) return;
+    float v = 0.0f;
+    for (int j = 0; j < a.top_k; ++j) {
+        const int r = t * a.top_k + j;
+        const float w = a.weights[r];
+        const float x = a.slot_out[(int64_t)a.pos[r] * a.hidden + h];
+        const float p = w * x;
+        v = v + p;
+    }
+    store_out(a.out, (int64_t)t * a.hidden + h, v, a.out_dtype);
+}

@@ -1,0 +1,73 @@
+// Device-side helpers for the gfx950 kernels: wavefront reductions and
+// vector types.  Wave size is 64 on CDNA4.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "nh_kernel_args.h"
+#include "nh_numerics.h"
+
+namespace nh {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+__device__ __forceinline__ int wave_min_i32(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = min(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Block-wide max of non-negative floats / min of ints through LDS; every
+// thread gets the result.  blockDim.x must be a multiple of 64, <= 1024.
+__device__ __forceinline__ float block_max(float v, float* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = wave_max(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int i = 1; i < nw; ++i) r = fmaxf(r, red[i]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ int block_min_i32(int v, int* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = wave_min_i32(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    int r = red[0];
+    for (int i = 1; i < nw; ++i) r = min(r, red[i]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ float load_as_f32(const void* p, int64_t i, int dtype) {
+    if (dtype == DT_BF16) return bf16_to_f32(((const uint16_t*)p)[i]);
+    return ((const float*)p)[i];
+}
+
+__device__ __forceinline__ void store_out(void* p, int64_t i, float v, int dtype) {
+    if (dtype == DT_BF16)
+        ((uint16_t*)p)[i] = f32_to_bf16(v);
+    else
+        ((float*)p)[i] = v;
+}
+
+__device__ __forceinline__ bool is_finite_f32(float v) { return (f32_bits(v) & 0x7f800000u) != 0x7f800000u; }
+
+}  // namespace nh

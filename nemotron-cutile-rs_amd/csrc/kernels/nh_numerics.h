@@ -1,0 +1,142 @@
+// Scalar numerics shared by the gfx950 kernels and the library's host twins.
+// Each function is the one rounding rule the path relies on; the kernels and
+// the host fallback call the same code, so they agree bit for bit.
+#pragma once
+#include <stdint.h>
+#include <string.h>
+
+#if defined(__HIPCC__)
+#define NH_HD __host__ __device__ __forceinline__
+#else
+#define NH_HD static inline
+#endif
+
+namespace nh {
+
+NH_HD uint32_t f32_bits(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    return u;
+}
+
+NH_HD float f32_from_bits(uint32_t u) {
+    float x;
+    memcpy(&x, &u, 4);
+    return x;
+}
+
+NH_HD uint64_t f64_bits(double x) {
+    uint64_t u;
+    memcpy(&u, &x, 8);
+    return u;
+}
+
+NH_HD double f64_from_bits(uint64_t u) {
+    double x;
+    memcpy(&x, &u, 8);
+    return x;
+}
+
+// f32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+NH_HD uint16_t f32_to_bf16(float x) {
+    uint32_t u = f32_bits(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+NH_HD float bf16_to_f32(uint16_t b) { return f32_from_bits((uint32_t)b << 16); }
+
+// Symmetric int8 code of v with row scale s (nemotron-kernels/src/quantize.rs:197-198
+// style: one RN division, round half away from zero, clamp; zero point 0).
+// s == 0 covers the all-zero row and an underflowed scale.
+NH_HD int8_t quantize_i8(float v, float s) {
+    if (s == 0.0f) return 0;
+    float q = roundf(v / s);
+    q = q > 127.0f ? 127.0f : q;
+    q = q < -127.0f ? -127.0f : q;
+    return (int8_t)(int)q;
+}
+
+// Row scale from the row's absolute maximum: one RN division by 127.
+NH_HD float scale_from_amax(float amax) { return amax / 127.0f; }
+
+// W8A8 epilogue: y = ((float)acc * sx) * sw [+ bias], two RN multiplies, no FMA.
+NH_HD float epilogue_w8a8(int32_t acc, float sx, float sw) {
+    float t = (float)acc * sx;
+    return t * sw;
+}
+
+// ReLU^2 with Rust f32::max semantics (max(NaN, 0) = 0): activations.rs:68-71.
+NH_HD float relu2(float x) {
+    float r = x > 0.0f ? x : 0.0f;
+    if (x != x) r = 0.0f;
+    return r * r;
+}
+
+// expf restated from the published table-driven method used by glibc
+// (ARM optimized-routines expf, Szabolcs Nagy 2017): 32-entry 2^(i/32) table,
+// kd = round(x*32/ln2) via the 1.5*2^52 shift, r = x*32/ln2 - kd evaluated
+// with one fused multiply-add, a degree-3 polynomial for 2^(r/32) with fused
+// multiply-adds, and one final rounding to f32.  This is the x86-64 FMA build
+// of that method, the one glibc selects on FMA-capable hosts; on this image it
+// returns the same f32 as glibc expf for every finite input in [-104, 88.72]
+// (checked exhaustively on the host).  Rust f32::exp calls glibc expf on
+// linux-gnu, so routing scores computed with it match the reference's
+// sigmoid_scalar (activations.rs:73-81) exactly.
+NH_HD double exp2_table(uint32_t i) {
+    // 2^(i/32) rounded to nearest double
+    const double t[32] = {
+        0x1.0000000000000p+0, 0x1.059b0d3158574p+0, 0x1.0b5586cf9890fp+0, 0x1.11301d0125b51p+0,
+        0x1.172b83c7d517bp+0, 0x1.1d4873168b9aap+0, 0x1.2387a6e756238p+0, 0x1.29e9df51fdee1p+0,
+        0x1.306fe0a31b715p+0, 0x1.371a7373aa9cbp+0, 0x1.3dea64c123422p+0, 0x1.44e086061892dp+0,
+        0x1.4bfdad5362a27p+0, 0x1.5342b569d4f82p+0, 0x1.5ab07dd485429p+0, 0x1.6247eb03a5585p+0,
+        0x1.6a09e667f3bcdp+0, 0x1.71f75e8ec5f74p+0, 0x1.7a11473eb0187p+0, 0x1.82589994cce13p+0,
+        0x1.8ace5422aa0dbp+0, 0x1.93737b0cdc5e5p+0, 0x1.9c49182a3f090p+0, 0x1.a5503b23e255dp+0,
+        0x1.ae89f995ad3adp+0, 0x1.b7f76f2fb5e47p+0, 0x1.c199bdd85529cp+0, 0x1.cb720dcef9069p+0,
+        0x1.d5818dcfba487p+0, 0x1.dfc97337b9b5fp+0, 0x1.ea4afa2a490dap+0, 0x1.f50765b6e4540p+0};
+    return t[i & 31];
+}
+
+NH_HD float expf_rn(float x) {
+    if (x != x) return x + x;
+    if (x > 0x1.62e42ep+6f) return __builtin_inff();  // expf overflows above 88.72283
+    if (x < -0x1.9fe368p+6f) return 0.0f;              // and underflows to +0 below -103.97208
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    double xd = (double)x;
+    double kd = __builtin_fma(inv_ln2_n, xd, shift);
+    uint64_t ki = f64_bits(kd);
+    kd -= shift;
+    double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    uint64_t t = f64_bits(exp2_table((uint32_t)(ki % 32))) - ((uint64_t)(ki % 32) << 47);
+    t += ki << 47;
+    double s = f64_from_bits(t);
+    double z = __builtin_fma(c0, r, c1);
+    double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+// Numerically stable sigmoid of activations.rs:73-81, with expf_rn.
+NH_HD float sigmoid_f32(float x) {
+    if (x >= 0.0f) {
+        float z = expf_rn(-x);
+        return 1.0f / (1.0f + z);
+    }
+    float z = expf_rn(x);
+    return z / (1.0f + z);
+}
+
+// f32::total_cmp ordering key (moe_routing.rs:176-180).
+NH_HD int32_t total_cmp_key(float v) {
+    int32_t b = (int32_t)f32_bits(v);
+    return b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
+}
+
+}  // namespace nh

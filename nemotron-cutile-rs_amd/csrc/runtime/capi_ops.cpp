@@ -1,0 +1,395 @@
+// Device entry points of the C ABI: validate on the host, then enqueue.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "nh_runtime.h"
+
+using namespace nh;
+
+namespace {
+
+constexpr int64_t kMaxGrid = 0x7fffffff;
+
+unsigned grid_for(int64_t items, int per_block) {
+    int64_t g = (items + per_block - 1) / per_block;
+    g = std::max<int64_t>(1, std::min<int64_t>(g, 1 << 20));
+    return (unsigned)g;
+}
+
+// K slice per wave of the GEMV family: 1 KiB of K per wave, at most 16 waves.
+void gemv_split(int K, int* kslice, int* waves) {
+    int ks = 1024;
+    int w = (K + ks - 1) / ks;
+    if (w > 16) {
+        ks = ((K + 16 * 64 - 1) / (16 * 64)) * 64;
+        w = (K + ks - 1) / ks;
+    }
+    if (w < 1) w = 1;
+    *kslice = ks;
+    *waves = w;
+}
+
+nh_status check_dtype(nh_dtype d, nh_error* err) {
+    if (d != NH_F32 && d != NH_BF16) return set_error(err, NH_INVALID_PARAMS, "unknown dtype %d", (int)d);
+    return NH_OK;
+}
+
+// Shared validation of the W8A8 GEMM family (GemmError::InvalidShape for a
+// zero or overflowing dimension, gemm.rs:192-208; envelope for the rest).
+nh_status check_w8a8_shape(size_t m, size_t n, size_t k, nh_error* err) {
+    size_t t;
+    if (m == 0 || n == 0 || k == 0 || !mul_ok(m, k, &t) || !mul_ok(n, k, &t) || !mul_ok(m, n, &t))
+        return set_error(err, NH_INVALID_SHAPE, "invalid GEMM shape m=%zu n=%zu k=%zu", m, n, k);
+    if (!nh_supports_gemm_w8a8(m, n, k))
+        return set_error(err, NH_UNSUPPORTED, "shape m=%zu n=%zu k=%zu outside the gfx950 envelope (k %% 16 == 0, "
+                         "dims < 2^31)", m, n, k);
+    return NH_OK;
+}
+
+nh_status launch_gemv(nh_context* ctx, const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
+                      const float* bias, int M, int N, int K, void* out, nh_dtype out_dtype, nh_stream stream,
+                      nh_error* err) {
+    GemvW8A8Args a{};
+    a.xq = xq;
+    a.sx = sx;
+    a.wq = wq;
+    a.sw = sw;
+    a.bias = bias;
+    a.out = out;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    int waves;
+    gemv_split(K, &a.kslice, &waves);
+    a.ntiles = (N + 15) / 16;
+    a.out_dtype = out_dtype;
+    return launch(ctx, K_GEMV_W8A8, (unsigned)a.ntiles, 64u * waves, 0, stream, a, err);
+}
+
+nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
+                      const float* bias, int M, int N, int K, void* out, nh_dtype out_dtype, int relu2,
+                      nh_stream stream, nh_error* err) {
+    GemmW8A8Args a{};
+    a.xq = xq;
+    a.sx = sx;
+    a.wq = wq;
+    a.sw = sw;
+    a.bias = bias;
+    a.out = out;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.out_dtype = out_dtype;
+    a.relu2 = relu2;
+    // 256x128 tiles when there are enough of them to fill the chip once,
+    // 128x128 otherwise (more, smaller tiles against wave quantization).
+    const size_t lds256 = 2 * (256 + 128) * 144, lds128 = 2 * (128 + 128) * 144;
+    const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 127) / 128);
+    bool big = t256 >= ctx->cu_count && lds256 <= ctx->max_shared_per_block;
+    if (!big && lds128 > ctx->max_shared_per_block) {
+        // LDS too small for the MFMA tiles: 16-row GEMV passes (still exact)
+        for (int m0 = 0; m0 < M; m0 += 16) {
+            const int mm = std::min(16, M - m0);
+            void* o = (char*)out + (size_t)m0 * N * (out_dtype == NH_BF16 ? 2 : 4);
+            nh_status st = launch_gemv(ctx, xq + (size_t)m0 * K, sx + m0, wq, sw, bias, mm, N, K, o, out_dtype,
+                                       stream, err);
+            if (st) return st;
+        }
+        return NH_OK;
+    }
+    if (big) {
+        a.tiles_m = (M + 255) / 256;
+        a.tiles_n = (N + 127) / 128;
+        return launch(ctx, K_GEMM_W8A8, (unsigned)(a.tiles_m * a.tiles_n), 256, lds256, stream, a, err);
+    }
+    a.tiles_m = (M + 127) / 128;
+    a.tiles_n = (N + 127) / 128;
+    return launch(ctx, K_GEMM_W8A8_128, (unsigned)(a.tiles_m * a.tiles_n), 256, lds128, stream, a, err);
+}
+
+}  // namespace
+
+extern "C" {
+
+int nh_supports_gemm_w8a8(size_t m, size_t n, size_t k) {
+    return m > 0 && n > 0 && k > 0 && m < (1u << 31) && n < (1u << 31) && k < (1u << 31) && (k % 16) == 0 &&
+           (uint64_t)m * k < (1ull << 40) && (uint64_t)n * k < (1ull << 40);
+}
+
+nh_status nh_quantize_rows_i8(nh_context* ctx, const void* x, nh_dtype dtype, size_t rows, size_t cols, int8_t* q,
+                              float* scales, int32_t* row_status, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    nh_status st = check_dtype(dtype, err);
+    if (st) return st;
+    if (rows > (size_t)kMaxGrid || cols > (size_t)kMaxGrid)
+        return set_error(err, NH_UNSUPPORTED, "rows/cols must be < 2^31");
+    if ((st = bind_device(ctx, err))) return st;
+    if (rows == 0 || cols == 0) return NH_OK;  // nothing to quantize (empty inputs are valid, quantize.rs:490-501)
+    QuantizeRowsArgs a{x, q, scales, row_status, (int64_t)rows, (int64_t)cols, dtype, 0};
+    return launch(ctx, K_QUANTIZE_ROWS, (unsigned)rows, 256, 0, stream, a, err);
+}
+
+nh_status nh_dequantize_i8(nh_context* ctx, const int8_t* q, const float* scales, size_t rows, size_t cols,
+                           float* out, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    size_t total;
+    if (!mul_ok(rows, cols, &total)) return set_error(err, NH_INVALID_SHAPE, "rows*cols overflows");
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    if (total == 0) return NH_OK;
+    DequantizeI8Args a{q, scales, out, (int64_t)rows, (int64_t)cols};
+    return launch(ctx, K_DEQUANT_I8, grid_for((int64_t)total, 256), 256, 0, stream, a, err);
+}
+
+nh_status nh_dequantize_int4(nh_context* ctx, const uint8_t* packed, size_t packed_len, size_t value_count,
+                             float scale, uint32_t zero_point, float* out, size_t out_len, nh_stream stream,
+                             nh_error* err) {
+    clear_error(err);
+    // same validation order as dequantize_int4_into_host (quantize.rs:156-178)
+    if (!std::isfinite(scale) || scale <= 0.0f || zero_point > 0x0F)
+        return set_error(err, NH_INVALID_PARAMS, "invalid INT4 params scale=%g zero_point=%u", (double)scale,
+                         zero_point);
+    if (out_len != value_count) return mismatch(err, "output", value_count, out_len);
+    if (packed_len != nh_packed_int4_len(value_count))
+        return mismatch(err, "packed", nh_packed_int4_len(value_count), packed_len);
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    if (value_count == 0) return NH_OK;
+    DequantizeInt4Args a{packed, out, (int64_t)value_count, scale, (float)zero_point};
+    return launch(ctx, K_DEQUANT_INT4, grid_for((int64_t)value_count, 256), 256, 0, stream, a, err);
+}
+
+nh_status nh_gemm_w8a8(nh_context* ctx, const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
+                       const float* bias, size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype,
+                       nh_stream stream, nh_error* err) {
+    clear_error(err);
+    nh_status st;
+    if ((st = check_dtype(out_dtype, err)) || (st = check_w8a8_shape(m, n, k, err))) return st;
+    if (!aligned16(xq) || !aligned16(wq))
+        return set_error(err, NH_UNSUPPORTED, "xq and wq must be 16-byte aligned");
+    if ((st = bind_device(ctx, err))) return st;
+    if (m <= 16) return launch_gemv(ctx, xq, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, stream, err);
+    return launch_gemm(ctx, xq, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, 0, stream, err);
+}
+
+size_t nh_linear_w8a8_workspace_size(size_t m, size_t k) {
+    if (m <= 4) return 0;
+    return ((m * k + 255) / 256) * 256 + m * sizeof(float);
+}
+
+nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* wq, const float* sw,
+                         const float* bias, size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype,
+                         void* workspace, size_t workspace_bytes, int8_t* xq_out, float* sx_out, nh_stream stream,
+                         nh_error* err) {
+    clear_error(err);
+    if (m == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
+    nh_status st;
+    if ((st = check_dtype(x_dtype, err)) || (st = check_dtype(out_dtype, err)) ||
+        (st = check_w8a8_shape(m, n, k, err)))
+        return st;
+    if (!aligned16(wq)) return set_error(err, NH_UNSUPPORTED, "wq must be 16-byte aligned");
+    if ((st = bind_device(ctx, err))) return st;
+    const size_t lds = m * (k + 16) + m * sizeof(float);
+    if (m <= 4 && lds <= 65536) {
+        LinearDecodeArgs a{};
+        a.x = x;
+        a.wq = wq;
+        a.sw = sw;
+        a.bias = bias;
+        a.out = out;
+        a.xq_out = xq_out;
+        a.sx_out = sx_out;
+        a.M = (int)m;
+        a.N = (int)n;
+        a.K = (int)k;
+        int waves;
+        gemv_split((int)k, &a.kslice, &waves);
+        a.ntiles = (int)((n + 15) / 16);
+        a.x_dtype = x_dtype;
+        a.out_dtype = out_dtype;
+        return launch(ctx, K_LINEAR_DECODE, (unsigned)a.ntiles, 64u * waves, (lds + 15) & ~(size_t)15, stream, a,
+                      err);
+    }
+    // two launches: Q2 into the workspace (or the caller's xq_out/sx_out), then G1/G3
+    int8_t* xq = xq_out;
+    float* sx = sx_out;
+    if (!xq || !sx) {
+        const size_t need = ((m * k + 255) / 256) * 256 + m * sizeof(float);
+        if (!workspace || workspace_bytes < need) return mismatch(err, "workspace", need, workspace_bytes);
+        xq = (int8_t*)workspace;
+        sx = (float*)((char*)workspace + ((m * k + 255) / 256) * 256);
+    }
+    st = nh_quantize_rows_i8(ctx, x, x_dtype, m, k, xq, sx, nullptr, stream, err);
+    if (st) return st;
+    if (m <= 16) return launch_gemv(ctx, xq, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, stream, err);
+    return launch_gemm(ctx, xq, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, 0, stream, err);
+}
+
+nh_status nh_gemv_w8a32(nh_context* ctx, const float* x, const int8_t* wq, const float* sw, size_t m, size_t n,
+                        size_t k, float* y, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    nh_status st;
+    if ((st = check_w8a8_shape(m, n, k, err))) return st;
+    if (!aligned16(x) || !aligned16(wq)) return set_error(err, NH_UNSUPPORTED, "x and wq must be 16-byte aligned");
+    if ((st = bind_device(ctx, err))) return st;
+    GemvW8A32Args a{x, wq, sw, y, (int)m, (int)n, (int)k, 4};
+    const int64_t waves = (n + a.rows_per_wave - 1) / a.rows_per_wave;
+    return launch(ctx, K_GEMV_W8A32, (unsigned)((waves + 3) / 4), 256, 0, stream, a, err);
+}
+
+// ---- MoE ------------------------------------------------------------------
+nh_status nh_moe_route_sigmoid_topk(nh_context* ctx, const float* scores, size_t tokens, size_t experts,
+                                    size_t top_k, int renormalize, float scaling, int32_t* indices, float* weights,
+                                    nh_stream stream, nh_error* err) {
+    clear_error(err);
+    if (experts == 0 || top_k == 0 || top_k > experts)  // validate_shape, moe_routing.rs:261-267
+        return set_error(err, NH_INVALID_SHAPE, "invalid routing shape tokens=%zu experts=%zu top_k=%zu", tokens,
+                         experts, top_k);
+    if (experts > 1024 || top_k > 64 || tokens > (size_t)kMaxGrid / 4)
+        return set_error(err, NH_UNSUPPORTED, "device routing needs experts <= 1024 and top_k <= 64");
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    if (tokens == 0) return NH_OK;
+    RouteArgs a{scores, indices, weights, (int)tokens, (int)experts, (int)top_k, renormalize ? 1 : 0, scaling, 0};
+    return launch(ctx, K_ROUTE_SIGMOID, (unsigned)((tokens + 3) / 4), 256, 0, stream, a, err);
+}
+
+nh_status nh_moe_permute(nh_context* ctx, const int32_t* indices, size_t tokens, size_t top_k, size_t experts,
+                         int32_t* offsets, int32_t* perm, int32_t* pos, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    if (experts == 0 || top_k == 0) return set_error(err, NH_INVALID_SHAPE, "experts and top_k must be non-zero");
+    size_t routes;
+    if (!mul_ok(tokens, top_k, &routes) || routes > (size_t)kMaxGrid || experts > 4096)
+        return set_error(err, NH_UNSUPPORTED, "device permutation needs routes < 2^31 and experts <= 4096");
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    PermuteArgs a{indices, offsets, perm, pos, (int)routes, (int)experts};
+    return launch(ctx, K_PERMUTE, 1, 1024, 2 * experts * sizeof(int), stream, a, err);
+}
+
+nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const float* sa, int gather, size_t top_k,
+                                   const int32_t* offsets, const int32_t* perm, size_t routes, size_t a_rows,
+                                   size_t experts, const int8_t* w, const float* sw, size_t n, size_t k, int relu2,
+                                   float* out, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    (void)a_rows;
+    if (experts == 0 || top_k == 0) return set_error(err, NH_INVALID_SHAPE, "experts and top_k must be non-zero");
+    nh_status st;
+    if ((st = check_w8a8_shape(routes ? routes : 1, n, k, err))) return st;
+    if (!aligned16(aq) || !aligned16(w)) return set_error(err, NH_UNSUPPORTED, "aq and w must be 16-byte aligned");
+    if (experts > 65535) return set_error(err, NH_UNSUPPORTED, "experts must be <= 65535");
+    if ((st = bind_device(ctx, err))) return st;
+    if (routes == 0) return NH_OK;
+    GroupedGemmArgs a{};
+    a.aq = aq;
+    a.sa = sa;
+    a.offsets = offsets;
+    a.perm = perm;
+    a.w = w;
+    a.sw = sw;
+    a.out = out;
+    a.experts = (int)experts;
+    a.N = (int)n;
+    a.K = (int)k;
+    a.top_k = (int)top_k;
+    a.gather = gather ? 1 : 0;
+    a.relu2 = relu2 ? 1 : 0;
+    a.ntiles = (int)((n + 15) / 16);
+    return launch(ctx, K_GROUPED_GEMM, (unsigned)a.ntiles, 512, 0, stream, a, err, (unsigned)experts);
+}
+
+nh_status nh_moe_combine(nh_context* ctx, const float* slot_out, const int32_t* pos, const float* weights,
+                         size_t tokens, size_t top_k, size_t hidden, void* out, nh_dtype out_dtype, nh_stream stream,
+                         nh_error* err) {
+    clear_error(err);
+    nh_status st;
+    if ((st = check_dtype(out_dtype, err))) return st;
+    if (tokens > (size_t)kMaxGrid || hidden > (size_t)kMaxGrid || top_k == 0)
+        return set_error(err, NH_INVALID_SHAPE, "invalid combine shape");
+    if ((st = bind_device(ctx, err))) return st;
+    if (tokens == 0 || hidden == 0) return NH_OK;
+    CombineArgs a{slot_out, pos, weights, out, (int)tokens, (int)top_k, (int)hidden, out_dtype};
+    return launch(ctx, K_COMBINE, (unsigned)((hidden + 255) / 256), 256, 0, stream, a, err, (unsigned)tokens);
+}
+
+// Workspace of the fused MoE layer, 256-byte aligned fields.
+static void moe_layout(size_t T, size_t H, size_t I, size_t E, size_t k, size_t off[12]) {
+    const size_t R = T * k;
+    size_t cur = 0;
+    auto take = [&](size_t bytes) {
+        size_t o = cur;
+        cur += ((bytes + 255) / 256) * 256;
+        return o;
+    };
+    off[0] = take(R * 4);        // indices
+    off[1] = take(R * 4);        // weights
+    off[2] = take((E + 1) * 4);  // offsets
+    off[3] = take(R * 4);        // perm
+    off[4] = take(R * 4);        // pos
+    off[5] = take(T * H);        // xq
+    off[6] = take(T * 4);        // sx
+    off[7] = take(R * I * 4);    // up output (f32, ReLU^2 applied)
+    off[8] = take(R * I);        // requantized up output
+    off[9] = take(R * 4);        // its scales
+    off[10] = take(R * H * 4);   // down output per slot (f32)
+    off[11] = cur;               // total
+}
+
+size_t nh_moe_forward_w8a8_workspace_size(size_t tokens, size_t hidden, size_t inter, size_t experts,
+                                          size_t top_k) {
+    size_t off[12];
+    moe_layout(tokens, hidden, inter, experts, top_k, off);
+    return off[11];
+}
+
+void nh_moe_workspace_layout(size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
+                             size_t offsets_out[5]) {
+    size_t off[12];
+    moe_layout(tokens, hidden, inter, experts, top_k, off);
+    for (int i = 0; i < 5; ++i) offsets_out[i] = off[i];
+}
+
+nh_status nh_moe_forward_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const float* logits, size_t tokens,
+                              size_t hidden, size_t inter, size_t experts, size_t top_k, int renormalize,
+                              float scaling, const int8_t* w_up, const float* s_up, const int8_t* w_down,
+                              const float* s_down, void* out, nh_dtype out_dtype, void* workspace,
+                              size_t workspace_bytes, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    if (tokens == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
+    if (hidden == 0 || experts == 0 || top_k == 0 || top_k > experts || inter == 0)
+        return set_error(err, NH_INVALID_SHAPE, "invalid MoE shape");
+    size_t off[12];
+    moe_layout(tokens, hidden, inter, experts, top_k, off);
+    if (!workspace || workspace_bytes < off[11]) return mismatch(err, "workspace", off[11], workspace_bytes);
+    if (!aligned16(workspace)) return set_error(err, NH_UNSUPPORTED, "workspace must be 16-byte aligned");
+    char* ws = (char*)workspace;
+    int32_t* idx = (int32_t*)(ws + off[0]);
+    float* wts = (float*)(ws + off[1]);
+    int32_t* offsets = (int32_t*)(ws + off[2]);
+    int32_t* perm = (int32_t*)(ws + off[3]);
+    int32_t* pos = (int32_t*)(ws + off[4]);
+    int8_t* xq = (int8_t*)(ws + off[5]);
+    float* sx = (float*)(ws + off[6]);
+    float* h = (float*)(ws + off[7]);
+    int8_t* hq = (int8_t*)(ws + off[8]);
+    float* sh = (float*)(ws + off[9]);
+    float* d = (float*)(ws + off[10]);
+    const size_t R = tokens * top_k;
+    nh_status st;
+    if ((st = nh_quantize_rows_i8(ctx, x, x_dtype, tokens, hidden, xq, sx, nullptr, stream, err))) return st;
+    if ((st = nh_moe_route_sigmoid_topk(ctx, logits, tokens, experts, top_k, renormalize, scaling, idx, wts, stream,
+                                        err)))
+        return st;
+    if ((st = nh_moe_permute(ctx, idx, tokens, top_k, experts, offsets, perm, pos, stream, err))) return st;
+    if ((st = nh_moe_grouped_gemm_w8a8(ctx, xq, sx, 1, top_k, offsets, perm, R, tokens, experts, w_up, s_up, inter,
+                                       hidden, 1, h, stream, err)))
+        return st;
+    if ((st = nh_quantize_rows_i8(ctx, h, NH_F32, R, inter, hq, sh, nullptr, stream, err))) return st;
+    if ((st = nh_moe_grouped_gemm_w8a8(ctx, hq, sh, 0, top_k, offsets, perm, R, R, experts, w_down, s_down, hidden,
+                                       inter, 0, d, stream, err)))
+        return st;
+    return nh_moe_combine(ctx, d, pos, wts, tokens, top_k, hidden, out, out_dtype, stream, err);
+}
+
+}  // extern "C"

@@ -1,0 +1,229 @@
+// Context, buffers, streams, registry and error plumbing of the C ABI.
+#include <cstdio>
+#include <cstring>
+#include <new>
+
+#include "nh_runtime.h"
+
+// The gfx950 code object, linked in by code_object.S (.incbin).
+extern "C" const unsigned char nh_gfx950_code_object[];
+extern "C" const unsigned char nh_gfx950_code_object_end[];
+
+namespace nh {
+
+const char* const kKernelSymbols[K_COUNT] = {
+    "nh_quantize_rows_i8_kernel", "nh_dequantize_i8_kernel",   "nh_dequantize_int4_kernel",
+    "nh_gemv_w8a8_kernel",        "nh_linear_decode_w8a8_kernel", "nh_gemv_w8a32_kernel",
+    "nh_gemm_w8a8_kernel",        "nh_gemm_w8a8_128x128_kernel", "nh_moe_route_sigmoid_kernel", "nh_moe_permute_kernel",
+    "nh_moe_grouped_gemm_kernel", "nh_moe_combine_kernel",
+};
+
+void clear_error(nh_error* err) {
+    if (err) std::memset(err, 0, sizeof(*err));
+}
+
+nh_status set_error(nh_error* err, nh_status st, const char* fmt, ...) {
+    if (err) {
+        va_list ap;
+        va_start(ap, fmt);
+        std::vsnprintf(err->message, sizeof(err->message), fmt, ap);
+        va_end(ap);
+    }
+    return st;
+}
+
+nh_status mismatch(nh_error* err, const char* argument, uint64_t expected, uint64_t actual) {
+    if (err) {
+        err->argument = argument;
+        err->expected = expected;
+        err->actual = actual;
+        std::snprintf(err->message, sizeof(err->message), "%s length mismatch: expected %llu, got %llu", argument,
+                      (unsigned long long)expected, (unsigned long long)actual);
+    }
+    return NH_LENGTH_MISMATCH;
+}
+
+nh_status device_error(nh_error* err, hipError_t e, const char* what) {
+    return set_error(err, NH_DEVICE_ERROR, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+nh_status bind_device(nh_context* ctx, nh_error* err) {
+    if (!ctx) return set_error(err, NH_INVALID_PARAMS, "null context");
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return device_error(err, e, "hipGetDevice");
+    if (cur != ctx->device) {
+        e = hipSetDevice(ctx->device);
+        if (e != hipSuccess) return device_error(err, e, "hipSetDevice");
+    }
+    return NH_OK;
+}
+
+}  // namespace nh
+
+using namespace nh;
+
+extern "C" {
+
+int nh_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+nh_status nh_context_create(int device, const char* code_object_path, nh_context** out, nh_error* err) {
+    clear_error(err);
+    if (!out) return set_error(err, NH_INVALID_PARAMS, "null output pointer");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return device_error(err, e, "hipGetDeviceCount");
+    if (device < 0 || device >= count)
+        return set_error(err, NH_DEVICE_ERROR, "device %d out of range (%d devices)", device, count);
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return device_error(err, e, "hipSetDevice");
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return device_error(err, e, "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return set_error(err, NH_DEVICE_ERROR, "device %d is %s; this library is built for gfx950 only", device,
+                         prop.gcnArchName);
+    nh_context* ctx = new (std::nothrow) nh_context();
+    if (!ctx) return set_error(err, NH_DEVICE_ERROR, "out of host memory");
+    ctx->device = device;
+    ctx->cu_count = prop.multiProcessorCount;
+    ctx->max_shared_per_block = prop.sharedMemPerBlock;
+    if (code_object_path)
+        e = hipModuleLoad(&ctx->module, code_object_path);
+    else
+        e = hipModuleLoadData(&ctx->module, nh_gfx950_code_object);
+    if (e != hipSuccess) {
+        delete ctx;
+        return device_error(err, e, "hipModuleLoad(gfx950 code object)");
+    }
+    for (int i = 0; i < K_COUNT; ++i) {
+        e = hipModuleGetFunction(&ctx->fn[i], ctx->module, kKernelSymbols[i]);
+        if (e != hipSuccess) {
+            (void)hipModuleUnload(ctx->module);
+            delete ctx;
+            return device_error(err, e, kKernelSymbols[i]);
+        }
+    }
+    *out = ctx;
+    return NH_OK;
+}
+
+void nh_context_destroy(nh_context* ctx) {
+    if (!ctx) return;
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) cur = -1;
+    (void)hipSetDevice(ctx->device);
+    (void)hipModuleUnload(ctx->module);
+    if (cur >= 0) (void)hipSetDevice(cur);
+    delete ctx;
+}
+
+int nh_context_device(const nh_context* ctx) { return ctx ? ctx->device : -1; }
+
+nh_status nh_malloc(nh_context* ctx, size_t bytes, void** ptr, nh_error* err) {
+    clear_error(err);
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    if (!ptr) return set_error(err, NH_INVALID_PARAMS, "null output pointer");
+    hipError_t e = hipMalloc(ptr, bytes ? bytes : 1);
+    if (e != hipSuccess) return device_error(err, e, "hipMalloc");
+    return NH_OK;
+}
+
+nh_status nh_free(nh_context* ctx, void* ptr, nh_error* err) {
+    clear_error(err);
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    hipError_t e = hipFree(ptr);
+    if (e != hipSuccess) return device_error(err, e, "hipFree");
+    return NH_OK;
+}
+
+nh_status nh_memcpy_htod(nh_context* ctx, void* dst, const void* src, size_t bytes, nh_error* err) {
+    clear_error(err);
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    if (bytes == 0) return NH_OK;
+    hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return device_error(err, e, "hipMemcpy(HtoD)");
+    return NH_OK;
+}
+
+nh_status nh_memcpy_dtoh(nh_context* ctx, void* dst, const void* src, size_t bytes, nh_error* err) {
+    clear_error(err);
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    if (bytes == 0) return NH_OK;
+    hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return device_error(err, e, "hipMemcpy(DtoH)");
+    return NH_OK;
+}
+
+nh_status nh_memset_d8(nh_context* ctx, void* dst, int value, size_t bytes, nh_error* err) {
+    clear_error(err);
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    if (bytes == 0) return NH_OK;
+    hipError_t e = hipMemset(dst, value, bytes);
+    if (e != hipSuccess) return device_error(err, e, "hipMemset");
+    return NH_OK;
+}
+
+nh_status nh_stream_create(nh_context* ctx, nh_stream* out, nh_error* err) {
+    clear_error(err);
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    hipStream_t s = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) return device_error(err, e, "hipStreamCreate");
+    *out = (nh_stream)s;
+    return NH_OK;
+}
+
+nh_status nh_stream_destroy(nh_context* ctx, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    hipError_t e = hipStreamDestroy((hipStream_t)stream);
+    if (e != hipSuccess) return device_error(err, e, "hipStreamDestroy");
+    return NH_OK;
+}
+
+nh_status nh_stream_synchronize(nh_context* ctx, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) return device_error(err, e, "hipStreamSynchronize");
+    return NH_OK;
+}
+
+// Registry in the spirit of supported_*_kernels(): every device kernel is
+// tagged 1 (gfx950), every host twin 0.
+static const struct {
+    const char* name;
+    int backend;
+} kRegistry[] = {
+    {"quantize_rows_i8", 1},     {"dequantize_i8", 1},          {"int4_affine_dequantize", 1},
+    {"gemv_w8a8", 1},            {"linear_decode_w8a8", 1},     {"gemv_w8a32", 1},
+    {"gemm_w8a8", 1},            {"moe_sigmoid_topk", 1},       {"moe_permute", 1},
+    {"moe_grouped_gemm_w8a8", 1}, {"moe_combine", 1},           {"gemm_host", 0},
+    {"int4_affine_host", 0},     {"quantize_rows_i8_host", 0},  {"gemm_w8a8_host", 0},
+    {"gemv_w8a32_host", 0},      {"moe_sigmoid_topk_host", 0},  {"moe_softmax_topk_host", 0},
+    {"moe_permute_host", 0},     {"moe_grouped_gemm_w8a8_host", 0}, {"moe_combine_host", 0},
+};
+
+int nh_kernel_count(void) { return (int)(sizeof(kRegistry) / sizeof(kRegistry[0])); }
+
+const char* nh_kernel_name(int i, int* backend) {
+    if (i < 0 || i >= nh_kernel_count()) return nullptr;
+    if (backend) *backend = kRegistry[i].backend;
+    return kRegistry[i].name;
+}
+
+}  // extern "C"

@@ -1,0 +1,66 @@
+// Internal runtime of libnemotron_hip: the context (one loaded gfx950 code
+// object per device), kernel launch, and error plumbing shared by the C ABI.
+#pragma once
+#include <hip/hip_runtime_api.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+
+#include "../kernels/nh_kernel_args.h"
+#include "nemotron_hip.h"
+
+namespace nh {
+
+enum KernelId : int {
+    K_QUANTIZE_ROWS = 0,
+    K_DEQUANT_I8,
+    K_DEQUANT_INT4,
+    K_GEMV_W8A8,
+    K_LINEAR_DECODE,
+    K_GEMV_W8A32,
+    K_GEMM_W8A8,
+    K_GEMM_W8A8_128,
+    K_ROUTE_SIGMOID,
+    K_PERMUTE,
+    K_GROUPED_GEMM,
+    K_COMBINE,
+    K_COUNT
+};
+
+extern const char* const kKernelSymbols[K_COUNT];
+
+}  // namespace nh
+
+struct nh_context {
+    int device;
+    hipModule_t module;
+    hipFunction_t fn[nh::K_COUNT];
+    int cu_count;
+    size_t max_shared_per_block;
+};
+
+namespace nh {
+
+nh_status set_error(nh_error* err, nh_status st, const char* fmt, ...);
+nh_status mismatch(nh_error* err, const char* argument, uint64_t expected, uint64_t actual);
+nh_status device_error(nh_error* err, hipError_t e, const char* what);
+void clear_error(nh_error* err);
+
+// Makes ctx->device current for the calling thread.
+nh_status bind_device(nh_context* ctx, nh_error* err);
+
+template <class Args>
+nh_status launch(nh_context* ctx, KernelId id, unsigned gx, unsigned bx, size_t shmem, nh_stream stream,
+                 const Args& args, nh_error* err, unsigned gy = 1) {
+    void* params[] = {const_cast<Args*>(&args)};
+    hipError_t e = hipModuleLaunchKernel(ctx->fn[id], gx, gy, 1, bx, 1, 1, (unsigned)shmem, (hipStream_t)stream,
+                                         params, nullptr);
+    if (e != hipSuccess) return device_error(err, e, kKernelSymbols[id]);
+    return NH_OK;
+}
+
+inline bool mul_ok(size_t a, size_t b, size_t* out) { return !__builtin_mul_overflow(a, b, out); }
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace nh

@@ -1,0 +1,256 @@
+"""CPU-side checks of libnemotron_hip.so: it loads, exports every symbol the
+C header declares, validates arguments before touching a device, and its host
+twins (the reference's *_host functions) agree with the oracle bit for bit.
+No device compute runs here."""
+import ctypes as C
+import json
+import math
+import os
+import re
+import struct
+
+import numpy as np
+import pytest
+
+import nemotron_hip as NH
+import oracle_ctypes as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nemotron_hip.h")
+KATS = json.load(open(os.path.join(ROOT, "tests", "golden", "reference_kats.json")))
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = NH.lib()
+    declared = header_functions()
+    assert len(declared) > 40
+    missing = [name for name in declared if not hasattr(L, name)]
+    assert missing == []
+    # and the Python binding declares exactly the header's functions
+    assert sorted(NH.exported_symbols()) == declared
+
+
+def test_code_object_is_gfx950_only():
+    data = open(NH.CODE_OBJECT_PATH, "rb").read()
+    assert data[:4] == b"\x7fELF"
+    assert b"gfx950" in data
+    for other in (b"gfx942", b"gfx90a", b"sm_"):
+        assert other not in data
+
+
+def test_kernel_registry_lists_device_and_host_backends():
+    L = NH.lib()
+    names = {}
+    for i in range(L.nh_kernel_count()):
+        b = C.c_int(-1)
+        name = L.nh_kernel_name(i, C.byref(b)).decode()
+        names[name] = b.value
+    assert names["gemm_w8a8"] == 1 and names["moe_sigmoid_topk"] == 1 and names["gemv_w8a8"] == 1
+    assert names["gemm_host"] == 0 and names["moe_sigmoid_topk_host"] == 0
+    assert L.nh_kernel_name(L.nh_kernel_count(), None) is None
+
+
+def test_device_entry_points_validate_before_touching_a_device():
+    # NULL context: validation errors must win over the missing device
+    st, err = NH.call_status("nh_gemm_w8a8", None, None, None, None, None, None, 0, 4, 16, None, NH.F32, None)
+    assert st == NH.INVALID_SHAPE
+    st, err = NH.call_status("nh_gemm_w8a8", None, None, None, None, None, None, 2, 4, 12, None, NH.F32, None)
+    assert st == NH.UNSUPPORTED  # k % 16 != 0 -> caller uses the host twin
+    st, err = NH.call_status("nh_linear_w8a8", None, None, NH.BF16, None, None, None, 0, 4, 16, None, NH.BF16,
+                             None, 0, None, None, None)
+    assert st == NH.INVALID_ROW_COUNT
+    st, err = NH.call_status("nh_moe_route_sigmoid_topk", None, None, 1, 2, 3, 0, 1.0, None, None, None)
+    assert st == NH.INVALID_SHAPE
+    st, err = NH.call_status("nh_dequantize_int4", None, None, 1, 2, 0.0, 8, None, 2, None)
+    assert st == NH.INVALID_PARAMS
+    st, err = NH.call_status("nh_dequantize_int4", None, None, 1, 2, 1.0, 0, None, 1, None)
+    assert st == NH.LENGTH_MISMATCH and err.argument == b"output" and (err.expected, err.actual) == (2, 1)
+    assert NH.lib().nh_supports_gemm_w8a8(2048, 4096, 4096) == 1
+    assert NH.lib().nh_supports_gemm_w8a8(2048, 4096, 4095) == 0
+    assert NH.lib().nh_supports_gemm_w8a8(0, 4096, 4096) == 0
+
+
+def test_generator_matches_oracle_bit_for_bit():
+    for seed, mean, std, n in [(0, 0.0, 0.02, 10001), (1, 0.0, 1.0, 4096), (102, 0.5, 3.0, 7)]:
+        assert np.array_equal(NH.normal_f32(seed, n, mean, std), O.normal_f32(seed, n, mean, std))
+
+
+# ---- host twins vs oracle ---------------------------------------------------
+@pytest.mark.parametrize("kat", [k for k in KATS["int4"] if k["op"] in ("quantize_dequantize", "quantize_into")],
+                         ids=lambda k: k["src"].split("/")[-1])
+def test_int4_host_twin_reference_kats(kat):
+    vals = np.array(kat["values"], dtype=np.float32)
+    packed = np.zeros(len(kat["packed"]), dtype=np.uint8)
+    NH.call("nh_quantize_int4_host", vals.ctypes.data, vals.size, kat["scale"], kat["zero_point"],
+            packed.ctypes.data, packed.size)
+    assert packed.tolist() == kat["packed"]
+    out = np.zeros(vals.size, dtype=np.float32)
+    NH.call("nh_dequantize_int4_host", packed.ctypes.data, packed.size, vals.size, kat["scale"], kat["zero_point"],
+            out.ctypes.data, out.size)
+    if "dequantized" in kat:
+        assert np.all(np.abs(out - np.array(kat["dequantized"])) <= kat["tol"])
+
+
+def test_int4_host_twin_errors_match_reference():
+    nan = np.array([np.nan], dtype=np.float32)
+    packed = np.zeros(1, dtype=np.uint8)
+    st, err = NH.call_status("nh_quantize_int4_host", nan.ctypes.data, 1, 1.0, 8, packed.ctypes.data, 1)
+    assert st == NH.NON_FINITE_INPUT and err.index == 0 and math.isnan(err.value)
+    st, err = NH.call_status("nh_pack_int4_host", np.array([16], dtype=np.uint8).ctypes.data, 1, packed.ctypes.data, 1)
+    assert st == NH.OUT_OF_RANGE and err.byte == 16
+    two = np.array([0.0, 1.0], dtype=np.float32)
+    st, err = NH.call_status("nh_quantize_int4_host", two.ctypes.data, 2, 1.0, 8, packed.ctypes.data, 0)
+    assert st == NH.LENGTH_MISMATCH and (err.argument, err.expected, err.actual) == (b"packed", 1, 0)
+
+
+def test_quantize_rows_host_twin_matches_oracle():
+    x = O.normal_f32(4, 37 * 129).reshape(37, 129)
+    _, q_ref, s_ref, _ = O.quantize_rows_f32(x)
+    q = np.zeros_like(q_ref)
+    s = np.zeros_like(s_ref)
+    NH.call("nh_quantize_rows_i8_host", x.ctypes.data, NH.F32, 37, 129, q.ctypes.data, s.ctypes.data)
+    assert np.array_equal(q, q_ref) and np.array_equal(s, s_ref)
+    xb = O.to_bf16(x)
+    _, qb_ref, sb_ref, _ = O.quantize_rows_bf16(xb)
+    NH.call("nh_quantize_rows_i8_host", xb.ctypes.data, NH.BF16, 37, 129, q.ctypes.data, s.ctypes.data)
+    assert np.array_equal(q, qb_ref) and np.array_equal(s, sb_ref)
+    x[3, 5] = np.inf
+    st, err = NH.call_status("nh_quantize_rows_i8_host", x.ctypes.data, NH.F32, 37, 129, q.ctypes.data, s.ctypes.data)
+    assert st == NH.NON_FINITE_INPUT and err.index == 3 * 129 + 5
+
+
+@pytest.mark.parametrize("kat", KATS["gemm"] + [dict(KATS["gemm_pattern"][0], lhs=None)],
+                         ids=lambda k: k["src"].split("/")[-1])
+def test_gemm_f32_host_twin_matches_oracle(kat):
+    m, k, n = kat["m"], kat["k"], kat["n"]
+    if kat["lhs"] is None:
+        lhs = np.array([((i % 11) - 5) * 0.25 for i in range(m * k)], dtype=np.float32)
+        rhs = np.array([((i % 7) - 3) * 0.5 for i in range(k * n)], dtype=np.float32)
+    else:
+        lhs = np.array(kat["lhs"], dtype=np.float32)
+        rhs = np.array(kat["rhs"], dtype=np.float32)
+    out = np.zeros(m * n, dtype=np.float32)
+    NH.call("nh_gemm_f32_host", lhs.ctypes.data, lhs.size, rhs.ctypes.data, rhs.size, m, k, n, out.ctypes.data, out.size)
+    _, ref, _ = O.gemm_f32(lhs, rhs, m, k, n)
+    assert np.array_equal(out, ref)
+
+
+def test_gemm_f32_host_twin_errors_match_reference():
+    one = np.ones(4, dtype=np.float32)
+    st, err = NH.call_status("nh_gemm_f32_host", one.ctypes.data, 1, one.ctypes.data, 2, 1, 2, 1, one.ctypes.data, 1)
+    assert st == NH.LENGTH_MISMATCH and (err.argument, err.expected, err.actual) == (b"lhs", 2, 1)
+    st, err = NH.call_status("nh_gemm_f32_host", one.ctypes.data, 1, one.ctypes.data, 1, 2, (1 << 64) - 1, 1,
+                             one.ctypes.data, 2)
+    assert st == NH.INVALID_SHAPE
+
+
+def test_w8a8_and_w8a32_host_twins_match_oracle():
+    rng = np.random.default_rng(2)
+    m, n, k = 5, 33, 96
+    xq = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    wq = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    sx = rng.uniform(1e-3, 1e-2, m).astype(np.float32)
+    sw = rng.uniform(1e-4, 1e-3, n).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    for dt, npdt, bf in ((NH.F32, np.float32, False), (NH.BF16, np.uint16, True)):
+        out = np.zeros((m, n), dtype=npdt)
+        NH.call("nh_gemm_w8a8_host", xq.ctypes.data, sx.ctypes.data, wq.ctypes.data, sw.ctypes.data, bias.ctypes.data,
+                m, n, k, out.ctypes.data, dt)
+        assert np.array_equal(out, O.linear_w8a8(xq, sx, wq, sw, bias=bias, out_bf16=bf))
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = np.zeros((m, n), dtype=np.float32)
+    NH.call("nh_gemv_w8a32_host", x.ctypes.data, wq.ctypes.data, sw.ctypes.data, m, n, k, y.ctypes.data)
+    assert np.array_equal(y, O.gemv_w8a32(x, wq, sw))
+
+
+def test_sigmoid_host_twin_equals_glibc_expf_sigmoid():
+    # The library evaluates expf with a restated table method; the oracle
+    # calls glibc expf.  Dense sweep of the N(0,1)-relevant range plus a
+    # strided sweep of every float exponent.
+    L = NH.lib()
+    xs = np.concatenate([np.linspace(-12, 12, 200001, dtype=np.float32),
+                         np.array([0.0, -0.0, 1e-30, -1e-30, 88.7, -88.7, 103.9, -103.9, 200.0, -200.0],
+                                  dtype=np.float32)])
+    bits = np.arange(0, 0x7F800000, 7919, dtype=np.uint32)
+    xs = np.concatenate([xs, bits.view(np.float32), (bits | 0x80000000).view(np.float32)])
+    lib_s = np.array([L.nh_sigmoid_f32_host(float(v)) for v in xs[::3]], dtype=np.float32)
+    ora_s = np.array([O.sigmoid(float(v)) for v in xs[::3]], dtype=np.float32)
+    assert np.array_equal(lib_s.view(np.uint32), ora_s.view(np.uint32))
+
+
+@pytest.mark.parametrize("kat", KATS["routing_sigmoid"], ids=lambda k: k["src"].split("/")[-1])
+def test_route_host_twin_reference_kats(kat):
+    t, e, k = kat["tokens"], kat["experts"], kat["top_k"]
+    scores = np.array(kat["scores"], dtype=np.float32)
+    idx = np.zeros(max(t * k, 1), dtype=np.int32)
+    w = np.zeros(max(t * k, 1), dtype=np.float32)
+    NH.call("nh_moe_route_sigmoid_topk_host", scores.ctypes.data, scores.size, t, e, k, 0, 1.0, idx.ctypes.data,
+            t * k, w.ctypes.data, t * k)
+    _, ridx, rw, _ = O.route_sigmoid(scores, t, e, k)
+    assert np.array_equal(idx[:t * k], ridx) and np.array_equal(w[:t * k], rw)
+
+
+def test_route_host_twins_match_oracle_on_random_logits():
+    t, e, k = 64, 128, 6
+    scores = O.normal_f32(2, t * e)
+    for renorm, scaling in ((0, 1.0), (1, 1.0), (1, 2.5)):
+        idx = np.zeros(t * k, dtype=np.int32)
+        w = np.zeros(t * k, dtype=np.float32)
+        NH.call("nh_moe_route_sigmoid_topk_host", scores.ctypes.data, scores.size, t, e, k, renorm, scaling,
+                idx.ctypes.data, t * k, w.ctypes.data, t * k)
+        _, ridx, rw, _ = O.route_sigmoid(scores, t, e, k, renormalize=bool(renorm), scaling=scaling)
+        assert np.array_equal(idx, ridx) and np.array_equal(w, rw)
+    idx = np.zeros(t * k, dtype=np.int32)
+    w = np.zeros(t * k, dtype=np.float32)
+    NH.call("nh_moe_route_softmax_topk_host", scores.ctypes.data, scores.size, t, e, k, idx.ctypes.data, t * k,
+            w.ctypes.data, t * k)
+    _, ridx, rw, _ = O.route_softmax(scores, t, e, k)
+    assert np.array_equal(idx, ridx) and np.array_equal(w, rw)
+
+
+@pytest.mark.parametrize("kat", KATS["routing_errors"], ids=lambda k: k["src"].split("/")[-1])
+def test_route_host_twin_reference_error_kats(kat):
+    buf = np.zeros(8, dtype=np.float32)
+    ibuf = np.zeros(8, dtype=np.int32)
+    st, err = NH.call_status("nh_moe_route_sigmoid_topk_host", buf.ctypes.data, kat["scores_len"], kat["tokens"],
+                             kat["experts"], kat["top_k"], 0, 1.0, ibuf.ctypes.data, kat["indices_len"],
+                             buf.ctypes.data, kat["weights_len"])
+    if kat["error"] == "InvalidShape":
+        assert st == NH.INVALID_SHAPE
+    else:
+        assert st == NH.LENGTH_MISMATCH
+        assert (err.argument.decode(), err.expected, err.actual) == (kat["argument"], kat["expected"], kat["actual"])
+
+
+def test_moe_host_twins_match_oracle():
+    rng = np.random.default_rng(11)
+    tokens, k_top, experts, hidden, inter = 19, 3, 7, 64, 32
+    idx = np.stack([rng.choice(experts, size=k_top, replace=False) for _ in range(tokens)]).astype(np.int32).ravel()
+    R = tokens * k_top
+    offsets = np.zeros(experts + 1, dtype=np.int32)
+    perm = np.zeros(R, dtype=np.int32)
+    pos = np.zeros(R, dtype=np.int32)
+    NH.call("nh_moe_permute_host", idx.ctypes.data, tokens, k_top, experts, offsets.ctypes.data, perm.ctypes.data,
+            pos.ctypes.data)
+    o_off, o_perm, o_pos = O.moe_permute(idx, tokens, k_top, experts)
+    assert np.array_equal(offsets, o_off) and np.array_equal(perm, o_perm) and np.array_equal(pos, o_pos)
+    xq = rng.integers(-127, 128, size=(tokens, hidden), dtype=np.int8)
+    sx = rng.uniform(1e-3, 1e-2, tokens).astype(np.float32)
+    w = rng.integers(-127, 128, size=(experts, inter, hidden), dtype=np.int8)
+    sw = rng.uniform(1e-4, 1e-3, (experts, inter)).astype(np.float32)
+    out = np.zeros((R, inter), dtype=np.float32)
+    NH.call("nh_moe_grouped_gemm_w8a8_host", xq.ctypes.data, sx.ctypes.data, 1, k_top, offsets.ctypes.data,
+            perm.ctypes.data, R, tokens, experts, w.ctypes.data, sw.ctypes.data, inter, hidden, 1, out.ctypes.data)
+    ref = O.moe_grouped(xq, sx, True, k_top, offsets, perm, w, sw, relu2=True)
+    assert np.array_equal(out, ref)
+    weights = rng.uniform(0, 1, R).astype(np.float32)
+    comb = np.zeros((tokens, inter), dtype=np.uint16)
+    NH.call("nh_moe_combine_host", out.ctypes.data, pos.ctypes.data, weights.ctypes.data, tokens, k_top, inter,
+            comb.ctypes.data, NH.BF16)
+    assert np.array_equal(comb, O.moe_combine(out, pos, weights, tokens, k_top, inter, out_bf16=True))

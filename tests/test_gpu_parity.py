@@ -1,0 +1,350 @@
+"""Parity of the gfx950 path with the CPU oracle, through the C ABI.
+
+Bar: int8 codes, scales, int32 accumulators,
+routing indices and permutations bit-exact; float outputs bit-exact where the
+arithmetic is the same sequence of IEEE operations (the W8A8 epilogue,
+combine), and within max_i |y-r| / max(|r_i|, 1e-6 max|r|) <= 1e-3 (f32) /
+1e-2 (bf16) where the summation order differs (W8A32).
+Inputs: the seeded generator (splitmix64 + Box-Muller), W ~ N(0, 0.02) seed 0,
+activations ~ N(0, 1) seed 1, router logits seed 2, expert e seed 100 + e.
+"""
+import ctypes
+import functools
+import sys
+
+import numpy as np
+import pytest
+
+import nemotron_hip as NH
+import oracle_ctypes as O
+
+pytestmark = pytest.mark.gpu
+
+
+def note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = NH.Context(0)
+    yield c
+    c.close()
+
+
+def rel_err(y, r):
+    y = np.asarray(y, dtype=np.float64)
+    r = np.asarray(r, dtype=np.float64)
+    floor = 1e-6 * np.max(np.abs(r)) if r.size else 0.0
+    return float(np.max(np.abs(y - r) / np.maximum(np.abs(r), floor))) if r.size else 0.0
+
+
+@functools.lru_cache(maxsize=8)
+def quantized_weights(n, k, seed=0):
+    w = O.normal_f32(seed, n * k, 0.0, 0.02).reshape(n, k)
+    st, q, s, _ = O.quantize_rows_f32(w)
+    assert st == O.OK
+    return w, q, s
+
+
+def activations_bf16(m, k, seed=1):
+    return O.to_bf16(O.normal_f32(seed, m * k)).reshape(m, k)
+
+
+# ---- Q1/Q2/Q3 ----------------------------------------------------------------
+@pytest.mark.parametrize("rows,cols,dtype", [(1, 4096, "bf16"), (16, 8192, "bf16"), (3072, 1856, "f32"),
+                                             (4096, 4096, "f32"), (7, 33, "f32"), (5, 1, "bf16")])
+def test_quantize_rows_bit_exact(ctx, rows, cols, dtype):
+    note(f"quantize_rows {rows}x{cols} {dtype}")
+    x = O.normal_f32(5, rows * cols, 0.0, 0.02 if dtype == "f32" else 1.0).reshape(rows, cols)
+    if dtype == "bf16":
+        xb = O.to_bf16(x)
+        st, q_ref, s_ref, _ = O.quantize_rows_bf16(xb)
+        dx, dt = ctx.upload(xb), NH.BF16
+    else:
+        st, q_ref, s_ref, _ = O.quantize_rows_f32(x)
+        dx, dt = ctx.upload(x), NH.F32
+    dq = ctx.empty((rows, cols), np.int8)
+    ds = ctx.empty(rows, np.float32)
+    dstat = ctx.empty(rows, np.int32)
+    NH.call("nh_quantize_rows_i8", ctx.handle, dx.ptr, dt, rows, cols, dq.ptr, ds.ptr, dstat.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(dq.numpy(), q_ref)
+    assert np.array_equal(ds.numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.all(dstat.numpy() == -1)
+
+
+def test_quantize_rows_special_rows(ctx):
+    note("quantize_rows special rows")
+    tiny = np.float32(1e-45)
+    x = np.zeros((5, 64), dtype=np.float32)
+    x[1, :7] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.49999988, -126.5]  # ties, s = 1
+    x[2, :3] = [tiny, 0.0, -tiny]                               # underflowed scale
+    x[3] = np.linspace(-3e-39, 3e-39, 64, dtype=np.float32)     # subnormal row
+    x[4] = 1.0
+    x[4, 9] = np.nan
+    x[4, 20] = np.inf
+    st, q_ref, s_ref, err = O.quantize_rows_f32(x[:4])
+    dx = ctx.upload(x)
+    dq = ctx.empty((5, 64), np.int8)
+    ds = ctx.empty(5, np.float32)
+    dstat = ctx.empty(5, np.int32)
+    NH.call("nh_quantize_rows_i8", ctx.handle, dx.ptr, NH.F32, 5, 64, dq.ptr, ds.ptr, dstat.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(dq.numpy()[:4], q_ref)
+    assert np.array_equal(ds.numpy()[:4].view(np.uint32), s_ref.view(np.uint32))
+    assert dstat.numpy().tolist() == [-1, -1, -1, -1, 9]
+
+
+def test_dequantize_i8_bit_exact(ctx):
+    note("dequantize_i8")
+    _, q, s = quantized_weights(256, 1024)
+    dq, ds = ctx.upload(q), ctx.upload(s)
+    out = ctx.empty(q.shape, np.float32)
+    NH.call("nh_dequantize_i8", ctx.handle, dq.ptr, ds.ptr, q.shape[0], q.shape[1], out.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(out.numpy(), O.dequantize_i8(q, s))
+
+
+# ---- Q0d --------------------------------------------------------------------
+@pytest.mark.parametrize("packed,count,scale,zp", [([0x76, 0x98, 0x0A], 5, 0.5, 8), ([0x76, 0x98], 4, 0.5, 8),
+                                                   (None, 1_000_003, 0.037, 3)])
+def test_dequantize_int4_matches_host_reference(ctx, packed, count, scale, zp):
+    note(f"dequantize_int4 n={count}")
+    if packed is None:
+        rng = np.random.default_rng(0)
+        packed = rng.integers(0, 256, size=(count + 1) // 2, dtype=np.uint8)
+    packed = np.array(packed, dtype=np.uint8)
+    ref = np.zeros(count, dtype=np.float32)
+    err = O.OrError()
+    assert O.lib().or_dequantize_int4(O.ptr(packed), packed.size, count, scale, zp, O.ptr(ref), count,
+                                      O.C.byref(err)) == O.OK
+    dp = ctx.upload(packed)
+    out = ctx.empty(count, np.float32)
+    NH.call("nh_dequantize_int4", ctx.handle, dp.ptr, packed.size, count, scale, zp, out.ptr, count, None)
+    ctx.synchronize()
+    assert np.array_equal(out.numpy(), ref)  # reference tolerance 1e-6 (quantize.rs:585-617); exact here
+
+
+# ---- G1: W8A8 GEMV (M <= 16) ----------------------------------------------------
+@pytest.mark.parametrize("m,n,k", [(1, 16384, 4096), (4, 16384, 4096), (16, 16384, 4096), (1, 4096, 8192),
+                                   (4, 4096, 8192), (16, 4096, 8192), (3, 1000, 80), (16, 20, 4112)])
+def test_gemv_w8a8_bit_exact(ctx, m, n, k):
+    note(f"gemv_w8a8 m={m} n={n} k={k}")
+    _, wq, sw = quantized_weights(n, k)
+    x = activations_bf16(m, k)
+    _, xq, sx, _ = O.quantize_rows_bf16(x)
+    bias = O.normal_f32(7, n, 0.0, 0.1)
+    d = {name: ctx.upload(a) for name, a in dict(xq=xq, sx=sx, wq=wq, sw=sw, bias=bias).items()}
+    for out_dt, np_dt, use_bias in ((NH.BF16, np.uint16, False), (NH.F32, np.float32, True)):
+        out = ctx.empty((m, n), np_dt)
+        NH.call("nh_gemm_w8a8", ctx.handle, d["xq"].ptr, d["sx"].ptr, d["wq"].ptr, d["sw"].ptr,
+                d["bias"].ptr if use_bias else None, m, n, k, out.ptr, out_dt, None)
+        ctx.synchronize()
+        ref = O.linear_w8a8(xq, sx, wq, sw, bias=bias if use_bias else None, out_bf16=(out_dt == NH.BF16))
+        got = out.numpy()
+        assert np.array_equal(got, ref), f"max diff {np.max(np.abs(got.astype(np.float64) - ref))}"
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 16])
+def test_linear_decode_unit_bit_exact(ctx, m):
+    n, k = 16384, 4096
+    note(f"linear_w8a8 decode m={m}")
+    _, wq, sw = quantized_weights(n, k)
+    x = activations_bf16(m, k, seed=1 + m)
+    _, xq_ref, sx_ref, _ = O.quantize_rows_bf16(x)
+    ref = O.linear_w8a8(xq_ref, sx_ref, wq, sw, out_bf16=True)
+    dx, dw, ds = ctx.upload(x), ctx.upload(wq), ctx.upload(sw)
+    out = ctx.empty((m, n), np.uint16)
+    xq = ctx.empty((m, k), np.int8)
+    sx = ctx.empty(m, np.float32)
+    ws_bytes = NH.lib().nh_linear_w8a8_workspace_size(m, k)
+    ws = ctx.empty(max(ws_bytes, 1), np.uint8)
+    NH.call("nh_linear_w8a8", ctx.handle, dx.ptr, NH.BF16, dw.ptr, ds.ptr, None, m, n, k, out.ptr, NH.BF16,
+            ws.ptr, ws_bytes, xq.ptr, sx.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(xq.numpy(), xq_ref)
+    assert np.array_equal(sx.numpy().view(np.uint32), sx_ref.view(np.uint32))
+    assert np.array_equal(out.numpy(), ref)
+    # without the optional quantized outputs (workspace path for m > 4)
+    out2 = ctx.empty((m, n), np.uint16)
+    NH.call("nh_linear_w8a8", ctx.handle, dx.ptr, NH.BF16, dw.ptr, ds.ptr, None, m, n, k, out2.ptr, NH.BF16,
+            ws.ptr, ws_bytes, None, None, None)
+    ctx.synchronize()
+    assert np.array_equal(out2.numpy(), ref)
+
+
+# ---- G2: W8A32 dequant GEMV ------------------------------------
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (2, 1000, 80)])
+def test_gemv_w8a32_within_tolerance(ctx, m, n, k):
+    note(f"gemv_w8a32 m={m} n={n} k={k}")
+    _, wq, sw = quantized_weights(n, k)
+    x = O.normal_f32(1, m * k).reshape(m, k)
+    ref = O.gemv_w8a32(x, wq, sw)
+    dx, dw, ds = ctx.upload(x), ctx.upload(wq), ctx.upload(sw)
+    y = ctx.empty((m, n), np.float32)
+    NH.call("nh_gemv_w8a32", ctx.handle, dx.ptr, dw.ptr, ds.ptr, m, n, k, y.ptr, None)
+    ctx.synchronize()
+    got = y.numpy()
+    assert rel_err(got, ref) <= 1e-3  # north_star f32 tolerance
+    # f64 accumulation in another order: at most one f32 ulp from the reference path
+    ulps = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1
+
+
+# ---- G3: W8A8 GEMM (prefill) -----------------------------------------------------
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 4096), (2048, 21504, 4096), (2048, 4096, 21504), (37, 100, 64),
+                                   (300, 130, 272), (17, 4096, 4096), (513, 2688, 1856)])
+def test_gemm_w8a8_bit_exact(ctx, m, n, k):
+    note(f"gemm_w8a8 m={m} n={n} k={k}")
+    _, wq, sw = quantized_weights(n, k)
+    x = activations_bf16(m, k)
+    _, xq, sx, _ = O.quantize_rows_bf16(x)
+    dxq, dsx, dw, dsw = ctx.upload(xq), ctx.upload(sx), ctx.upload(wq), ctx.upload(sw)
+    out = ctx.empty((m, n), np.uint16)
+    NH.call("nh_gemm_w8a8", ctx.handle, dxq.ptr, dsx.ptr, dw.ptr, dsw.ptr, None, m, n, k, out.ptr, NH.BF16, None)
+    ctx.synchronize()
+    got = out.numpy()
+    rows = np.arange(m) if m * n * k <= 2e9 else np.unique(np.concatenate(
+        [np.arange(0, m, max(1, m // 24)), [m - 1, 255, 256, 1023, 1024]]))
+    rows = rows[rows < m]
+    ref = O.linear_w8a8(xq[rows], sx[rows], wq, sw, out_bf16=True)
+    assert np.array_equal(got[rows], ref)
+
+
+# ---- R1..R4: MoE -----------------------------------------------------------------
+def route_on_device(ctx, scores, t, e, k, renorm, scaling=1.0):
+    ds = ctx.upload(scores)
+    di = ctx.empty(t * k, np.int32)
+    dw = ctx.empty(t * k, np.float32)
+    NH.call("nh_moe_route_sigmoid_topk", ctx.handle, ds.ptr, t, e, k, renorm, scaling, di.ptr, dw.ptr, None)
+    ctx.synchronize()
+    return di.numpy(), dw.numpy()
+
+
+@pytest.mark.parametrize("t,e,k,renorm,scaling", [(512, 128, 6, 1, 1.0), (512, 128, 6, 0, 1.0), (64, 128, 6, 1, 2.5),
+                                                  (3, 1000, 8, 1, 1.0), (5, 7, 7, 0, 1.0)])
+def test_route_sigmoid_bit_exact(ctx, t, e, k, renorm, scaling):
+    note(f"route t={t} e={e} k={k} renorm={renorm}")
+    scores = O.normal_f32(2, t * e)
+    idx, w = route_on_device(ctx, scores, t, e, k, renorm, scaling)
+    _, ridx, rw, _ = O.route_sigmoid(scores, t, e, k, renormalize=bool(renorm), scaling=scaling)
+    assert np.array_equal(idx, ridx)
+    assert np.array_equal(w.view(np.uint32), rw.view(np.uint32))
+
+
+def test_route_reference_kats_on_device(ctx):
+    note("route KATs")
+    for scores, t, e, k, want_idx, want_w in [
+            ([0.0, 1.0, -1.0, 2.0], 1, 4, 2, [3, 1], [0.880797, 0.7310586]),  # moe_routing.rs:618-623
+            ([0.0, 1.0, -1.0, 2.0, 5.0, -5.0, 0.5, 0.6], 2, 4, 2, [3, 1, 0, 3],
+             [0.880797, 0.7310586, 0.9933072, 0.6456563]),                       # :629-641
+            ([0.0, 0.0, 1.0], 1, 3, 2, [2, 0], [0.7310586, 0.5]),                # :647-653 ties
+            ([0.1, 0.9, 0.4, 0.6], 2, 2, 1, None, None)]:                        # :809-822
+        s = np.array(scores, dtype=np.float32)
+        idx, w = route_on_device(ctx, s, t, e, k, 0)
+        _, ridx, rw, _ = O.route_sigmoid(s, t, e, k)
+        assert np.array_equal(idx, ridx) and np.all(np.abs(w - rw) <= 5e-6)
+        if want_idx is not None:
+            assert idx.tolist() == want_idx and np.all(np.abs(w - np.array(want_w)) <= 1e-6)
+    # moe_routing.rs:846-864: 128 experts, top-6, heavily tied pattern
+    t, e, k = 2, 128, 6
+    s = np.array([((x % 17) - 8.0) * 0.375 + tt * 0.125 - 0.05 for tt in range(t) for x in range(e)], dtype=np.float32)
+    idx, w = route_on_device(ctx, s, t, e, k, 0)
+    _, ridx, rw, _ = O.route_sigmoid(s, t, e, k)
+    assert np.array_equal(idx, ridx) and np.array_equal(w, rw)
+
+
+@pytest.mark.parametrize("t,k,e", [(512, 6, 128), (1, 1, 1), (1000, 8, 64), (3, 2, 1000), (2000, 6, 128)])
+def test_permute_bit_exact(ctx, t, k, e):
+    note(f"permute t={t} k={k} e={e}")
+    rng = np.random.default_rng(t + e)
+    idx = np.stack([rng.choice(e, size=k, replace=False) for _ in range(t)]).astype(np.int32).ravel()
+    ref = O.moe_permute(idx, t, k, e)
+    di = ctx.upload(idx)
+    off = ctx.empty(e + 1, np.int32)
+    perm = ctx.empty(t * k, np.int32)
+    pos = ctx.empty(t * k, np.int32)
+    NH.call("nh_moe_permute", ctx.handle, di.ptr, t, k, e, off.ptr, perm.ptr, pos.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(off.numpy(), ref[0])
+    assert np.array_equal(perm.numpy(), ref[1])
+    assert np.array_equal(pos.numpy(), ref[2])
+
+
+def moe_weights(experts, inter, hidden):
+    up = np.empty((experts, inter, hidden), dtype=np.int8)
+    down = np.empty((experts, hidden, inter), dtype=np.int8)
+    su = np.empty((experts, inter), dtype=np.float32)
+    sd = np.empty((experts, hidden), dtype=np.float32)
+    for e in range(experts):
+        w = O.normal_f32(100 + e, inter * hidden + hidden * inter, 0.0, 0.02)
+        _, q, s, _ = O.quantize_rows_f32(w[: inter * hidden].reshape(inter, hidden))
+        up[e], su[e] = q, s
+        _, q, s, _ = O.quantize_rows_f32(w[inter * hidden:].reshape(hidden, inter))
+        down[e], sd[e] = q, s
+    return up, su, down, sd
+
+
+@functools.lru_cache(maxsize=2)
+def moe_case(tokens, hidden, inter, experts, top_k):
+    x = activations_bf16(tokens, hidden)
+    logits = O.normal_f32(2, tokens * experts)
+    up, su, down, sd = moe_weights(experts, inter, hidden)
+    return x, logits, up, su, down, sd
+
+
+@pytest.mark.parametrize("tokens,hidden,inter,experts,top_k", [(64, 2688, 1856, 128, 6), (13, 64, 32, 8, 3)])
+def test_moe_stages_bit_exact(ctx, tokens, hidden, inter, experts, top_k):
+    note(f"moe stages t={tokens} h={hidden} i={inter} e={experts} k={top_k}")
+    x, logits, up, su, down, sd = moe_case(tokens, hidden, inter, experts, top_k)
+    _, xq, sx, _ = O.quantize_rows_bf16(x)
+    _, idx, w, _ = O.route_sigmoid(logits, tokens, experts, top_k, renormalize=True)
+    offsets, perm, pos = O.moe_permute(idx, tokens, top_k, experts)
+    R = tokens * top_k
+    h_ref = O.moe_grouped(xq, sx, True, top_k, offsets, perm, up, su, relu2=True)
+    d = {n: ctx.upload(a) for n, a in dict(xq=xq, sx=sx, off=offsets, perm=perm, pos=pos, w=w, up=up, su=su,
+                                           down=down, sd=sd).items()}
+    h = ctx.empty((R, inter), np.float32)
+    NH.call("nh_moe_grouped_gemm_w8a8", ctx.handle, d["xq"].ptr, d["sx"].ptr, 1, top_k, d["off"].ptr, d["perm"].ptr,
+            R, tokens, experts, d["up"].ptr, d["su"].ptr, inter, hidden, 1, h.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(h.numpy(), h_ref)
+    _, hq, sh, _ = O.quantize_rows_f32(h_ref)
+    d_ref = O.moe_grouped(hq, sh, False, top_k, offsets, perm, down, sd, relu2=False)
+    dhq, dsh = ctx.upload(hq), ctx.upload(sh)
+    dd = ctx.empty((R, hidden), np.float32)
+    NH.call("nh_moe_grouped_gemm_w8a8", ctx.handle, dhq.ptr, dsh.ptr, 0, top_k, d["off"].ptr, d["perm"].ptr, R, R,
+            experts, d["down"].ptr, d["sd"].ptr, hidden, inter, 0, dd.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(dd.numpy(), d_ref)
+    out = ctx.empty((tokens, hidden), np.uint16)
+    NH.call("nh_moe_combine", ctx.handle, dd.ptr, d["pos"].ptr, d["w"].ptr, tokens, top_k, hidden, out.ptr, NH.BF16,
+            None)
+    ctx.synchronize()
+    assert np.array_equal(out.numpy(), O.moe_combine(d_ref, pos, w, tokens, top_k, hidden, out_bf16=True))
+
+
+@pytest.mark.parametrize("tokens,hidden,inter,experts,top_k", [(64, 2688, 1856, 128, 6), (13, 64, 32, 8, 3)])
+def test_moe_forward_bit_exact(ctx, tokens, hidden, inter, experts, top_k):
+    note(f"moe forward t={tokens} h={hidden} i={inter} e={experts} k={top_k}")
+    x, logits, up, su, down, sd = moe_case(tokens, hidden, inter, experts, top_k)
+    st, ref, idx, w, offsets, perm, pos = O.moe_forward_w8a8(x, logits, up, su, down, sd, top_k, renormalize=True)
+    assert st == O.OK
+    ws_bytes = NH.lib().nh_moe_forward_w8a8_workspace_size(tokens, hidden, inter, experts, top_k)
+    ws = ctx.empty(ws_bytes, np.uint8)
+    dx, dl = ctx.upload(x), ctx.upload(logits)
+    dup, dsu, ddown, dsd = ctx.upload(up), ctx.upload(su), ctx.upload(down), ctx.upload(sd)
+    out = ctx.empty((tokens, hidden), np.uint16)
+    NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
+            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, None)
+    ctx.synchronize()
+    lay = (ctypes.c_size_t * 5)()
+    NH.lib().nh_moe_workspace_layout(tokens, hidden, inter, experts, top_k, lay)
+    wsh = ws.numpy()
+    R = tokens * top_k
+    assert np.array_equal(wsh[lay[0]:lay[0] + 4 * R].view(np.int32), idx)
+    assert np.array_equal(wsh[lay[2]:lay[2] + 4 * (experts + 1)].view(np.int32), offsets)
+    assert np.array_equal(wsh[lay[3]:lay[3] + 4 * R].view(np.int32), perm)
+    assert np.array_equal(out.numpy(), ref)
