@@ -70,4 +70,16 @@ __device__ __forceinline__ void store_out(void* p, int64_t i, float v, int dtype
 
 __device__ __forceinline__ bool is_finite_f32(float v) { return (f32_bits(v) & 0x7f800000u) != 0x7f800000u; }
 
+// Raw buffer resource over [base, base + bytes): a buffer load whose offset
+// falls outside returns zeros instead of touching memory (bytes < 2^31).
+// Loads address through one VGPR offset plus a 12-bit immediate, so a run of
+// loads at fixed strides needs a single address register.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ v4i buffer_load16(__amdgpu_buffer_rsrc_t r, int offset) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0));
+}
+
 }  // namespace nh

@@ -58,6 +58,25 @@ NH_HD int8_t quantize_i8(float v, float s) {
     return (int8_t)(int)q;
 }
 
+// quantize_i8 without a division on the common path.  With r = RN(1/s) and
+// s normal, t = RN(v * r) is within 2^-23 |v/s| <= 1.6e-5 of v/s, and RN(v/s)
+// within 3.9e-6 of it, so both lie on the same side of every half-integer
+// unless t is within 2^-15 of one; only then is the exact division done.
+// Returns exactly quantize_i8(v, s) for every finite v and s >= 0.
+NH_HD int8_t quantize_i8_rcp(float v, float s, float r) {
+    if (s < 0x1p-126f) return quantize_i8(v, s);  // zero or subnormal scale: exact path
+    const float t = v * r;
+    // nearest integer of t by the 1.5 * 2^23 shift (exact for |t| < 2^22);
+    // away from half-integers that is also round-half-away-from-zero
+    const float q = (t + 0x1.8p23f) - 0x1.8p23f;
+    const float d = t - q;
+    if ((d < 0.0f ? -d : d) >= 0.5f - 0x1p-15f) return quantize_i8(v, s);
+    int qi = (int)q;
+    qi = qi > 127 ? 127 : qi;
+    qi = qi < -127 ? -127 : qi;
+    return (int8_t)qi;
+}
+
 // Row scale from the row's absolute maximum: one RN division by 127.
 NH_HD float scale_from_amax(float amax) { return amax / 127.0f; }
 

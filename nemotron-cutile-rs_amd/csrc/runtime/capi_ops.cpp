@@ -17,12 +17,13 @@ unsigned grid_for(int64_t items, int per_block) {
     return (unsigned)g;
 }
 
-// K slice per wave of the GEMV family: 1 KiB of K per wave, at most 16 waves.
+// K slice per wave of the GEMV family: 1 KiB of K per wave, at most 8 waves
+// (longer slices are streamed as several 1 KiB slabs).
 void gemv_split(int K, int* kslice, int* waves) {
     int ks = 1024;
     int w = (K + ks - 1) / ks;
-    if (w > 16) {
-        ks = ((K + 16 * 64 - 1) / (16 * 64)) * 64;
+    if (w > 8) {
+        ks = ((K + 8 * 64 - 1) / (8 * 64)) * 64;
         w = (K + ks - 1) / ks;
     }
     if (w < 1) w = 1;
@@ -190,8 +191,12 @@ nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
         return st;
     if (!aligned16(wq)) return set_error(err, NH_UNSUPPORTED, "wq must be 16-byte aligned");
     if ((st = bind_device(ctx, err))) return st;
-    const size_t lds = m * (k + 16) + m * sizeof(float);
-    if (m <= 4 && lds <= 65536) {
+    const size_t lds = m * (k + 16);
+    // the fused kernel keeps each thread's share of the bf16 rows in registers
+    // (K <= 16 * threads, i.e. K <= 8192 with the GEMV split)
+    const bool fusable = m <= 4 && k <= 8192 && x_dtype == NH_BF16 && lds <= 65536 && aligned16(x) &&
+                         ((uintptr_t)xq_out & 7u) == 0;
+    if (fusable) {
         LinearDecodeArgs a{};
         a.x = x;
         a.wq = wq;
@@ -208,7 +213,8 @@ nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
         a.ntiles = (int)((n + 15) / 16);
         a.x_dtype = x_dtype;
         a.out_dtype = out_dtype;
-        return launch(ctx, K_LINEAR_DECODE, (unsigned)a.ntiles, 64u * waves, (lds + 15) & ~(size_t)15, stream, a,
+        const KernelId kid = m == 1 ? K_LINEAR_DECODE_M1 : (m == 2 ? K_LINEAR_DECODE_M2 : K_LINEAR_DECODE);
+        return launch(ctx, kid, (unsigned)a.ntiles, 64u * waves, (lds + 15) & ~(size_t)15, stream, a,
                       err);
     }
     // two launches: Q2 into the workspace (or the caller's xq_out/sx_out), then G1/G3

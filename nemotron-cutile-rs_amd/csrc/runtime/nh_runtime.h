@@ -17,7 +17,9 @@ enum KernelId : int {
     K_DEQUANT_I8,
     K_DEQUANT_INT4,
     K_GEMV_W8A8,
-    K_LINEAR_DECODE,
+    K_LINEAR_DECODE,     // M <= 4
+    K_LINEAR_DECODE_M1,  // M == 1
+    K_LINEAR_DECODE_M2,  // M <= 2
     K_GEMV_W8A32,
     K_GEMM_W8A8,
     K_GEMM_W8A8_128,
