@@ -155,10 +155,20 @@ extern "C" __global__ __launch_bounds__(1024) void nh_moe_permute_kernel(Permute
     }
 }
 
-// R3: grouped W8A8 GEMM.  grid.x = N tiles of 16 rows, grid.y = experts.
-// The workgroup streams its [16 x K] weight tile of expert e once per 16-row
-// block of the expert's segment (one block for a typical ~24-row segment;
-// later blocks hit L2) with K split across its waves, as the GEMV does.
+// R3: grouped W8A8 GEMM.  grid.x = N tiles of 16 rows, grid.y = experts,
+// blockDim = 64 * ceil(K / 1024).
+// HBM-bound like the GEMV: the workgroup's waves split K in slices of up to
+// 1 KiB and each wave issues its whole [16 x slice] weight slab (16 buffer
+// loads of 16 B per lane) at once; the slab then stays in registers while
+// the expert's segment is walked in blocks of 16 routed rows (one block for
+// a typical ~24-row segment), so each expert weight byte leaves HBM once.
+// A rows are gathered per lane (token perm[slot] / top_k for the up
+// projection, the slot itself for the down projection).  Steps past the
+// wave's slice and rows past the segment load from an out-of-range buffer
+// offset, which returns zeros without touching memory.
+constexpr int kGroupedSteps = 16;
+constexpr int kOutOfRange = 0x7ffffff0;
+
 extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(GroupedGemmArgs a) {
     __shared__ v4i red[8 * 64];
     const int e = blockIdx.y;
@@ -168,46 +178,53 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(Gro
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
     const int N = a.N, K = a.K;
-    const int kslice = ((K + nw * 64 - 1) / (nw * 64)) * 64;
-    const int kbeg = wave * kslice;
-    const int kend = min(K, kbeg + kslice);
-    const int n = tile * 16 + r16;
-    const bool nok = n < N;
-    const int8_t* wrow = a.w + ((int64_t)e * N + (nok ? n : 0)) * K;
+    const int kbeg = wave * 64 * kGroupedSteps;
+    const int kend = min(K, kbeg + 64 * kGroupedSteps);
+    const __amdgpu_buffer_rsrc_t wr =
+        make_rsrc(a.w + ((int64_t)e * N + tile * 16) * K, (uint32_t)min(16, N - tile * 16) * (uint32_t)K);
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.aq, (uint32_t)a.a_rows * (uint32_t)K);
+    v4i b[kGroupedSteps];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < kGroupedSteps; ++s) {
+        const int k = kbeg + s * 64 + g * 16;
+        b[s] = buffer_load16(wr, k < kend ? r16 * K + k : kOutOfRange);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     for (int m0 = seg0; m0 < seg1; m0 += 16) {
         const int slot = m0 + r16;
         const bool mok = slot < seg1;
         const int arow = mok ? (a.gather ? a.perm[slot] / a.top_k : slot) : 0;
-        const int8_t* xrow = a.aq + (int64_t)arow * K;
-        v4i acc = {0, 0, 0, 0};
-        for (int k0 = kbeg; k0 < kend; k0 += 64 * 8) {
-            v4i b[8], x[8];
+        v4i x[kGroupedSteps];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const int k = k0 + s * 64 + g * 16;
-                const bool kok = k < kend;
-                b[s] = (nok && kok) ? *(const v4i*)(wrow + k) : v4i{0, 0, 0, 0};
-                x[s] = (mok && kok) ? *(const v4i*)(xrow + k) : v4i{0, 0, 0, 0};
-            }
-#pragma unroll
-            for (int s = 0; s < 8; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[s], b[s], acc, 0, 0, 0);
+        for (int s = 0; s < kGroupedSteps; ++s) {
+            const int k = kbeg + s * 64 + g * 16;
+            x[s] = buffer_load16(ar, (mok && k < kend) ? arow * K + k : kOutOfRange);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < kGroupedSteps; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[s], b[s], acc, 0, 0, 0);
         if (nw > 1) {
             red[wave * 64 + lane] = acc;
             __syncthreads();
             if (wave == 0)
                 for (int w = 1; w < nw; ++w) acc += red[w * 64 + lane];
         }
-        if (wave == 0 && nok) {
-            const float swn = a.sw[(int64_t)e * N + n];
+        if (wave == 0) {
+            const int n = tile * 16 + r16;
+            if (n < N) {
+                const float swn = a.sw[(int64_t)e * N + n];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int srow = m0 + 4 * g + r;
-                if (srow < seg1) {
-                    const int ar = a.gather ? a.perm[srow] / a.top_k : srow;
-                    float y = epilogue_w8a8(acc[r], a.sa[ar], swn);
-                    if (a.relu2) y = relu2(y);
-                    a.out[(int64_t)srow * N + n] = y;
+                for (int r = 0; r < 4; ++r) {
+                    const int srow = m0 + 4 * g + r;
+                    if (srow < seg1) {
+                        const int ar_ = a.gather ? a.perm[srow] / a.top_k : srow;
+                        float y = epilogue_w8a8(acc[r], a.sa[ar_], swn);
+                        if (a.relu2) y = relu2(y);
+                        a.out[(int64_t)srow * N + n] = y;
+                    }
                 }
             }
         }

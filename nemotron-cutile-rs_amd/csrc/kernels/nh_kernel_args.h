@@ -131,7 +131,7 @@ struct GroupedGemmArgs {
     int32_t gather;
     int32_t relu2;
     int32_t ntiles;
-    int32_t pad_;
+    int32_t a_rows;          // rows of aq (tokens when gathering, routes otherwise)
 };
 
 // R4: scatter-combine.

@@ -279,12 +279,12 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
                                    size_t experts, const int8_t* w, const float* sw, size_t n, size_t k, int relu2,
                                    float* out, nh_stream stream, nh_error* err) {
     clear_error(err);
-    (void)a_rows;
     if (experts == 0 || top_k == 0) return set_error(err, NH_INVALID_SHAPE, "experts and top_k must be non-zero");
     nh_status st;
     if ((st = check_w8a8_shape(routes ? routes : 1, n, k, err))) return st;
     if (!aligned16(aq) || !aligned16(w)) return set_error(err, NH_UNSUPPORTED, "aq and w must be 16-byte aligned");
-    if (experts > 65535) return set_error(err, NH_UNSUPPORTED, "experts must be <= 65535");
+    if (experts > 65535 || k > 8192 || a_rows * k >= (1ull << 31) || 16 * k >= (1ull << 31))
+        return set_error(err, NH_UNSUPPORTED, "grouped GEMM envelope: experts <= 65535, k <= 8192, a_rows * k < 2^31");
     if ((st = bind_device(ctx, err))) return st;
     if (routes == 0) return NH_OK;
     GroupedGemmArgs a{};
@@ -302,7 +302,9 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
     a.gather = gather ? 1 : 0;
     a.relu2 = relu2 ? 1 : 0;
     a.ntiles = (int)((n + 15) / 16);
-    return launch(ctx, K_GROUPED_GEMM, (unsigned)a.ntiles, 512, 0, stream, a, err, (unsigned)experts);
+    a.a_rows = (int)a_rows;
+    const unsigned waves = (unsigned)((k + 1023) / 1024);
+    return launch(ctx, K_GROUPED_GEMM, (unsigned)a.ntiles, 64u * waves, 0, stream, a, err, (unsigned)experts);
 }
 
 nh_status nh_moe_combine(nh_context* ctx, const float* slot_out, const int32_t* pos, const float* weights,
