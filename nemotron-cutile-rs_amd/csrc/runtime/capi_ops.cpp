@@ -44,7 +44,7 @@ nh_status check_w8a8_shape(size_t m, size_t n, size_t k, nh_error* err) {
         return set_error(err, NH_INVALID_SHAPE, "invalid GEMM shape m=%zu n=%zu k=%zu", m, n, k);
     if (!nh_supports_gemm_w8a8(m, n, k))
         return set_error(err, NH_UNSUPPORTED, "shape m=%zu n=%zu k=%zu outside the gfx950 envelope (k %% 16 == 0, "
-                         "dims < 2^31)", m, n, k);
+                         "k <= 131072, dims < 2^31)", m, n, k);
     return NH_OK;
 }
 
@@ -114,7 +114,8 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
 extern "C" {
 
 int nh_supports_gemm_w8a8(size_t m, size_t n, size_t k) {
-    return m > 0 && n > 0 && k > 0 && m < (1u << 31) && n < (1u << 31) && k < (1u << 31) && (k % 16) == 0 &&
+    // k <= 2^17 keeps the int32 accumulator exact: |acc| <= k * 127 * 127 < 2^31
+    return m > 0 && n > 0 && k > 0 && m < (1u << 31) && n < (1u << 31) && k <= (1u << 17) && (k % 16) == 0 &&
            (uint64_t)m * k < (1ull << 40) && (uint64_t)n * k < (1ull << 40);
 }
 

@@ -74,6 +74,9 @@ def test_device_entry_points_validate_before_touching_a_device():
     assert NH.lib().nh_supports_gemm_w8a8(2048, 4096, 4096) == 1
     assert NH.lib().nh_supports_gemm_w8a8(2048, 4096, 4095) == 0
     assert NH.lib().nh_supports_gemm_w8a8(0, 4096, 4096) == 0
+    # int32 accumulator exactness bound: 131072 * 127^2 < 2^31
+    assert NH.lib().nh_supports_gemm_w8a8(1, 16, 131072) == 1
+    assert NH.lib().nh_supports_gemm_w8a8(1, 16, 131088) == 0
 
 
 def test_generator_matches_oracle_bit_for_bit():
