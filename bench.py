@@ -213,7 +213,21 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain device-to-device copies of MIB MiB (torch's copy kernel), the "
+                         "calibration run for the FETCH_SIZE / WRITE_SIZE counters, and exit")
     args = ap.parse_args()
+    if args.copy_probe:
+        import torch
+
+        nbytes = args.copy_probe << 20
+        src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": nbytes, "copy_probe_bytes_written": nbytes, "launches": 5}))
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the int8 linear path has no "
               f"multi-GPU mode in this build", file=sys.stderr)
@@ -283,7 +297,7 @@ def main():
                    "m": m, "k": k, "n": n, "weight_pool_MiB": POOL_BYTES >> 20},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "nh_linear_decode_w8a8_kernel", "bytes_per_launch": nbytes},
+                     "kernel": "nh_linear_decode_w8a8_m1_kernel", "bytes_per_launch": nbytes},
         "cpu_baseline": cpu,
     }
     line.update(extra)
