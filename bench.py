@@ -41,32 +41,37 @@ class Bench:
         self.ctx = NH.Context(0)
         self.ev = NH.HipEvents()
         self.e0, self.e1 = self.ev.create(), self.ev.create()
+        s = ctypes.c_void_p()
+        NH.call("nh_stream_create", self.ctx.handle, ctypes.byref(s))
+        self.stream = s
 
     def time_ms(self, fn, steps, warmup):
+        """Mean time per step of fn(i) on self.stream: `warmup` untimed calls,
+        then `steps` calls bracketed by HIP events recorded on that stream."""
         for i in range(warmup):
             fn(i)
-        self.ctx.synchronize()
-        self.ev.record(self.e0, None)
+        self.ctx.synchronize(self.stream)
+        self.ev.record(self.e0, self.stream)
         for i in range(steps):
             fn(warmup + i)
-        self.ev.record(self.e1, None)
+        self.ev.record(self.e1, self.stream)
         ms = self.ev.elapsed_ms(self.e0, self.e1)
-        self.ctx.synchronize()
+        self.ctx.synchronize(self.stream)
         return ms / steps
 
     def quantized_pool(self, n, k, copies, seed=0):
-        """copies x (int8 [n][k], f32 [n]) quantized on the device from N(0, 0.02)."""
+        """copies x (tiled int8 [n][k], f32 [n]) quantized on the device from N(0, 0.02) and tiled
+        (nh_quantize_rows_i8 then nh_tile_weights_i8, the offline weight path)."""
         w = NH.normal_f32(seed, n * k, 0.0, 0.02)
         dw = self.ctx.upload(w)
         del w
-        pool = []
-        for _ in range(copies):
-            q = self.ctx.empty((n, k), np.int8)
-            s = self.ctx.empty(n, np.float32)
-            NH.call("nh_quantize_rows_i8", self.ctx.handle, dw.ptr, NH.F32, n, k, q.ptr, s.ptr, None, None)
-            pool.append((q, s))
+        q = self.ctx.empty((n, k), np.int8)
+        s = self.ctx.empty(n, np.float32)
+        NH.call("nh_quantize_rows_i8", self.ctx.handle, dw.ptr, NH.F32, n, k, q.ptr, s.ptr, None, None)
+        pool = [(NH.tile_weights(self.ctx, q, n, k), s) for _ in range(copies)]
         self.ctx.synchronize()
         dw.free()
+        q.free()
         return pool
 
     # ---- decode unit ---------------------------------------------------------
@@ -83,7 +88,7 @@ class Bench:
         def step(i):
             q, s = pool[i % len(pool)]
             st = L.nh_linear_w8a8(h, x.ptr, NH.BF16, q.ptr, s.ptr, None, m, n, k, out.ptr, NH.BF16, ws.ptr,
-                                  ws_bytes, None, None, None, ctypes.byref(err))
+                                  ws_bytes, None, None, self.stream, ctypes.byref(err))
             if st:
                 NH.check(st, err)
 
@@ -99,7 +104,7 @@ class Bench:
         err = NH.NhError()
 
         def step(i):
-            st = L.nh_gemm_w8a8(h, xq.ptr, sx.ptr, q.ptr, s.ptr, None, m, n, k, out.ptr, NH.BF16, None,
+            st = L.nh_gemm_w8a8(h, xq.ptr, sx.ptr, q.ptr, s.ptr, None, m, n, k, out.ptr, NH.BF16, self.stream,
                                 ctypes.byref(err))
             if st:
                 NH.check(st, err)
@@ -116,18 +121,21 @@ class Bench:
 
         def step(i):
             q, s = pool[i % len(pool)]
-            st = L.nh_gemv_w8a32(h, x.ptr, q.ptr, s.ptr, 1, n, k, y.ptr, None, ctypes.byref(err))
+            st = L.nh_gemv_w8a32(h, x.ptr, q.ptr, s.ptr, 1, n, k, y.ptr, self.stream, ctypes.byref(err))
             if st:
                 NH.check(st, err)
 
         return self.time_ms(step, steps, warmup)
 
     def moe(self, steps, warmup, tokens=512, hidden=2688, inter=1856, experts=128, top_k=6):
-        up_q = self.ctx.empty((experts, inter, hidden), np.int8)
-        down_q = self.ctx.empty((experts, hidden, inter), np.int8)
+        L = NH.lib()
+        tb_up, tb_down = L.nh_tiled_weights_bytes(inter, hidden), L.nh_tiled_weights_bytes(hidden, inter)
+        up_q = self.ctx.empty(experts * tb_up, np.int8)
+        down_q = self.ctx.empty(experts * tb_down, np.int8)
+        rows_q = self.ctx.empty(inter * hidden, np.int8)
         up_s = self.ctx.empty((experts, inter), np.float32)
         down_s = self.ctx.empty((experts, hidden), np.float32)
-        L, h = NH.lib(), self.ctx.handle
+        h = self.ctx.handle
         # 8 distinct N(0, 0.02) expert weight sets (seeds 100..107) reused
         # cyclically: the timing does not depend on the values, and drawing
         # 1.28 G normals on the host would dominate the run
@@ -136,11 +144,14 @@ class Bench:
             sets.append(self.ctx.upload(NH.normal_f32(100 + i, 2 * inter * hidden, 0.0, 0.02)))
         for e in range(experts):
             dw = sets[e % 8]
-            NH.call("nh_quantize_rows_i8", h, dw.ptr, NH.F32, inter, hidden, up_q.offset(e * inter * hidden),
-                    up_s.offset(4 * e * inter), None, None)
-            NH.call("nh_quantize_rows_i8", h, dw.offset(4 * inter * hidden), NH.F32, hidden, inter,
-                    down_q.offset(e * hidden * inter), down_s.offset(4 * e * hidden), None, None)
+            NH.call("nh_quantize_rows_i8", h, dw.ptr, NH.F32, inter, hidden, rows_q.ptr, up_s.offset(4 * e * inter),
+                    None, None)
+            NH.call("nh_tile_weights_i8", h, rows_q.ptr, inter, hidden, up_q.offset(e * tb_up), tb_up, None)
+            NH.call("nh_quantize_rows_i8", h, dw.offset(4 * inter * hidden), NH.F32, hidden, inter, rows_q.ptr,
+                    down_s.offset(4 * e * hidden), None, None)
+            NH.call("nh_tile_weights_i8", h, rows_q.ptr, hidden, inter, down_q.offset(e * tb_down), tb_down, None)
         self.ctx.synchronize()
+        rows_q.free()
         for dw in sets:
             dw.free()
         x = self.ctx.upload(NH_bf16(NH.normal_f32(1, tokens * hidden)))
@@ -153,7 +164,7 @@ class Bench:
         def step(i):
             st = L.nh_moe_forward_w8a8(h, x.ptr, NH.BF16, logits.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
                                        up_q.ptr, up_s.ptr, down_q.ptr, down_s.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes,
-                                       None, ctypes.byref(err))
+                                       self.stream, ctypes.byref(err))
             if st:
                 NH.check(st, err)
 

@@ -16,9 +16,17 @@
  *     implementation (the reference's *_host functions).
  *   - Lengths are element counts.  Status codes mirror the reference error
  *     enums; nh_error (optional, may be NULL) carries their payload.
- *   - int8 weights are [N][K] row-major (K contiguous) with one f32 scale per
- *     output row N.  The reference stores f32 linear weights [K][N]
- *     (linear.rs:324); quantization transposes once, offline.
+ *   - int8 weights (the wq / w / w_up / w_down arguments of the W8A8 and
+ *     W8A32 entry points) are TILED, with one f32 scale per output row N:
+ *     a logical [N][K] matrix is stored as ceil(N/16) x KT tiles of 1024
+ *     bytes, KT = ceil(K/64); tile (nt, kt) starts at byte (nt*KT + kt)*1024
+ *     and its byte 16*(16*g + r) + b holds W[16*nt + r][64*kt + 16*g + b]
+ *     (zero outside the matrix).  That is the lane order of the int8 MFMA
+ *     operand, so every weight load reads one contiguous KiB.  Quantize the
+ *     rows with nh_quantize_rows_i8, then tile them once, offline, with
+ *     nh_tile_weights_i8 (size: nh_tiled_weights_bytes).  The reference
+ *     stores f32 linear weights [K][N] (linear.rs:324); the quantized row n
+ *     is column n of that matrix.  Activations stay row-major [M][K].
  *   - Functions never abort the process.
  */
 #ifndef NEMOTRON_HIP_H
@@ -119,6 +127,15 @@ nh_status nh_dequantize_i8(nh_context *ctx, const int8_t *q, const float *scales
 nh_status nh_dequantize_i8_host(const int8_t *q, const float *scales, size_t rows, size_t cols, float *out,
                                 nh_error *err);
 
+/* Tiled int8 weight layout (see Conventions): bytes of the tiled form of
+ * an [n][k] matrix (0 for an invalid shape), and the conversion from
+ * row-major codes.  New: the reference has no int8 weight format. */
+size_t nh_tiled_weights_bytes(size_t n, size_t k);
+nh_status nh_tile_weights_i8(nh_context *ctx, const int8_t *wq, size_t n, size_t k, int8_t *tiled,
+                             size_t tiled_len, nh_stream stream, nh_error *err);
+nh_status nh_tile_weights_i8_host(const int8_t *wq, size_t n, size_t k, int8_t *tiled, size_t tiled_len,
+                                  nh_error *err);
+
 /* ---- G0/G1/G2/G3: GEMM family (gemm.rs, linear.rs:283-342) ------------- */
 /* G0: gemm_into_host restated (gemm.rs:91-147): f32 in, f64 accumulation. */
 nh_status nh_gemm_f32_host(const float *lhs, size_t lhs_len, const float *rhs, size_t rhs_len, size_t m,
@@ -126,8 +143,8 @@ nh_status nh_gemm_f32_host(const float *lhs, size_t lhs_len, const float *rhs, s
 /* Device envelope of the W8A8 GEMM family (supports_shape, gemm.rs:247-254). */
 int nh_supports_gemm_w8a8(size_t m, size_t n, size_t k);
 /* G1/G3: out[m,n] = ((float)sum_k xq[m,k]*wq[n,k] * sx[m]) * sw[n] (+ bias[n])
- * in f32 or bf16 (RNE).  int32 accumulation is exact.  M <= 16 runs the
- * HBM-bound GEMV, larger M the MFMA GEMM. */
+ * in f32 or bf16 (RNE); wq tiled.  int32 accumulation is exact.  M <= 16
+ * runs the HBM-bound GEMV, larger M the MFMA GEMM. */
 nh_status nh_gemm_w8a8(nh_context *ctx, const int8_t *xq, const float *sx, const int8_t *wq, const float *sw,
                        const float *bias, size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype,
                        nh_stream stream, nh_error *err);
@@ -174,7 +191,8 @@ nh_status nh_moe_permute(nh_context *ctx, const int32_t *indices, size_t tokens,
                          int32_t *offsets, int32_t *perm, int32_t *pos, nh_stream stream, nh_error *err);
 nh_status nh_moe_permute_host(const int32_t *indices, size_t tokens, size_t top_k, size_t experts,
                               int32_t *offsets, int32_t *perm, int32_t *pos, nh_error *err);
-/* R3: grouped W8A8 GEMM over the expert segments of offsets.  gather != 0:
+/* R3: grouped W8A8 GEMM over the expert segments of offsets (w = E tiled
+ * [n][k] matrices at a stride of nh_tiled_weights_bytes(n, k)).  gather != 0:
  * the A row of slot i is token perm[i] / top_k (up projection); otherwise
  * the A row is slot i (down projection).  out is f32 [routes][n]; relu2
  * applies ReLU^2 after the epilogue (mlp.rs:205). */
@@ -196,7 +214,8 @@ nh_status nh_moe_combine_host(const float *slot_out, const int32_t *pos, const f
 /* Whole int8 MoE layer on the device: Q2(x) -> R1 -> R2 -> up (R3, gather,
  * ReLU^2) -> Q2 -> down (R3) -> R4.  Replaces MoeLayer::forward_into
  * (moe.rs:154-249) for routed experts with int8 per-row weights
- * w_up [E][inter][hidden], w_down [E][hidden][inter].  The routing stages
+ * w_up = E tiled [inter][hidden] matrices, w_down = E tiled [hidden][inter]
+ * matrices, each expert at a stride of nh_tiled_weights_bytes of its shape.  The routing stages
  * leave indices, weights, offsets, perm and pos in the workspace at the byte
  * offsets reported by nh_moe_workspace_layout. */
 size_t nh_moe_forward_w8a8_workspace_size(size_t tokens, size_t hidden, size_t inter, size_t experts,

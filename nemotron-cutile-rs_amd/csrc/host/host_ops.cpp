@@ -139,7 +139,8 @@ nh_status nh_quantize_rows_i8_host(const void* x, nh_dtype dtype, size_t rows, s
         for (size_t c = 0; c < cols; ++c) amax = std::max(amax, std::fabs(load_f32(x, r * cols + c, dtype)));
         const float s = scale_from_amax(amax);
         scales[r] = s;
-        for (size_t c = 0; c < cols; ++c) q[r * cols + c] = quantize_i8(load_f32(x, r * cols + c, dtype), s);
+        const float rcp = s > 0.0f ? 1.0f / s : 0.0f;
+        for (size_t c = 0; c < cols; ++c) q[r * cols + c] = (int8_t)quantize_i8_fast(load_f32(x, r * cols + c, dtype), s, rcp);
     }
     return NH_OK;
 }
@@ -172,6 +173,29 @@ nh_status nh_gemm_f32_host(const float* lhs, size_t lhs_len, const float* rhs, s
     return NH_OK;
 }
 
+// Row c of a tiled [n][k] int8 matrix, gathered into row[0..k).
+static void untile_row(const int8_t* w, size_t c, size_t k, int8_t* row) {
+    const uint64_t kt = tiled_k_tiles(k);
+    for (size_t d = 0; d < k; d += 16) {
+        const int8_t* src = w + tiled_offset(c, d, kt);
+        for (size_t b = 0; b < 16 && d + b < k; ++b) row[d + b] = src[b];
+    }
+}
+
+nh_status nh_tile_weights_i8_host(const int8_t* wq, size_t n, size_t k, int8_t* tiled, size_t tiled_len,
+                                  nh_error* err) {
+    clear_error(err);
+    if (n == 0 || k == 0 || n > (1ull << 40) || k > (1ull << 40))
+        return set_error(err, NH_INVALID_SHAPE, "invalid weight shape n=%zu k=%zu", n, k);
+    const size_t need = (size_t)tiled_bytes(n, k);
+    if (tiled_len != need) return mismatch(err, "tiled", need, tiled_len);
+    std::memset(tiled, 0, need);
+    const uint64_t kt = tiled_k_tiles(k);
+    for (size_t c = 0; c < n; ++c)
+        for (size_t d = 0; d < k; ++d) tiled[tiled_offset(c, d, kt)] = wq[c * k + d];
+    return NH_OK;
+}
+
 nh_status nh_gemm_w8a8_host(const int8_t* xq, const float* sx, const int8_t* wq, const float* sw, const float* bias,
                             size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype, nh_error* err) {
     clear_error(err);
@@ -179,14 +203,17 @@ nh_status nh_gemm_w8a8_host(const int8_t* xq, const float* sx, const int8_t* wq,
     if (m == 0 || n == 0 || k == 0 || !mul_ok(m, k, &t) || !mul_ok(n, k, &t) || !mul_ok(m, n, &t))
         return set_error(err, NH_INVALID_SHAPE, "invalid GEMM shape");
     if (out_dtype != NH_F32 && out_dtype != NH_BF16) return set_error(err, NH_INVALID_PARAMS, "unknown dtype");
-    for (size_t r = 0; r < m; ++r)
-        for (size_t c = 0; c < n; ++c) {
+    std::vector<int8_t> row(k);
+    for (size_t c = 0; c < n; ++c) {
+        untile_row(wq, c, k, row.data());
+        for (size_t r = 0; r < m; ++r) {
             int32_t acc = 0;
-            for (size_t d = 0; d < k; ++d) acc += (int32_t)xq[r * k + d] * (int32_t)wq[c * k + d];
+            for (size_t d = 0; d < k; ++d) acc += (int32_t)xq[r * k + d] * (int32_t)row[d];
             float y = epilogue_w8a8(acc, sx[r], sw[c]);
             if (bias) y = y + bias[c];
             store_f32(out, r * n + c, y, out_dtype);
         }
+    }
     return NH_OK;
 }
 
@@ -196,12 +223,15 @@ nh_status nh_gemv_w8a32_host(const float* x, const int8_t* wq, const float* sw, 
     size_t t;
     if (m == 0 || n == 0 || k == 0 || !mul_ok(m, k, &t) || !mul_ok(n, k, &t))
         return set_error(err, NH_INVALID_SHAPE, "invalid GEMV shape");
-    for (size_t r = 0; r < m; ++r)
-        for (size_t c = 0; c < n; ++c) {
+    std::vector<int8_t> row(k);
+    for (size_t c = 0; c < n; ++c) {
+        untile_row(wq, c, k, row.data());
+        for (size_t r = 0; r < m; ++r) {
             double acc = 0.0;
-            for (size_t d = 0; d < k; ++d) acc += (double)x[r * k + d] * (double)((float)wq[c * k + d] * sw[c]);
+            for (size_t d = 0; d < k; ++d) acc += (double)x[r * k + d] * (double)((float)row[d] * sw[c]);
             y[r * n + c] = (float)acc;
         }
+    }
     return NH_OK;
 }
 
@@ -287,14 +317,16 @@ nh_status nh_moe_grouped_gemm_w8a8_host(const int8_t* aq, const float* sa, int g
     (void)routes;
     (void)a_rows;
     if (experts == 0 || top_k == 0 || n == 0 || k == 0) return set_error(err, NH_INVALID_SHAPE, "invalid shape");
+    std::vector<int8_t> wrow(k);
     for (size_t e = 0; e < experts; ++e) {
-        const int8_t* we = w + e * n * k;
-        for (int32_t slot = offsets[e]; slot < offsets[e + 1]; ++slot) {
-            const size_t row = gather ? (size_t)perm[slot] / top_k : (size_t)slot;
-            const int8_t* a = aq + row * k;
-            for (size_t c = 0; c < n; ++c) {
+        const int8_t* we = w + e * (size_t)tiled_bytes(n, k);
+        for (size_t c = 0; c < n; ++c) {
+            untile_row(we, c, k, wrow.data());
+            for (int32_t slot = offsets[e]; slot < offsets[e + 1]; ++slot) {
+                const size_t row = gather ? (size_t)perm[slot] / top_k : (size_t)slot;
+                const int8_t* a = aq + row * k;
                 int32_t acc = 0;
-                for (size_t d = 0; d < k; ++d) acc += (int32_t)a[d] * (int32_t)we[c * k + d];
+                for (size_t d = 0; d < k; ++d) acc += (int32_t)a[d] * (int32_t)wrow[d];
                 float y = epilogue_w8a8(acc, sa[row], sw[e * n + c]);
                 if (relu2_flag) y = relu2(y);
                 out[(size_t)slot * n + c] = y;

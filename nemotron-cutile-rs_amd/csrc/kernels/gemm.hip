@@ -1,4 +1,6 @@
 // G3: W8A8 GEMM for prefill-sized M on int8 MFMA (v_mfma_i32_32x32x32_i8).
+// Weights (B) are in the tiled layout (nh_numerics.h); activations (A) are
+// row-major [M][K].
 //
 // Workgroup = 256 threads = 4 waves in a 2 x 2 grid over a BM x BN output
 // tile.  K advances in 128-byte steps; A (activations, [M][K]) and B (weights,
@@ -61,7 +63,7 @@ __device__ __forceinline__ void gemm_tile(const GemmW8A8Args& a, int8_t* smem) {
             const int c = tid + i * kThreads;
             const int row = c >> 3, col = (c & 7) * 16;
             const int gn = n0 + row, gk = k0 + col;
-            gb[i] = (gn < N && gk < K) ? *(const v4i*)(a.wq + (int64_t)gn * K + gk) : v4i{0, 0, 0, 0};
+            gb[i] = (gn < N && gk < K) ? *(const v4i*)(a.wq + tiled_offset(gn, gk, a.kt)) : v4i{0, 0, 0, 0};
         }
     };
     auto store_stage = [&](int buf) {
@@ -136,312 +138,7 @@ __device__ __forceinline__ void gemm_tile(const GemmW8A8Args& a, int8_t* smem) {
     }
 }
 
-// v2 mainloop: WGM x WGN waves, global loads through buffer resources (rows
-// past M/N and K positions past K read zeros, no branches), LDS double
-// buffer, and MFMA fragments double-buffered in registers so the LDS reads of
-// step ks+1 are in flight while the MFMAs of step ks issue.
-template <int BM, int BN, int WGM, int WGN>
-__device__ __forceinline__ void gemm_tile_v2(const GemmW8A8Args& a, int8_t* smem) {
-    constexpr int kT = 64 * WGM * WGN;
-    constexpr int WM = BM / WGM, WN = BN / WGN;   // per-wave tile
-    constexpr int TM = WM / 32, TN = WN / 32;     // 32x32 MFMA tiles per wave
-    constexpr int CA = BM * kBK / 16 / kT;        // 16-byte chunks per thread (A)
-    constexpr int CB = BN * kBK / 16 / kT;        // (B)
-    constexpr int kStage = (BM + BN) * kPitch;
-    constexpr int KS = kBK / 32;                  // MFMA K steps per stage
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WGN, wn = wave % WGN;
-    const int M = a.M, N = a.N, K = a.K;
-
-    const int nblk = a.tiles_m * a.tiles_n;
-    int b = blockIdx.x;
-    if ((nblk & 7) == 0) b = (b & 7) * (nblk >> 3) + (b >> 3);
-    const int tm_idx = b % a.tiles_m, tn_idx = b / a.tiles_m;
-    const int m0 = tm_idx * BM, n0 = tn_idx * BN;
-
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.xq + (int64_t)m0 * K, (uint32_t)min(BM, M - m0) * (uint32_t)K);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.wq + (int64_t)n0 * K, (uint32_t)min(BN, N - n0) * (uint32_t)K);
-    // per-thread chunk coordinates (row, 16-byte column) are fixed across stages
-    int offa[CA], offb[CB];
-#pragma unroll
-    for (int i = 0; i < CA; ++i) {
-        const int c = tid + i * kT;
-        offa[i] = (c >> 3) * K + (c & 7) * 16;
-    }
-#pragma unroll
-    for (int i = 0; i < CB; ++i) {
-        const int c = tid + i * kT;
-        offb[i] = (c >> 3) * K + (c & 7) * 16;
-    }
-    v4i ga[CA], gb[CB];
-    auto load_stage = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < CA; ++i) {
-            const int col = ((tid + i * kT) & 7) * 16;
-            ga[i] = buffer_load16(ra, k0 + col < K ? offa[i] + k0 : 0x7ffffff0);
-        }
-#pragma unroll
-        for (int i = 0; i < CB; ++i) {
-            const int col = ((tid + i * kT) & 7) * 16;
-            gb[i] = buffer_load16(rb, k0 + col < K ? offb[i] + k0 : 0x7ffffff0);
-        }
-    };
-    auto store_stage = [&](int buf) {
-        int8_t* sa = smem + buf * kStage;
-        int8_t* sb = sa + BM * kPitch;
-#pragma unroll
-        for (int i = 0; i < CA; ++i) {
-            const int c = tid + i * kT;
-            *(v4i*)(sa + (c >> 3) * kPitch + (c & 7) * 16) = ga[i];
-        }
-#pragma unroll
-        for (int i = 0; i < CB; ++i) {
-            const int c = tid + i * kT;
-            *(v4i*)(sb + (c >> 3) * kPitch + (c & 7) * 16) = gb[i];
-        }
-    };
-
-    v16i acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = v16i{};
-
-    const int nk = (K + kBK - 1) / kBK;
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
-    const int fr = lane & 31, fk = (lane >> 5) * 16;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) load_stage((kt + 1) * kBK);
-        const int8_t* sa = smem + buf * kStage + (wm * WM + fr) * kPitch + fk;
-        const int8_t* sb = smem + buf * kStage + BM * kPitch + (wn * WN + fr) * kPitch + fk;
-        v4i af[2][TM], bf[2][TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i) af[0][i] = *(const v4i*)(sa + i * 32 * kPitch);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) bf[0][j] = *(const v4i*)(sb + j * 32 * kPitch);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const int cur = ks & 1;
-            if (ks + 1 < KS) {
-#pragma unroll
-                for (int i = 0; i < TM; ++i) af[cur ^ 1][i] = *(const v4i*)(sa + i * 32 * kPitch + (ks + 1) * 32);
-#pragma unroll
-                for (int j = 0; j < TN; ++j) bf[cur ^ 1][j] = *(const v4i*)(sb + j * 32 * kPitch + (ks + 1) * 32);
-            }
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[cur][i], bf[cur][j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < nk) store_stage(buf ^ 1);
-        __syncthreads();
-    }
-
-    const int quad = lane >> 5;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int n = n0 + wn * WN + j * 32 + (lane & 31);
-        if (n >= N) continue;
-        const float swn = a.sw[n];
-        const float bn = a.bias ? a.bias[n] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * quad + (r & 3);
-                if (m < M) {
-                    float y = epilogue_w8a8(acc[i][j][r], a.sx[m], swn);
-                    if (a.bias) y = y + bn;
-                    if (a.relu2) y = relu2(y);
-                    store_out(a.out, (int64_t)m * N + n, y, a.out_dtype);
-                }
-            }
-        }
-    }
-}
-
-// v3 mainloop: as v2, but the global loads run two stages ahead (two
-// register staging sets, the k loop unrolled by two so both stay static):
-// stage t+2 is requested while stage t is multiplied and stage t+1 lands.
-template <int BM, int BN, int WGM, int WGN>
-__device__ __forceinline__ void gemm_tile_v3(const GemmW8A8Args& a, int8_t* smem) {
-    constexpr int kT = 64 * WGM * WGN;
-    constexpr int WM = BM / WGM, WN = BN / WGN;
-    constexpr int TM = WM / 32, TN = WN / 32;
-    constexpr int CA = BM * kBK / 16 / kT;
-    constexpr int CB = BN * kBK / 16 / kT;
-    constexpr int kStage = (BM + BN) * kPitch;
-    constexpr int KS = kBK / 32;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WGN, wn = wave % WGN;
-    const int M = a.M, N = a.N, K = a.K;
-
-    const int nblk = a.tiles_m * a.tiles_n;
-    int b = blockIdx.x;
-    if ((nblk & 7) == 0) b = (b & 7) * (nblk >> 3) + (b >> 3);
-    const int tm_idx = b % a.tiles_m, tn_idx = b / a.tiles_m;
-    const int m0 = tm_idx * BM, n0 = tn_idx * BN;
-
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.xq + (int64_t)m0 * K, (uint32_t)min(BM, M - m0) * (uint32_t)K);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.wq + (int64_t)n0 * K, (uint32_t)min(BN, N - n0) * (uint32_t)K);
-    int offa[CA], offb[CB];
-#pragma unroll
-    for (int i = 0; i < CA; ++i) {
-        const int c = tid + i * kT;
-        offa[i] = (c >> 3) * K + (c & 7) * 16;
-    }
-#pragma unroll
-    for (int i = 0; i < CB; ++i) {
-        const int c = tid + i * kT;
-        offb[i] = (c >> 3) * K + (c & 7) * 16;
-    }
-    struct Stage {
-        v4i a[CA], b[CB];
-    };
-    auto load_stage = [&](Stage& st, int k0) {
-#pragma unroll
-        for (int i = 0; i < CA; ++i) {
-            const int col = ((tid + i * kT) & 7) * 16;
-            st.a[i] = buffer_load16(ra, k0 + col < K ? offa[i] + k0 : 0x7ffffff0);
-        }
-#pragma unroll
-        for (int i = 0; i < CB; ++i) {
-            const int col = ((tid + i * kT) & 7) * 16;
-            st.b[i] = buffer_load16(rb, k0 + col < K ? offb[i] + k0 : 0x7ffffff0);
-        }
-    };
-    auto store_stage = [&](const Stage& st, int buf) {
-        int8_t* sa = smem + buf * kStage;
-        int8_t* sb = sa + BM * kPitch;
-#pragma unroll
-        for (int i = 0; i < CA; ++i) {
-            const int c = tid + i * kT;
-            *(v4i*)(sa + (c >> 3) * kPitch + (c & 7) * 16) = st.a[i];
-        }
-#pragma unroll
-        for (int i = 0; i < CB; ++i) {
-            const int c = tid + i * kT;
-            *(v4i*)(sb + (c >> 3) * kPitch + (c & 7) * 16) = st.b[i];
-        }
-    };
-
-    v16i acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = v16i{};
-
-    const int fr = lane & 31, fk = (lane >> 5) * 16;
-    auto compute = [&](int buf) {
-        const int8_t* sa = smem + buf * kStage + (wm * WM + fr) * kPitch + fk;
-        const int8_t* sb = smem + buf * kStage + BM * kPitch + (wn * WN + fr) * kPitch + fk;
-        v4i af[2][TM], bf[2][TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i) af[0][i] = *(const v4i*)(sa + i * 32 * kPitch);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) bf[0][j] = *(const v4i*)(sb + j * 32 * kPitch);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const int cur = ks & 1;
-            if (ks + 1 < KS) {
-#pragma unroll
-                for (int i = 0; i < TM; ++i) af[cur ^ 1][i] = *(const v4i*)(sa + i * 32 * kPitch + (ks + 1) * 32);
-#pragma unroll
-                for (int j = 0; j < TN; ++j) bf[cur ^ 1][j] = *(const v4i*)(sb + j * 32 * kPitch + (ks + 1) * 32);
-            }
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[cur][i], bf[cur][j], acc[i][j], 0, 0, 0);
-        }
-    };
-
-    const int nk = (K + kBK - 1) / kBK;
-    Stage s0, s1;
-    load_stage(s0, 0);
-    if (nk > 1) load_stage(s1, kBK);
-    store_stage(s0, 0);
-    __syncthreads();
-    // invariant at the top of step kt: LDS[kt & 1] holds stage kt, the
-    // registers of stage kt+1 are in flight (s1 when kt is even, s0 when odd)
-    for (int kt = 0; kt < nk; kt += 2) {
-        if (kt + 2 < nk) load_stage(s0, (kt + 2) * kBK);
-        compute(0);
-        if (kt + 1 < nk) store_stage(s1, 1);
-        __syncthreads();
-        if (kt + 1 >= nk) break;
-        if (kt + 3 < nk) load_stage(s1, (kt + 3) * kBK);
-        compute(1);
-        if (kt + 2 < nk) store_stage(s0, 0);
-        __syncthreads();
-    }
-
-    const int quad = lane >> 5;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int n = n0 + wn * WN + j * 32 + (lane & 31);
-        if (n >= N) continue;
-        const float swn = a.sw[n];
-        const float bn = a.bias ? a.bias[n] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * quad + (r & 3);
-                if (m < M) {
-                    float y = epilogue_w8a8(acc[i][j][r], a.sx[m], swn);
-                    if (a.bias) y = y + bn;
-                    if (a.relu2) y = relu2(y);
-                    store_out(a.out, (int64_t)m * N + n, y, a.out_dtype);
-                }
-            }
-        }
-    }
-}
-
 }  // namespace
-
-extern "C" __global__ __launch_bounds__(256) void nh_gemm_v3_128x128_kernel(GemmW8A8Args a) {
-    extern __shared__ __align__(16) int8_t smem[];
-    gemm_tile_v3<128, 128, 2, 2>(a, smem);
-}
-
-extern "C" __global__ __launch_bounds__(512) void nh_gemm_v3_256x128_w8_kernel(GemmW8A8Args a) {
-    extern __shared__ __align__(16) int8_t smem[];
-    gemm_tile_v3<256, 128, 4, 2>(a, smem);
-}
-
-extern "C" __global__ __launch_bounds__(256) void nh_gemm_v3_256x128_kernel(GemmW8A8Args a) {
-    extern __shared__ __align__(16) int8_t smem[];
-    gemm_tile_v3<256, 128, 2, 2>(a, smem);
-}
-
-extern "C" __global__ __launch_bounds__(256) void nh_gemm_v2_128x128_kernel(GemmW8A8Args a) {
-    extern __shared__ __align__(16) int8_t smem[];
-    gemm_tile_v2<128, 128, 2, 2>(a, smem);
-}
-
-extern "C" __global__ __launch_bounds__(256) void nh_gemm_v2_256x128_kernel(GemmW8A8Args a) {
-    extern __shared__ __align__(16) int8_t smem[];
-    gemm_tile_v2<256, 128, 2, 2>(a, smem);
-}
-
-extern "C" __global__ __launch_bounds__(512) void nh_gemm_v2_256x128_w8_kernel(GemmW8A8Args a) {
-    extern __shared__ __align__(16) int8_t smem[];
-    gemm_tile_v2<256, 128, 4, 2>(a, smem);
-}
-
-extern "C" __global__ __launch_bounds__(256) void nh_gemm_v2_256x256_kernel(GemmW8A8Args a) {
-    extern __shared__ __align__(16) int8_t smem[];
-    gemm_tile_v2<256, 256, 2, 2>(a, smem);
-}
 
 extern "C" __global__ __launch_bounds__(256) void nh_gemm_w8a8_kernel(GemmW8A8Args a) {
     extern __shared__ __align__(16) int8_t smem[];

@@ -2,229 +2,202 @@
 // int8 weight matrix from HBM exactly once, so they are HBM-bound: the design
 // goal is bytes in flight from the first cycle to the last.
 //
-// Layout: W is [N][K] int8 (K contiguous), one f32 scale per output row.
-// A workgroup owns one 16-row N tile; its waves split K into slices of up to
-// 1 KiB.  Each wave issues the loads of its whole [16 x 1 KiB] weight slab
-// (16 buffer loads of 16 B per lane through one address register, 16 KiB per
-// wave) before doing anything else, so the activation prologue and the MFMAs
-// run while the slab is in flight.  The int32 partial tiles of the waves are
-// summed through LDS and the epilogue y = ((float)acc * sx[m]) * sw[n]
-// [+ bias[n]] is applied by wave 0.
+// Weights are in the tiled layout (nh_numerics.h): the KT = ceil(K/64) tiles
+// of one 16-row N tile are KT contiguous KiB, and one 64-lane 16-byte load of
+// a tile is the B operand of one v_mfma_i32_16x16x64_i8 K step, so every
+// weight load instruction reads one contiguous KiB.  A workgroup owns one
+// 16-row N tile; wave w of W owns K tiles w, w + W, w + 2W, ...  Each wave
+// issues the loads of a whole 16-tile slab (16 KiB) before doing anything
+// else, with the non-temporal policy (the weights are read once), so the
+// activation prologue and the MFMAs run while the slab is in flight.  The
+// waves' int32 partial tiles are summed through LDS and wave 0 applies the
+// epilogue y = ((float)acc * sx[m]) * sw[n] [+ bias[n]].
 //
-// MFMA operand convention used throughout (16x16x64, int8):
-//   lane l supplies row (l % 16) of its operand and bytes [16*(l/16), +16)
-//   of the current 64-wide K step; the same convention for A and B makes the
-//   dot product independent of how the hardware orders K inside a lane.
-//   Result: lane l holds D[m = 4*(l/16) + r][n = l % 16] in register r.
+// MFMA operand convention (16x16x64, int8): lane l supplies row (l % 16) of
+// its operand and bytes [16*(l/16), +16) of the 64-byte K step; the same
+// convention for A and B makes the dot product independent of how the
+// hardware orders K inside a lane.  Result: lane l holds
+// D[m = 4*(l/16) + r][n = l % 16] in register r.
 //
-// Weight fragments are never masked: a K position past the wave's slice
-// meets a zeroed activation fragment, and a row past N reads zeros from the
-// buffer resource and only feeds output columns that are not stored.
+// Tiles past KT (when W does not divide KT) read zeros from the buffer
+// resource and meet zero activation codes.
 #include "nh_device.h"
 
 using namespace nh;
 
 namespace {
 
-constexpr int kSteps = 16;  // 64-byte K steps per wave slab: 1 KiB of K
+constexpr int kSlab = 16;                // K tiles per wave in flight at once
 
-// Buffer resource over the 16 weight rows of `tile` (rows past N read zeros).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const int8_t* wq, int tile, int N, int K) {
-    const int rows = min(16, N - tile * 16);
-    return make_rsrc(wq + (int64_t)tile * 16 * K, (uint32_t)rows * (uint32_t)K);
+// The KT KiB of 16-row N tile `tile`.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_tile_rsrc(const int8_t* wq, int tile, int kt) {
+    return make_rsrc(wq + (int64_t)tile * kt * 1024, (uint32_t)kt * 1024u);
 }
 
-// The 16 loads of one slab: lane offset `off` (row r16, byte g*16 of the
-// step) plus 64 * s.  Scheduling barriers around the call keep every load
-// issued before the first wait (the default schedule sinks them two deep).
-__device__ __forceinline__ void load_slab(v4i (&b)[kSteps], __amdgpu_buffer_rsrc_t r, int off) {
+// Loads of one slab: K tiles first, first + stride, ... (16 of them).
+__device__ __forceinline__ void load_slab(v4i (&b)[kSlab], __amdgpu_buffer_rsrc_t r, int first, int stride,
+                                          int lane) {
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s) b[s] = buffer_load16(r, off + s * 64);
+    for (int s = 0; s < kSlab; ++s) b[s] = buffer_load16_stream(r, (first + s * stride) * 1024 + lane * 16);
 }
 
-__device__ __forceinline__ v4i zero_unless(bool ok, v4i v) { return ok ? v : v4i{0, 0, 0, 0}; }
-
-// Sum the partial tiles held by the waves of this workgroup and write the
-// epilogue for the 16 x 16 tile.  `red` holds blockDim/64 * 64 v4i.
-__device__ __forceinline__ void reduce_and_store(v4i acc, v4i* red, int tile, int M, int N, const float* sx,
-                                                 const float* sw, const float* bias, void* out, int out_dtype) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    if (nw > 1) {
+// Sum the waves' partial tiles into wave 0 (which returns true); `red`
+// holds W * 64 v4i.
+__device__ __forceinline__ bool reduce_waves(v4i& acc, v4i* red, int W) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (W > 1) {
         red[wave * 64 + lane] = acc;
         __syncthreads();
-        if (wave == 0) {
-            for (int w = 1; w < nw; ++w) acc += red[w * 64 + lane];
-        }
+        if (wave == 0)
+            for (int w = 1; w < W; ++w) acc += red[w * 64 + lane];
     }
-    if (wave == 0) {
-        const int n = tile * 16 + (lane & 15);
-        if (n < N) {
-            const float swn = sw[n];
-            const float bn = bias ? bias[n] : 0.0f;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = 4 * (lane >> 4) + r;
-                if (m < M) {
-                    float y = epilogue_w8a8(acc[r], sx[m], swn);
-                    if (bias) y = y + bn;
-                    store_out(out, (int64_t)m * N + n, y, out_dtype);
-                }
-            }
-        }
-    }
+    return wave == 0;
+}
+
+__device__ __forceinline__ void store_y(void* out, int out_dtype, int64_t i, int32_t acc, float sx, float swn,
+                                        const float* bias, float bn) {
+    float y = epilogue_w8a8(acc, sx, swn);
+    if (bias) y = y + bn;
+    store_out(out, i, y, out_dtype);
 }
 
 }  // namespace
 
-// G1: quantized activations already in HBM (xq, sx); A fragments come from
-// L2 (xq is at most 16 x K bytes and shared by every workgroup).
+// G1: quantized activations already in memory (xq [M][K] row-major, M <= 16);
+// the A fragments come from L2 (xq is at most 16 x K bytes, shared by every
+// workgroup).  Any K <= 131072: waves walk their K tiles slab by slab.
 extern "C" __global__ __launch_bounds__(512) void nh_gemv_w8a8_kernel(GemvW8A8Args a) {
     __shared__ v4i red[8 * 64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = a.waves;
     const int r16 = lane & 15, g = lane >> 4;
-    const int M = a.M, N = a.N, K = a.K;
+    const int M = a.M, N = a.N, K = a.K, kt = a.kt;
     const int tile = blockIdx.x;
-    const int kbeg = wave * a.kslice;
-    const int kend = min(K, kbeg + a.kslice);
-    const __amdgpu_buffer_rsrc_t wr = tile_rsrc(a.wq, tile, N, K);
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xq, (uint32_t)M * (uint32_t)K);  // rows >= M read zeros
-    const int lane_off = r16 * K + g * 16;
+    const __amdgpu_buffer_rsrc_t wr = row_tile_rsrc(a.wq, tile, kt);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xq, (uint32_t)M * (uint32_t)K);
+    // epilogue operands first, ahead of the weight stream
+    const int n = tile * 16 + r16;
+    const float swn = n < N ? a.sw[n] : 0.0f;
+    const float bn = (a.bias && n < N) ? a.bias[n] : 0.0f;
+    float sxl[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sxl[r] = 4 * g + r < M ? a.sx[4 * g + r] : 0.0f;
+    const int steps = (kt + W - 1) / W;
     v4i acc = {0, 0, 0, 0};
-    for (int k0 = kbeg; k0 < kend; k0 += 64 * kSteps) {
-        v4i b[kSteps], x[kSteps];
-        __builtin_amdgcn_sched_barrier(0);
-        load_slab(x, xr, lane_off + k0);  // activation fragments (L2) first
-        load_slab(b, wr, lane_off + k0);  // then the weight slab (HBM)
+    for (int s0 = 0; s0 < steps; s0 += kSlab) {
+        v4i x[kSlab], b[kSlab];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < kSteps; ++s) {
-            const v4i xa = zero_unless(k0 + s * 64 + g * 16 < kend, x[s]);
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, b[s], acc, 0, 0, 0);
+        for (int s = 0; s < kSlab; ++s) {  // activation fragments (L2) first
+            const int k = (wave + (s0 + s) * W) * 64 + g * 16;
+            x[s] = buffer_load16(xr, (r16 < M && k < K) ? r16 * K + k : kOutOfRange);
         }
+        load_slab(b, wr, wave + s0 * W, W, lane);  // then the weight slab (HBM)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < kSlab; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[s], b[s], acc, 0, 0, 0);
     }
-    reduce_and_store(acc, red, tile, M, N, a.sx, a.sw, a.bias, a.out, a.out_dtype);
+    if (reduce_waves(acc, red, W) && n < N) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (4 * g + r < M) store_y(a.out, a.out_dtype, (int64_t)(4 * g + r) * N + n, acc[r], sxl[r], swn, a.bias, bn);
+    }
 }
 
-// Decode unit, M <= MM <= 4: per-token quantization of the bf16 activation
-// rows (Q2) fused in front of the GEMV.  Every workgroup quantizes the rows
-// into LDS itself while its weight slab is in flight, so the unit is one
-// launch and the int8 activations never round-trip through HBM.  Codes and
-// scales are bit-identical in every workgroup (quantize_i8_rcp is exactly
-// quantize_i8); workgroup 0 also writes them out when asked.
+// Decode unit, M <= MM <= 4, K <= 8192: per-token quantization of the bf16
+// activation rows (Q2) fused in front of the GEMV.  Every workgroup quantizes
+// the rows into LDS itself while its weight slab is in flight, so the unit is
+// one launch and the int8 activations never round-trip through HBM.  The
+// quantizer multiplies by the reciprocal scale (quantize8_bf16) with an exact
+// tie decision for the rare value next to a rounding tie, so codes and scales
+// are bit-identical to quantize_i8 in every workgroup; workgroup 0 also
+// writes them out when asked.
 template <int MM>
 __device__ __forceinline__ void linear_decode(const LinearDecodeArgs& a, int8_t* xs) {
     __shared__ v4i red[8 * 64];
     __shared__ float redf[8][MM];
-    __shared__ float srow[MM];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int r16 = lane & 15, g = lane >> 4;
-    const int M = a.M, N = a.N, K = a.K;
-    const int ldx = K + 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = a.waves;
+    const int T = 64 * W;
+    const int M = a.M, N = a.N, K = a.K, kt = a.kt;
+    const int ldx = W * 1024 + 16;  // LDS row pitch: every K tile a wave can own (16 per wave)
     const int tile = blockIdx.x;
-    const int kbeg = wave * a.kslice;
-    const int kend = min(K, kbeg + a.kslice);
-    const __amdgpu_buffer_rsrc_t wr = tile_rsrc(a.wq, tile, N, K);
-    const int lane_off = r16 * K + g * 16;
 
-    // 1. this thread's share of the M bf16 rows (8 values per 16-byte load,
-    //    2 loads per row: K <= 16 * blockDim) goes into registers, then the
-    //    weight slab goes in flight.  Loads complete in issue order, so the
-    //    prologue waits only for the activations.
+    // 1. this thread's two 16-byte chunks (8 bf16 values each: chunks t and
+    //    t + T, 2 * T * 8 = W * 1024 values) of each row, the epilogue
+    //    operands, then the weight slab.  Loads complete in issue order, so
+    //    the quantizer waits only for the activations.
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)M * (uint32_t)K * 2u);
-    v4i xr[MM][2];
-    v4i b[kSteps];
+    v4i xv[MM][2];
+    v4i b[kSlab];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int m = 0; m < MM; ++m)
 #pragma unroll
-        for (int v = 0; v < 2; ++v) xr[m][v] = buffer_load16(xrs, (m * K + (threadIdx.x + v * blockDim.x) * 8) * 2);
-    load_slab(b, wr, lane_off + kbeg);
+        for (int v = 0; v < 2; ++v) {
+            const int c = (threadIdx.x + v * T) * 8;
+            xv[m][v] = buffer_load16(xrs, (m < M && c < K) ? (m * K + c) * 2 : kOutOfRange);
+        }
+    const int n = tile * 16 + (lane & 15);
+    const float swn = n < N ? a.sw[n] : 0.0f;
+    const float bn = (a.bias && n < N) ? a.bias[n] : 0.0f;
+    load_slab(b, row_tile_rsrc(a.wq, tile, kt), wave, W, lane);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int m = 0; m < MM; ++m)
-#pragma unroll
-        for (int v = 0; v < 2; ++v) xr[m][v] = zero_unless((int)((threadIdx.x + v * blockDim.x) * 8) < K, xr[m][v]);
 
-    // 2. Q2 of the rows into LDS: row absmax, then codes
-    float amax[MM];
+    // 2. row absmax over the workgroup; every thread derives the scales
+    float sx[MM];
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
-        amax[m] = 0.0f;
+        float amax = 0.0f;
 #pragma unroll
         for (int v = 0; v < 2; ++v)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t w = (uint32_t)xr[m][v][j];
-                amax[m] = fmaxf(amax[m], fabsf(f32_from_bits(w << 16)));
-                amax[m] = fmaxf(amax[m], fabsf(f32_from_bits(w & 0xffff0000u)));
+                const uint32_t u = (uint32_t)xv[m][v][j];
+                amax = fmaxf(amax, fmaxf(fabsf(f32_from_bits(u << 16)), fabsf(f32_from_bits(u & 0xffff0000u))));
             }
-        const float wm = wave_max(amax[m]);
-        if (lane == 0) redf[wave][m] = wm;
-    }
-    __syncthreads();
-    if (threadIdx.x < M) {
-        float r = redf[0][threadIdx.x];
-        for (int i = 1; i < nw; ++i) r = fmaxf(r, redf[i][threadIdx.x]);
-        const float s = scale_from_amax(r);
-        srow[threadIdx.x] = s;
-        if (blockIdx.x == 0 && a.sx_out) a.sx_out[threadIdx.x] = s;
+        amax = wave_max(amax);
+        if (lane == 0) redf[wave][m] = amax;
     }
     __syncthreads();
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
-        if (m < M) {
-            const float s = srow[m];
-            const float rcp = 1.0f / s;
+        float r = redf[0][m];
+        for (int i = 1; i < W; ++i) r = fmaxf(r, redf[i][m]);
+        sx[m] = scale_from_amax(r);
+    }
+    // 3. codes into LDS (zeros past K and for rows >= M)
 #pragma unroll
-            for (int v = 0; v < 2; ++v) {
-                const int c = (threadIdx.x + v * blockDim.x) * 8;
-                if (c < K) {
-                    uint32_t code[2] = {0, 0};
+    for (int m = 0; m < MM; ++m) {
+        const float rcp = 1.0f / sx[m];
+        const bool pow2 = scale_is_pow2(sx[m]);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint32_t w = (uint32_t)xr[m][v][j];
-                        const uint32_t q0 = (uint8_t)quantize_i8_rcp(f32_from_bits(w << 16), s, rcp);
-                        const uint32_t q1 = (uint8_t)quantize_i8_rcp(f32_from_bits(w & 0xffff0000u), s, rcp);
-                        code[j >> 1] |= (q0 | (q1 << 8)) << (16 * (j & 1));
-                    }
-                    *(uint2*)(xs + m * ldx + c) = make_uint2(code[0], code[1]);
-                    if (blockIdx.x == 0 && a.xq_out)
-                        *(uint2*)(a.xq_out + (int64_t)m * K + c) = make_uint2(code[0], code[1]);
-                }
+        for (int v = 0; v < 2; ++v) {
+            const int c = (threadIdx.x + v * T) * 8;
+            uint32_t code[2] = {0, 0};
+            if (m < M && c < K) {
+                quantize8_bf16(xv[m][v], sx[m], rcp, pow2, code);
+                if (blockIdx.x == 0 && a.xq_out) *(uint2*)(a.xq_out + (int64_t)m * K + c) = make_uint2(code[0], code[1]);
             }
+            *(uint2*)(xs + m * ldx + c) = make_uint2(code[0], code[1]);
         }
+        if (blockIdx.x == 0 && threadIdx.x == 0 && a.sx_out && m < M) a.sx_out[m] = sx[m];
     }
     __syncthreads();
 
-    // 3. MFMAs with A from LDS; further slabs only when a wave owns > 1 KiB of K
-    const int8_t* xrow = xs + (r16 < M ? r16 : 0) * ldx;  // rows >= M feed discarded outputs
+    // 4. MFMAs with A from LDS (lanes of rows >= MM read row 0: discarded outputs)
+    const int8_t* xrow = xs + ((lane & 15) < MM ? (lane & 15) : 0) * ldx + (lane >> 4) * 16;
     v4i acc = {0, 0, 0, 0};
-    if (kend - kbeg == 64 * kSteps) {  // one full slab (the common case): no K tail to mask
 #pragma unroll
-        for (int s = 0; s < kSteps; ++s)
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const v4i*)(xrow + kbeg + s * 64 + g * 16), b[s], acc, 0,
-                                                        0, 0);
-        reduce_and_store(acc, red, tile, M, N, srow, a.sw, a.bias, a.out, a.out_dtype);
-        return;
-    }
-    for (int k0 = kbeg; k0 < kend; k0 += 64 * kSteps) {
-        if (k0 != kbeg) {
-            __builtin_amdgcn_sched_barrier(0);
-            load_slab(b, wr, lane_off + k0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+    for (int s = 0; s < kSlab; ++s)
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const v4i*)(xrow + (wave + s * W) * 64), b[s], acc, 0, 0, 0);
+    if (reduce_waves(acc, red, W) && n < N && (lane >> 4) == 0) {
 #pragma unroll
-        for (int s = 0; s < kSteps; ++s) {
-            const int k = k0 + s * 64 + g * 16;
-            const v4i x = zero_unless(k < kend, *(const v4i*)(xrow + (k < kend ? k : k0)));
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x, b[s], acc, 0, 0, 0);
-        }
+        for (int r = 0; r < MM; ++r)
+            if (r < M) store_y(a.out, a.out_dtype, (int64_t)r * N + n, acc[r], sx[r], swn, a.bias, bn);
     }
-    reduce_and_store(acc, red, tile, M, N, srow, a.sw, a.bias, a.out, a.out_dtype);
 }
 
 extern "C" __global__ __launch_bounds__(512) void nh_linear_decode_w8a8_m1_kernel(LinearDecodeArgs a) {
-    extern __shared__ __align__(16) int8_t xs[];  // [M][K + 16] codes
+    extern __shared__ __align__(16) int8_t xs[];  // [MM][W * 1024 + 16] codes
     linear_decode<1>(a, xs);
 }
 
@@ -243,39 +216,67 @@ extern "C" __global__ __launch_bounds__(512) void nh_linear_decode_w8a8_kernel(L
 // gemm.rs:99-109); this kernel does the same arithmetic per element (f32
 // multiply, exact f64 product, f64 sum) in a different summation order, so
 // it agrees with that path to a few f64 ulps before the final f32 rounding.
-// One wave per weight row; lanes split K in 16-byte chunks (1 KiB per wave
-// per load, fully coalesced).
-extern "C" __global__ __launch_bounds__(256) void nh_gemv_w8a32_kernel(GemvW8A32Args a) {
-    const int lane = threadIdx.x & 63;
-    const int gw = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int K = a.K, N = a.N, M = a.M;
-    const int nbeg = gw * a.rows_per_wave;
-    const int nend = min(N, nbeg + a.rows_per_wave);
-    for (int n = nbeg; n < nend; ++n) {
-        const int8_t* wrow = a.wq + (int64_t)n * K;
-        const float s = a.sw[n];
-        for (int m = 0; m < M; ++m) {
-            const float* x = a.x + (int64_t)m * K;
-            double acc = 0.0;
-            for (int k = lane * 16; k < K; k += 64 * 16) {
-                const v4i w4 = *(const v4i*)(wrow + k);
-                const float4* xv = (const float4*)(x + k);
+// grid = (N tiles, ceil(M / 4)): a workgroup owns 16 weight rows and 4
+// activation rows; lane (r, g) dequantizes 16 weights of row r per K tile
+// and the f64 partial sums meet through shuffles and LDS.
+extern "C" __global__ __launch_bounds__(512) void nh_gemv_w8a32_kernel(GemvW8A32Args a) {
+    __shared__ double redd[8][4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = a.waves;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int M = a.M, N = a.N, K = a.K, kt = a.kt;
+    const int tile = blockIdx.x, m0 = blockIdx.y * 4;
+    const __amdgpu_buffer_rsrc_t wr = row_tile_rsrc(a.wq, tile, kt);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)M * (uint32_t)K * 4u);
+    const int n = tile * 16 + r16;
+    const float s = n < N ? a.sw[n] : 0.0f;
+    const int steps = (kt + W - 1) / W;
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int s0 = 0; s0 < steps; s0 += kSlab) {
+        v4i b[kSlab];
+        __builtin_amdgcn_sched_barrier(0);
+        load_slab(b, wr, wave + s0 * W, W, lane);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float4 xx = xv[j];
-                    const int word = w4[j];
-                    const float xs[4] = {xx.x, xx.y, xx.z, xx.w};
+        for (int st = 0; st < kSlab; ++st) {
+            const int k = (wave + (s0 + st) * W) * 64 + g * 16;
+            if (k >= K) continue;
+            float wv[16];
 #pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const float wv = (float)(int8_t)(word >> (8 * b)) * s;
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) wv[4 * j + e] = (float)(int8_t)(b[st][j] >> (8 * e)) * s;
+#pragma unroll
+            for (int mm = 0; mm < 4; ++mm) {
+                const int m = m0 + mm;
+                if (m >= M) break;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const v4i xx = buffer_load16(xr, (m * K + k + 4 * q) * 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
                         // the f64 product of two f32 values is exact, so the fused
                         // form rounds exactly like the reference's acc += a * b
-                        acc = __builtin_fma((double)xs[b], (double)wv, acc);
-                    }
+                        acc[mm] = __builtin_fma((double)f32_from_bits((uint32_t)xx[e]), (double)wv[4 * q + e], acc[mm]);
                 }
             }
-            acc = wave_sum_f64(acc);
-            if (lane == 0) a.y[(int64_t)m * N + n] = (float)acc;
+        }
+    }
+    // the 4 lanes of a row (g = 0..3), then the waves
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+        acc[mm] += __shfl_xor(acc[mm], 16, kWave);
+        acc[mm] += __shfl_xor(acc[mm], 32, kWave);
+        redd[wave][mm][lane] = acc[mm];
+    }
+    __syncthreads();
+    if (wave == 0 && g == 0 && n < N) {
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+            const int m = m0 + mm;
+            if (m >= M) break;
+            double t = redd[0][mm][lane];
+            for (int w = 1; w < W; ++w) t += redd[w][mm][lane];
+            a.y[(int64_t)m * N + n] = (float)t;
         }
     }
 }

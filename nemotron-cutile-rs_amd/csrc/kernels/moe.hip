@@ -156,18 +156,18 @@ extern "C" __global__ __launch_bounds__(1024) void nh_moe_permute_kernel(Permute
 }
 
 // R3: grouped W8A8 GEMM.  grid.x = N tiles of 16 rows, grid.y = experts,
-// blockDim = 64 * ceil(K / 1024).
-// HBM-bound like the GEMV: the workgroup's waves split K in slices of up to
-// 1 KiB and each wave issues its whole [16 x slice] weight slab (16 buffer
-// loads of 16 B per lane) at once; the slab then stays in registers while
-// the expert's segment is walked in blocks of 16 routed rows (one block for
-// a typical ~24-row segment), so each expert weight byte leaves HBM once.
-// A rows are gathered per lane (token perm[slot] / top_k for the up
-// projection, the slot itself for the down projection).  Steps past the
-// wave's slice and rows past the segment load from an out-of-range buffer
-// offset, which returns zeros without touching memory.
+// blockDim = 64 * waves, waves = ceil(KT / 16) (K <= 8192).
+// HBM-bound like the GEMV: expert e's weights are tiled (nh_numerics.h) at
+// w + e * tiled_bytes(N, K); wave w owns K tiles w, w + waves, ... and issues
+// the loads of all of them (at most 16, one contiguous KiB each, streaming
+// policy) at once; the slab then stays in registers while the expert's
+// segment is walked in blocks of 16 routed rows (one block for a typical
+// ~24-row segment), so each expert weight byte leaves HBM once.  A rows are
+// gathered per lane (token perm[slot] / top_k for the up projection, the slot
+// itself for the down projection).  Tiles past KT and rows past the segment
+// load from an out-of-range buffer offset, which returns zeros without
+// touching memory.
 constexpr int kGroupedSteps = 16;
-constexpr int kOutOfRange = 0x7ffffff0;
 
 extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(GroupedGemmArgs a) {
     __shared__ v4i red[8 * 64];
@@ -175,21 +175,18 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(Gro
     const int tile = blockIdx.x;
     const int seg0 = a.offsets[e], seg1 = a.offsets[e + 1];
     if (seg0 >= seg1) return;  // no routes: this expert's weights are never read
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = a.waves;
     const int r16 = lane & 15, g = lane >> 4;
-    const int N = a.N, K = a.K;
-    const int kbeg = wave * 64 * kGroupedSteps;
-    const int kend = min(K, kbeg + 64 * kGroupedSteps);
+    const int N = a.N, K = a.K, kt = a.kt;
     const __amdgpu_buffer_rsrc_t wr =
-        make_rsrc(a.w + ((int64_t)e * N + tile * 16) * K, (uint32_t)min(16, N - tile * 16) * (uint32_t)K);
+        make_rsrc(a.w + (int64_t)e * tiled_bytes(N, K) + (int64_t)tile * kt * 1024, (uint32_t)kt * 1024u);
     const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.aq, (uint32_t)a.a_rows * (uint32_t)K);
+    const int n = tile * 16 + r16;
+    const float swn = n < N ? a.sw[(int64_t)e * N + n] : 0.0f;
     v4i b[kGroupedSteps];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int s = 0; s < kGroupedSteps; ++s) {
-        const int k = kbeg + s * 64 + g * 16;
-        b[s] = buffer_load16(wr, k < kend ? r16 * K + k : kOutOfRange);
-    }
+    for (int s = 0; s < kGroupedSteps; ++s) b[s] = buffer_load16_stream(wr, (wave + s * W) * 1024 + lane * 16);
     __builtin_amdgcn_sched_barrier(0);
     for (int m0 = seg0; m0 < seg1; m0 += 16) {
         const int slot = m0 + r16;
@@ -199,36 +196,32 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(Gro
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < kGroupedSteps; ++s) {
-            const int k = kbeg + s * 64 + g * 16;
-            x[s] = buffer_load16(ar, (mok && k < kend) ? arow * K + k : kOutOfRange);
+            const int k = (wave + s * W) * 64 + g * 16;
+            x[s] = buffer_load16(ar, (mok && k < K) ? arow * K + k : kOutOfRange);
         }
         __builtin_amdgcn_sched_barrier(0);
         v4i acc = {0, 0, 0, 0};
 #pragma unroll
         for (int s = 0; s < kGroupedSteps; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[s], b[s], acc, 0, 0, 0);
-        if (nw > 1) {
+        if (W > 1) {
             red[wave * 64 + lane] = acc;
             __syncthreads();
             if (wave == 0)
-                for (int w = 1; w < nw; ++w) acc += red[w * 64 + lane];
+                for (int w = 1; w < W; ++w) acc += red[w * 64 + lane];
         }
-        if (wave == 0) {
-            const int n = tile * 16 + r16;
-            if (n < N) {
-                const float swn = a.sw[(int64_t)e * N + n];
+        if (wave == 0 && n < N) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int srow = m0 + 4 * g + r;
-                    if (srow < seg1) {
-                        const int ar_ = a.gather ? a.perm[srow] / a.top_k : srow;
-                        float y = epilogue_w8a8(acc[r], a.sa[ar_], swn);
-                        if (a.relu2) y = relu2(y);
-                        a.out[(int64_t)srow * N + n] = y;
-                    }
+            for (int r = 0; r < 4; ++r) {
+                const int srow = m0 + 4 * g + r;
+                if (srow < seg1) {
+                    const int ar_ = a.gather ? a.perm[srow] / a.top_k : srow;
+                    float y = epilogue_w8a8(acc[r], a.sa[ar_], swn);
+                    if (a.relu2) y = relu2(y);
+                    a.out[(int64_t)srow * N + n] = y;
                 }
             }
         }
-        if (nw > 1) __syncthreads();
+        if (W > 1) __syncthreads();
     }
 }
 

@@ -39,54 +39,70 @@ struct DequantizeInt4Args {
     float zero_point;
 };
 
-// G1: W8A8 GEMV for M <= 16 on int8 MFMA.  Workgroup = ksplit waves that
-// share one 16-row N tile; wave w owns K range [w*kslice, (w+1)*kslice).
+// Weights of every W8A8 / W8A32 kernel are in the tiled layout of
+// nh_numerics.h: KT = ceil(K / 64) tiles of 1 KiB per 16-row N tile.
+
+// G1 (M <= 16, activations already quantized): a workgroup owns one 16-row
+// N tile; wave w of `waves` owns K tiles w, w + waves, w + 2 waves, ...
 struct GemvW8A8Args {
-    const int8_t* xq;     // [M][K]
+    const int8_t* xq;     // [M][K] row-major
     const float* sx;      // [M]
-    const int8_t* wq;     // [N][K]
+    const int8_t* wq;     // tiled [N][K]
     const float* sw;      // [N]
     const float* bias;    // [N] or null
     void* out;            // f32 or bf16 [M][N]
     int32_t M, N, K;
-    int32_t kslice;       // bytes of K per wave, multiple of 64
-    int32_t ntiles;       // ceil(N / 16)
+    int32_t kt;           // ceil(K / 64)
+    int32_t waves;
     int32_t out_dtype;
 };
 
-// Decode unit: dynamic per-token quantization fused in front of the GEMV.
-// Each workgroup quantizes the (few) activation rows into LDS itself.
+// Decode unit (M <= 4, K <= 8192): per-token quantization (Q2) of bf16 rows
+// fused in front of G1; blockDim = 64 * waves, waves * 1024 >= 64 * kt.
 struct LinearDecodeArgs {
-    const void* x;        // f32 or bf16 [M][K]
-    const int8_t* wq;
+    const void* x;        // bf16 [M][K]
+    const int8_t* wq;     // tiled [N][K]
     const float* sw;
     const float* bias;
     void* out;
     int8_t* xq_out;       // optional: block 0 writes the quantized rows here
     float* sx_out;        // optional: and their scales
     int32_t M, N, K;
-    int32_t kslice;
-    int32_t ntiles;
+    int32_t kt;
+    int32_t waves;
     int32_t x_dtype;
     int32_t out_dtype;
     int32_t pad_;
 };
 
-// G2: W8A32 dequant GEMV (f64 accumulation of x * ((float)q * s)).
+// G2: W8A32 dequant GEMV; grid = (N tiles, ceil(M / 4)).
 struct GemvW8A32Args {
     const float* x;       // [M][K]
-    const int8_t* wq;     // [N][K]
+    const int8_t* wq;     // tiled [N][K]
     const float* sw;      // [N]
     float* y;             // [M][N]
     int32_t M, N, K;
-    int32_t rows_per_wave;
+    int32_t kt;
+    int32_t waves;
+    int32_t pad_;
 };
+
+// Row-major int8 [N][K] -> tiled, one 16-byte tile chunk per thread.
+struct TileWeightsArgs {
+    const int8_t* w;      // [rows][cols] row-major
+    int8_t* tiled;        // tiled_bytes(rows, cols)
+    int64_t rows, cols;
+    int64_t chunks;       // tiled_bytes / 16
+    int32_t kt;
+    int32_t pad_;
+};
+
 
 // G3: W8A8 GEMM on int8 MFMA with LDS-staged tiles.
 struct GemmW8A8Args {
     const int8_t* xq;     // [M][K]
     const float* sx;      // [M]
-    const int8_t* wq;     // [N][K]
+    const int8_t* wq;     // tiled [N][K]
     const float* sw;      // [N]
     const float* bias;    // [N] or null
     void* out;            // [M][N]
@@ -94,7 +110,7 @@ struct GemmW8A8Args {
     int32_t tiles_m, tiles_n;
     int32_t out_dtype;
     int32_t relu2;
-    int32_t pad_;
+    int32_t kt;           // ceil(K / 64)
 };
 
 // R1: sigmoid top-k routing, one wave per token.
@@ -123,7 +139,7 @@ struct GroupedGemmArgs {
     const float* sa;         // gather ? [T] : [R]
     const int32_t* offsets;  // [E+1]
     const int32_t* perm;     // [R]
-    const int8_t* w;         // [E][N][K]
+    const int8_t* w;         // [E] x tiled [N][K], expert stride tiled_bytes(N, K)
     const float* sw;         // [E][N]
     float* out;              // [R][N]
     int32_t experts, N, K;
@@ -132,6 +148,8 @@ struct GroupedGemmArgs {
     int32_t relu2;
     int32_t ntiles;
     int32_t a_rows;          // rows of aq (tokens when gathering, routes otherwise)
+    int32_t kt;
+    int32_t waves;
 };
 
 // R4: scatter-combine.

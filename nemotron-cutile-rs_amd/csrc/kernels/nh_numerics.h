@@ -2,6 +2,7 @@
 // Each function is the one rounding rule the path relies on; the kernels and
 // the host fallback call the same code, so they agree bit for bit.
 #pragma once
+#include <math.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -58,23 +59,60 @@ NH_HD int8_t quantize_i8(float v, float s) {
     return (int8_t)(int)q;
 }
 
-// quantize_i8 without a division on the common path.  With r = RN(1/s) and
-// s normal, t = RN(v * r) is within 2^-23 |v/s| <= 1.6e-5 of v/s, and RN(v/s)
-// within 3.9e-6 of it, so both lie on the same side of every half-integer
-// unless t is within 2^-15 of one; only then is the exact division done.
-// Returns exactly quantize_i8(v, s) for every finite v and s >= 0.
-NH_HD int8_t quantize_i8_rcp(float v, float s, float r) {
-    if (s < 0x1p-126f) return quantize_i8(v, s);  // zero or subnormal scale: exact path
-    const float t = v * r;
-    // nearest integer of t by the 1.5 * 2^23 shift (exact for |t| < 2^22);
-    // away from half-integers that is also round-half-away-from-zero
-    const float q = (t + 0x1.8p23f) - 0x1.8p23f;
-    const float d = t - q;
-    if ((d < 0.0f ? -d : d) >= 0.5f - 0x1p-15f) return quantize_i8(v, s);
-    int qi = (int)q;
-    qi = qi > 127 ? 127 : qi;
-    qi = qi < -127 ? -127 : qi;
-    return (int8_t)qi;
+// quantize_i8 without a division, for a row scale s = RN(amax / 127) with
+// r = RN(1/s) (the per-token activation quantizer of the fused kernels):
+//  * s a power of two (and normal): 1/s is exact, so v * r = v / s exactly
+//    and roundf of it is the reference's rounding.
+//  * otherwise y = fma(v, r, 1.5 * 2^23) holds n = round-to-nearest(v * r)
+//    (exact product) in its low mantissa bits.  |v*r - v/s| and
+//    |RN(v/s) - v/s| are both below 127 * 2^-24, so n equals
+//    roundf(RN(v / s)) whenever v * r is more than 2^-15 from a
+//    half-integer; d = fma(v, r, -n) measures that distance with one
+//    rounding.  The rare value closer to a tie goes to quantize_near_tie.
+//  * zero or subnormal s: the division (quantize_i8).
+// |v| <= amax makes |v * r| < 127.5, so no clamp is needed.
+constexpr float kQuantMagic = 0x1.8p23f;
+constexpr float kQuantTieBand = 0.5f - 0x1p-15f;
+
+NH_HD bool scale_is_pow2(float s) { return s >= 0x1p-126f && (f32_bits(s) & 0x007fffffu) == 0; }
+
+// roundf(RN(|v| / s)) for |v| / s within 2^-14 of h = k + 0.5 (k = floor|t|,
+// t = RN(v * r)), decided without dividing: RN(|v|/s) >= h exactly when
+// |v| / s exceeds the midpoint m between h and its f32 predecessor, or
+// equals it and h is even (round-to-nearest-even at the midpoint).  m has 25
+// significant bits and s 24, so m * s is exact in f64 and the sign of
+// |v| - m * s (one rounding) is exact.
+NH_HD int quantize_near_tie(float v, float s, float t) {
+    const float k = floorf(fabsf(t));
+    const float h = k + 0.5f;
+    const uint32_t hb = f32_bits(h);
+    const double m = 0.5 * ((double)h + (double)f32_from_bits(hb - 1u));
+    const double d = (double)fabsf(v) - m * (double)s;
+    int q = (int)k + ((d > 0.0 || (d == 0.0 && (hb & 1u) == 0u)) ? 1 : 0);
+    q = q > 127 ? 127 : q;
+    return v < 0.0f ? -q : q;
+}
+
+NH_HD int quantize_i8_fast(float v, float s, float r) {
+    if (!(s >= 0x1p-126f)) return quantize_i8(v, s);
+    if (scale_is_pow2(s)) return (int)roundf(v * r);
+    const float y = fmaf(v, r, kQuantMagic);
+    const float n = y - kQuantMagic;
+    const float d = fmaf(v, r, -n);
+    if (fabsf(d) < kQuantTieBand) return (int)n;
+    return quantize_near_tie(v, s, v * r);
+}
+
+// Tiled int8 weight layout: the operand order of v_mfma_i32_16x16x64_i8.
+// A logical [N][K] matrix is stored as ceil(N/16) x KT tiles, KT = ceil(K/64);
+// tile (nt, kt) is 1024 contiguous bytes at (nt * KT + kt) * 1024, and byte
+// 16 * (16 * g + r) + b of it holds W[16 nt + r][64 kt + 16 g + b] (zero
+// outside the matrix).  One 64-lane 16-byte load of a tile is exactly the B
+// operand of one MFMA K step, and a row tile's KT KiB are contiguous.
+NH_HD uint64_t tiled_k_tiles(uint64_t k) { return (k + 63) / 64; }
+NH_HD uint64_t tiled_bytes(uint64_t n, uint64_t k) { return (n + 15) / 16 * 16 * tiled_k_tiles(k) * 64; }
+NH_HD uint64_t tiled_offset(uint64_t n, uint64_t k, uint64_t kt_count) {
+    return (((n >> 4) * kt_count + (k >> 6)) << 10) + (((((k >> 4) & 3) << 4) | (n & 15)) << 4) + (k & 15);
 }
 
 // Row scale from the row's absolute maximum: one RN division by 127.

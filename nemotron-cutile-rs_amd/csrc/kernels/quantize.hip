@@ -7,7 +7,7 @@
 using namespace nh;
 
 // One workgroup per row: pass 1 = absmax + first non-finite column, pass 2 =
-// codes.  Rows of the decode/MoE/weight shapes are 1.8-21.5 K elements, so the
+// codes (quantize_i8_fast: bit-identical to the division, without it).  Rows of the decode/MoE/weight shapes are 1.8-21.5 K elements, so the
 // second pass hits L2.
 extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_i8_kernel(QuantizeRowsArgs a) {
     __shared__ float redf[4];
@@ -41,12 +41,40 @@ extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_i8_kernel(Qua
         if (a.row_status) a.row_status[row] = bad == 0x7fffffff ? -1 : bad;
     }
     int8_t* q = a.q + base;
+    const float r = s > 0.0f ? 1.0f / s : 0.0f;
     if (a.x_dtype == DT_BF16) {
         const uint16_t* x = (const uint16_t*)a.x + base;
-        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) q[c] = quantize_i8(bf16_to_f32(x[c]), s);
+        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) q[c] = (int8_t)quantize_i8_fast(bf16_to_f32(x[c]), s, r);
     } else {
         const float* x = (const float*)a.x + base;
-        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) q[c] = quantize_i8(x[c], s);
+        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) q[c] = (int8_t)quantize_i8_fast(x[c], s, r);
+    }
+}
+
+// Row-major int8 [rows][cols] -> the tiled layout (nh_numerics.h): thread c
+// writes 16-byte chunk c of the tiled buffer (lane c % 64 of tile c / 64),
+// zeros outside the matrix.
+extern "C" __global__ __launch_bounds__(256) void nh_tile_weights_kernel(TileWeightsArgs a) {
+    for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < a.chunks;
+         c += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = c >> 6;
+        const int lane = (int)(c & 63);
+        const int64_t row = (t / a.kt) * 16 + (lane & 15);
+        const int64_t k0 = (t % a.kt) * 64 + (lane >> 4) * 16;
+        v4i v = {0, 0, 0, 0};
+        if (row < a.rows && k0 < a.cols) {
+            const int8_t* src = a.w + row * a.cols + k0;
+            if (k0 + 16 <= a.cols && ((uintptr_t)src & 15) == 0) {
+                v = *(const v4i*)src;
+            } else {
+                uint8_t bytes[16];
+                for (int b = 0; b < 16; ++b) bytes[b] = k0 + b < a.cols ? (uint8_t)src[b] : 0;
+                for (int j = 0; j < 4; ++j)
+                    v[j] = (int)(bytes[4 * j] | (bytes[4 * j + 1] << 8) | (bytes[4 * j + 2] << 16) |
+                                 ((uint32_t)bytes[4 * j + 3] << 24));
+            }
+        }
+        *(v4i*)(a.tiled + c * 16) = v;
     }
 }
 

@@ -17,19 +17,10 @@ unsigned grid_for(int64_t items, int per_block) {
     return (unsigned)g;
 }
 
-// K slice per wave of the GEMV family: 1 KiB of K per wave, at most 8 waves
-// (longer slices are streamed as several 1 KiB slabs).
-void gemv_split(int K, int* kslice, int* waves) {
-    int ks = 1024;
-    int w = (K + ks - 1) / ks;
-    if (w > 8) {
-        ks = ((K + 8 * 64 - 1) / (8 * 64)) * 64;
-        w = (K + ks - 1) / ks;
-    }
-    if (w < 1) w = 1;
-    *kslice = ks;
-    *waves = w;
-}
+// Waves per workgroup of the GEMV family: wave w owns K tiles w, w + W, ...,
+// at most 16 of them per register slab; W = ceil(KT / 16) up to 8 waves
+// (longer K is walked slab by slab).
+int gemv_waves(int kt) { return std::max(1, std::min(8, (kt + 15) / 16)); }
 
 nh_status check_dtype(nh_dtype d, nh_error* err) {
     if (d != NH_F32 && d != NH_BF16) return set_error(err, NH_INVALID_PARAMS, "unknown dtype %d", (int)d);
@@ -61,11 +52,10 @@ nh_status launch_gemv(nh_context* ctx, const int8_t* xq, const float* sx, const 
     a.M = M;
     a.N = N;
     a.K = K;
-    int waves;
-    gemv_split(K, &a.kslice, &waves);
-    a.ntiles = (N + 15) / 16;
+    a.kt = (int)tiled_k_tiles(K);
+    a.waves = gemv_waves(a.kt);
     a.out_dtype = out_dtype;
-    return launch(ctx, K_GEMV_W8A8, (unsigned)a.ntiles, 64u * waves, 0, stream, a, err);
+    return launch(ctx, K_GEMV_W8A8, (unsigned)((N + 15) / 16), 64u * a.waves, 0, stream, a, err);
 }
 
 nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
@@ -83,6 +73,7 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
     a.K = K;
     a.out_dtype = out_dtype;
     a.relu2 = relu2;
+    a.kt = (int)tiled_k_tiles(K);
     // 256x128 tiles when there are enough of them to fill the chip once,
     // 128x128 otherwise (more, smaller tiles against wave quantization).
     const size_t lds256 = 2 * (256 + 128) * 144, lds128 = 2 * (128 + 128) * 144;
@@ -130,6 +121,25 @@ nh_status nh_quantize_rows_i8(nh_context* ctx, const void* x, nh_dtype dtype, si
     if (rows == 0 || cols == 0) return NH_OK;  // nothing to quantize (empty inputs are valid, quantize.rs:490-501)
     QuantizeRowsArgs a{x, q, scales, row_status, (int64_t)rows, (int64_t)cols, dtype, 0};
     return launch(ctx, K_QUANTIZE_ROWS, (unsigned)rows, 256, 0, stream, a, err);
+}
+
+size_t nh_tiled_weights_bytes(size_t n, size_t k) {
+    if (n == 0 || k == 0 || n > (1ull << 40) || k > (1ull << 40)) return 0;
+    return (size_t)tiled_bytes(n, k);
+}
+
+nh_status nh_tile_weights_i8(nh_context* ctx, const int8_t* wq, size_t n, size_t k, int8_t* tiled, size_t tiled_len,
+                             nh_stream stream, nh_error* err) {
+    clear_error(err);
+    if (n == 0 || k == 0) return set_error(err, NH_INVALID_SHAPE, "invalid weight shape n=%zu k=%zu", n, k);
+    if (n >= (1u << 31) || k >= (1u << 31)) return set_error(err, NH_UNSUPPORTED, "n and k must be < 2^31");
+    const size_t need = nh_tiled_weights_bytes(n, k);
+    if (tiled_len != need) return mismatch(err, "tiled", need, tiled_len);
+    if (!aligned16(tiled)) return set_error(err, NH_UNSUPPORTED, "tiled must be 16-byte aligned");
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    TileWeightsArgs a{wq, tiled, (int64_t)n, (int64_t)k, (int64_t)(need / 16), (int)tiled_k_tiles(k), 0};
+    return launch(ctx, K_TILE_WEIGHTS, grid_for(a.chunks, 256), 256, 0, stream, a, err);
 }
 
 nh_status nh_dequantize_i8(nh_context* ctx, const int8_t* q, const float* scales, size_t rows, size_t cols,
@@ -192,11 +202,9 @@ nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
         return st;
     if (!aligned16(wq)) return set_error(err, NH_UNSUPPORTED, "wq must be 16-byte aligned");
     if ((st = bind_device(ctx, err))) return st;
-    const size_t lds = m * (k + 16);
-    // the fused kernel keeps each thread's share of the bf16 rows in registers
-    // (K <= 16 * threads, i.e. K <= 8192 with the GEMV split)
-    const bool fusable = m <= 4 && k <= 8192 && x_dtype == NH_BF16 && lds <= 65536 && aligned16(x) &&
-                         ((uintptr_t)xq_out & 7u) == 0;
+    // the fused kernel keeps each thread's two 8-value chunks of every bf16
+    // row in registers: K <= 16 * threads = 1024 * waves, i.e. K <= 8192
+    const bool fusable = m <= 4 && k <= 8192 && x_dtype == NH_BF16 && aligned16(x) && ((uintptr_t)xq_out & 7u) == 0;
     if (fusable) {
         LinearDecodeArgs a{};
         a.x = x;
@@ -209,14 +217,14 @@ nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
         a.M = (int)m;
         a.N = (int)n;
         a.K = (int)k;
-        int waves;
-        gemv_split((int)k, &a.kslice, &waves);
-        a.ntiles = (int)((n + 15) / 16);
+        a.kt = (int)tiled_k_tiles(k);
+        a.waves = gemv_waves(a.kt);
         a.x_dtype = x_dtype;
         a.out_dtype = out_dtype;
         const KernelId kid = m == 1 ? K_LINEAR_DECODE_M1 : (m == 2 ? K_LINEAR_DECODE_M2 : K_LINEAR_DECODE);
-        return launch(ctx, kid, (unsigned)a.ntiles, 64u * waves, (lds + 15) & ~(size_t)15, stream, a,
-                      err);
+        const size_t rows = m == 1 ? 1 : (m == 2 ? 2 : 4);  // the kernel's row template
+        const size_t lds = rows * ((size_t)a.waves * 1024 + 16);
+        return launch(ctx, kid, (unsigned)((n + 15) / 16), 64u * a.waves, lds, stream, a, err);
     }
     // two launches: Q2 into the workspace (or the caller's xq_out/sx_out), then G1/G3
     int8_t* xq = xq_out;
@@ -240,9 +248,12 @@ nh_status nh_gemv_w8a32(nh_context* ctx, const float* x, const int8_t* wq, const
     if ((st = check_w8a8_shape(m, n, k, err))) return st;
     if (!aligned16(x) || !aligned16(wq)) return set_error(err, NH_UNSUPPORTED, "x and wq must be 16-byte aligned");
     if ((st = bind_device(ctx, err))) return st;
-    GemvW8A32Args a{x, wq, sw, y, (int)m, (int)n, (int)k, 4};
-    const int64_t waves = (n + a.rows_per_wave - 1) / a.rows_per_wave;
-    return launch(ctx, K_GEMV_W8A32, (unsigned)((waves + 3) / 4), 256, 0, stream, a, err);
+    if ((m + 3) / 4 > 65535) return set_error(err, NH_UNSUPPORTED, "device W8A32 GEMV needs m <= 262140");
+    GemvW8A32Args a{x, wq, sw, y, (int)m, (int)n, (int)k, 0, 0, 0};
+    a.kt = (int)tiled_k_tiles(k);
+    a.waves = gemv_waves(a.kt);
+    return launch(ctx, K_GEMV_W8A32, (unsigned)((n + 15) / 16), 64u * a.waves, 0, stream, a, err,
+                  (unsigned)((m + 3) / 4));
 }
 
 // ---- MoE ------------------------------------------------------------------
@@ -304,8 +315,9 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
     a.relu2 = relu2 ? 1 : 0;
     a.ntiles = (int)((n + 15) / 16);
     a.a_rows = (int)a_rows;
-    const unsigned waves = (unsigned)((k + 1023) / 1024);
-    return launch(ctx, K_GROUPED_GEMM, (unsigned)a.ntiles, 64u * waves, 0, stream, a, err, (unsigned)experts);
+    a.kt = (int)tiled_k_tiles(k);
+    a.waves = (a.kt + 15) / 16;  // k <= 8192: one 16-tile slab per wave
+    return launch(ctx, K_GROUPED_GEMM, (unsigned)a.ntiles, 64u * a.waves, 0, stream, a, err, (unsigned)experts);
 }
 
 nh_status nh_moe_combine(nh_context* ctx, const float* slot_out, const int32_t* pos, const float* weights,

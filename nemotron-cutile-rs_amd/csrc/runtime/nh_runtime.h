@@ -8,6 +8,7 @@
 #include <cstdint>
 
 #include "../kernels/nh_kernel_args.h"
+#include "../kernels/nh_numerics.h"
 #include "nemotron_hip.h"
 
 namespace nh {
@@ -27,6 +28,7 @@ enum KernelId : int {
     K_PERMUTE,
     K_GROUPED_GEMM,
     K_COMBINE,
+    K_TILE_WEIGHTS,
     K_COUNT
 };
 

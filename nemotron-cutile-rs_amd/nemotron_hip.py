@@ -85,6 +85,9 @@ _SIGNATURES = {
     "nh_quantize_rows_i8_host": (ST, [P, C.c_int, SZ, SZ, P, P, E]),
     "nh_dequantize_i8": (ST, [P, P, P, SZ, SZ, P, P, E]),
     "nh_dequantize_i8_host": (ST, [P, P, SZ, SZ, P, E]),
+    "nh_tiled_weights_bytes": (SZ, [SZ, SZ]),
+    "nh_tile_weights_i8": (ST, [P, P, SZ, SZ, P, SZ, P, E]),
+    "nh_tile_weights_i8_host": (ST, [P, SZ, SZ, P, SZ, E]),
     "nh_gemm_f32_host": (ST, [P, SZ, P, SZ, SZ, SZ, SZ, P, SZ, E]),
     "nh_supports_gemm_w8a8": (C.c_int, [SZ, SZ, SZ]),
     "nh_gemm_w8a8": (ST, [P, P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, P, E]),
@@ -258,6 +261,14 @@ class HipEvents:
 
     def destroy(self, ev):
         self.hip.hipEventDestroy(ev)
+
+
+def tile_weights(ctx, wq_dev, n, k, stream=None):
+    """Device int8 [n][k] row-major -> a new device buffer in the tiled layout."""
+    nbytes = lib().nh_tiled_weights_bytes(n, k)
+    out = ctx.empty(nbytes, np.int8)
+    call("nh_tile_weights_i8", ctx.handle, wq_dev.ptr, n, k, out.ptr, nbytes, stream)
+    return out
 
 
 def normal_f32(seed, n, mean=0.0, std=1.0):

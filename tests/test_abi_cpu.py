@@ -14,6 +14,7 @@ import pytest
 
 import nemotron_hip as NH
 import oracle_ctypes as O
+from tiling import tile_16x64, tile_experts, tiled_bytes
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "nemotron_hip.h")
@@ -128,6 +129,65 @@ def test_quantize_rows_host_twin_matches_oracle():
     assert st == NH.NON_FINITE_INPUT and err.index == 3 * 129 + 5
 
 
+def _bf16_rows_every_value(amax_bits_list):
+    """One row per row maximum: every finite bf16 value v with |v| <= amax, both signs, and amax itself."""
+    pos = np.arange(0, 0x7f80, dtype=np.uint32)
+    rows = []
+    for ab in amax_bits_list:
+        p = pos[pos <= ab].astype(np.uint16)
+        rows.append(np.concatenate([p, p | 0x8000, [ab]]).astype(np.uint16))
+    width = max(r.size for r in rows)
+    # pad with zeros (they quantize to 0 and do not change the row maximum)
+    return np.stack([np.concatenate([r, np.zeros(width - r.size, np.uint16)]) for r in rows])
+
+
+@pytest.mark.slow
+def test_quantize_rows_host_twin_every_bf16_value():
+    """The division-free quantizer (quantize_i8_fast: multiply by the
+    reciprocal, exact tie decision next to half-integers, power-of-two scales
+    rounded exactly; the fused decode kernels run the same rule) against the
+    oracle's division, on every bf16 value below each of 96 row maxima.  The
+    maxima include 127 * 2^e (power-of-two scales: hundreds of exact ties per
+    row) and random ones (the value amax / 2 is an exact tie of every row)."""
+    rng = np.random.default_rng(21)
+    special = [127.0 * 2.0 ** e for e in (-20, -5, 0, 3)] + [3.96875, 4.125, 1.0, 0.1, 250.0, 1e-30]
+    specials = O.to_bf16(np.array(special, dtype=np.float32)).ravel()
+    rand = rng.integers(0x3000, 0x4800, size=86).astype(np.uint16)
+    xb = _bf16_rows_every_value([int(b) for b in np.concatenate([specials, rand])])
+    rows, cols = xb.shape
+    _, q_ref, s_ref, _ = O.quantize_rows_bf16(xb)
+    q = np.zeros_like(q_ref)
+    s = np.zeros_like(s_ref)
+    NH.call("nh_quantize_rows_i8_host", xb.ctypes.data, NH.BF16, rows, cols, q.ctypes.data, s.ctypes.data)
+    assert np.array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(q, q_ref)
+    # the sweep does reach the tie branches: exact half-integer quotients exist
+    t = O.bf16_to_f32(xb).astype(np.float64) / s_ref[:, None].astype(np.float64)
+    assert int(np.sum(np.abs(t - np.floor(t) - 0.5) < 2.0 ** -15)) > 1000
+
+
+def test_quantize_rows_host_twin_f32_near_ties():
+    """f32 values placed within a few ulps of (j + 0.5) * s for non-power-of-two
+    scales, where the reciprocal multiply alone would round the wrong way."""
+    rng = np.random.default_rng(22)
+    rows = []
+    for _ in range(64):
+        amax = np.float32(rng.uniform(0.01, 100.0))
+        s = np.float32(amax / np.float32(127.0))
+        j = rng.integers(0, 127, size=500)
+        base = ((j + 0.5) * np.float64(s)).astype(np.float32)
+        ulp = rng.integers(-3, 4, size=500).astype(np.int32)
+        vals = (base.view(np.int32) + ulp).view(np.float32) * rng.choice([-1, 1], size=500).astype(np.float32)
+        vals = np.clip(vals, -amax, amax)
+        rows.append(np.concatenate([[amax], vals]).astype(np.float32))
+    x = np.stack(rows)
+    _, q_ref, s_ref, _ = O.quantize_rows_f32(x)
+    q = np.zeros_like(q_ref)
+    s = np.zeros_like(s_ref)
+    NH.call("nh_quantize_rows_i8_host", x.ctypes.data, NH.F32, x.shape[0], x.shape[1], q.ctypes.data, s.ctypes.data)
+    assert np.array_equal(q, q_ref)
+
+
 @pytest.mark.parametrize("kat", KATS["gemm"] + [dict(KATS["gemm_pattern"][0], lhs=None)],
                          ids=lambda k: k["src"].split("/")[-1])
 def test_gemm_f32_host_twin_matches_oracle(kat):
@@ -161,15 +221,46 @@ def test_w8a8_and_w8a32_host_twins_match_oracle():
     sx = rng.uniform(1e-3, 1e-2, m).astype(np.float32)
     sw = rng.uniform(1e-4, 1e-3, n).astype(np.float32)
     bias = rng.standard_normal(n).astype(np.float32)
+    wt = tile_16x64(wq)
     for dt, npdt, bf in ((NH.F32, np.float32, False), (NH.BF16, np.uint16, True)):
         out = np.zeros((m, n), dtype=npdt)
-        NH.call("nh_gemm_w8a8_host", xq.ctypes.data, sx.ctypes.data, wq.ctypes.data, sw.ctypes.data, bias.ctypes.data,
+        NH.call("nh_gemm_w8a8_host", xq.ctypes.data, sx.ctypes.data, wt.ctypes.data, sw.ctypes.data, bias.ctypes.data,
                 m, n, k, out.ctypes.data, dt)
         assert np.array_equal(out, O.linear_w8a8(xq, sx, wq, sw, bias=bias, out_bf16=bf))
     x = rng.standard_normal((m, k)).astype(np.float32)
     y = np.zeros((m, n), dtype=np.float32)
-    NH.call("nh_gemv_w8a32_host", x.ctypes.data, wq.ctypes.data, sw.ctypes.data, m, n, k, y.ctypes.data)
+    NH.call("nh_gemv_w8a32_host", x.ctypes.data, wt.ctypes.data, sw.ctypes.data, m, n, k, y.ctypes.data)
     assert np.array_equal(y, O.gemv_w8a32(x, wq, sw))
+
+
+@pytest.mark.parametrize("n,k", [(1, 1), (16, 64), (33, 96), (17, 200), (48, 4112)])
+def test_tile_weights_host_twin_matches_layout(n, k):
+    rng = np.random.default_rng(n * 1000 + k)
+    wq = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    nbytes = NH.lib().nh_tiled_weights_bytes(n, k)
+    assert nbytes == tiled_bytes(n, k) == -(-n // 16) * 16 * -(-k // 64) * 64
+    out = np.full(nbytes, 0x55, dtype=np.int8)
+    NH.call("nh_tile_weights_i8_host", wq.ctypes.data, n, k, out.ctypes.data, nbytes)
+    ref = tile_16x64(wq)
+    assert np.array_equal(out, ref)
+    # spot check of the layout formula itself: W[n][k] sits at tile (n/16, k/64), byte 16*(16*g + r) + b
+    kt = -(-k // 64)
+    for (r_, c_) in [(0, 0), (n - 1, k - 1), (n // 2, k // 3)]:
+        off = ((r_ // 16) * kt + c_ // 64) * 1024 + 16 * (16 * ((c_ % 64) // 16) + r_ % 16) + c_ % 16
+        assert out[off] == wq[r_, c_]
+    # the padding is zero and every matrix byte appears once
+    assert np.count_nonzero(out) == np.count_nonzero(wq)
+
+
+def test_tile_weights_host_twin_errors():
+    one = np.zeros(64, dtype=np.int8)
+    st, err = NH.call_status("nh_tile_weights_i8_host", one.ctypes.data, 1, 1, one.ctypes.data, 63)
+    assert st == NH.LENGTH_MISMATCH and (err.argument, err.expected, err.actual) == (b"tiled", 1024, 63)
+    st, _ = NH.call_status("nh_tile_weights_i8_host", one.ctypes.data, 0, 1, one.ctypes.data, 0)
+    assert st == NH.INVALID_SHAPE
+    assert NH.lib().nh_tiled_weights_bytes(0, 5) == 0
+    st, _ = NH.call_status("nh_tile_weights_i8", None, one.ctypes.data, 1, 1, one.ctypes.data, 63, None)
+    assert st == NH.LENGTH_MISMATCH  # validated before the (absent) device is touched
 
 
 def test_sigmoid_host_twin_equals_glibc_expf_sigmoid():
@@ -248,8 +339,9 @@ def test_moe_host_twins_match_oracle():
     w = rng.integers(-127, 128, size=(experts, inter, hidden), dtype=np.int8)
     sw = rng.uniform(1e-4, 1e-3, (experts, inter)).astype(np.float32)
     out = np.zeros((R, inter), dtype=np.float32)
+    wt = tile_experts(w)
     NH.call("nh_moe_grouped_gemm_w8a8_host", xq.ctypes.data, sx.ctypes.data, 1, k_top, offsets.ctypes.data,
-            perm.ctypes.data, R, tokens, experts, w.ctypes.data, sw.ctypes.data, inter, hidden, 1, out.ctypes.data)
+            perm.ctypes.data, R, tokens, experts, wt.ctypes.data, sw.ctypes.data, inter, hidden, 1, out.ctypes.data)
     ref = O.moe_grouped(xq, sx, True, k_top, offsets, perm, w, sw, relu2=True)
     assert np.array_equal(out, ref)
     weights = rng.uniform(0, 1, R).astype(np.float32)

@@ -17,6 +17,7 @@ import pytest
 
 import nemotron_hip as NH
 import oracle_ctypes as O
+from tiling import tile_16x64, tile_experts
 
 pytestmark = pytest.mark.gpu
 
@@ -127,6 +128,17 @@ def test_dequantize_int4_matches_host_reference(ctx, packed, count, scale, zp):
     assert np.array_equal(out.numpy(), ref)  # reference tolerance 1e-6 (quantize.rs:585-617); exact here
 
 
+# ---- tiled weight layout -----------------------------------------------------------
+@pytest.mark.parametrize("n,k", [(1, 1), (33, 96), (17, 200), (4096, 4096), (20, 4112)])
+def test_tile_weights_on_device_matches_layout(ctx, n, k):
+    note(f"tile_weights n={n} k={k}")
+    wq = np.random.default_rng(n + k).integers(-127, 128, size=(n, k), dtype=np.int8)
+    dwq = ctx.upload(wq)
+    t = NH.tile_weights(ctx, dwq, n, k)
+    ctx.synchronize()
+    assert np.array_equal(t.numpy(), tile_16x64(wq))
+
+
 # ---- G1: W8A8 GEMV (M <= 16) ----------------------------------------------------
 @pytest.mark.parametrize("m,n,k", [(1, 16384, 4096), (4, 16384, 4096), (16, 16384, 4096), (1, 4096, 8192),
                                    (4, 4096, 8192), (16, 4096, 8192), (3, 1000, 80), (16, 20, 4112)])
@@ -136,7 +148,7 @@ def test_gemv_w8a8_bit_exact(ctx, m, n, k):
     x = activations_bf16(m, k)
     _, xq, sx, _ = O.quantize_rows_bf16(x)
     bias = O.normal_f32(7, n, 0.0, 0.1)
-    d = {name: ctx.upload(a) for name, a in dict(xq=xq, sx=sx, wq=wq, sw=sw, bias=bias).items()}
+    d = {name: ctx.upload(a) for name, a in dict(xq=xq, sx=sx, wq=tile_16x64(wq), sw=sw, bias=bias).items()}
     for out_dt, np_dt, use_bias in ((NH.BF16, np.uint16, False), (NH.F32, np.float32, True)):
         out = ctx.empty((m, n), np_dt)
         NH.call("nh_gemm_w8a8", ctx.handle, d["xq"].ptr, d["sx"].ptr, d["wq"].ptr, d["sw"].ptr,
@@ -155,7 +167,8 @@ def test_linear_decode_unit_bit_exact(ctx, m):
     x = activations_bf16(m, k, seed=1 + m)
     _, xq_ref, sx_ref, _ = O.quantize_rows_bf16(x)
     ref = O.linear_w8a8(xq_ref, sx_ref, wq, sw, out_bf16=True)
-    dx, dw, ds = ctx.upload(x), ctx.upload(wq), ctx.upload(sw)
+    dwq = ctx.upload(wq)
+    dx, dw, ds = ctx.upload(x), NH.tile_weights(ctx, dwq, n, k), ctx.upload(sw)  # the device tiler
     out = ctx.empty((m, n), np.uint16)
     xq = ctx.empty((m, k), np.int8)
     sx = ctx.empty(m, np.float32)
@@ -175,6 +188,49 @@ def test_linear_decode_unit_bit_exact(ctx, m):
     assert np.array_equal(out2.numpy(), ref)
 
 
+@pytest.mark.parametrize("m", [1, 3])
+def test_linear_decode_unit_rounding_ties(ctx, m):
+    """Rows whose scale is a power of two carry exact half-integer quotients
+    (x/s = j + 0.5): round-half-away-from-zero and round-half-even disagree on
+    every one of them, so a fused quantizer that rounds ties the wrong way, or
+    skips its exact-division fallback next to a tie, changes codes."""
+    n, k = 4096, 4096
+    note(f"linear_w8a8 decode rounding ties m={m}")
+    _, wq, sw = quantized_weights(n, k)
+    rng = np.random.default_rng(11 + m)
+    rows = []
+    for r in range(m):
+        e = (0, -3, 2)[r % 3]
+        amax = 127.0 * 2.0 ** e
+        row = np.clip(rng.standard_normal(k) * amax / 4, -amax, amax).astype(np.float32)
+        ties = np.array([(j + 0.5) * 2.0 ** e for j in range(127)], dtype=np.float32)
+        vals = np.concatenate([[amax], ties, -ties])
+        cols = rng.permutation(k)[:vals.size]
+        row[cols] = vals
+        rows.append(row)
+    x = O.to_bf16(np.stack(rows))
+    _, xq_ref, sx_ref, _ = O.quantize_rows_bf16(x)
+    xf = O.bf16_to_f32(x)
+    for r in range(m):
+        e = (0, -3, 2)[r % 3]
+        assert sx_ref[r] == np.float32(2.0 ** e)  # power-of-two scale: every j + 0.5 is an exact tie
+        t = xf[r] / sx_ref[r]
+        tie = (t - np.floor(t)) == 0.5
+        assert tie.sum() >= 254
+        assert np.array_equal(xq_ref[r][tie], (np.sign(t[tie]) * np.ceil(np.abs(t[tie]))).astype(np.int8))
+    ref = O.linear_w8a8(xq_ref, sx_ref, wq, sw, out_bf16=True)
+    dx, dw, ds = ctx.upload(x), ctx.upload(tile_16x64(wq)), ctx.upload(sw)
+    out = ctx.empty((m, n), np.uint16)
+    xq = ctx.empty((m, k), np.int8)
+    sx = ctx.empty(m, np.float32)
+    NH.call("nh_linear_w8a8", ctx.handle, dx.ptr, NH.BF16, dw.ptr, ds.ptr, None, m, n, k, out.ptr, NH.BF16,
+            None, 0, xq.ptr, sx.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(sx.numpy().view(np.uint32), sx_ref.view(np.uint32))
+    assert np.array_equal(xq.numpy(), xq_ref)
+    assert np.array_equal(out.numpy(), ref)
+
+
 # ---- G2: W8A32 dequant GEMV (BASELINE config 1) ------------------------------------
 @pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (2, 1000, 80)])
 def test_gemv_w8a32_within_tolerance(ctx, m, n, k):
@@ -182,7 +238,7 @@ def test_gemv_w8a32_within_tolerance(ctx, m, n, k):
     _, wq, sw = quantized_weights(n, k)
     x = O.normal_f32(1, m * k).reshape(m, k)
     ref = O.gemv_w8a32(x, wq, sw)
-    dx, dw, ds = ctx.upload(x), ctx.upload(wq), ctx.upload(sw)
+    dx, dw, ds = ctx.upload(x), ctx.upload(tile_16x64(wq)), ctx.upload(sw)
     y = ctx.empty((m, n), np.float32)
     NH.call("nh_gemv_w8a32", ctx.handle, dx.ptr, dw.ptr, ds.ptr, m, n, k, y.ptr, None)
     ctx.synchronize()
@@ -201,7 +257,7 @@ def test_gemm_w8a8_bit_exact(ctx, m, n, k):
     _, wq, sw = quantized_weights(n, k)
     x = activations_bf16(m, k)
     _, xq, sx, _ = O.quantize_rows_bf16(x)
-    dxq, dsx, dw, dsw = ctx.upload(xq), ctx.upload(sx), ctx.upload(wq), ctx.upload(sw)
+    dxq, dsx, dw, dsw = ctx.upload(xq), ctx.upload(sx), ctx.upload(tile_16x64(wq)), ctx.upload(sw)
     out = ctx.empty((m, n), np.uint16)
     NH.call("nh_gemm_w8a8", ctx.handle, dxq.ptr, dsx.ptr, dw.ptr, dsw.ptr, None, m, n, k, out.ptr, NH.BF16, None)
     ctx.synchronize()
@@ -304,8 +360,8 @@ def test_moe_stages_bit_exact(ctx, tokens, hidden, inter, experts, top_k):
     offsets, perm, pos = O.moe_permute(idx, tokens, top_k, experts)
     R = tokens * top_k
     h_ref = O.moe_grouped(xq, sx, True, top_k, offsets, perm, up, su, relu2=True)
-    d = {n: ctx.upload(a) for n, a in dict(xq=xq, sx=sx, off=offsets, perm=perm, pos=pos, w=w, up=up, su=su,
-                                           down=down, sd=sd).items()}
+    d = {n: ctx.upload(a) for n, a in dict(xq=xq, sx=sx, off=offsets, perm=perm, pos=pos, w=w, up=tile_experts(up),
+                                           su=su, down=tile_experts(down), sd=sd).items()}
     h = ctx.empty((R, inter), np.float32)
     NH.call("nh_moe_grouped_gemm_w8a8", ctx.handle, d["xq"].ptr, d["sx"].ptr, 1, top_k, d["off"].ptr, d["perm"].ptr,
             R, tokens, experts, d["up"].ptr, d["su"].ptr, inter, hidden, 1, h.ptr, None)
@@ -335,7 +391,7 @@ def test_moe_forward_bit_exact(ctx, tokens, hidden, inter, experts, top_k):
     ws_bytes = NH.lib().nh_moe_forward_w8a8_workspace_size(tokens, hidden, inter, experts, top_k)
     ws = ctx.empty(ws_bytes, np.uint8)
     dx, dl = ctx.upload(x), ctx.upload(logits)
-    dup, dsu, ddown, dsd = ctx.upload(up), ctx.upload(su), ctx.upload(down), ctx.upload(sd)
+    dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
     out = ctx.empty((tokens, hidden), np.uint16)
     NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
             dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, None)
