@@ -1,151 +1,257 @@
-// G3: W8A8 GEMM for prefill-sized M on int8 MFMA (v_mfma_i32_32x32x32_i8).
+// G3: W8A8 GEMM for prefill-sized M on int8 MFMA (v_mfma_i32_16x16x64_i8).
 // Weights (B) are in the tiled layout (nh_numerics.h); activations (A) are
 // row-major [M][K].
 //
-// Workgroup = 256 threads = 4 waves in a 2 x 2 grid over a BM x BN output
-// tile.  K advances in 128-byte steps; A (activations, [M][K]) and B (weights,
-// [N][K]) tiles are staged through LDS with a 144-byte row pitch (9 x 16 B:
-// eight consecutive rows read by a ds_read_b128 land in distinct banks) and
-// double-buffered: the global loads of step t+1 are in flight while the MFMAs
-// of step t run.  The fused epilogue applies the per-token and per-channel
-// scales (+bias, +ReLU^2) and writes f32 or bf16.
+// A workgroup of WGM x WGN waves owns a BM x BN output tile.  Its operands
+// stream through a ring of S stages in LDS, each 128 bytes of K, filled by
+// direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds: lane l writes its
+// 16 bytes at M0 + 16 l), so staging costs no VGPRs and S - 1 stages stay in
+// flight.  Per stage and wave: wait for this wave's loads of the stage
+// (vmcnt), one barrier, refill the slot consumed in the previous iteration,
+// then two MFMA K steps of 64 bytes.  The barrier is a bare s_barrier:
+// __syncthreads' release fence would wait for every in-flight LDS load
+// (vmcnt(0)) and serialize the ring.
 //
-// 32x32x32 int8 MFMA operand convention: lane l supplies row (l % 32) of its
-// operand and bytes [16*(l/32), +16) of the current 32-byte K step (same
-// convention for A and B).  Result: lane l, register r holds
-// D[m = 8*(r/4) + 4*(l/32) + (r%4)][n = l % 32].
+// Operand layout in LDS:
+//  * A: each load instruction covers 8 rows x 128 bytes, i.e. whole cache
+//    lines (measured: 4x the L2->LDS throughput of 16 rows x 64 bytes).
+//    Lane l writes LDS slot l % 8 of row l / 8 and picks which 16-byte chunk
+//    of its row to fetch, so that chunk c of local row R lands in slot
+//    c ^ (R % 8) ^ ((R / 8) % 2): the 16 rows of an MFMA fragment read then
+//    cover all 64 banks.
+//  * B: one 1 KiB tile of the tiled weights per instruction, already in the
+//    MFMA operand order (fragment reads are linear ds_read_b128).
+//
+// Epilogue: the per-token and per-channel scales (+bias, +ReLU^2) are applied
+// in registers, the tile is staged through LDS and every lane stores 16
+// contiguous bytes of an output row (f32 or bf16).
 //
 // blockIdx -> tile mapping is XCD-aware: workgroups are dealt round-robin to
 // the 8 XCDs, so consecutive ids are re-packed to make each XCD own a
-// contiguous range of tiles (column-major: neighbours share B columns and
-// the A panel), which keeps both panels in that XCD's L2.
+// contiguous range of tiles (column-major: neighbours share the A panel and
+// B columns stay in that XCD's L2).
 #include "nh_device.h"
 
 using namespace nh;
 
 namespace {
 
-constexpr int kBK = 128;            // bytes of K per pipeline step
-constexpr int kPitch = kBK + 16;    // LDS row pitch
-constexpr int kThreads = 256;
+__device__ __forceinline__ void wait_vmcnt_le(int n) {
+    // s_waitcnt immediates (gfx9): vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] << 14
+#define NH_VMCNT(n) ((((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14)))
+    switch (n) {
+        case 0: __builtin_amdgcn_s_waitcnt(NH_VMCNT(0)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(NH_VMCNT(1)); break;
+        case 2: __builtin_amdgcn_s_waitcnt(NH_VMCNT(2)); break;
+        case 3: __builtin_amdgcn_s_waitcnt(NH_VMCNT(3)); break;
+        case 4: __builtin_amdgcn_s_waitcnt(NH_VMCNT(4)); break;
+        case 6: __builtin_amdgcn_s_waitcnt(NH_VMCNT(6)); break;
+        case 8: __builtin_amdgcn_s_waitcnt(NH_VMCNT(8)); break;
+        case 9: __builtin_amdgcn_s_waitcnt(NH_VMCNT(9)); break;
+        case 12: __builtin_amdgcn_s_waitcnt(NH_VMCNT(12)); break;
+        case 16: __builtin_amdgcn_s_waitcnt(NH_VMCNT(16)); break;
+        case 18: __builtin_amdgcn_s_waitcnt(NH_VMCNT(18)); break;
+        case 24: __builtin_amdgcn_s_waitcnt(NH_VMCNT(24)); break;
+        default: __builtin_amdgcn_s_waitcnt(NH_VMCNT(0)); break;
+    }
+#undef NH_VMCNT
+}
 
-template <int BM, int BN>
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Epilogue of a wave's WM x WN accumulator tile (16x16 fragments, lane l
+// holding D[4 (l / 16) + r][l % 16]): y = ((float)acc * sx[m]) * sw[n]
+// [+ bias][ReLU^2], staged through this wave's LDS area (64 rows at a time,
+// rows padded by 16 bytes) so that every lane stores 16 contiguous bytes of
+// an output row.  `et` holds 64 * (WN * 4 + 16) bytes.
+template <int WM, int WN, int FM, int FN>
+__device__ __forceinline__ void store_tile_through_lds(const GemmW8A8Args& a, const v4i (&acc)[FM][FN],
+                                                       const float (&sxv)[FM][4], const float (&swv)[FN], int8_t* et,
+                                                       int gm0, int gn0, int lane) {
+    const int M = a.M, N = a.N;
+    const int esz = a.out_dtype == DT_BF16 ? 2 : 4;
+    const int pitch = WN * esz + 16;
+    const int lpr = WN * esz / 16;           // lanes per output row
+    const int rows_per_pass = 64 / lpr;
+    const int rl = lane / lpr, cl = (lane % lpr) * 16;
+    const bool full_n = gn0 + WN <= N && ((N * esz) & 15) == 0;
+    constexpr int kPassFrags = 4;            // 64 rows = 4 fragment rows per pass
+    float bnv[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bnv[j] = a.bias ? a.bias[min(gn0 + j * 16 + (lane & 15), N - 1)] : 0.0f;
+#pragma unroll
+    for (int i0 = 0; i0 < FM; i0 += kPassFrags) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int nl = j * 16 + (lane & 15);
+#pragma unroll
+            for (int i = i0; i < i0 + kPassFrags && i < FM; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float y = epilogue_w8a8(acc[i][j][r], sxv[i][r], swv[j]);
+                    if (a.bias) y = y + bnv[j];
+                    if (a.relu2) y = relu2(y);
+                    const int ml = (i - i0) * 16 + 4 * (lane >> 4) + r;
+                    if (esz == 2)
+                        *(uint16_t*)(et + ml * pitch + nl * 2) = f32_to_bf16(y);
+                    else
+                        *(float*)(et + ml * pitch + nl * 4) = y;
+                }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
+        const int prow = min(WM - i0 * 16, 64);
+        for (int ml = rl; ml < prow; ml += rows_per_pass) {
+            const int m = gm0 + i0 * 16 + ml;
+            if (m >= M) break;
+            const v4i v = *(const v4i*)(et + ml * pitch + cl);
+            int8_t* dst = (int8_t*)a.out + ((int64_t)m * N + gn0) * esz + cl;
+            if (full_n) {
+                *(v4i*)dst = v;
+            } else {
+                const int valid = (N - gn0) * esz - cl;
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    if (e < valid) dst[e] = (int8_t)(v[e >> 2] >> (8 * (e & 3)));
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next pass overwrites
+    }
+}
+
+__device__ __forceinline__ int a_slot(int row, int chunk) { return chunk ^ (row & 7) ^ ((row >> 3) & 1); }
+
+template <int BM, int BN, int WGM, int WGN, int S>
 __device__ __forceinline__ void gemm_tile(const GemmW8A8Args& a, int8_t* smem) {
-    constexpr int WM = BM / 2, WN = BN / 2;       // per-wave tile
-    constexpr int TM = WM / 32, TN = WN / 32;     // 32x32 MFMA tiles per wave
-    constexpr int CA = BM * kBK / 16 / kThreads;  // 16-byte chunks per thread (A)
-    constexpr int CB = BN * kBK / 16 / kThreads;  // (B)
-    constexpr int kStage = (BM + BN) * kPitch;
+    constexpr int NW = WGM * WGN;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int FM = WM / 16, FN = WN / 16;
+    constexpr int TB = BN / 16;
+    constexpr int IA = BM / 8;                   // A load instructions per stage
+    constexpr int IB = 2 * TB;                   // B load instructions per stage (two K tiles)
+    constexpr int LPW = (IA + IB) / NW;
+    static_assert((IA + IB) % NW == 0, "stage loads must split evenly over the waves");
+    constexpr int kA = BM * 128;                 // A bytes per stage
+    constexpr int kStage = kA + IB * 1024;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int M = a.M, N = a.N, K = a.K;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int M = a.M, N = a.N, K = a.K, KT = a.kt;
 
-    // XCD-aware tile id
     const int nblk = a.tiles_m * a.tiles_n;
     int b = blockIdx.x;
     if ((nblk & 7) == 0) b = (b & 7) * (nblk >> 3) + (b >> 3);
     const int tm_idx = b % a.tiles_m, tn_idx = b / a.tiles_m;
     const int m0 = tm_idx * BM, n0 = tn_idx * BN;
 
-    // global -> register staging
-    v4i ga[CA], gb[CB];
-    auto load_stage = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < CA; ++i) {
-            const int c = tid + i * kThreads;
-            const int row = c >> 3, col = (c & 7) * 16;
-            const int gm = m0 + row, gk = k0 + col;
-            ga[i] = (gm < M && gk < K) ? *(const v4i*)(a.xq + (int64_t)gm * K + gk) : v4i{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int i = 0; i < CB; ++i) {
-            const int c = tid + i * kThreads;
-            const int row = c >> 3, col = (c & 7) * 16;
-            const int gn = n0 + row, gk = k0 + col;
-            gb[i] = (gn < N && gk < K) ? *(const v4i*)(a.wq + tiled_offset(gn, gk, a.kt)) : v4i{0, 0, 0, 0};
-        }
-    };
-    auto store_stage = [&](int buf) {
-        int8_t* sa = smem + buf * kStage;
-        int8_t* sb = sa + BM * kPitch;
-#pragma unroll
-        for (int i = 0; i < CA; ++i) {
-            const int c = tid + i * kThreads;
-            *(v4i*)(sa + (c >> 3) * kPitch + (c & 7) * 16) = ga[i];
-        }
-#pragma unroll
-        for (int i = 0; i < CB; ++i) {
-            const int c = tid + i * kThreads;
-            *(v4i*)(sb + (c >> 3) * kPitch + (c & 7) * 16) = gb[i];
-        }
-    };
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a.xq, (uint32_t)M * (uint32_t)K);
+    const int nt0 = n0 / 16, ntiles = (N + 15) / 16;
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc(a.wq + (int64_t)nt0 * KT * 1024, (uint32_t)min(TB, ntiles - nt0) * (uint32_t)KT * 1024u);
 
-    v16i acc[TM][TN];
+    float swv[FN], sxv[FM][4];
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int j = 0; j < FN; ++j) swv[j] = a.sw[min(n0 + wn * WN + j * 16 + (lane & 15), N - 1)];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = v16i{};
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sxv[i][r] = a.sx[min(m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r, M - 1)];
 
-    const int nk = (K + kBK - 1) / kBK;
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
-    const int fr = lane & 31, fk = (lane >> 5) * 16;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) load_stage((kt + 1) * kBK);
-        const int8_t* sa = smem + buf * kStage + (wm * WM + fr) * kPitch + fk;
-        const int8_t* sb = smem + buf * kStage + BM * kPitch + (wn * WN + fr) * kPitch + fk;
+    // A: instruction q covers local rows 8q .. 8q + 7; lane l -> row 8q + l / 8,
+    // LDS slot l % 8, global chunk c = slot ^ (row % 8) ^ ((row / 8) % 2)
+    const int a_r = lane >> 3, a_s = lane & 7;
+    const uint32_t b_lane = (uint32_t)lane * 16u;
+    auto issue = [&](int st, int slot) {
 #pragma unroll
-        for (int ks = 0; ks < kBK; ks += 32) {
-            v4i af[TM], bf[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) af[i] = *(const v4i*)(sa + i * 32 * kPitch + ks);
-#pragma unroll
-            for (int j = 0; j < TN; ++j) bf[j] = *(const v4i*)(sb + j * 32 * kPitch + ks);
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < nk) store_stage(buf ^ 1);
-        __syncthreads();
-    }
-
-    // fused epilogue
-    const int quad = lane >> 5;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int n = n0 + wn * WN + j * 32 + (lane & 31);
-        if (n >= N) continue;
-        const float swn = a.sw[n];
-        const float bn = a.bias ? a.bias[n] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * quad + (r & 3);
-                if (m < M) {
-                    float y = epilogue_w8a8(acc[i][j][r], a.sx[m], swn);
-                    if (a.bias) y = y + bn;
-                    if (a.relu2) y = relu2(y);
-                    store_out(a.out, (int64_t)m * N + n, y, a.out_dtype);
-                }
+        for (int i = 0; i < LPW; ++i) {
+            const int q = wave * LPW + i;  // uniform
+            if (q < IA) {
+                const int row = 8 * q + a_r;
+                const int c = a_slot(row, a_s);  // the swizzle is an involution in the chunk
+                const int k = st * 128 + c * 16;
+                const uint32_t off = (uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)k;
+                lds_void_t* dst = (lds_void_t*)(smem + slot * kStage + q * 1024);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, dst, 16, k < K ? off : (uint32_t)kOutOfRange, 0, 0, 0);
+            } else {
+                const int u = q - IA;            // k tile u / TB of the stage, n tile u % TB
+                const int kt = st * 2 + u / TB;
+                const uint32_t off = (uint32_t)((u % TB) * KT + kt) * 1024u + b_lane;
+                lds_void_t* dst = (lds_void_t*)(smem + slot * kStage + kA + u * 1024);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, dst, 16, kt < KT ? off : (uint32_t)kOutOfRange, 0, 0, 2);
             }
         }
+    };
+
+    // fragment read offsets: A row R = wm * WM + 16 i + lane % 16, chunk 4 w + lane / 16
+    int a_off[FM][2];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int row = wm * WM + i * 16 + (lane & 15);
+#pragma unroll
+        for (int w = 0; w < 2; ++w)
+            a_off[i][w] = (row >> 3) * 1024 + (row & 7) * 128 + a_slot(row, 4 * w + (lane >> 4)) * 16;
     }
+
+    v4i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    const int ns = (KT + 1) / 2;
+#pragma unroll
+    for (int s0 = 0; s0 < S - 1; ++s0)
+        if (s0 < ns) issue(s0, s0);
+    for (int st = 0; st < ns; ++st) {
+        if (st + S - 2 < ns) wait_vmcnt_le((S - 2) * LPW); else wait_vmcnt_le(0);
+        lds_barrier();
+        if (st + S - 1 < ns) issue(st + S - 1, (st + S - 1) % S);
+        const int8_t* sb = smem + (st % S) * kStage;
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            v4i af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) af[i] = *(const v4i*)(sb + a_off[i][w]);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(sb + kA + (w * TB + wn * FN + j) * 1024 + lane * 16);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+
+    lds_barrier();
+    store_tile_through_lds<WM, WN, FM, FN>(a, acc, sxv, swv, smem + wave * (64 * (WN * 4 + 16)), m0 + wm * WM,
+                                            n0 + wn * WN, lane);
 }
+
 
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256) void nh_gemm_w8a8_kernel(GemmW8A8Args a) {
-    extern __shared__ __align__(16) int8_t smem[];
-    gemm_tile<256, 128>(a, smem);
+// 256 x 128 tiles, 8 waves of 64 x 64, 3 stages: the workhorse (M = 2048,
+// N = 4096 gives exactly one tile per CU).
+extern "C" __global__ __launch_bounds__(512) void nh_gemm_w8a8_256x128_kernel(GemmW8A8Args a) {
+    extern __shared__ __align__(1024) int8_t smem[];
+    gemm_tile<256, 128, 4, 2, 3>(a, smem);
 }
 
+// 256 x 256 tiles, 8 waves of 128 x 64, 2 stages: half the operand bytes per
+// MAC, for shapes with at least two such tiles per CU.
+extern "C" __global__ __launch_bounds__(512) void nh_gemm_w8a8_256x256_kernel(GemmW8A8Args a) {
+    extern __shared__ __align__(1024) int8_t smem[];
+    gemm_tile<256, 256, 2, 4, 2>(a, smem);
+}
+
+// 128 x 128 tiles, 4 waves of 64 x 64, 3 stages: small problems (more tiles).
 extern "C" __global__ __launch_bounds__(256) void nh_gemm_w8a8_128x128_kernel(GemmW8A8Args a) {
-    extern __shared__ __align__(16) int8_t smem[];
-    gemm_tile<128, 128>(a, smem);
+    extern __shared__ __align__(1024) int8_t smem[];
+    gemm_tile<128, 128, 2, 2, 3>(a, smem);
 }

@@ -28,6 +28,11 @@ using namespace nh;
 namespace {
 
 constexpr int kSlab = 16;                // K tiles per wave in flight at once
+// The decode unit issues the first kSlabHead tiles of its slab, quantizes the
+// activations while they stream (the activation loads went first, so they
+// return first), then issues the rest: the quantizer's VALU work no longer
+// waits for the whole slab to have been issued (measured 0.1-0.2 us faster).
+constexpr int kSlabHead = 4;
 
 // The KT KiB of 16-row N tile `tile`.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_tile_rsrc(const int8_t* wq, int tile, int kt) {
@@ -123,8 +128,8 @@ __device__ __forceinline__ void linear_decode(const LinearDecodeArgs& a, int8_t*
 
     // 1. this thread's two 16-byte chunks (8 bf16 values each: chunks t and
     //    t + T, 2 * T * 8 = W * 1024 values) of each row, the epilogue
-    //    operands, then the weight slab.  Loads complete in issue order, so
-    //    the quantizer waits only for the activations.
+    //    operands, then the head of the weight slab.  Loads complete in
+    //    issue order, so the quantizer waits only for the activations.
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)M * (uint32_t)K * 2u);
     v4i xv[MM][2];
     v4i b[kSlab];
@@ -139,7 +144,9 @@ __device__ __forceinline__ void linear_decode(const LinearDecodeArgs& a, int8_t*
     const int n = tile * 16 + (lane & 15);
     const float swn = n < N ? a.sw[n] : 0.0f;
     const float bn = (a.bias && n < N) ? a.bias[n] : 0.0f;
-    load_slab(b, row_tile_rsrc(a.wq, tile, kt), wave, W, lane);
+    const __amdgpu_buffer_rsrc_t wr = row_tile_rsrc(a.wq, tile, kt);
+#pragma unroll
+    for (int s = 0; s < kSlabHead; ++s) b[s] = buffer_load16_stream(wr, (wave + s * W) * 1024 + lane * 16);
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. row absmax over the workgroup; every thread derives the scales
@@ -181,6 +188,11 @@ __device__ __forceinline__ void linear_decode(const LinearDecodeArgs& a, int8_t*
         }
         if (blockIdx.x == 0 && threadIdx.x == 0 && a.sx_out && m < M) a.sx_out[m] = sx[m];
     }
+    // the rest of the slab: its loads queue behind the head's while the MFMAs wait
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = kSlabHead; s < kSlab; ++s) b[s] = buffer_load16_stream(wr, (wave + s * W) * 1024 + lane * 16);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
 
     // 4. MFMAs with A from LDS (lanes of rows >= MM read row 0: discarded outputs)

@@ -22,6 +22,16 @@ unsigned grid_for(int64_t items, int per_block) {
 // (longer K is walked slab by slab).
 int gemv_waves(int kt) { return std::max(1, std::min(8, (kt + 15) / 16)); }
 
+// Dynamic LDS of the GEMM kernels: a ring of `stages` stages (BM rows x 128
+// bytes of A plus 2 * BN/16 weight tiles of 1 KiB), or the epilogue staging
+// of `waves` waves (64 rows x (wave tile width * 4 + 16) bytes each),
+// whichever is larger.
+size_t gemm_lds_bytes(int bm, int bn, int stages, int waves, int wave_n) {
+    const size_t ring = (size_t)stages * ((size_t)bm * 128 + 2 * (size_t)(bn / 16) * 1024);
+    const size_t epi = (size_t)waves * 64 * ((size_t)wave_n * 4 + 16);
+    return ring > epi ? ring : epi;
+}
+
 nh_status check_dtype(nh_dtype d, nh_error* err) {
     if (d != NH_F32 && d != NH_BF16) return set_error(err, NH_INVALID_PARAMS, "unknown dtype %d", (int)d);
     return NH_OK;
@@ -74,12 +84,26 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
     a.out_dtype = out_dtype;
     a.relu2 = relu2;
     a.kt = (int)tiled_k_tiles(K);
-    // 256x128 tiles when there are enough of them to fill the chip once,
-    // 128x128 otherwise (more, smaller tiles against wave quantization).
-    const size_t lds256 = 2 * (256 + 128) * 144, lds128 = 2 * (128 + 128) * 144;
-    const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 127) / 128);
-    bool big = t256 >= ctx->cu_count && lds256 <= ctx->max_shared_per_block;
-    if (!big && lds128 > ctx->max_shared_per_block) {
+    // Tile choice: 256x256 when every CU gets at least two of them (half the
+    // operand bytes per MAC), else 256x128 when they fill the chip once,
+    // else 128x128 (more, smaller tiles against idle CUs).
+    struct Cfg {
+        KernelId id;
+        int bm, bn, threads;
+        size_t lds;  // max(ring of stages, epilogue staging)
+    };
+    const Cfg c256x256{K_GEMM_W8A8_256, 256, 256, 512, gemm_lds_bytes(256, 256, 2, 8, 64)};
+    const Cfg c256x128{K_GEMM_W8A8, 256, 128, 512, gemm_lds_bytes(256, 128, 3, 8, 64)};
+    const Cfg c128x128{K_GEMM_W8A8_128, 128, 128, 256, gemm_lds_bytes(128, 128, 3, 4, 64)};
+    auto tiles = [&](const Cfg& c) { return (int64_t)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn); };
+    const Cfg* cfg = nullptr;
+    if (tiles(c256x256) >= 2 * (int64_t)ctx->cu_count && c256x256.lds <= ctx->max_shared_per_block)
+        cfg = &c256x256;
+    else if (tiles(c256x128) >= ctx->cu_count && c256x128.lds <= ctx->max_shared_per_block)
+        cfg = &c256x128;
+    else if (c128x128.lds <= ctx->max_shared_per_block)
+        cfg = &c128x128;
+    if (!cfg) {
         // LDS too small for the MFMA tiles: 16-row GEMV passes (still exact)
         for (int m0 = 0; m0 < M; m0 += 16) {
             const int mm = std::min(16, M - m0);
@@ -90,14 +114,9 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
         }
         return NH_OK;
     }
-    if (big) {
-        a.tiles_m = (M + 255) / 256;
-        a.tiles_n = (N + 127) / 128;
-        return launch(ctx, K_GEMM_W8A8, (unsigned)(a.tiles_m * a.tiles_n), 256, lds256, stream, a, err);
-    }
-    a.tiles_m = (M + 127) / 128;
-    a.tiles_n = (N + 127) / 128;
-    return launch(ctx, K_GEMM_W8A8_128, (unsigned)(a.tiles_m * a.tiles_n), 256, lds128, stream, a, err);
+    a.tiles_m = (M + cfg->bm - 1) / cfg->bm;
+    a.tiles_n = (N + cfg->bn - 1) / cfg->bn;
+    return launch(ctx, cfg->id, (unsigned)(a.tiles_m * a.tiles_n), (unsigned)cfg->threads, cfg->lds, stream, a, err);
 }
 
 }  // namespace

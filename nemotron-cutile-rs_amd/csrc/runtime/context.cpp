@@ -15,8 +15,9 @@ const char* const kKernelSymbols[K_COUNT] = {
     "nh_quantize_rows_i8_kernel", "nh_dequantize_i8_kernel",   "nh_dequantize_int4_kernel",
     "nh_gemv_w8a8_kernel",        "nh_linear_decode_w8a8_kernel", "nh_linear_decode_w8a8_m1_kernel",
     "nh_linear_decode_w8a8_m2_kernel", "nh_gemv_w8a32_kernel",
-    "nh_gemm_w8a8_kernel",        "nh_gemm_w8a8_128x128_kernel", "nh_moe_route_sigmoid_kernel", "nh_moe_permute_kernel",
+    "nh_gemm_w8a8_256x128_kernel", "nh_gemm_w8a8_128x128_kernel", "nh_moe_route_sigmoid_kernel", "nh_moe_permute_kernel",
     "nh_moe_grouped_gemm_kernel", "nh_moe_combine_kernel",     "nh_tile_weights_kernel",
+    "nh_gemm_w8a8_256x256_kernel",
 };
 
 void clear_error(nh_error* err) {

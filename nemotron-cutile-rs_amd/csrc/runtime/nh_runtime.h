@@ -29,6 +29,7 @@ enum KernelId : int {
     K_GROUPED_GEMM,
     K_COMBINE,
     K_TILE_WEIGHTS,
+    K_GEMM_W8A8_256,
     K_COUNT
 };
 
