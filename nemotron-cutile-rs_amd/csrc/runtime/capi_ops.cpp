@@ -124,9 +124,12 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
 extern "C" {
 
 int nh_supports_gemm_w8a8(size_t m, size_t n, size_t k) {
-    // k <= 2^17 keeps the int32 accumulator exact: |acc| <= k * 127 * 127 < 2^31
+    // k <= 2^17 keeps the int32 accumulator exact: |acc| <= k * 127 * 127 < 2^31.
+    // The kernels address the activations and each weight panel through
+    // 32-bit buffer offsets: m * k < 2^31 (plus a tile's overshoot of at most
+    // 255 rows) and the tiled weights below 2^40 bytes.
     return m > 0 && n > 0 && k > 0 && m < (1u << 31) && n < (1u << 31) && k <= (1u << 17) && (k % 16) == 0 &&
-           (uint64_t)m * k < (1ull << 40) && (uint64_t)n * k < (1ull << 40);
+           (uint64_t)m * k < (1ull << 31) && (uint64_t)n * k < (1ull << 40);
 }
 
 nh_status nh_quantize_rows_i8(nh_context* ctx, const void* x, nh_dtype dtype, size_t rows, size_t cols, int8_t* q,
@@ -267,7 +270,8 @@ nh_status nh_gemv_w8a32(nh_context* ctx, const float* x, const int8_t* wq, const
     if ((st = check_w8a8_shape(m, n, k, err))) return st;
     if (!aligned16(x) || !aligned16(wq)) return set_error(err, NH_UNSUPPORTED, "x and wq must be 16-byte aligned");
     if ((st = bind_device(ctx, err))) return st;
-    if ((m + 3) / 4 > 65535) return set_error(err, NH_UNSUPPORTED, "device W8A32 GEMV needs m <= 262140");
+    if ((m + 3) / 4 > 65535 || (uint64_t)m * k * 4 >= (1ull << 32))
+        return set_error(err, NH_UNSUPPORTED, "device W8A32 GEMV needs m <= 262140 and m * k * 4 < 2^32");
     GemvW8A32Args a{x, wq, sw, y, (int)m, (int)n, (int)k, 0, 0, 0};
     a.kt = (int)tiled_k_tiles(k);
     a.waves = gemv_waves(a.kt);

@@ -78,6 +78,9 @@ def test_device_entry_points_validate_before_touching_a_device():
     # int32 accumulator exactness bound: 131072 * 127^2 < 2^31
     assert NH.lib().nh_supports_gemm_w8a8(1, 16, 131072) == 1
     assert NH.lib().nh_supports_gemm_w8a8(1, 16, 131088) == 0
+    # 32-bit buffer offsets of the activation panel: m * k < 2^31
+    assert NH.lib().nh_supports_gemm_w8a8(16384, 16, 131072) == 0
+    assert NH.lib().nh_supports_gemm_w8a8(16383, 16, 131072) == 1
 
 
 def test_generator_matches_oracle_bit_for_bit():
