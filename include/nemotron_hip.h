@@ -140,6 +140,15 @@ nh_status nh_tile_weights_i8_host(const int8_t *wq, size_t n, size_t k, int8_t *
 /* G0: gemm_into_host restated (gemm.rs:91-147): f32 in, f64 accumulation. */
 nh_status nh_gemm_f32_host(const float *lhs, size_t lhs_len, const float *rhs, size_t rhs_len, size_t m,
                            size_t k, size_t n, float *out, size_t out_len, nh_error *err);
+/* G0d: the device GEMM of gemm / gemm_into (gemm.rs:318-363), f32 [m][k] x
+ * f32 [k][n] -> f32 [m][n], accumulated in f64 with k ascending for every
+ * output: bit-identical to nh_gemm_f32_host.  Same validation and error
+ * payloads as gemm_into; any alignment of m, k, n (the reference's cutile
+ * kernel needed tile multiples, gemm.rs:247-254, and bridged through the
+ * host otherwise).  nh_supports_gemm_f32 is its envelope. */
+int nh_supports_gemm_f32(size_t m, size_t k, size_t n);
+nh_status nh_gemm_f32(nh_context *ctx, const float *lhs, size_t lhs_len, const float *rhs, size_t rhs_len,
+                      size_t m, size_t k, size_t n, float *out, size_t out_len, nh_stream stream, nh_error *err);
 /* Device envelope of the W8A8 GEMM family (supports_shape, gemm.rs:247-254). */
 int nh_supports_gemm_w8a8(size_t m, size_t n, size_t k);
 /* G1/G3: out[m,n] = ((float)sum_k xq[m,k]*wq[n,k] * sx[m]) * sw[n] (+ bias[n])

@@ -98,6 +98,14 @@ struct TileWeightsArgs {
 };
 
 
+// G0d: f32 GEMM with f64 accumulation (the reference's gemm_into order).
+struct GemmF32Args {
+    const float* lhs;     // [M][K]
+    const float* rhs;     // [K][N]
+    float* out;           // [M][N]
+    int64_t M, K, N;
+};
+
 // G3: W8A8 GEMM on int8 MFMA with LDS-staged tiles.
 struct GemmW8A8Args {
     const int8_t* xq;     // [M][K]

@@ -3,4 +3,5 @@
 #include "quantize.hip"
 #include "gemv.hip"
 #include "gemm.hip"
+#include "gemm_f32.hip"
 #include "moe.hip"

@@ -1,5 +1,7 @@
 // Device entry points of the C ABI: validate on the host, then enqueue.
 #include <algorithm>
+#include <climits>
+#include <cstdint>
 #include <cmath>
 #include <cstring>
 
@@ -192,6 +194,31 @@ nh_status nh_dequantize_int4(nh_context* ctx, const uint8_t* packed, size_t pack
     if (value_count == 0) return NH_OK;
     DequantizeInt4Args a{packed, out, (int64_t)value_count, scale, (float)zero_point};
     return launch(ctx, K_DEQUANT_INT4, grid_for((int64_t)value_count, 256), 256, 0, stream, a, err);
+}
+
+int nh_supports_gemm_f32(size_t m, size_t k, size_t n) {
+    // i32 shape bounds of the reference's device GEMM (gemm.rs:247-254), any
+    // alignment; the grid holds ceil(m / 64) <= 65535 row tiles
+    return m > 0 && k > 0 && n > 0 && m <= INT32_MAX && k <= INT32_MAX && n <= INT32_MAX && (m + 63) / 64 <= 65535;
+}
+
+nh_status nh_gemm_f32(nh_context* ctx, const float* lhs, size_t lhs_len, const float* rhs, size_t rhs_len, size_t m,
+                      size_t k, size_t n, float* out, size_t out_len, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    // the validation of gemm_into (gemm.rs:341-363): shape, operand lengths, output length
+    size_t ll, rl, ol;
+    if (m == 0 || k == 0 || n == 0 || !mul_ok(m, k, &ll) || !mul_ok(k, n, &rl) || !mul_ok(m, n, &ol))
+        return set_error(err, NH_INVALID_SHAPE, "invalid GEMM shape m=%zu k=%zu n=%zu", m, k, n);
+    if (lhs_len != ll) return mismatch(err, "lhs", ll, lhs_len);
+    if (rhs_len != rl) return mismatch(err, "rhs", rl, rhs_len);
+    if (out_len != ol) return mismatch(err, "output", ol, out_len);
+    if (!nh_supports_gemm_f32(m, k, n))
+        return set_error(err, NH_UNSUPPORTED, "shape m=%zu k=%zu n=%zu outside the device envelope", m, k, n);
+    if (!aligned16(out)) return set_error(err, NH_UNSUPPORTED, "out must be 16-byte aligned");
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    GemmF32Args a{lhs, rhs, out, (int64_t)m, (int64_t)k, (int64_t)n};
+    return launch(ctx, K_GEMM_F32, (unsigned)((n + 63) / 64), 256, 0, stream, a, err, (unsigned)((m + 63) / 64));
 }
 
 nh_status nh_gemm_w8a8(nh_context* ctx, const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,

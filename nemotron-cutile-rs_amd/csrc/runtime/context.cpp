@@ -17,7 +17,7 @@ const char* const kKernelSymbols[K_COUNT] = {
     "nh_linear_decode_w8a8_m2_kernel", "nh_gemv_w8a32_kernel",
     "nh_gemm_w8a8_256x128_kernel", "nh_gemm_w8a8_128x128_kernel", "nh_moe_route_sigmoid_kernel", "nh_moe_permute_kernel",
     "nh_moe_grouped_gemm_kernel", "nh_moe_combine_kernel",     "nh_tile_weights_kernel",
-    "nh_gemm_w8a8_256x256_kernel",
+    "nh_gemm_w8a8_256x256_kernel", "nh_gemm_f32_kernel",
 };
 
 void clear_error(nh_error* err) {
@@ -218,7 +218,7 @@ static const struct {
     {"int4_affine_host", 0},     {"quantize_rows_i8_host", 0},  {"gemm_w8a8_host", 0},
     {"gemv_w8a32_host", 0},      {"moe_sigmoid_topk_host", 0},  {"moe_softmax_topk_host", 0},
     {"moe_permute_host", 0},     {"moe_grouped_gemm_w8a8_host", 0}, {"moe_combine_host", 0},
-    {"tile_weights_i8", 1},      {"tile_weights_i8_host", 0},
+    {"tile_weights_i8", 1},      {"tile_weights_i8_host", 0},  {"gemm_f32", 1},
 };
 
 int nh_kernel_count(void) { return (int)(sizeof(kRegistry) / sizeof(kRegistry[0])); }

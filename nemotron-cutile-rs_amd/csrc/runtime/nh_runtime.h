@@ -30,6 +30,7 @@ enum KernelId : int {
     K_COMBINE,
     K_TILE_WEIGHTS,
     K_GEMM_W8A8_256,
+    K_GEMM_F32,
     K_COUNT
 };
 

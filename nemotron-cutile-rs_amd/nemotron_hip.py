@@ -89,6 +89,8 @@ _SIGNATURES = {
     "nh_tile_weights_i8": (ST, [P, P, SZ, SZ, P, SZ, P, E]),
     "nh_tile_weights_i8_host": (ST, [P, SZ, SZ, P, SZ, E]),
     "nh_gemm_f32_host": (ST, [P, SZ, P, SZ, SZ, SZ, SZ, P, SZ, E]),
+    "nh_supports_gemm_f32": (C.c_int, [SZ, SZ, SZ]),
+    "nh_gemm_f32": (ST, [P, P, SZ, P, SZ, SZ, SZ, SZ, P, SZ, P, E]),
     "nh_supports_gemm_w8a8": (C.c_int, [SZ, SZ, SZ]),
     "nh_gemm_w8a8": (ST, [P, P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, P, E]),
     "nh_gemm_w8a8_host": (ST, [P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, E]),

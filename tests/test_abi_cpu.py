@@ -216,6 +216,23 @@ def test_gemm_f32_host_twin_errors_match_reference():
     assert st == NH.INVALID_SHAPE
 
 
+@pytest.mark.parametrize("kat", KATS["gemm_errors"], ids=lambda k: k["src"].split(":")[-1])
+def test_device_gemm_f32_validates_like_gemm_into(kat):
+    """G0d's device entry point returns the reference's error variants and
+    payloads (gemm.rs:490-621) before it touches a device (NULL context)."""
+    usize_max = (1 << 64) - 1
+    k = usize_max if kat["k"] == "usize::MAX" else kat["k"]
+    st, err = NH.call_status("nh_gemm_f32", None, None, kat["lhs_len"], None, kat["rhs_len"], kat["m"], k, kat["n"],
+                             None, kat["out_len"], None)
+    if kat["error"] == "InvalidShape":
+        assert st == NH.INVALID_SHAPE
+    else:
+        assert st == NH.LENGTH_MISMATCH
+        assert (err.argument.decode(), err.expected, err.actual) == (kat["argument"], kat["expected"], kat["actual"])
+    assert NH.lib().nh_supports_gemm_f32(3, 5, 7) == 1 and NH.lib().nh_supports_gemm_f32(0, 5, 7) == 0
+    assert NH.lib().nh_supports_gemm_f32(1 << 31, 1, 1) == 0
+
+
 def test_w8a8_and_w8a32_host_twins_match_oracle():
     rng = np.random.default_rng(2)
     m, n, k = 5, 33, 96

@@ -10,6 +10,8 @@ activations ~ N(0, 1) seed 1, router logits seed 2, expert e seed 100 + e.
 """
 import ctypes
 import functools
+import json
+import os
 import sys
 
 import numpy as np
@@ -137,6 +139,62 @@ def test_tile_weights_on_device_matches_layout(ctx, n, k):
     t = NH.tile_weights(ctx, dwq, n, k)
     ctx.synchronize()
     assert np.array_equal(t.numpy(), tile_16x64(wq))
+
+
+# ---- G0d: f32 device GEMM (f64 accumulation, the host order) ----------------------
+def _gemm_f32_case(kat):
+    m, k, n = kat["m"], kat["k"], kat["n"]
+    if kat.get("lhs") is None:
+        lhs = np.array([((i % 11) - 5) * 0.25 for i in range(m * k)], dtype=np.float32)
+        rhs = np.array([((i % 7) - 3) * 0.5 for i in range(k * n)], dtype=np.float32)
+    else:
+        lhs = np.array(kat["lhs"], dtype=np.float32)
+        rhs = np.array(kat["rhs"], dtype=np.float32)
+    return m, k, n, lhs, rhs
+
+
+_GEMM_KATS = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                         "reference_kats.json")))
+
+
+@pytest.mark.parametrize("case", _GEMM_KATS["gemm"] + [dict(_GEMM_KATS["gemm_pattern"][0], lhs=None)]
+                         + [dict(m=m, k=k, n=n, lhs="rand") for (m, k, n) in
+                            [(1, 4096, 4096), (37, 100, 65), (130, 257, 71), (64, 16, 64), (3, 1, 5)]],
+                         ids=lambda c: f"{c['m']}x{c['k']}x{c['n']}")
+def test_gemm_f32_device_bit_exact_with_host_order(ctx, case):
+    note(f"gemm_f32 {case['m']}x{case['k']}x{case['n']}")
+    if case.get("lhs") == "rand":
+        m, k, n = case["m"], case["k"], case["n"]
+        lhs = O.normal_f32(31, m * k)
+        rhs = O.normal_f32(32, k * n, 0.0, 0.02)
+    else:
+        m, k, n, lhs, rhs = _gemm_f32_case(case)
+    _, ref, _ = O.gemm_f32(lhs, rhs, m, k, n)
+    dl, dr = ctx.upload(lhs), ctx.upload(rhs)
+    out = ctx.empty(m * n, np.float32)
+    NH.call("nh_gemm_f32", ctx.handle, dl.ptr, lhs.size, dr.ptr, rhs.size, m, k, n, out.ptr, m * n, None)
+    ctx.synchronize()
+    got = out.numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    if "out" in case:  # the reference KAT's own expected values (tolerance 1e-6)
+        assert np.all(np.abs(got - np.array(case["out"], dtype=np.float32)) <= case["tol"])
+
+
+def test_gemm_f32_device_signed_zero_and_specials(ctx):
+    """Signed zeros, Inf and NaN propagate as on the host (NaN compared by
+    position: the host's default NaN is negative, the GPU's positive)."""
+    m, k, n = 2, 3, 2
+    lhs = np.array([-0.0, -0.0, -0.0, 1.0, np.inf, 2.0], dtype=np.float32)
+    rhs = np.array([1.0, 2.0, 3.0, 0.0, -1.0, np.nan], dtype=np.float32)
+    _, ref, _ = O.gemm_f32(lhs, rhs, m, k, n)
+    dl, dr = ctx.upload(lhs), ctx.upload(rhs)
+    out = ctx.empty(m * n, np.float32)
+    NH.call("nh_gemm_f32", ctx.handle, dl.ptr, lhs.size, dr.ptr, rhs.size, m, k, n, out.ptr, m * n, None)
+    ctx.synchronize()
+    got = out.numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.isnan(ref).sum() == 2
+    keep = ~np.isnan(ref)
+    assert np.array_equal(got[keep].view(np.uint32), ref[keep].view(np.uint32))
 
 
 # ---- G1: W8A8 GEMV (M <= 16) ----------------------------------------------------
