@@ -36,33 +36,6 @@ using namespace nh;
 
 namespace {
 
-__device__ __forceinline__ void wait_vmcnt_le(int n) {
-    // s_waitcnt immediates (gfx9): vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] << 14
-#define NH_VMCNT(n) ((((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14)))
-    switch (n) {
-        case 0: __builtin_amdgcn_s_waitcnt(NH_VMCNT(0)); break;
-        case 1: __builtin_amdgcn_s_waitcnt(NH_VMCNT(1)); break;
-        case 2: __builtin_amdgcn_s_waitcnt(NH_VMCNT(2)); break;
-        case 3: __builtin_amdgcn_s_waitcnt(NH_VMCNT(3)); break;
-        case 4: __builtin_amdgcn_s_waitcnt(NH_VMCNT(4)); break;
-        case 6: __builtin_amdgcn_s_waitcnt(NH_VMCNT(6)); break;
-        case 8: __builtin_amdgcn_s_waitcnt(NH_VMCNT(8)); break;
-        case 9: __builtin_amdgcn_s_waitcnt(NH_VMCNT(9)); break;
-        case 12: __builtin_amdgcn_s_waitcnt(NH_VMCNT(12)); break;
-        case 16: __builtin_amdgcn_s_waitcnt(NH_VMCNT(16)); break;
-        case 18: __builtin_amdgcn_s_waitcnt(NH_VMCNT(18)); break;
-        case 24: __builtin_amdgcn_s_waitcnt(NH_VMCNT(24)); break;
-        default: __builtin_amdgcn_s_waitcnt(NH_VMCNT(0)); break;
-    }
-#undef NH_VMCNT
-}
-
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-}
-
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Epilogue of a wave's WM x WN accumulator tile (16x16 fragments, lane l

@@ -68,17 +68,27 @@ __device__ __forceinline__ void store_y(void* out, int out_dtype, int64_t i, int
 
 }  // namespace
 
-// G1: quantized activations already in memory (xq [M][K] row-major, M <= 16);
-// the A fragments come from L2 (xq is at most 16 x K bytes, shared by every
-// workgroup).  Any K <= 131072: waves walk their K tiles slab by slab.
-extern "C" __global__ __launch_bounds__(512) void nh_gemv_w8a8_kernel(GemvW8A8Args a) {
-    __shared__ v4i red[8 * 64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = a.waves;
+// G1: quantized activations already in memory, M <= 16, any K <= 131072
+// (waves walk their K tiles slab by slab).  The A fragments come from L2
+// (at most 16 x K bytes, shared by every workgroup), issued ahead of the
+// weight slab so they return first.  Two activation layouts:
+//  * row-major xq [M][K] (the public entry point): a fragment is M rows x
+//    64 bytes, M half-used cache lines;
+//  * activation tiles [KT][4][M][16] (written by the row quantizer for the
+//    linear entry point): the fragment of K tile t is the M * 64 contiguous
+//    bytes at 64 M t, lane (r, g) reading 16 of them.  Measured 12.3 vs
+//    12.9 us at M = 8 and 12.9 vs 15.9 us at M = 16 (K = 4096, N = 16384).
+// Bytes of the last K tile past K are not read as zero by the tiled form;
+// the weight tiles are zero there, so they add nothing.
+template <bool XT>
+__device__ __forceinline__ void gemv_w8a8(const GemvW8A8Args& a, v4i* red) {
+    const int lane = threadIdx.x & 63, W = a.waves;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
     const int M = a.M, N = a.N, K = a.K, kt = a.kt;
     const int tile = blockIdx.x;
     const __amdgpu_buffer_rsrc_t wr = row_tile_rsrc(a.wq, tile, kt);
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xq, (uint32_t)M * (uint32_t)K);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xq, XT ? (uint32_t)M * (uint32_t)kt * 64u : (uint32_t)M * (uint32_t)K);
     // epilogue operands first, ahead of the weight stream
     const int n = tile * 16 + r16;
     const float swn = n < N ? a.sw[n] : 0.0f;
@@ -86,17 +96,30 @@ extern "C" __global__ __launch_bounds__(512) void nh_gemv_w8a8_kernel(GemvW8A8Ar
     float sxl[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) sxl[r] = 4 * g + r < M ? a.sx[4 * g + r] : 0.0f;
+    // per-lane parts of the load offsets; the K tile enters as a scalar
+    const bool xrow = r16 < M;
+    const int xlane = XT ? (g * M + r16) * 16 : r16 * K + g * 16;
+    const int wlane = lane * 16;
     const int steps = (kt + W - 1) / W;
     v4i acc = {0, 0, 0, 0};
     for (int s0 = 0; s0 < steps; s0 += kSlab) {
         v4i x[kSlab], b[kSlab];
+        // The slab's first K tile as an opaque scalar: every offset is then
+        // a per-lane invariant plus a scalar computed next to its load, so
+        // no per-load offset registers are hoisted out of the loop (32 of
+        // them would halve the occupancy).
+        int t0 = wave + s0 * W;
+        asm volatile("" : "+s"(t0));
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < kSlab; ++s) {  // activation fragments (L2) first
-            const int k = (wave + (s0 + s) * W) * 64 + g * 16;
-            x[s] = buffer_load16(xr, (r16 < M && k < K) ? r16 * K + k : kOutOfRange);
+            const int t = t0 + s * W;
+            const int off = XT ? xlane + t * 64 * M : xlane + t * 64;
+            x[s] = buffer_load16(xr, (xrow && (XT ? t < kt : t * 64 + g * 16 < K)) ? off : kOutOfRange);
         }
-        load_slab(b, wr, wave + s0 * W, W, lane);  // then the weight slab (HBM)
+#pragma unroll
+        for (int s = 0; s < kSlab; ++s)  // then the weight slab (HBM)
+            b[s] = buffer_load16_stream(wr, (t0 + s * W) * 1024 + wlane);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < kSlab; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[s], b[s], acc, 0, 0, 0);
@@ -108,16 +131,30 @@ extern "C" __global__ __launch_bounds__(512) void nh_gemv_w8a8_kernel(GemvW8A8Ar
     }
 }
 
-// Decode unit, M <= MM <= 4, K <= 8192: per-token quantization of the bf16
-// activation rows (Q2) fused in front of the GEMV.  Every workgroup quantizes
-// the rows into LDS itself while its weight slab is in flight, so the unit is
-// one launch and the int8 activations never round-trip through HBM.  The
+extern "C" __global__ __launch_bounds__(512) void nh_gemv_w8a8_kernel(GemvW8A8Args a) {
+    __shared__ v4i red[8 * 64];
+    gemv_w8a8<false>(a, red);
+}
+
+extern "C" __global__ __launch_bounds__(512) void nh_gemv_w8a8_xt_kernel(GemvW8A8Args a) {
+    __shared__ v4i red[8 * 64];
+    gemv_w8a8<true>(a, red);
+}
+
+// Decode unit for M <= MM <= 4 rows, K <= 8192: per-token quantization of
+// the bf16 activation rows (Q2) fused in front of the GEMV, one N tile per
+// workgroup (used for one row, and for 2..4 rows when K = 8192).  Every workgroup quantizes the row into LDS itself while its
+// weight slab is in flight, so the unit is one launch and the int8
+// activations never round-trip through HBM.  At one row the redundant
+// quantization is cheap, and four independent workgroups per CU keep the
+// weight stream smoother than one wide workgroup (12.4 vs 13.0 us at
+// K = 4096, N = 16384).  The
 // quantizer multiplies by the reciprocal scale (quantize8_bf16) with an exact
 // tie decision for the rare value next to a rounding tie, so codes and scales
 // are bit-identical to quantize_i8 in every workgroup; workgroup 0 also
 // writes them out when asked.
 template <int MM>
-__device__ __forceinline__ void linear_decode(const LinearDecodeArgs& a, int8_t* xs) {
+__device__ __forceinline__ void linear_decode_row(const LinearDecodeArgs& a, int8_t* xs) {
     __shared__ v4i red[8 * 64];
     __shared__ float redf[8][MM];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = a.waves;
@@ -208,19 +245,163 @@ __device__ __forceinline__ void linear_decode(const LinearDecodeArgs& a, int8_t*
     }
 }
 
+// Decode unit, 2 <= M <= MM <= 8, K <= 8192, K % 512 == 0: per-token
+// quantization of the bf16 activation rows (Q2) fused in front of the GEMV,
+// one launch (a separate quantizer launch costs ~4 us of dependent-launch
+// latency on its own).  The quantizer runs in every workgroup, so one
+// workgroup owns up to four 16-row N tiles (16 waves): the chip quantizes
+// once per CU instead of once per N tile, and its VALU work runs while the
+// weight slab is in flight:
+//  1. every thread loads its XR 16-byte activation chunks (L2), the epilogue
+//     operands, then the first KH KiB of its wave's 16 KiB weight slab (HBM;
+//     all of it when the registers allow, else the rest after step 2: half
+//     a slab per wave is 128 KiB per CU in flight, enough for its share of
+//     HBM bandwidth);
+//  2. it waits for the activation loads only (the slab stays in flight),
+//     takes the per-row absmax (an LDS max per row), derives the row scales
+//     and writes the codes into LDS in the A operand order [KT][4][MM][16];
+//  3. the waves run their 16 MFMAs with A from LDS as the slab lands, the
+//     K waves of each N tile meet in LDS and the first applies the epilogue.
+// Codes and scales are bit-identical to quantize_i8 (quantize8_bf16); the
+// first workgroup also writes them out when asked.  K % 512 == 0 keeps each
+// wave's 64 consecutive chunks inside one row, so a row's partial max is a
+// wave reduction plus one LDS max per wave.
+template <int MM, int XR, int KH>
+__device__ __forceinline__ void linear_decode_wide(const LinearDecodeArgs& a, int8_t* lds) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int W = a.waves, NTW = a.ntw, NW = W * NTW, T = 64 * NW;
+    const int M = a.M, N = a.N, K = a.K, kt = a.kt;
+    const int sub = wave / W, kw = wave - sub * W;  // N tile of the workgroup, K wave within it
+    const int tile = blockIdx.x * NTW + sub;
+    const bool live = tile < (N + 15) / 16;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int cpr = K >> 3;  // 16-byte chunks per row
+    int8_t* xs = lds;                                  // codes, kt * 64 * MM bytes
+    v4i* red = (v4i*)(lds + kt * 64 * MM);             // NW * 64 partial tiles
+    int* rowmax = (int*)(red + NW * 64);               // MM row absmax (f32 bits)
+    if ((int)threadIdx.x < MM) rowmax[threadIdx.x] = 0;
+
+    // 1. activation chunks, epilogue operands, then the weight slab
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)M * (uint32_t)K * 2u);
+    v4i xv[XR];
+    v4i b[kSlab];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+        const int c = j * T + (int)threadIdx.x;
+        xv[j] = buffer_load16(xrs, c < M * cpr ? c * 16 : kOutOfRange);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int n = tile * 16 + r16;
+    const float swn = (live && n < N) ? a.sw[n] : 0.0f;
+    const float bn = (a.bias && live && n < N) ? a.bias[n] : 0.0f;
+    const __amdgpu_buffer_rsrc_t wr = live ? row_tile_rsrc(a.wq, tile, kt) : make_rsrc(a.wq, 0);
+#pragma unroll
+    for (int s = 0; s < KH; ++s) b[s] = buffer_load16_stream(wr, (kw + s * W) * 1024 + lane * 16);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. activations in (the slab stays in flight); row absmax
+    wait_vmcnt_le(KH);
+    lds_publish();  // rowmax zeroed
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+        const int c0 = j * T + wave * 64;  // the wave's first chunk: uniform
+        if (c0 < M * cpr) {
+            float m = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t u = (uint32_t)xv[j][q];
+                m = fmaxf(m, fmaxf(fabsf(f32_from_bits(u << 16)), fabsf(f32_from_bits(u & 0xffff0000u))));
+            }
+            m = wave_max(m);
+            if (lane == 0) atomicMax(&rowmax[c0 / cpr], (int)f32_bits(m));  // non-negative: int order = float order
+        }
+    }
+    lds_publish();
+    // codes into LDS: chunk c = 8 values of row c / cpr at k = 8 (c % cpr)
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+        const int c0 = j * T + wave * 64;
+        if (c0 < M * cpr) {
+            const int row = c0 / cpr;
+            const float sx = scale_from_amax(f32_from_bits((uint32_t)rowmax[row]));
+            const float rcp = 1.0f / sx;
+            uint32_t code[2];
+            quantize8_bf16(xv[j], sx, rcp, scale_is_pow2(sx), code);
+            const int k = (c0 + lane - row * cpr) * 8;
+            *(uint2*)(xs + (((k >> 6) * 4 + ((k >> 4) & 3)) * MM + row) * 16 + (k & 15)) = make_uint2(code[0], code[1]);
+            if (blockIdx.x == 0 && a.xq_out) *(uint2*)(a.xq_out + (int64_t)row * K + k) = make_uint2(code[0], code[1]);
+        }
+    }
+    if (blockIdx.x == 0 && a.sx_out && (int)threadIdx.x < M)
+        a.sx_out[threadIdx.x] = scale_from_amax(f32_from_bits((uint32_t)rowmax[threadIdx.x]));
+    // the rest of the slab, when its registers had to wait for the activations'
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = KH; s < kSlab; ++s) b[s] = buffer_load16_stream(wr, (kw + s * W) * 1024 + lane * 16);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_publish();
+
+    // 3. MFMAs with A from LDS as the slab lands (lanes of rows >= MM read
+    //    row 0: their outputs are discarded; K tiles past kt meet zero weights)
+    const int arow = r16 < MM ? r16 : 0;
+    v4i acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < kSlab; ++s) {
+        const int t = kw + s * W;
+        const v4i xa = *(const v4i*)(xs + (((t < kt ? t : 0) * 4 + g) * MM + arow) * 16);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, b[s], acc, 0, 0, 0);
+    }
+    if (W > 1) {
+        red[wave * 64 + lane] = acc;
+        __syncthreads();
+        if (kw == 0)
+            for (int w = 1; w < W; ++w) acc += red[(wave + w) * 64 + lane];
+    }
+    if (kw == 0 && live && n < N) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * g + r;
+            if (m < M) {
+                const float sx = scale_from_amax(f32_from_bits((uint32_t)rowmax[m]));
+                store_y(a.out, a.out_dtype, (int64_t)m * N + n, acc[r], sx, swn, a.bias, bn);
+            }
+        }
+    }
+}
+
 extern "C" __global__ __launch_bounds__(512) void nh_linear_decode_w8a8_m1_kernel(LinearDecodeArgs a) {
-    extern __shared__ __align__(16) int8_t xs[];  // [MM][W * 1024 + 16] codes
-    linear_decode<1>(a, xs);
+    extern __shared__ __align__(16) int8_t xs[];  // [W * 1024 + 16] codes
+    linear_decode_row<1>(a, xs);
 }
 
-extern "C" __global__ __launch_bounds__(512) void nh_linear_decode_w8a8_m2_kernel(LinearDecodeArgs a) {
-    extern __shared__ __align__(16) int8_t xs[];
-    linear_decode<2>(a, xs);
+// Rows 2..4 where the wide workgroup would own one N tile anyway (K = 8192:
+// 8 K waves per tile): one N tile per workgroup, 12.5 vs 15.2 us at M = 4,
+// K = 8192, N = 4096.
+extern "C" __global__ __launch_bounds__(512) void nh_linear_decode_w8a8_row2_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t xs[];  // [2][W * 1024 + 16] codes
+    linear_decode_row<2>(a, xs);
 }
 
-extern "C" __global__ __launch_bounds__(512) void nh_linear_decode_w8a8_kernel(LinearDecodeArgs a) {
-    extern __shared__ __align__(16) int8_t xs[];
-    linear_decode<4>(a, xs);
+extern "C" __global__ __launch_bounds__(512) void nh_linear_decode_w8a8_row4_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t xs[];  // [4][W * 1024 + 16] codes
+    linear_decode_row<4>(a, xs);
+}
+
+extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_w8a8_m2_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t lds[];
+    linear_decode_wide<2, 4, 12>(a, lds);
+}
+
+extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_w8a8_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t lds[];
+    linear_decode_wide<4, 8, 8>(a, lds);
+}
+
+extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_w8a8_m8_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t lds[];
+    linear_decode_wide<8, 8, 8>(a, lds);
 }
 
 // G2: W8A32 dequant GEMV.  The reference's quantized-weight path materialises

@@ -74,51 +74,115 @@ __device__ __forceinline__ void store_out(void* p, int64_t i, float v, int dtype
 
 __device__ __forceinline__ bool is_finite_f32(float v) { return (f32_bits(v) & 0x7f800000u) != 0x7f800000u; }
 
-// Q2 codes of 8 bf16 values (one 16-byte load: value 2j in the low half of
-// word j) with row scale s and r = RN(1/s), packed little-endian into
-// code[0..1]: quantize_i8_fast (nh_numerics.h) vectorized, so bit-identical
-// to quantize_i8.  pow2 = scale_is_pow2(s) and the zero/subnormal test are
+// Codes of NV values with row scale s and r = RN(1/s): quantize_i8_fast
+// (nh_numerics.h) vectorized, so bit-identical to quantize_i8; q[i]'s low
+// byte is the code.  pow2 = scale_is_pow2(s) and the zero/subnormal test are
 // per row, so those branches are uniform; the exact tie decision runs only
-// for a group of 8 that holds a value within 2^-15 of a half-integer.
-// Non-finite inputs give unspecified codes.
-__device__ __forceinline__ void quantize8_bf16(v4i xv, float s, float r, bool pow2, uint32_t (&code)[2]) {
-    float v[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t u = (uint32_t)xv[j];
-        v[2 * j] = f32_from_bits(u << 16);
-        v[2 * j + 1] = f32_from_bits(u & 0xffff0000u);
-    }
-    uint32_t q[8];
+// for a group that holds a value within 2^-15 of a half-integer.  Non-finite
+// inputs give unspecified codes (the row is reported as non-finite instead).
+template <int NV>
+__device__ __forceinline__ void quantize_values(const float (&v)[NV], float s, float r, bool pow2, uint32_t (&q)[NV]) {
     if (!(s >= 0x1p-126f)) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = (uint32_t)(int)quantize_i8(v[i], s);
+        for (int i = 0; i < NV; ++i) q[i] = (uint32_t)(int)quantize_i8(v[i], s);
     } else if (pow2) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = (uint32_t)(int)roundf(v[i] * r);
+        for (int i = 0; i < NV; ++i) q[i] = (uint32_t)(int)roundf(v[i] * r);
     } else {
         float dmax = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NV; ++i) {
             const float y = __builtin_fmaf(v[i], r, kQuantMagic);
             dmax = fmaxf(dmax, fabsf(__builtin_fmaf(v[i], r, -(y - kQuantMagic))));
             q[i] = f32_bits(y);  // low byte = the code
         }
         if (dmax >= kQuantTieBand) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < NV; ++i) {
                 const float y = __builtin_fmaf(v[i], r, kQuantMagic);
                 if (fabsf(__builtin_fmaf(v[i], r, -(y - kQuantMagic))) >= kQuantTieBand)
                     q[i] = (uint32_t)quantize_near_tie(v[i], s, v[i] * r);
             }
         }
     }
+}
+
+// The low bytes of q[0..3] as one little-endian word.
+__device__ __forceinline__ uint32_t pack_codes4(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3) {
+    const uint32_t lo = __builtin_amdgcn_perm(q1, q0, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(q3, q2, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+// The 8 bf16 values of one 16-byte load (value 2j in the low half of word j).
+__device__ __forceinline__ void unpack_bf16x8(v4i xv, float (&v)[8]) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint32_t lo = __builtin_amdgcn_perm(q[4 * h + 1], q[4 * h], 0x0c0c0400u);
-        const uint32_t hi = __builtin_amdgcn_perm(q[4 * h + 3], q[4 * h + 2], 0x0c0c0400u);
-        code[h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t u = (uint32_t)xv[j];
+        v[2 * j] = f32_from_bits(u << 16);
+        v[2 * j + 1] = f32_from_bits(u & 0xffff0000u);
     }
+}
+
+// Codes of 8 bf16 values (one 16-byte load), packed into code[0..1].
+__device__ __forceinline__ void quantize8_bf16(v4i xv, float s, float r, bool pow2, uint32_t (&code)[2]) {
+    float v[8];
+    unpack_bf16x8(xv, v);
+    uint32_t q[8];
+    quantize_values<8>(v, s, r, pow2, q);
+    code[0] = pack_codes4(q[0], q[1], q[2], q[3]);
+    code[1] = pack_codes4(q[4], q[5], q[6], q[7]);
+}
+
+// Codes of 4 f32 values (one 16-byte load), packed into one word.
+__device__ __forceinline__ uint32_t quantize4_f32(v4i xv, float s, float r, bool pow2) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = f32_from_bits((uint32_t)xv[j]);
+    uint32_t q[4];
+    quantize_values<4>(v, s, r, pow2, q);
+    return pack_codes4(q[0], q[1], q[2], q[3]);
+}
+
+// s_waitcnt vmcnt(<= n) with the other counters left alone (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] << 14).
+// The wait is an immediate, hence the switch over the counts in use.
+__device__ __forceinline__ void wait_vmcnt_le(int n) {
+#define NH_VMCNT(n) ((((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14)))
+    switch (n) {
+        case 0: __builtin_amdgcn_s_waitcnt(NH_VMCNT(0)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(NH_VMCNT(1)); break;
+        case 2: __builtin_amdgcn_s_waitcnt(NH_VMCNT(2)); break;
+        case 3: __builtin_amdgcn_s_waitcnt(NH_VMCNT(3)); break;
+        case 4: __builtin_amdgcn_s_waitcnt(NH_VMCNT(4)); break;
+        case 6: __builtin_amdgcn_s_waitcnt(NH_VMCNT(6)); break;
+        case 8: __builtin_amdgcn_s_waitcnt(NH_VMCNT(8)); break;
+        case 9: __builtin_amdgcn_s_waitcnt(NH_VMCNT(9)); break;
+        case 12: __builtin_amdgcn_s_waitcnt(NH_VMCNT(12)); break;
+        case 16: __builtin_amdgcn_s_waitcnt(NH_VMCNT(16)); break;
+        case 18: __builtin_amdgcn_s_waitcnt(NH_VMCNT(18)); break;
+        case 24: __builtin_amdgcn_s_waitcnt(NH_VMCNT(24)); break;
+        default: __builtin_amdgcn_s_waitcnt(NH_VMCNT(0)); break;
+    }
+#undef NH_VMCNT
+}
+
+// Workgroup barrier that leaves vector-memory loads in flight (__syncthreads
+// would first wait for every outstanding load).  The caller waits for the
+// loads whose data the barrier publishes.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// LDS stores of this wave complete (lgkmcnt(0)), then lds_barrier: the
+// stores are visible to the workgroup, loads still in flight.
+__device__ __forceinline__ void lds_publish() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 // Raw buffer resource over [base, base + bytes): a buffer load whose offset

@@ -12,13 +12,14 @@ enum DType : int32_t { DT_F32 = 0, DT_BF16 = 1 };
 // Q1/Q2: one workgroup per row.
 struct QuantizeRowsArgs {
     const void* x;        // f32 or bf16 [rows][cols]
-    int8_t* q;            // [rows][cols]
+    int8_t* q;            // [rows][cols] or null
     float* scales;        // [rows]
     int32_t* row_status;  // [rows] or null: -1 = all finite, else first non-finite column
+    int8_t* q_act;        // activation tiles [ceil(cols/64)][4][rows][16] (rows <= 16) or null
     int64_t rows;
     int64_t cols;
     int32_t x_dtype;
-    int32_t pad_;
+    int32_t vec;          // 1: rows are 16-byte aligned and a whole number of 16-byte chunks
 };
 
 // Q3: out[r][c] = (float)q[r][c] * scales[r]
@@ -45,7 +46,7 @@ struct DequantizeInt4Args {
 // G1 (M <= 16, activations already quantized): a workgroup owns one 16-row
 // N tile; wave w of `waves` owns K tiles w, w + waves, w + 2 waves, ...
 struct GemvW8A8Args {
-    const int8_t* xq;     // [M][K] row-major
+    const int8_t* xq;     // [M][K] row-major, or activation tiles [KT][4][M][16] (x_tiled)
     const float* sx;      // [M]
     const int8_t* wq;     // tiled [N][K]
     const float* sw;      // [N]
@@ -55,10 +56,14 @@ struct GemvW8A8Args {
     int32_t kt;           // ceil(K / 64)
     int32_t waves;
     int32_t out_dtype;
+    int32_t x_tiled;
+    int32_t pad_;
 };
 
-// Decode unit (M <= 4, K <= 8192): per-token quantization (Q2) of bf16 rows
-// fused in front of G1; blockDim = 64 * waves, waves * 1024 >= 64 * kt.
+// Decode unit (M <= 16, K <= 8192, K % 512 == 0): per-token quantization
+// (Q2) of bf16 rows fused in front of G1.  A workgroup owns ntw 16-row N
+// tiles with `waves` waves each: blockDim = 64 * waves * ntw <= 1024 and
+// waves * 1024 >= 64 * kt.
 struct LinearDecodeArgs {
     const void* x;        // bf16 [M][K]
     const int8_t* wq;     // tiled [N][K]
@@ -72,7 +77,7 @@ struct LinearDecodeArgs {
     int32_t waves;
     int32_t x_dtype;
     int32_t out_dtype;
-    int32_t pad_;
+    int32_t ntw;          // N tiles per workgroup
 };
 
 // G2: W8A32 dequant GEMV; grid = (N tiles, ceil(M / 4)).

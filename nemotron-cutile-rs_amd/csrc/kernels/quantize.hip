@@ -1,37 +1,99 @@
 // Q1/Q2/Q3 and Q0d kernels: symmetric int8 row quantization, int8
 // dequantization, affine INT4 dequantization.  HBM-bound elementwise work:
-// one workgroup per row for the row quantizer (two passes over a row that
-// stays in L2), grid-stride loops for the dequantizers.
+// one workgroup per row for the row quantizer, grid-stride loops for the
+// dequantizers and the weight tiler.
 #include "nh_device.h"
 
 using namespace nh;
 
-// One workgroup per row: pass 1 = absmax + first non-finite column, pass 2 =
-// codes (quantize_i8_fast: bit-identical to the division, without it).  Rows of the decode/MoE/weight shapes are 1.8-21.5 K elements, so the
-// second pass hits L2.
-extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_i8_kernel(QuantizeRowsArgs a) {
-    __shared__ float redf[4];
-    __shared__ int redi[4];
+namespace {
+
+// Vector path: one workgroup per row, 16-byte chunks (8 bf16 or 4 f32
+// values).  The first kRegChunks chunks of every thread stay in registers
+// between the absmax pass and the code pass, so rows up to 8192 bf16 / 4096
+// f32 values are read from memory once; longer rows read the rest again (L2).
+// Codes go to the row-major matrix and/or the activation tiles
+// [KT][4][rows][16] (byte 16 * ((4 kt + g) * rows + m) + b holds code
+// (m, 64 kt + 16 g + b)), the A operand order of the M <= 16 GEMV.
+constexpr int kRegChunks = 4;
+
+template <int DT>
+__device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, float* redf, int* redi) {
+    constexpr int VPC = DT == DT_BF16 ? 8 : 4;  // values per 16-byte chunk
     const int64_t row = blockIdx.x;
-    if (row >= a.rows) return;
+    const int cols = (int)a.cols;
+    const int chunks = cols / VPC;
+    const uint32_t rb = (uint32_t)cols * (DT == DT_BF16 ? 2u : 4u);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc((const char*)a.x + row * (int64_t)rb, rb);
+    v4i xv[kRegChunks];
+#pragma unroll
+    for (int r = 0; r < kRegChunks; ++r) {
+        const int c = threadIdx.x + r * 256;
+        xv[r] = buffer_load16(xr, c < chunks ? c * 16 : kOutOfRange);
+    }
+    float amax = 0.0f;
+    int bad = 0x7fffffff;
+    auto scan = [&](v4i v, int c) {
+        float f[VPC];
+        if constexpr (DT == DT_BF16) {
+            unpack_bf16x8(v, f);
+        } else {
+#pragma unroll
+            for (int j = 0; j < VPC; ++j) f[j] = f32_from_bits((uint32_t)v[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < VPC; ++j) {
+            if (!is_finite_f32(f[j])) bad = min(bad, c * VPC + j);
+            else amax = fmaxf(amax, fabsf(f[j]));
+        }
+    };
+#pragma unroll
+    for (int r = 0; r < kRegChunks; ++r) scan(xv[r], threadIdx.x + r * 256);  // chunks past the row read zeros
+    for (int c = threadIdx.x + kRegChunks * 256; c < chunks; c += 256) scan(buffer_load16(xr, c * 16), c);
+    amax = block_max(amax, redf);
+    bad = block_min_i32(bad, redi);
+    const float s = scale_from_amax(amax);
+    if (threadIdx.x == 0) {
+        a.scales[row] = s;
+        if (a.row_status) a.row_status[row] = bad == 0x7fffffff ? -1 : bad;
+    }
+    const float rcp = s > 0.0f ? 1.0f / s : 0.0f;
+    const bool pow2 = scale_is_pow2(s);
+    auto emit = [&](v4i v, int c) {
+        const int k = c * VPC;
+        int8_t* tile = a.q_act ? a.q_act + ((int64_t)((k >> 6) * 4 + ((k >> 4) & 3)) * a.rows + row) * 16 + (k & 15)
+                               : nullptr;
+        if constexpr (DT == DT_BF16) {
+            uint32_t code[2];
+            quantize8_bf16(v, s, rcp, pow2, code);
+            if (a.q) *(uint2*)(a.q + row * cols + k) = make_uint2(code[0], code[1]);
+            if (tile) *(uint2*)tile = make_uint2(code[0], code[1]);
+        } else {
+            const uint32_t code = quantize4_f32(v, s, rcp, pow2);
+            if (a.q) *(uint32_t*)(a.q + row * cols + k) = code;
+            if (tile) *(uint32_t*)tile = code;
+        }
+    };
+#pragma unroll
+    for (int r = 0; r < kRegChunks; ++r) {
+        const int c = threadIdx.x + r * 256;
+        if (c < chunks) emit(xv[r], c);
+    }
+    for (int c = threadIdx.x + kRegChunks * 256; c < chunks; c += 256) emit(buffer_load16(xr, c * 16), c);
+}
+
+// Scalar path (any alignment, any column count): pass 1 = absmax + first
+// non-finite column, pass 2 = codes; the row stays in L2 between the passes.
+__device__ __forceinline__ void quantize_row_scalar(const QuantizeRowsArgs& a, float* redf, int* redi) {
+    const int64_t row = blockIdx.x;
     const int64_t cols = a.cols;
     const int64_t base = row * cols;
     float amax = 0.0f;
     int bad = 0x7fffffff;
-    if (a.x_dtype == DT_BF16) {
-        const uint16_t* x = (const uint16_t*)a.x + base;
-        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
-            float v = bf16_to_f32(x[c]);
-            if (!is_finite_f32(v)) bad = min(bad, (int)c);
-            else amax = fmaxf(amax, fabsf(v));
-        }
-    } else {
-        const float* x = (const float*)a.x + base;
-        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
-            float v = x[c];
-            if (!is_finite_f32(v)) bad = min(bad, (int)c);
-            else amax = fmaxf(amax, fabsf(v));
-        }
+    for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+        const float v = load_as_f32(a.x, base + c, a.x_dtype);
+        if (!is_finite_f32(v)) bad = min(bad, (int)c);
+        else amax = fmaxf(amax, fabsf(v));
     }
     amax = block_max(amax, redf);
     bad = block_min_i32(bad, redi);
@@ -40,15 +102,28 @@ extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_i8_kernel(Qua
         a.scales[row] = s;
         if (a.row_status) a.row_status[row] = bad == 0x7fffffff ? -1 : bad;
     }
-    int8_t* q = a.q + base;
     const float r = s > 0.0f ? 1.0f / s : 0.0f;
-    if (a.x_dtype == DT_BF16) {
-        const uint16_t* x = (const uint16_t*)a.x + base;
-        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) q[c] = (int8_t)quantize_i8_fast(bf16_to_f32(x[c]), s, r);
-    } else {
-        const float* x = (const float*)a.x + base;
-        for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) q[c] = (int8_t)quantize_i8_fast(x[c], s, r);
+    for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+        const int8_t code = (int8_t)quantize_i8_fast(load_as_f32(a.x, base + c, a.x_dtype), s, r);
+        if (a.q) a.q[base + c] = code;
+        if (a.q_act) a.q_act[((((c >> 6) * 4 + ((c >> 4) & 3)) * a.rows + row) << 4) + (c & 15)] = code;
     }
+}
+
+}  // namespace
+
+// Q1/Q2: one workgroup per row; codes bit-identical to quantize_i8 (the
+// reference's division) without dividing (quantize_i8_fast).
+extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_i8_kernel(QuantizeRowsArgs a) {
+    __shared__ float redf[4];
+    __shared__ int redi[4];
+    if ((int64_t)blockIdx.x >= a.rows) return;
+    if (!a.vec)
+        quantize_row_scalar(a, redf, redi);
+    else if (a.x_dtype == DT_BF16)
+        quantize_row_vec<DT_BF16>(a, redf, redi);
+    else
+        quantize_row_vec<DT_F32>(a, redf, redi);
 }
 
 // Row-major int8 [rows][cols] -> the tiled layout (nh_numerics.h): thread c

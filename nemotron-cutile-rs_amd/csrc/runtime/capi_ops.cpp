@@ -24,6 +24,54 @@ unsigned grid_for(int64_t items, int per_block) {
 // (longer K is walked slab by slab).
 int gemv_waves(int kt) { return std::max(1, std::min(8, (kt + 15) / 16)); }
 
+// The linear entry point's M ranges: the fused decode unit (quantizer inside
+// the GEMV, one launch) for up to 4 bf16 rows (K <= 8192) and for 5..8 bf16
+// rows (K <= 8192, K % 512 == 0); otherwise quantization into activation tiles +
+// the tiled-A GEMV up to 16 rows, and the MFMA GEMM beyond.  A dependent
+// second launch costs ~4 us; at 16 rows the two launches win (19.5 vs
+// 21.6 us fused, K = 4096, N = 16384).
+constexpr size_t kTiledActRows = 16;
+
+// Fused decode unit: kernel, N tiles per workgroup, block size, LDS bytes.
+struct DecodePlan {
+    KernelId kid;
+    int ntw, threads;
+    size_t lds;
+};
+
+bool plan_decode(const nh_context* ctx, size_t m, size_t n, size_t k, DecodePlan* p) {
+    if (m == 0 || m > 8 || k > 8192) return false;
+    const int kt = (int)tiled_k_tiles(k);
+    const int w = gemv_waves(kt);
+    // one N tile per workgroup, the rows' codes in LDS (up to 4 rows)
+    auto row_plan = [&]() {
+        const size_t rows = m == 1 ? 1 : m <= 2 ? 2 : 4;
+        const KernelId kid = m == 1 ? K_LINEAR_DECODE_M1 : m <= 2 ? K_LINEAR_DECODE_ROW2 : K_LINEAR_DECODE_ROW4;
+        *p = DecodePlan{kid, 1, 64 * w, rows * ((size_t)w * 1024 + 16)};
+        return p->lds <= ctx->max_shared_per_block;
+    };
+    if (m == 1) return row_plan();
+    // several N tiles per workgroup: the widest (up to 16 waves) that still
+    // gives every CU one; at one N tile the row kernel is faster up to 4 rows
+    if (k % 512 == 0) {
+        const int mm = m <= 2 ? 2 : m <= 4 ? 4 : 8;
+        const int xr = mm == 2 ? 4 : 8;  // activation chunks each thread holds
+        const KernelId kid = mm == 2 ? K_LINEAR_DECODE_M2 : mm == 4 ? K_LINEAR_DECODE : K_LINEAR_DECODE_M8;
+        const size_t tiles = (n + 15) / 16;
+        for (int ntw = 16 / w; ntw >= 1; ntw /= 2) {
+            if (ntw > 1 && (tiles + ntw - 1) / ntw < (size_t)ctx->cu_count) continue;
+            if (ntw == 1 && m <= 4) break;
+            const int threads = 64 * w * ntw;
+            if (m * (k / 8) > (size_t)xr * threads) continue;
+            const size_t lds = (size_t)kt * 64 * mm + (size_t)w * ntw * 1024 + (size_t)mm * 4;
+            if (lds > ctx->max_shared_per_block) break;
+            *p = DecodePlan{kid, ntw, threads, lds};
+            return true;
+        }
+    }
+    return m <= 4 && row_plan();
+}
+
 // Dynamic LDS of the GEMM kernels: a ring of `stages` stages (BM rows x 128
 // bytes of A plus 2 * BN/16 weight tiles of 1 KiB), or the epilogue staging
 // of `waves` waves (64 rows x (wave tile width * 4 + 16) bytes each),
@@ -51,9 +99,26 @@ nh_status check_w8a8_shape(size_t m, size_t n, size_t k, nh_error* err) {
     return NH_OK;
 }
 
+// Row quantizer launch (Q1/Q2): codes row-major into q and/or into the
+// activation tiles q_act (rows <= 16).  The vector path needs 16-byte aligned
+// rows of whole 16-byte chunks and code stores aligned to a chunk's codes.
+nh_status launch_quantize(nh_context* ctx, const void* x, nh_dtype dtype, size_t rows, size_t cols, int8_t* q,
+                          float* scales, int32_t* row_status, int8_t* q_act, nh_stream stream, nh_error* err) {
+    const size_t esz = dtype == NH_BF16 ? 2 : 4;
+    const size_t row_bytes = cols * esz;
+    const bool vec = aligned16(x) && row_bytes % 16 == 0 && row_bytes < (1ull << 31) &&
+                     ((uintptr_t)q % (16 / esz)) == 0 && aligned16(q_act);
+    QuantizeRowsArgs a{x, q, scales, row_status, q_act, (int64_t)rows, (int64_t)cols, dtype, vec ? 1 : 0};
+    return launch(ctx, K_QUANTIZE_ROWS, (unsigned)rows, 256, 0, stream, a, err);
+}
+
+// Bytes of the activation tiles of m <= 16 rows of k codes.
+size_t act_tiles_bytes(size_t m, size_t k) { return m * (size_t)tiled_k_tiles(k) * 64; }
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
 nh_status launch_gemv(nh_context* ctx, const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
-                      const float* bias, int M, int N, int K, void* out, nh_dtype out_dtype, nh_stream stream,
-                      nh_error* err) {
+                      const float* bias, int M, int N, int K, void* out, nh_dtype out_dtype, bool x_tiled,
+                      nh_stream stream, nh_error* err) {
     GemvW8A8Args a{};
     a.xq = xq;
     a.sx = sx;
@@ -67,7 +132,9 @@ nh_status launch_gemv(nh_context* ctx, const int8_t* xq, const float* sx, const 
     a.kt = (int)tiled_k_tiles(K);
     a.waves = gemv_waves(a.kt);
     a.out_dtype = out_dtype;
-    return launch(ctx, K_GEMV_W8A8, (unsigned)((N + 15) / 16), 64u * a.waves, 0, stream, a, err);
+    a.x_tiled = x_tiled ? 1 : 0;
+    return launch(ctx, x_tiled ? K_GEMV_W8A8_XT : K_GEMV_W8A8, (unsigned)((N + 15) / 16), 64u * a.waves, 0, stream,
+                  a, err);
 }
 
 nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
@@ -111,7 +178,7 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
             const int mm = std::min(16, M - m0);
             void* o = (char*)out + (size_t)m0 * N * (out_dtype == NH_BF16 ? 2 : 4);
             nh_status st = launch_gemv(ctx, xq + (size_t)m0 * K, sx + m0, wq, sw, bias, mm, N, K, o, out_dtype,
-                                       stream, err);
+                                       false, stream, err);
             if (st) return st;
         }
         return NH_OK;
@@ -143,8 +210,7 @@ nh_status nh_quantize_rows_i8(nh_context* ctx, const void* x, nh_dtype dtype, si
         return set_error(err, NH_UNSUPPORTED, "rows/cols must be < 2^31");
     if ((st = bind_device(ctx, err))) return st;
     if (rows == 0 || cols == 0) return NH_OK;  // nothing to quantize (empty inputs are valid, quantize.rs:490-501)
-    QuantizeRowsArgs a{x, q, scales, row_status, (int64_t)rows, (int64_t)cols, dtype, 0};
-    return launch(ctx, K_QUANTIZE_ROWS, (unsigned)rows, 256, 0, stream, a, err);
+    return launch_quantize(ctx, x, dtype, rows, cols, q, scales, row_status, nullptr, stream, err);
 }
 
 size_t nh_tiled_weights_bytes(size_t n, size_t k) {
@@ -230,13 +296,15 @@ nh_status nh_gemm_w8a8(nh_context* ctx, const int8_t* xq, const float* sx, const
     if (!aligned16(xq) || !aligned16(wq))
         return set_error(err, NH_UNSUPPORTED, "xq and wq must be 16-byte aligned");
     if ((st = bind_device(ctx, err))) return st;
-    if (m <= 16) return launch_gemv(ctx, xq, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, stream, err);
+    if (m <= 16)
+        return launch_gemv(ctx, xq, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, false, stream, err);
     return launch_gemm(ctx, xq, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, 0, stream, err);
 }
 
 size_t nh_linear_w8a8_workspace_size(size_t m, size_t k) {
-    if (m <= 4) return 0;
-    return ((m * k + 255) / 256) * 256 + m * sizeof(float);
+    if (m == 0 || k == 0 || m > (1ull << 31) || k > (1ull << 31)) return 0;
+    if (m <= kTiledActRows) return align256(act_tiles_bytes(m, k)) + align256(m * sizeof(float));
+    return align256(m * k) + align256(m * sizeof(float));
 }
 
 nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* wq, const float* sw,
@@ -251,10 +319,9 @@ nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
         return st;
     if (!aligned16(wq)) return set_error(err, NH_UNSUPPORTED, "wq must be 16-byte aligned");
     if ((st = bind_device(ctx, err))) return st;
-    // the fused kernel keeps each thread's two 8-value chunks of every bf16
-    // row in registers: K <= 16 * threads = 1024 * waves, i.e. K <= 8192
-    const bool fusable = m <= 4 && k <= 8192 && x_dtype == NH_BF16 && aligned16(x) && ((uintptr_t)xq_out & 7u) == 0;
-    if (fusable) {
+    // bf16 rows: the fused decode unit when it fits (one launch, no workspace)
+    DecodePlan plan;
+    if (x_dtype == NH_BF16 && aligned16(x) && ((uintptr_t)xq_out & 7u) == 0 && plan_decode(ctx, m, n, k, &plan)) {
         LinearDecodeArgs a{};
         a.x = x;
         a.wq = wq;
@@ -270,23 +337,31 @@ nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
         a.waves = gemv_waves(a.kt);
         a.x_dtype = x_dtype;
         a.out_dtype = out_dtype;
-        const KernelId kid = m == 1 ? K_LINEAR_DECODE_M1 : (m == 2 ? K_LINEAR_DECODE_M2 : K_LINEAR_DECODE);
-        const size_t rows = m == 1 ? 1 : (m == 2 ? 2 : 4);  // the kernel's row template
-        const size_t lds = rows * ((size_t)a.waves * 1024 + 16);
-        return launch(ctx, kid, (unsigned)((n + 15) / 16), 64u * a.waves, lds, stream, a, err);
+        a.ntw = plan.ntw;
+        const size_t tiles = (n + 15) / 16;
+        return launch(ctx, plan.kid, (unsigned)((tiles + plan.ntw - 1) / plan.ntw), (unsigned)plan.threads, plan.lds,
+                      stream, a, err);
     }
-    // two launches: Q2 into the workspace (or the caller's xq_out/sx_out), then G1/G3
+    const size_t need = nh_linear_w8a8_workspace_size(m, k);
+    if (m <= kTiledActRows) {
+        // Q2 into activation tiles (and the caller's row-major xq_out), then
+        // the GEMV reads each K tile's codes as M * 64 contiguous bytes
+        if (!workspace || workspace_bytes < need) return mismatch(err, "workspace", need, workspace_bytes);
+        if (!aligned16(workspace)) return set_error(err, NH_UNSUPPORTED, "workspace must be 16-byte aligned");
+        int8_t* tiles = (int8_t*)workspace;
+        float* sx = sx_out ? sx_out : (float*)((char*)workspace + align256(act_tiles_bytes(m, k)));
+        if ((st = launch_quantize(ctx, x, x_dtype, m, k, xq_out, sx, nullptr, tiles, stream, err))) return st;
+        return launch_gemv(ctx, tiles, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, true, stream, err);
+    }
+    // two launches: Q2 into the workspace (or the caller's xq_out/sx_out), then G3
     int8_t* xq = xq_out;
     float* sx = sx_out;
     if (!xq || !sx) {
-        const size_t need = ((m * k + 255) / 256) * 256 + m * sizeof(float);
         if (!workspace || workspace_bytes < need) return mismatch(err, "workspace", need, workspace_bytes);
         xq = (int8_t*)workspace;
-        sx = (float*)((char*)workspace + ((m * k + 255) / 256) * 256);
+        sx = (float*)((char*)workspace + align256(m * k));
     }
-    st = nh_quantize_rows_i8(ctx, x, x_dtype, m, k, xq, sx, nullptr, stream, err);
-    if (st) return st;
-    if (m <= 16) return launch_gemv(ctx, xq, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, stream, err);
+    if ((st = launch_quantize(ctx, x, x_dtype, m, k, xq, sx, nullptr, nullptr, stream, err))) return st;
     return launch_gemm(ctx, xq, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, 0, stream, err);
 }
 

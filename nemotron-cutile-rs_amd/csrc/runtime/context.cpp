@@ -17,7 +17,8 @@ const char* const kKernelSymbols[K_COUNT] = {
     "nh_linear_decode_w8a8_m2_kernel", "nh_gemv_w8a32_kernel",
     "nh_gemm_w8a8_256x128_kernel", "nh_gemm_w8a8_128x128_kernel", "nh_moe_route_sigmoid_kernel", "nh_moe_permute_kernel",
     "nh_moe_grouped_gemm_kernel", "nh_moe_combine_kernel",     "nh_tile_weights_kernel",
-    "nh_gemm_w8a8_256x256_kernel", "nh_gemm_f32_kernel",
+    "nh_gemm_w8a8_256x256_kernel", "nh_gemm_f32_kernel",       "nh_gemv_w8a8_xt_kernel",
+    "nh_linear_decode_w8a8_m8_kernel", "nh_linear_decode_w8a8_row2_kernel", "nh_linear_decode_w8a8_row4_kernel",
 };
 
 void clear_error(nh_error* err) {

@@ -31,6 +31,10 @@ enum KernelId : int {
     K_TILE_WEIGHTS,
     K_GEMM_W8A8_256,
     K_GEMM_F32,
+    K_GEMV_W8A8_XT,      // activation tiles
+    K_LINEAR_DECODE_M8,  // M <= 8
+    K_LINEAR_DECODE_ROW2,  // M <= 2, one N tile per workgroup
+    K_LINEAR_DECODE_ROW4,  // M <= 4, one N tile per workgroup
     K_COUNT
 };
 

@@ -57,7 +57,8 @@ def activations_bf16(m, k, seed=1):
 
 # ---- Q1/Q2/Q3 ----------------------------------------------------------------
 @pytest.mark.parametrize("rows,cols,dtype", [(1, 4096, "bf16"), (16, 8192, "bf16"), (3072, 1856, "f32"),
-                                             (4096, 4096, "f32"), (7, 33, "f32"), (5, 1, "bf16")])
+                                             (4096, 4096, "f32"), (7, 33, "f32"), (5, 1, "bf16"),
+                                             (3, 21504, "f32"), (2, 40000, "bf16"), (4, 12, "f32")])
 def test_quantize_rows_bit_exact(ctx, rows, cols, dtype):
     note(f"quantize_rows {rows}x{cols} {dtype}")
     x = O.normal_f32(5, rows * cols, 0.0, 0.02 if dtype == "f32" else 1.0).reshape(rows, cols)
@@ -76,6 +77,29 @@ def test_quantize_rows_bit_exact(ctx, rows, cols, dtype):
     assert np.array_equal(dq.numpy(), q_ref)
     assert np.array_equal(ds.numpy().view(np.uint32), s_ref.view(np.uint32))
     assert np.all(dstat.numpy() == -1)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_quantize_rows_unaligned_rows_take_the_scalar_path(ctx, dtype):
+    """Rows that start off a 16-byte boundary (x offset by one element) give
+    the same codes as aligned ones."""
+    rows, cols = 6, 520
+    note(f"quantize_rows unaligned {dtype}")
+    x = O.normal_f32(9, rows * cols + 1).astype(np.float32)
+    if dtype == "bf16":
+        xs = O.to_bf16(x)
+        st, q_ref, s_ref, _ = O.quantize_rows_bf16(xs[1:].reshape(rows, cols))
+        dx, dt, esz = ctx.upload(xs), NH.BF16, 2
+    else:
+        xs = x
+        st, q_ref, s_ref, _ = O.quantize_rows_f32(xs[1:].reshape(rows, cols))
+        dx, dt, esz = ctx.upload(xs), NH.F32, 4
+    dq = ctx.empty((rows, cols), np.int8)
+    ds = ctx.empty(rows, np.float32)
+    NH.call("nh_quantize_rows_i8", ctx.handle, dx.offset(esz), dt, rows, cols, dq.ptr, ds.ptr, None, None)
+    ctx.synchronize()
+    assert np.array_equal(dq.numpy(), q_ref)
+    assert np.array_equal(ds.numpy().view(np.uint32), s_ref.view(np.uint32))
 
 
 def test_quantize_rows_special_rows(ctx):
@@ -217,7 +241,7 @@ def test_gemv_w8a8_bit_exact(ctx, m, n, k):
         assert np.array_equal(got, ref), f"max diff {np.max(np.abs(got.astype(np.float64) - ref))}"
 
 
-@pytest.mark.parametrize("m", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 13, 16])
 def test_linear_decode_unit_bit_exact(ctx, m):
     n, k = 16384, 4096
     note(f"linear_w8a8 decode m={m}")
@@ -244,6 +268,44 @@ def test_linear_decode_unit_bit_exact(ctx, m):
             ws.ptr, ws_bytes, None, None, None)
     ctx.synchronize()
     assert np.array_equal(out2.numpy(), ref)
+
+
+@pytest.mark.parametrize("m,n,k,dtype", [(8, 4096, 21504, "bf16"), (8, 1040, 4112, "bf16"), (5, 528, 4160, "f32"),
+                                         (1, 4096, 16384, "bf16"), (16, 96, 64, "f32"), (2, 300, 8192, "f32"),
+                                         (3, 4096, 8192, "bf16"), (2, 1000, 4112, "bf16"), (7, 4096, 8192, "bf16"),
+                                         (6, 6144, 4096, "bf16")])
+def test_linear_small_m_shapes_bit_exact(ctx, m, n, k, dtype):
+    """The M <= 16 linear path off the headline shape: several K slabs per
+    wave (K = 16384, 21504), a last K tile only partly inside the matrix
+    (K = 4112, 4160: the activation tiles hold stale bytes there and meet
+    zero weight padding), N not a multiple of 16, f32 activations, the
+    one-tile-per-workgroup decode kernels for 2..4 rows (K = 8192 or
+    K % 512 != 0) and the wide one at N = 6144."""
+    note(f"linear_w8a8 m={m} n={n} k={k} {dtype}")
+    _, wq, sw = quantized_weights(n, k)
+    bias = O.normal_f32(3, n, 0.0, 0.1)
+    if dtype == "bf16":
+        x = activations_bf16(m, k, seed=40 + m)
+        _, xq_ref, sx_ref, _ = O.quantize_rows_bf16(x)
+        dt = NH.BF16
+    else:
+        x = O.normal_f32(40 + m, m * k).reshape(m, k)
+        _, xq_ref, sx_ref, _ = O.quantize_rows_f32(x)
+        dt = NH.F32
+    ref = O.linear_w8a8(xq_ref, sx_ref, wq, sw, bias=bias, out_bf16=False)
+    dx, dw, ds, db = ctx.upload(x), ctx.upload(tile_16x64(wq)), ctx.upload(sw), ctx.upload(bias)
+    ws_bytes = NH.lib().nh_linear_w8a8_workspace_size(m, k)
+    ws = ctx.empty(max(ws_bytes, 1), np.uint8)
+    ws.fill_bytes(0x5a)  # stale bytes in the activation tiles
+    out = ctx.empty((m, n), np.float32)
+    xq = ctx.empty((m, k), np.int8)
+    sx = ctx.empty(m, np.float32)
+    NH.call("nh_linear_w8a8", ctx.handle, dx.ptr, dt, dw.ptr, ds.ptr, db.ptr, m, n, k, out.ptr, NH.F32,
+            ws.ptr, ws_bytes, xq.ptr, sx.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(xq.numpy(), xq_ref)
+    assert np.array_equal(sx.numpy().view(np.uint32), sx_ref.view(np.uint32))
+    assert np.array_equal(out.numpy().view(np.uint32), ref.view(np.uint32))
 
 
 @pytest.mark.parametrize("m", [1, 3])
@@ -281,8 +343,10 @@ def test_linear_decode_unit_rounding_ties(ctx, m):
     out = ctx.empty((m, n), np.uint16)
     xq = ctx.empty((m, k), np.int8)
     sx = ctx.empty(m, np.float32)
+    ws_bytes = NH.lib().nh_linear_w8a8_workspace_size(m, k)
+    ws = ctx.empty(max(ws_bytes, 1), np.uint8)
     NH.call("nh_linear_w8a8", ctx.handle, dx.ptr, NH.BF16, dw.ptr, ds.ptr, None, m, n, k, out.ptr, NH.BF16,
-            None, 0, xq.ptr, sx.ptr, None)
+            ws.ptr, ws_bytes, xq.ptr, sx.ptr, None)
     ctx.synchronize()
     assert np.array_equal(sx.numpy().view(np.uint32), sx_ref.view(np.uint32))
     assert np.array_equal(xq.numpy(), xq_ref)
