@@ -162,10 +162,14 @@ nh_status nh_gemm_w8a8_host(const int8_t *xq, const float *sx, const int8_t *wq,
                             nh_error *err);
 /* Quantized linear layer, the drop-in for LinearProjection::project_into
  * with int8 per-row weights (linear.rs:283-342): dynamic per-token
- * quantization of x (f32 or bf16) then G1/G3 + bias.  For m <= 4 the
- * quantization is fused into the GEMV (one launch, no workspace); otherwise
- * it needs a workspace of nh_linear_w8a8_workspace_size(m, k) bytes.
- * xq_out/sx_out (optional) receive the quantized activations. */
+ * quantization of x (f32 or bf16) then G1/G3 + bias.  For bf16 x with
+ * k <= 8192 and m <= 4 (m <= 8 when k % 512 == 0) the quantization is fused
+ * into the GEMV (one launch; the workspace is not touched); otherwise it
+ * runs as its own launch into a workspace of
+ * nh_linear_w8a8_workspace_size(m, k) bytes, 16-byte aligned (for m <= 16
+ * it holds the codes in the GEMV's operand order).  Pass that workspace on
+ * every call.  xq_out/sx_out (optional) receive the quantized activations
+ * (row-major codes, scales). */
 size_t nh_linear_w8a8_workspace_size(size_t m, size_t k);
 nh_status nh_linear_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const int8_t *wq, const float *sw,
                          const float *bias, size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype,
