@@ -175,6 +175,20 @@ nh_status nh_linear_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const
                          const float *bias, size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype,
                          void *workspace, size_t workspace_bytes, int8_t *xq_out, float *sx_out,
                          nh_stream stream, nh_error *err);
+/* L2: int8 MLP layer, the drop-in for MlpLayer::forward_into with int8
+ * per-row weights (mlp.rs:157-211): h = ReLU^2(x W_up^T + b_up) in f32
+ * (ReLU^2 after the bias, mlp.rs:205), then out = h W_down^T + b_down, each
+ * projection with per-token quantization of its input (nh_linear_w8a8).
+ * w_up is tiled [inter][hidden], w_down tiled [hidden][inter]; biases may
+ * be NULL.  Errors: INVALID_SHAPE for hidden or inter == 0 (MlpError::
+ * InvalidShape), INVALID_ROW_COUNT for m == 0, LENGTH_MISMATCH "workspace"
+ * for a workspace smaller than nh_mlp_w8a8_workspace_size(m, hidden, inter)
+ * (16-byte aligned; it also holds h). */
+size_t nh_mlp_w8a8_workspace_size(size_t m, size_t hidden, size_t inter);
+nh_status nh_mlp_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const int8_t *w_up, const float *s_up,
+                      const float *b_up, const int8_t *w_down, const float *s_down, const float *b_down, size_t m,
+                      size_t hidden, size_t inter, void *out, nh_dtype out_dtype, void *workspace,
+                      size_t workspace_bytes, nh_stream stream, nh_error *err);
 /* G2: W8A32 dequant GEMV, y = x * ((float)q * s)^T with f64 accumulation,
  * the arithmetic of materialize_dense + gemm_into_host (linear.rs:126-131). */
 nh_status nh_gemv_w8a32(nh_context *ctx, const float *x, const int8_t *wq, const float *sw, size_t m, size_t n,

@@ -59,10 +59,12 @@ __device__ __forceinline__ bool reduce_waves(v4i& acc, v4i* red, int W) {
     return wave == 0;
 }
 
+// y = ((float)acc * sx) * sw [+ bias] [ReLU^2] -> out (f32 or bf16 RNE).
 __device__ __forceinline__ void store_y(void* out, int out_dtype, int64_t i, int32_t acc, float sx, float swn,
-                                        const float* bias, float bn) {
+                                        const float* bias, float bn, int relu) {
     float y = epilogue_w8a8(acc, sx, swn);
     if (bias) y = y + bn;
+    if (relu) y = relu2(y);
     store_out(out, i, y, out_dtype);
 }
 
@@ -127,7 +129,8 @@ __device__ __forceinline__ void gemv_w8a8(const GemvW8A8Args& a, v4i* red) {
     if (reduce_waves(acc, red, W) && n < N) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            if (4 * g + r < M) store_y(a.out, a.out_dtype, (int64_t)(4 * g + r) * N + n, acc[r], sxl[r], swn, a.bias, bn);
+            if (4 * g + r < M)
+                store_y(a.out, a.out_dtype, (int64_t)(4 * g + r) * N + n, acc[r], sxl[r], swn, a.bias, bn, a.relu2);
     }
 }
 
@@ -241,7 +244,7 @@ __device__ __forceinline__ void linear_decode_row(const LinearDecodeArgs& a, int
     if (reduce_waves(acc, red, W) && n < N && (lane >> 4) == 0) {
 #pragma unroll
         for (int r = 0; r < MM; ++r)
-            if (r < M) store_y(a.out, a.out_dtype, (int64_t)r * N + n, acc[r], sx[r], swn, a.bias, bn);
+            if (r < M) store_y(a.out, a.out_dtype, (int64_t)r * N + n, acc[r], sx[r], swn, a.bias, bn, a.relu2);
     }
 }
 
@@ -365,7 +368,7 @@ __device__ __forceinline__ void linear_decode_wide(const LinearDecodeArgs& a, in
             const int m = 4 * g + r;
             if (m < M) {
                 const float sx = scale_from_amax(f32_from_bits((uint32_t)rowmax[m]));
-                store_y(a.out, a.out_dtype, (int64_t)m * N + n, acc[r], sx, swn, a.bias, bn);
+                store_y(a.out, a.out_dtype, (int64_t)m * N + n, acc[r], sx, swn, a.bias, bn, a.relu2);
             }
         }
     }

@@ -57,7 +57,7 @@ struct GemvW8A8Args {
     int32_t waves;
     int32_t out_dtype;
     int32_t x_tiled;
-    int32_t pad_;
+    int32_t relu2;        // ReLU^2 after the bias (the MLP up projection)
 };
 
 // Decode unit (M <= 16, K <= 8192, K % 512 == 0): per-token quantization
@@ -78,6 +78,8 @@ struct LinearDecodeArgs {
     int32_t x_dtype;
     int32_t out_dtype;
     int32_t ntw;          // N tiles per workgroup
+    int32_t relu2;        // ReLU^2 after the bias (the MLP up projection)
+    int32_t pad_;
 };
 
 // G2: W8A32 dequant GEMV; grid = (N tiles, ceil(M / 4)).

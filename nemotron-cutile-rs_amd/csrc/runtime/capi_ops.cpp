@@ -118,7 +118,7 @@ size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
 nh_status launch_gemv(nh_context* ctx, const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
                       const float* bias, int M, int N, int K, void* out, nh_dtype out_dtype, bool x_tiled,
-                      nh_stream stream, nh_error* err) {
+                      nh_stream stream, nh_error* err, int relu2 = 0) {
     GemvW8A8Args a{};
     a.xq = xq;
     a.sx = sx;
@@ -133,6 +133,7 @@ nh_status launch_gemv(nh_context* ctx, const int8_t* xq, const float* sx, const 
     a.waves = gemv_waves(a.kt);
     a.out_dtype = out_dtype;
     a.x_tiled = x_tiled ? 1 : 0;
+    a.relu2 = relu2;
     return launch(ctx, x_tiled ? K_GEMV_W8A8_XT : K_GEMV_W8A8, (unsigned)((N + 15) / 16), 64u * a.waves, 0, stream,
                   a, err);
 }
@@ -178,7 +179,7 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
             const int mm = std::min(16, M - m0);
             void* o = (char*)out + (size_t)m0 * N * (out_dtype == NH_BF16 ? 2 : 4);
             nh_status st = launch_gemv(ctx, xq + (size_t)m0 * K, sx + m0, wq, sw, bias, mm, N, K, o, out_dtype,
-                                       false, stream, err);
+                                       false, stream, err, relu2);
             if (st) return st;
         }
         return NH_OK;
@@ -307,18 +308,17 @@ size_t nh_linear_w8a8_workspace_size(size_t m, size_t k) {
     return align256(m * k) + align256(m * sizeof(float));
 }
 
-nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* wq, const float* sw,
-                         const float* bias, size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype,
-                         void* workspace, size_t workspace_bytes, int8_t* xq_out, float* sx_out, nh_stream stream,
-                         nh_error* err) {
-    clear_error(err);
-    if (m == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
+}  // extern "C"
+
+namespace {
+
+// nh_linear_w8a8 with an optional ReLU^2 after the bias (the MLP's up
+// projection, mlp.rs:205), validated by the caller up to the device binding.
+nh_status linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* wq, const float* sw,
+                      const float* bias, size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype,
+                      void* workspace, size_t workspace_bytes, int8_t* xq_out, float* sx_out, int relu2,
+                      nh_stream stream, nh_error* err) {
     nh_status st;
-    if ((st = check_dtype(x_dtype, err)) || (st = check_dtype(out_dtype, err)) ||
-        (st = check_w8a8_shape(m, n, k, err)))
-        return st;
-    if (!aligned16(wq)) return set_error(err, NH_UNSUPPORTED, "wq must be 16-byte aligned");
-    if ((st = bind_device(ctx, err))) return st;
     // bf16 rows: the fused decode unit when it fits (one launch, no workspace)
     DecodePlan plan;
     if (x_dtype == NH_BF16 && aligned16(x) && ((uintptr_t)xq_out & 7u) == 0 && plan_decode(ctx, m, n, k, &plan)) {
@@ -338,6 +338,7 @@ nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
         a.x_dtype = x_dtype;
         a.out_dtype = out_dtype;
         a.ntw = plan.ntw;
+        a.relu2 = relu2;
         const size_t tiles = (n + 15) / 16;
         return launch(ctx, plan.kid, (unsigned)((tiles + plan.ntw - 1) / plan.ntw), (unsigned)plan.threads, plan.lds,
                       stream, a, err);
@@ -351,7 +352,8 @@ nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
         int8_t* tiles = (int8_t*)workspace;
         float* sx = sx_out ? sx_out : (float*)((char*)workspace + align256(act_tiles_bytes(m, k)));
         if ((st = launch_quantize(ctx, x, x_dtype, m, k, xq_out, sx, nullptr, tiles, stream, err))) return st;
-        return launch_gemv(ctx, tiles, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, true, stream, err);
+        return launch_gemv(ctx, tiles, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, true, stream, err,
+                           relu2);
     }
     // two launches: Q2 into the workspace (or the caller's xq_out/sx_out), then G3
     int8_t* xq = xq_out;
@@ -362,7 +364,63 @@ nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
         sx = (float*)((char*)workspace + align256(m * k));
     }
     if ((st = launch_quantize(ctx, x, x_dtype, m, k, xq, sx, nullptr, nullptr, stream, err))) return st;
-    return launch_gemm(ctx, xq, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, 0, stream, err);
+    return launch_gemm(ctx, xq, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, relu2, stream, err);
+}
+
+}  // namespace
+
+extern "C" {
+
+nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* wq, const float* sw,
+                         const float* bias, size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype,
+                         void* workspace, size_t workspace_bytes, int8_t* xq_out, float* sx_out, nh_stream stream,
+                         nh_error* err) {
+    clear_error(err);
+    if (m == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
+    nh_status st;
+    if ((st = check_dtype(x_dtype, err)) || (st = check_dtype(out_dtype, err)) ||
+        (st = check_w8a8_shape(m, n, k, err)))
+        return st;
+    if (!aligned16(wq)) return set_error(err, NH_UNSUPPORTED, "wq must be 16-byte aligned");
+    if ((st = bind_device(ctx, err))) return st;
+    return linear_w8a8(ctx, x, x_dtype, wq, sw, bias, m, n, k, out, out_dtype, workspace, workspace_bytes, xq_out,
+                       sx_out, 0, stream, err);
+}
+
+size_t nh_mlp_w8a8_workspace_size(size_t m, size_t hidden, size_t inter) {
+    if (m == 0 || hidden == 0 || inter == 0 || m > (1ull << 31) || inter > (1ull << 31)) return 0;
+    const size_t a = nh_linear_w8a8_workspace_size(m, hidden), b = nh_linear_w8a8_workspace_size(m, inter);
+    return align256(m * inter * sizeof(float)) + (a > b ? a : b);
+}
+
+nh_status nh_mlp_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* w_up, const float* s_up,
+                      const float* b_up, const int8_t* w_down, const float* s_down, const float* b_down, size_t m,
+                      size_t hidden, size_t inter, void* out, nh_dtype out_dtype, void* workspace,
+                      size_t workspace_bytes, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    if (hidden == 0 || inter == 0)
+        return set_error(err, NH_INVALID_SHAPE, "mlp shape must be non-zero, got hidden_dim=%zu, intermediate_dim=%zu",
+                         hidden, inter);
+    if (m == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
+    nh_status st;
+    if ((st = check_dtype(x_dtype, err)) || (st = check_dtype(out_dtype, err)) ||
+        (st = check_w8a8_shape(m, inter, hidden, err)) || (st = check_w8a8_shape(m, hidden, inter, err)))
+        return st;
+    if (!aligned16(w_up) || !aligned16(w_down)) return set_error(err, NH_UNSUPPORTED, "weights must be 16-byte aligned");
+    const size_t need = nh_mlp_w8a8_workspace_size(m, hidden, inter);
+    if (!workspace || workspace_bytes < need) return mismatch(err, "workspace", need, workspace_bytes);
+    if (!aligned16(workspace)) return set_error(err, NH_UNSUPPORTED, "workspace must be 16-byte aligned");
+    if ((st = bind_device(ctx, err))) return st;
+    // h = ReLU^2(x W_up^T + b_up) in f32 (the reference's intermediate), then
+    // out = h W_down^T + b_down with h quantized per row
+    float* h = (float*)workspace;
+    void* lin_ws = (char*)workspace + align256(m * inter * sizeof(float));
+    const size_t lin_bytes = workspace_bytes - align256(m * inter * sizeof(float));
+    if ((st = linear_w8a8(ctx, x, x_dtype, w_up, s_up, b_up, m, inter, hidden, h, NH_F32, lin_ws, lin_bytes, nullptr,
+                          nullptr, 1, stream, err)))
+        return st;
+    return linear_w8a8(ctx, h, NH_F32, w_down, s_down, b_down, m, hidden, inter, out, out_dtype, lin_ws, lin_bytes,
+                       nullptr, nullptr, 0, stream, err);
 }
 
 nh_status nh_gemv_w8a32(nh_context* ctx, const float* x, const int8_t* wq, const float* sw, size_t m, size_t n,

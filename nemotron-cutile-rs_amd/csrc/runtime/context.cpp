@@ -220,6 +220,7 @@ static const struct {
     {"gemv_w8a32_host", 0},      {"moe_sigmoid_topk_host", 0},  {"moe_softmax_topk_host", 0},
     {"moe_permute_host", 0},     {"moe_grouped_gemm_w8a8_host", 0}, {"moe_combine_host", 0},
     {"tile_weights_i8", 1},      {"tile_weights_i8_host", 0},  {"gemm_f32", 1},
+    {"mlp_w8a8", 1},
 };
 
 int nh_kernel_count(void) { return (int)(sizeof(kRegistry) / sizeof(kRegistry[0])); }

@@ -96,6 +96,8 @@ _SIGNATURES = {
     "nh_gemm_w8a8_host": (ST, [P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, E]),
     "nh_linear_w8a8_workspace_size": (SZ, [SZ, SZ]),
     "nh_linear_w8a8": (ST, [P, P, C.c_int, P, P, P, SZ, SZ, SZ, P, C.c_int, P, SZ, P, P, P, E]),
+    "nh_mlp_w8a8_workspace_size": (SZ, [SZ, SZ, SZ]),
+    "nh_mlp_w8a8": (ST, [P, P, C.c_int, P, P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, P, SZ, P, E]),
     "nh_gemv_w8a32": (ST, [P, P, P, P, SZ, SZ, SZ, P, P, E]),
     "nh_gemv_w8a32_host": (ST, [P, P, P, SZ, SZ, SZ, P, E]),
     "nh_sigmoid_f32_host": (C.c_float, [C.c_float]),

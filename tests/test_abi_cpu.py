@@ -57,6 +57,34 @@ def test_kernel_registry_lists_device_and_host_backends():
     assert L.nh_kernel_name(L.nh_kernel_count(), None) is None
 
 
+def test_mlp_validates_like_mlp_layer_before_touching_a_device():
+    """nh_mlp_w8a8 (MlpLayer::forward_into, mlp.rs:157-211): InvalidShape for a
+    zero dimension (mlp.rs:230-236), InvalidRowCount for m == 0 (:163-165),
+    then the workspace, all before the (NULL) context is used."""
+    mlp = lambda m, hidden, inter, ws, ws_bytes: NH.call_status(
+        "nh_mlp_w8a8", None, None, NH.BF16, None, None, None, None, None, None, m, hidden, inter, None, NH.BF16,
+        ws, ws_bytes, None)
+    assert mlp(1, 0, 64, None, 0)[0] == NH.INVALID_SHAPE
+    assert mlp(1, 64, 0, None, 0)[0] == NH.INVALID_SHAPE
+    assert mlp(0, 64, 64, None, 0)[0] == NH.INVALID_ROW_COUNT
+    assert mlp(2, 64, 40, None, 0)[0] == NH.UNSUPPORTED  # inter % 16 != 0: the host path's job
+    need = NH.lib().nh_mlp_w8a8_workspace_size(8, 4096, 21504)
+    # h (f32 [8][21504]) + the larger projection workspace (activation tiles + scales)
+    assert need == 8 * 21504 * 4 + (8 * 21504 + 255) // 256 * 256 + 256
+    st, err = mlp(8, 4096, 21504, None, need - 1)
+    assert st == NH.LENGTH_MISMATCH and err.argument == b"workspace" and (err.expected, err.actual) == (need, need - 1)
+    assert NH.lib().nh_mlp_w8a8_workspace_size(0, 4096, 21504) == 0
+
+
+def test_linear_workspace_sizes():
+    L = NH.lib()
+    # m <= 16: activation tiles (K rounded up to 64) + scales; beyond: row-major codes + scales
+    assert L.nh_linear_w8a8_workspace_size(8, 4096) == 8 * 4096 + 256
+    assert L.nh_linear_w8a8_workspace_size(3, 4112) == (3 * 4160 + 255) // 256 * 256 + 256
+    assert L.nh_linear_w8a8_workspace_size(2048, 4096) == 2048 * 4096 + 8192
+    assert L.nh_linear_w8a8_workspace_size(0, 4096) == 0
+
+
 def test_device_entry_points_validate_before_touching_a_device():
     # NULL context: validation errors must win over the missing device
     st, err = NH.call_status("nh_gemm_w8a8", None, None, None, None, None, None, 0, 4, 16, None, NH.F32, None)

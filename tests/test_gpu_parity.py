@@ -308,6 +308,48 @@ def test_linear_small_m_shapes_bit_exact(ctx, m, n, k, dtype):
     assert np.array_equal(out.numpy().view(np.uint32), ref.view(np.uint32))
 
 
+# ---- L2: int8 MLP layer (MlpLayer::forward_into, mlp.rs:157-211) -----------------
+def mlp_oracle(x, xdt, w_up, s_up, b_up, w_down, s_down, b_down, out_bf16):
+    """Per-token Q2, up projection + bias, ReLU^2 (mlp.rs:205) in f32, Q2 of
+    the f32 intermediate, down projection + bias: the oracle's parts."""
+    _, xq, sx, _ = O.quantize_rows_bf16(x) if xdt == NH.BF16 else O.quantize_rows_f32(x)
+    h = O.epilogue(O.gemm_i8_i32(xq, w_up), sx, s_up, bias=b_up, relu2=True)
+    st, hq, sh, _ = O.quantize_rows_f32(h)
+    assert st == O.OK
+    return h, O.epilogue(O.gemm_i8_i32(hq, w_down), sh, s_down, bias=b_down, out_bf16=out_bf16)
+
+
+@functools.lru_cache(maxsize=2)
+def mlp_weights(hidden, inter):
+    _, w_up, s_up = quantized_weights(inter, hidden, seed=20)
+    _, w_down, s_down = quantized_weights(hidden, inter, seed=21)
+    return w_up, s_up, w_down, s_down
+
+
+@pytest.mark.parametrize("m,hidden,inter,dtype", [(8, 4096, 21504, "bf16"), (1, 4096, 21504, "bf16"),
+                                                  (37, 1024, 2560, "bf16"), (5, 512, 1856, "f32")])
+def test_mlp_bit_exact(ctx, m, hidden, inter, dtype):
+    note(f"mlp_w8a8 m={m} hidden={hidden} inter={inter} {dtype}")
+    w_up, s_up, w_down, s_down = mlp_weights(hidden, inter)
+    b_up = O.normal_f32(22, inter, 0.0, 0.05)
+    b_down = O.normal_f32(23, hidden, 0.0, 0.05)
+    if dtype == "bf16":
+        x, xdt = activations_bf16(m, hidden, seed=24), NH.BF16
+    else:
+        x, xdt = O.normal_f32(24, m * hidden).reshape(m, hidden), NH.F32
+    _, ref = mlp_oracle(x, xdt, w_up, s_up, b_up, w_down, s_down, b_down, out_bf16=True)
+    dx, db_up, db_down = ctx.upload(x), ctx.upload(b_up), ctx.upload(b_down)
+    dwu, dsu = ctx.upload(tile_16x64(w_up)), ctx.upload(s_up)
+    dwd, dsd = ctx.upload(tile_16x64(w_down)), ctx.upload(s_down)
+    ws_bytes = NH.lib().nh_mlp_w8a8_workspace_size(m, hidden, inter)
+    ws = ctx.empty(ws_bytes, np.uint8)
+    out = ctx.empty((m, hidden), np.uint16)
+    NH.call("nh_mlp_w8a8", ctx.handle, dx.ptr, xdt, dwu.ptr, dsu.ptr, db_up.ptr, dwd.ptr, dsd.ptr, db_down.ptr,
+            m, hidden, inter, out.ptr, NH.BF16, ws.ptr, ws_bytes, None)
+    ctx.synchronize()
+    assert np.array_equal(out.numpy(), ref)
+
+
 @pytest.mark.parametrize("m", [1, 3])
 def test_linear_decode_unit_rounding_ties(ctx, m):
     """Rows whose scale is a power of two carry exact half-integer quotients
