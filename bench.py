@@ -7,7 +7,8 @@ kernel.  value = algorithmic bytes of the unit / time per unit, in GB/s.
 Weights rotate through a >512 MiB pool so the 256 MiB Infinity Cache never
 serves them.  The same JSON line also reports the prefill GEMM (M=2048, TOPS
 vs the int8 MFMA peak), the other decode shapes, the W8A32 GEMV
-and the MoE layer, plus the reference's CPU path timed on this host.
+the MoE layer and the 52-layer decode stack at batch 8, plus
+the reference's CPU path timed on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -175,6 +176,84 @@ class Bench:
         return ms, wbytes + abytes, 2.0 * tokens * top_k * hidden * inter * 2
 
 
+    def decode_stack(self, steps, warmup, m=8):
+        """the 52 linear layers of one decode step of a
+        Nemotron-H-8B-like stack at batch m: 24 Mamba blocks (in_proj
+        4096 -> 16384, out_proj 8192 -> 4096), 4 attention blocks (qkv
+        4096 -> 6144, o 4096 -> 4096) and 24 MLPs (4096 -> 21504 -> 4096,
+        nh_mlp_w8a8), every layer with its own tiled int8 weights (6.81 GB
+        resident in HBM).  The mixers between the projections (SSM scan,
+        attention core) are not part of this path: the out/o projections read
+        a fixed bf16 activation of their width.  Returns (ms per step, weight
+        + scale bytes per step)."""
+        L, h = NH.lib(), self.ctx.handle
+        shapes = {"in": (16384, 4096), "out": (4096, 8192), "qkv": (6144, 4096), "o": (4096, 4096),
+                  "up": (21504, 4096), "down": (4096, 21504)}
+        # 24 x (Mamba, MLP) with an attention block after every 6th pair
+        pattern = []
+        for i in range(24):
+            pattern += ["M", "-"]
+            if i % 6 == 5:
+                pattern.append("*")
+        counts = {"in": 24, "out": 24, "qkv": 4, "o": 4, "up": 24, "down": 24}
+        layers, wbytes = {}, 0
+        for j, (name, (n, k)) in enumerate(shapes.items()):
+            # one N(0, 0.02) matrix per shape, quantized once on the device and
+            # tiled into every layer's own buffer
+            dw = self.ctx.upload(NH.normal_f32(200 + j, n * k, 0.0, 0.02))
+            q = self.ctx.empty((n, k), np.int8)
+            s = self.ctx.empty(n, np.float32)
+            NH.call("nh_quantize_rows_i8", h, dw.ptr, NH.F32, n, k, q.ptr, s.ptr, None, None)
+            dw.free()
+            tb = L.nh_tiled_weights_bytes(n, k)
+            bufs = []
+            for _ in range(counts[name]):
+                d = self.ctx.empty(tb, np.int8)
+                NH.call("nh_tile_weights_i8", h, q.ptr, n, k, d.ptr, tb, None)
+                bufs.append(d)
+                wbytes += n * k + 4 * n
+            self.ctx.synchronize()
+            q.free()
+            layers[name] = (bufs, s)
+        acts = {w: self.ctx.upload(NH_bf16(NH.normal_f32(300 + w, m * w))) for w in (4096, 8192)}
+        outs = {n: self.ctx.empty((m, n), np.uint16) for n in (16384, 6144, 4096)}
+        lin_ws = max(L.nh_linear_w8a8_workspace_size(m, k) for (n, k) in shapes.values())
+        ws = self.ctx.empty(max(lin_ws, L.nh_mlp_w8a8_workspace_size(m, 4096, 21504)), np.uint8)
+        err = NH.NhError()
+        eb = ctypes.byref(err)
+
+        def linear(name, idx, x):
+            (n, k), (bufs, s) = shapes[name], layers[name]
+            st = L.nh_linear_w8a8(h, x.ptr, NH.BF16, bufs[idx].ptr, s.ptr, None, m, n, k, outs[n].ptr, NH.BF16,
+                                  ws.ptr, ws.nbytes, None, None, self.stream, eb)
+            if st:
+                NH.check(st, err)
+
+        def step(_):
+            cnt = {"M": 0, "*": 0, "-": 0}
+            for t in pattern:
+                i = cnt[t]
+                cnt[t] += 1
+                if t == "M":
+                    linear("in", i, acts[4096])
+                    linear("out", i, acts[8192])
+                elif t == "*":
+                    linear("qkv", i, acts[4096])
+                    linear("o", i, acts[4096])
+                else:
+                    (bu, su), (bd, sd) = layers["up"], layers["down"]
+                    st = L.nh_mlp_w8a8(h, acts[4096].ptr, NH.BF16, bu[i].ptr, su.ptr, None, bd[i].ptr, sd.ptr, None,
+                                       m, 4096, 21504, outs[4096].ptr, NH.BF16, ws.ptr, ws.nbytes, self.stream, eb)
+                    if st:
+                        NH.check(st, err)
+
+        ms = self.time_ms(step, steps, warmup)
+        for bufs, s in layers.values():
+            for d in bufs:
+                d.free()
+        return ms, wbytes
+
+
 def NH_bf16(x):
     """f32 -> bf16 bits, round to nearest even (numpy)."""
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
@@ -254,8 +333,8 @@ def main():
     extra = {}
     if not args.quick:
         sweep = {}
-        for (mm, nn, kk) in [(4, 16384, 4096), (16, 16384, 4096), (1, 4096, 8192), (4, 4096, 8192),
-                             (16, 4096, 8192)]:
+        for (mm, nn, kk) in [(4, 16384, 4096), (8, 16384, 4096), (16, 16384, 4096), (1, 4096, 8192),
+                             (4, 4096, 8192), (8, 4096, 8192), (16, 4096, 8192)]:
             log(f"[bench] decode m={mm} k={kk} n={nn}")
             p = pool if (nn, kk) == (n, k) else None
             t, _, _, _ = b.decode(mm, nn, kk, max(20, args.steps // 4), 5, pool=p)
@@ -275,6 +354,11 @@ def main():
             gemms[f"m{mm}_n{nn}_k{kk}"] = {"us": round(t * 1e3, 1), "TOPS": round(tops, 1),
                                           "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
         extra["prefill_gemm"] = gemms
+        log("[bench] decode stack, 52 layers, m=8")
+        t, sbytes = b.decode_stack(20, 3)
+        extra["decode_stack_52l_m8"] = {"ms": round(t, 4), "GBps": round(sbytes / (t * 1e-3) / 1e9, 1),
+                                        "frac_hbm_peak": round(sbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                        "weight_bytes": sbytes}
         log("[bench] moe layer 512 tokens, 128 experts, top-6")
         t, mbytes, mops = b.moe(10, 2)
         extra["moe_512tok_128exp_top6"] = {"us": round(t * 1e3, 1), "GBps": round(mbytes / (t * 1e-3) / 1e9, 1),
