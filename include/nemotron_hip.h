@@ -157,6 +157,14 @@ int nh_supports_gemm_w8a8(size_t m, size_t n, size_t k);
 nh_status nh_gemm_w8a8(nh_context *ctx, const int8_t *xq, const float *sx, const int8_t *wq, const float *sw,
                        const float *bias, size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype,
                        nh_stream stream, nh_error *err);
+/* G3 with A also tiled: xq_tiled is nh_tile_weights_i8 of the row-major
+ * [m][k] codes (nh_tiled_weights_bytes(m, k) bytes), so every A load is one
+ * contiguous KiB as well; same result as nh_gemm_w8a8 on the row-major
+ * codes (the tiled-A GEMM is the faster one: the linear entry point uses it
+ * for m > 16).  No reference counterpart: G3 is new. */
+nh_status nh_gemm_w8a8_ta(nh_context *ctx, const int8_t *xq_tiled, const float *sx, const int8_t *wq,
+                          const float *sw, const float *bias, size_t m, size_t n, size_t k, void *out,
+                          nh_dtype out_dtype, nh_stream stream, nh_error *err);
 nh_status nh_gemm_w8a8_host(const int8_t *xq, const float *sx, const int8_t *wq, const float *sw,
                             const float *bias, size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype,
                             nh_error *err);

@@ -207,23 +207,164 @@ __device__ __forceinline__ void gemm_tile(const GemmW8A8Args& a, int8_t* smem) {
 }
 
 
+// Loader-wave form: NC = WGM x WGN compute waves only read LDS and run
+// MFMAs; NL loader waves only issue the direct-to-LDS loads of the ring and
+// wait for them.  Counters of the single-role kernel (gemm_tile) showed the
+// texture-address FIFO full for long stretches, every wave stalling while
+// it issued its loads; with the roles split those stalls no longer hold up
+// an MFMA wave (256 x 128, 3 stages, 8 loaders: 1.78 vs 1.43 POPS at
+// (2048, 4096, 4096), 2.21 vs 1.55 at K = 21504).  One bare barrier per
+// stage: the loaders wait for the stage's loads (vmcnt) before it, the
+// compute waves read it after it; the compute waves' reads of a stage are
+// done (they fed its MFMAs) before they reach the barrier that lets the
+// loaders refill its slot.
+//
+// ATILED: A in the weights' tiled layout ([ceil(M/16)][KT][1 KiB], written
+// by the row quantizer), every A load one contiguous KiB; otherwise
+// row-major A through the swizzled 8-row x 128-byte loads of gemm_tile.
+// Tiled A measured 1.66 vs 1.40 POPS at (2048, 21504, 4096).
+template <int BM, int BN, int WGM, int WGN, int S, int NL, bool ATILED>
+__device__ __forceinline__ void gemm_ws(const GemmW8A8Args& a, int8_t* smem) {
+    constexpr int NC = WGM * WGN;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int FM = WM / 16, FN = WN / 16;
+    constexpr int TA = BM / 16, TB = BN / 16;
+    constexpr int IA = ATILED ? 2 * TA : BM / 8;  // A load instructions per 128-byte stage
+    constexpr int IB = 2 * TB;
+    constexpr int LPW = (IA + IB) / NL;
+    static_assert((IA + IB) % NL == 0, "stage loads must split evenly over the loader waves");
+    constexpr int kA = BM * 128;
+    constexpr int kStage = kA + IB * 1024;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int M = a.M, N = a.N, K = a.K, KT = a.kt;
+    const int nblk = a.tiles_m * a.tiles_n;
+    int b = blockIdx.x;
+    if ((nblk & 7) == 0) b = (b & 7) * (nblk >> 3) + (b >> 3);
+    const int tm_idx = b % a.tiles_m, tn_idx = b / a.tiles_m;
+    const int m0 = tm_idx * BM, n0 = tn_idx * BN;
+    const int ns = (KT + 1) / 2;
+
+    if (wave >= NC) {  // ---- loader wave
+        const int mt0 = m0 / 16, mtiles = (M + 15) / 16;
+        const int nt0 = n0 / 16, ntiles = (N + 15) / 16;
+        const __amdgpu_buffer_rsrc_t ra =
+            ATILED ? make_rsrc(a.xq + (int64_t)mt0 * KT * 1024, (uint32_t)min(TA, mtiles - mt0) * (uint32_t)KT * 1024u)
+                   : make_rsrc(a.xq, (uint32_t)M * (uint32_t)K);
+        const __amdgpu_buffer_rsrc_t rb =
+            make_rsrc(a.wq + (int64_t)nt0 * KT * 1024, (uint32_t)min(TB, ntiles - nt0) * (uint32_t)KT * 1024u);
+        const uint32_t l16 = (uint32_t)lane * 16u;
+        const int a_r = lane >> 3, a_s = lane & 7;
+        const int lw = wave - NC;
+        auto issue = [&](int st, int slot) {
+#pragma unroll
+            for (int i = 0; i < LPW; ++i) {
+                const int q = lw * LPW + i;  // uniform
+                lds_void_t* dst = (lds_void_t*)(smem + slot * kStage + q * 1024);
+                if (q < IA) {
+                    if constexpr (ATILED) {  // K tile q / TA of the stage, M tile q % TA
+                        const int kt = st * 2 + q / TA;
+                        const uint32_t off = (uint32_t)((q % TA) * KT + kt) * 1024u + l16;
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, dst, 16, kt < KT ? off : (uint32_t)kOutOfRange,
+                                                                 0, 0, 0);
+                    } else {  // local rows 8q .. 8q + 7, swizzled chunks
+                        const int row = 8 * q + a_r;
+                        const int k = st * 128 + a_slot(row, a_s) * 16;
+                        const uint32_t off = (uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)k;
+                        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, dst, 16, k < K ? off : (uint32_t)kOutOfRange, 0,
+                                                                 0, 0);
+                    }
+                } else {  // K tile u / TB of the stage, N tile u % TB
+                    const int u = q - IA;
+                    const int kt = st * 2 + u / TB;
+                    const uint32_t off = (uint32_t)((u % TB) * KT + kt) * 1024u + l16;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, dst, 16, kt < KT ? off : (uint32_t)kOutOfRange, 0, 0,
+                                                             2);
+                }
+            }
+        };
+#pragma unroll
+        for (int s0 = 0; s0 < S - 1; ++s0)
+            if (s0 < ns) issue(s0, s0);
+        for (int st = 0; st < ns; ++st) {
+            if (st + S - 2 < ns) wait_vmcnt_le((S - 2) * LPW); else wait_vmcnt_le(0);
+            lds_barrier();
+            if (st + S - 1 < ns) issue(st + S - 1, (st + S - 1) % S);
+        }
+        lds_barrier();  // the compute waves' last reads are done before the epilogue reuses the LDS
+        return;
+    }
+
+    // ---- compute wave
+    const int wm = wave / WGN, wn = wave % WGN;
+    float swv[FN], sxv[FM][4];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) swv[j] = a.sw[min(n0 + wn * WN + j * 16 + (lane & 15), N - 1)];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sxv[i][r] = a.sx[min(m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r, M - 1)];
+    // A fragment (M fragment i, K step w) read offsets within a stage
+    int a_off[FM][2];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            if constexpr (ATILED) {
+                a_off[i][w] = (w * TA + wm * FM + i) * 1024 + lane * 16;
+            } else {
+                const int row = wm * WM + i * 16 + (lane & 15);
+                a_off[i][w] = (row >> 3) * 1024 + (row & 7) * 128 + a_slot(row, 4 * w + (lane >> 4)) * 16;
+            }
+        }
+    v4i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    for (int st = 0; st < ns; ++st) {
+        lds_barrier();
+        const int8_t* sb = smem + (st % S) * kStage;
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            v4i af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) af[i] = *(const v4i*)(sb + a_off[i][w]);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) bf[j] = *(const v4i*)(sb + kA + (w * TB + wn * FN + j) * 1024 + lane * 16);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    lds_barrier();
+    store_tile_through_lds<WM, WN, FM, FN>(a, acc, sxv, swv, smem + wave * (64 * (WN * 4 + 16)), m0 + wm * WM,
+                                            n0 + wn * WN, lane);
+}
+
 }  // namespace
 
-// 256 x 128 tiles, 8 waves of 64 x 64, 3 stages: the workhorse (M = 2048,
-// N = 4096 gives exactly one tile per CU).
-extern "C" __global__ __launch_bounds__(512) void nh_gemm_w8a8_256x128_kernel(GemmW8A8Args a) {
+// 256 x 128 tiles: 8 compute waves of 64 x 64 + 8 loader waves, 3 stages.
+extern "C" __global__ __launch_bounds__(1024) void nh_gemm_w8a8_256x128_kernel(GemmW8A8Args a) {
     extern __shared__ __align__(1024) int8_t smem[];
-    gemm_tile<256, 128, 4, 2, 3>(a, smem);
+    gemm_ws<256, 128, 4, 2, 3, 8, false>(a, smem);
 }
 
-// 256 x 256 tiles, 8 waves of 128 x 64, 2 stages: half the operand bytes per
-// MAC, for shapes with at least two such tiles per CU.
-extern "C" __global__ __launch_bounds__(512) void nh_gemm_w8a8_256x256_kernel(GemmW8A8Args a) {
+// The same with A in the tiled layout (the linear entry point's quantizer writes it).
+extern "C" __global__ __launch_bounds__(1024) void nh_gemm_w8a8_ta_256x128_kernel(GemmW8A8Args a) {
     extern __shared__ __align__(1024) int8_t smem[];
-    gemm_tile<256, 256, 2, 4, 2>(a, smem);
+    gemm_ws<256, 128, 4, 2, 3, 8, true>(a, smem);
 }
 
-// 128 x 128 tiles, 4 waves of 64 x 64, 3 stages: small problems (more tiles).
+// 128 x 128 tiles, tiled A: 4 compute waves of 64 x 64 + 4 loader waves (fewer, smaller tiles).
+extern "C" __global__ __launch_bounds__(512) void nh_gemm_w8a8_ta_128x128_kernel(GemmW8A8Args a) {
+    extern __shared__ __align__(1024) int8_t smem[];
+    gemm_ws<128, 128, 2, 2, 3, 4, true>(a, smem);
+}
+
+// 128 x 128 tiles, row-major A, 4 waves of 64 x 64, 3 stages (single-role).
 extern "C" __global__ __launch_bounds__(256) void nh_gemm_w8a8_128x128_kernel(GemmW8A8Args a) {
     extern __shared__ __align__(1024) int8_t smem[];
     gemm_tile<128, 128, 2, 2, 3>(a, smem);

@@ -15,11 +15,16 @@ struct QuantizeRowsArgs {
     int8_t* q;            // [rows][cols] or null
     float* scales;        // [rows]
     int32_t* row_status;  // [rows] or null: -1 = all finite, else first non-finite column
-    int8_t* q_act;        // activation tiles [ceil(cols/64)][4][rows][16] (rows <= 16) or null
+    int8_t* q_act;        // codes in MFMA A-operand tiles (see act_p) or null
     int64_t rows;
     int64_t cols;
     int32_t x_dtype;
     int32_t vec;          // 1: rows are 16-byte aligned and a whole number of 16-byte chunks
+    int32_t act_p;        // rows per tile of q_act: code (m, k) at byte
+                          // ((m / P * KT + k / 64) * 4 + (k / 16) % 4) * P * 16 + (m % P) * 16 + k % 16,
+                          // KT = ceil(cols / 64): P = rows (<= 16) gives the GEMV's [KT][4][rows][16],
+                          // P = 16 the weights' tiled layout (the GEMM's A operand)
+    int32_t pad_;
 };
 
 // Q3: out[r][c] = (float)q[r][c] * scales[r]

@@ -8,13 +8,19 @@ using namespace nh;
 
 namespace {
 
+// Byte of code (m, k) in the A-operand tiles with P rows per tile (the
+// layout comment of QuantizeRowsArgs::act_p).
+__device__ __forceinline__ int64_t act_tile_offset(int64_t m, int64_t k, int64_t p, int64_t kt) {
+    return (((m / p) * kt + (k >> 6)) * 4 + ((k >> 4) & 3)) * p * 16 + (m % p) * 16 + (k & 15);
+}
+
 // Vector path: one workgroup per row, 16-byte chunks (8 bf16 or 4 f32
 // values).  The first kRegChunks chunks of every thread stay in registers
 // between the absmax pass and the code pass, so rows up to 8192 bf16 / 4096
 // f32 values are read from memory once; longer rows read the rest again (L2).
-// Codes go to the row-major matrix and/or the activation tiles
-// [KT][4][rows][16] (byte 16 * ((4 kt + g) * rows + m) + b holds code
-// (m, 64 kt + 16 g + b)), the A operand order of the M <= 16 GEMV.
+// Codes go to the row-major matrix and/or the A-operand tiles (act_p rows
+// per tile: the compact [KT][4][rows][16] of the M <= 16 GEMV, or 16, the
+// weights' tiled layout read by the GEMM).
 constexpr int kRegChunks = 4;
 
 template <int DT>
@@ -59,10 +65,10 @@ __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, floa
     }
     const float rcp = s > 0.0f ? 1.0f / s : 0.0f;
     const bool pow2 = scale_is_pow2(s);
+    const int64_t kt = (cols + 63) / 64;
     auto emit = [&](v4i v, int c) {
         const int k = c * VPC;
-        int8_t* tile = a.q_act ? a.q_act + ((int64_t)((k >> 6) * 4 + ((k >> 4) & 3)) * a.rows + row) * 16 + (k & 15)
-                               : nullptr;
+        int8_t* tile = a.q_act ? a.q_act + act_tile_offset(row, k, a.act_p, kt) : nullptr;
         if constexpr (DT == DT_BF16) {
             uint32_t code[2];
             quantize8_bf16(v, s, rcp, pow2, code);
@@ -106,7 +112,7 @@ __device__ __forceinline__ void quantize_row_scalar(const QuantizeRowsArgs& a, f
     for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
         const int8_t code = (int8_t)quantize_i8_fast(load_as_f32(a.x, base + c, a.x_dtype), s, r);
         if (a.q) a.q[base + c] = code;
-        if (a.q_act) a.q_act[((((c >> 6) * 4 + ((c >> 4) & 3)) * a.rows + row) << 4) + (c & 15)] = code;
+        if (a.q_act) a.q_act[act_tile_offset(row, c, a.act_p, (cols + 63) / 64)] = code;
     }
 }
 

@@ -108,12 +108,14 @@ nh_status check_w8a8_shape(size_t m, size_t n, size_t k, nh_error* err) {
 // activation tiles q_act (rows <= 16).  The vector path needs 16-byte aligned
 // rows of whole 16-byte chunks and code stores aligned to a chunk's codes.
 nh_status launch_quantize(nh_context* ctx, const void* x, nh_dtype dtype, size_t rows, size_t cols, int8_t* q,
-                          float* scales, int32_t* row_status, int8_t* q_act, nh_stream stream, nh_error* err) {
+                          float* scales, int32_t* row_status, int8_t* q_act, nh_stream stream, nh_error* err,
+                          int act_p = 0) {
     const size_t esz = dtype == NH_BF16 ? 2 : 4;
     const size_t row_bytes = cols * esz;
     const bool vec = aligned16(x) && row_bytes % 16 == 0 && row_bytes < (1ull << 31) &&
                      ((uintptr_t)q % (16 / esz)) == 0 && aligned16(q_act);
-    QuantizeRowsArgs a{x, q, scales, row_status, q_act, (int64_t)rows, (int64_t)cols, dtype, vec ? 1 : 0};
+    QuantizeRowsArgs a{x, q, scales, row_status, q_act, (int64_t)rows, (int64_t)cols, dtype, vec ? 1 : 0,
+                       act_p > 0 ? act_p : (int)rows, 0};
     return launch(ctx, K_QUANTIZE_ROWS, (unsigned)rows, 256, 0, stream, a, err);
 }
 
@@ -143,9 +145,11 @@ nh_status launch_gemv(nh_context* ctx, const int8_t* xq, const float* sx, const 
                   a, err);
 }
 
+// G3 launch.  a_tiled: xq holds A in the weights' tiled layout (written by
+// the row quantizer with 16 rows per tile), else row-major [M][K].
 nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
                       const float* bias, int M, int N, int K, void* out, nh_dtype out_dtype, int relu2,
-                      nh_stream stream, nh_error* err) {
+                      nh_stream stream, nh_error* err, bool a_tiled = false) {
     GemmW8A8Args a{};
     a.xq = xq;
     a.sx = sx;
@@ -159,26 +163,24 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
     a.out_dtype = out_dtype;
     a.relu2 = relu2;
     a.kt = (int)tiled_k_tiles(K);
-    // Tile choice: 256x256 when every CU gets at least two of them (half the
-    // operand bytes per MAC), else 256x128 when they fill the chip once,
-    // else 128x128 (more, smaller tiles against idle CUs).
+    // Tile choice: 256x128 (8 compute + 8 loader waves) unless that leaves
+    // most CUs idle, then 128x128 (more, smaller tiles).
     struct Cfg {
         KernelId id;
         int bm, bn, threads;
-        size_t lds;  // max(ring of stages, epilogue staging)
+        size_t lds;  // max(ring of stages, epilogue staging of the compute waves)
     };
-    const Cfg c256x256{K_GEMM_W8A8_256, 256, 256, 512, gemm_lds_bytes(256, 256, 2, 8, 64)};
-    const Cfg c256x128{K_GEMM_W8A8, 256, 128, 512, gemm_lds_bytes(256, 128, 3, 8, 64)};
-    const Cfg c128x128{K_GEMM_W8A8_128, 128, 128, 256, gemm_lds_bytes(128, 128, 3, 4, 64)};
+    const Cfg big = {a_tiled ? K_GEMM_TA_256 : K_GEMM_W8A8, 256, 128, 1024, gemm_lds_bytes(256, 128, 3, 8, 64)};
+    const Cfg small = a_tiled ? Cfg{K_GEMM_TA_128, 128, 128, 512, gemm_lds_bytes(128, 128, 3, 4, 64)}
+                              : Cfg{K_GEMM_W8A8_128, 128, 128, 256, gemm_lds_bytes(128, 128, 3, 4, 64)};
     auto tiles = [&](const Cfg& c) { return (int64_t)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn); };
     const Cfg* cfg = nullptr;
-    if (tiles(c256x256) >= 2 * (int64_t)ctx->cu_count && c256x256.lds <= ctx->max_shared_per_block)
-        cfg = &c256x256;
-    else if (tiles(c256x128) >= ctx->cu_count && c256x128.lds <= ctx->max_shared_per_block)
-        cfg = &c256x128;
-    else if (c128x128.lds <= ctx->max_shared_per_block)
-        cfg = &c128x128;
+    if (tiles(big) >= ctx->cu_count / 4 && big.lds <= ctx->max_shared_per_block)
+        cfg = &big;
+    else if (small.lds <= ctx->max_shared_per_block)
+        cfg = &small;
     if (!cfg) {
+        if (a_tiled) return set_error(err, NH_UNSUPPORTED, "LDS too small for the GEMM tiles");
         // LDS too small for the MFMA tiles: 16-row GEMV passes (still exact)
         for (int m0 = 0; m0 < M; m0 += 16) {
             const int mm = std::min(16, M - m0);
@@ -307,10 +309,22 @@ nh_status nh_gemm_w8a8(nh_context* ctx, const int8_t* xq, const float* sx, const
     return launch_gemm(ctx, xq, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, 0, stream, err);
 }
 
+nh_status nh_gemm_w8a8_ta(nh_context* ctx, const int8_t* xq_tiled, const float* sx, const int8_t* wq, const float* sw,
+                          const float* bias, size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype,
+                          nh_stream stream, nh_error* err) {
+    clear_error(err);
+    nh_status st;
+    if ((st = check_dtype(out_dtype, err)) || (st = check_w8a8_shape(m, n, k, err))) return st;
+    if (!aligned16(xq_tiled) || !aligned16(wq))
+        return set_error(err, NH_UNSUPPORTED, "xq_tiled and wq must be 16-byte aligned");
+    if ((st = bind_device(ctx, err))) return st;
+    return launch_gemm(ctx, xq_tiled, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, 0, stream, err, true);
+}
+
 size_t nh_linear_w8a8_workspace_size(size_t m, size_t k) {
     if (m == 0 || k == 0 || m > (1ull << 31) || k > (1ull << 31)) return 0;
     if (m <= kTiledActRows) return align256(act_tiles_bytes(m, k)) + align256(m * sizeof(float));
-    return align256(m * k) + align256(m * sizeof(float));
+    return align256(tiled_bytes(m, k)) + align256(m * sizeof(float));
 }
 
 }  // extern "C"
@@ -360,16 +374,15 @@ nh_status linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const in
         return launch_gemv(ctx, tiles, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, true, stream, err,
                            relu2);
     }
-    // two launches: Q2 into the workspace (or the caller's xq_out/sx_out), then G3
-    int8_t* xq = xq_out;
-    float* sx = sx_out;
-    if (!xq || !sx) {
-        if (!workspace || workspace_bytes < need) return mismatch(err, "workspace", need, workspace_bytes);
-        xq = (int8_t*)workspace;
-        sx = (float*)((char*)workspace + align256(m * k));
-    }
-    if ((st = launch_quantize(ctx, x, x_dtype, m, k, xq, sx, nullptr, nullptr, stream, err))) return st;
-    return launch_gemm(ctx, xq, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, relu2, stream, err);
+    // two launches: Q2 into A tiles in the workspace (and the caller's
+    // row-major xq_out), then G3 on the tiled A
+    if (!workspace || workspace_bytes < need) return mismatch(err, "workspace", need, workspace_bytes);
+    if (!aligned16(workspace)) return set_error(err, NH_UNSUPPORTED, "workspace must be 16-byte aligned");
+    int8_t* atiles = (int8_t*)workspace;
+    float* sx = sx_out ? sx_out : (float*)((char*)workspace + align256(tiled_bytes(m, k)));
+    if ((st = launch_quantize(ctx, x, x_dtype, m, k, xq_out, sx, nullptr, atiles, stream, err, 16))) return st;
+    return launch_gemm(ctx, atiles, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, relu2, stream, err,
+                       true);
 }
 
 }  // namespace

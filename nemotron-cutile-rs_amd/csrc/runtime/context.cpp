@@ -11,14 +11,29 @@ extern "C" const unsigned char nh_gfx950_code_object_end[];
 
 namespace nh {
 
-const char* const kKernelSymbols[K_COUNT] = {
-    "nh_quantize_rows_i8_kernel", "nh_dequantize_i8_kernel",   "nh_dequantize_int4_kernel",
-    "nh_gemv_w8a8_kernel",        "nh_linear_decode_w8a8_kernel", "nh_linear_decode_w8a8_m1_kernel",
-    "nh_linear_decode_w8a8_m2_kernel", "nh_gemv_w8a32_kernel",
-    "nh_gemm_w8a8_256x128_kernel", "nh_gemm_w8a8_128x128_kernel", "nh_moe_route_sigmoid_kernel", "nh_moe_permute_kernel",
-    "nh_moe_grouped_gemm_kernel", "nh_moe_combine_kernel",     "nh_tile_weights_kernel",
-    "nh_gemm_w8a8_256x256_kernel", "nh_gemm_f32_kernel",       "nh_gemv_w8a8_xt_kernel",
-    "nh_linear_decode_w8a8_m8_kernel", "nh_linear_decode_w8a8_row2_kernel", "nh_linear_decode_w8a8_row4_kernel",
+const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
+    "nh_quantize_rows_i8_kernel",        // K_QUANTIZE_ROWS
+    "nh_dequantize_i8_kernel",           // K_DEQUANT_I8
+    "nh_dequantize_int4_kernel",         // K_DEQUANT_INT4
+    "nh_gemv_w8a8_kernel",               // K_GEMV_W8A8
+    "nh_linear_decode_w8a8_kernel",      // K_LINEAR_DECODE
+    "nh_linear_decode_w8a8_m1_kernel",   // K_LINEAR_DECODE_M1
+    "nh_linear_decode_w8a8_m2_kernel",   // K_LINEAR_DECODE_M2
+    "nh_gemv_w8a32_kernel",              // K_GEMV_W8A32
+    "nh_gemm_w8a8_256x128_kernel",       // K_GEMM_W8A8
+    "nh_gemm_w8a8_128x128_kernel",       // K_GEMM_W8A8_128
+    "nh_moe_route_sigmoid_kernel",       // K_ROUTE_SIGMOID
+    "nh_moe_permute_kernel",             // K_PERMUTE
+    "nh_moe_grouped_gemm_kernel",        // K_GROUPED_GEMM
+    "nh_moe_combine_kernel",             // K_COMBINE
+    "nh_tile_weights_kernel",            // K_TILE_WEIGHTS
+    "nh_gemm_w8a8_ta_256x128_kernel",    // K_GEMM_TA_256
+    "nh_gemm_w8a8_ta_128x128_kernel",    // K_GEMM_TA_128
+    "nh_gemm_f32_kernel",                // K_GEMM_F32
+    "nh_gemv_w8a8_xt_kernel",            // K_GEMV_W8A8_XT
+    "nh_linear_decode_w8a8_m8_kernel",   // K_LINEAR_DECODE_M8
+    "nh_linear_decode_w8a8_row2_kernel", // K_LINEAR_DECODE_ROW2
+    "nh_linear_decode_w8a8_row4_kernel", // K_LINEAR_DECODE_ROW4
 };
 
 void clear_error(nh_error* err) {
@@ -220,7 +235,7 @@ static const struct {
     {"gemv_w8a32_host", 0},      {"moe_sigmoid_topk_host", 0},  {"moe_softmax_topk_host", 0},
     {"moe_permute_host", 0},     {"moe_grouped_gemm_w8a8_host", 0}, {"moe_combine_host", 0},
     {"tile_weights_i8", 1},      {"tile_weights_i8_host", 0},  {"gemm_f32", 1},
-    {"mlp_w8a8", 1},
+    {"mlp_w8a8", 1},             {"gemm_w8a8_tiled_a", 1},
 };
 
 int nh_kernel_count(void) { return (int)(sizeof(kRegistry) / sizeof(kRegistry[0])); }

@@ -29,7 +29,8 @@ enum KernelId : int {
     K_GROUPED_GEMM,
     K_COMBINE,
     K_TILE_WEIGHTS,
-    K_GEMM_W8A8_256,
+    K_GEMM_TA_256,       // tiled A, 256 x 128
+    K_GEMM_TA_128,       // tiled A, 128 x 128
     K_GEMM_F32,
     K_GEMV_W8A8_XT,      // activation tiles
     K_LINEAR_DECODE_M8,  // M <= 8

@@ -93,6 +93,7 @@ _SIGNATURES = {
     "nh_gemm_f32": (ST, [P, P, SZ, P, SZ, SZ, SZ, SZ, P, SZ, P, E]),
     "nh_supports_gemm_w8a8": (C.c_int, [SZ, SZ, SZ]),
     "nh_gemm_w8a8": (ST, [P, P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, P, E]),
+    "nh_gemm_w8a8_ta": (ST, [P, P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, P, E]),
     "nh_gemm_w8a8_host": (ST, [P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, E]),
     "nh_linear_w8a8_workspace_size": (SZ, [SZ, SZ]),
     "nh_linear_w8a8": (ST, [P, P, C.c_int, P, P, P, SZ, SZ, SZ, P, C.c_int, P, SZ, P, P, P, E]),

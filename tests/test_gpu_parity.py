@@ -273,9 +273,11 @@ def test_linear_decode_unit_bit_exact(ctx, m):
 @pytest.mark.parametrize("m,n,k,dtype", [(8, 4096, 21504, "bf16"), (8, 1040, 4112, "bf16"), (5, 528, 4160, "f32"),
                                          (1, 4096, 16384, "bf16"), (16, 96, 64, "f32"), (2, 300, 8192, "f32"),
                                          (3, 4096, 8192, "bf16"), (2, 1000, 4112, "bf16"), (7, 4096, 8192, "bf16"),
-                                         (6, 6144, 4096, "bf16")])
+                                         (6, 6144, 4096, "bf16"), (17, 300, 4160, "bf16"), (100, 2688, 1856, "f32"),
+                                         (257, 1024, 4096, "bf16")])
 def test_linear_small_m_shapes_bit_exact(ctx, m, n, k, dtype):
-    """The M <= 16 linear path off the headline shape: several K slabs per
+    """The linear path off the headline shape (and past 16 rows, the GEMM on
+    A tiles written by the quantizer, M and K tails included): several K slabs per
     wave (K = 16384, 21504), a last K tile only partly inside the matrix
     (K = 4112, 4160: the activation tiles hold stale bytes there and meet
     zero weight padding), N not a multiple of 16, f32 activations, the
@@ -416,14 +418,17 @@ def test_gemv_w8a32_within_tolerance(ctx, m, n, k):
 # ---- G3: W8A8 GEMM (prefill) -----------------------------------------------------
 @pytest.mark.parametrize("m,n,k", [(2048, 4096, 4096), (2048, 21504, 4096), (2048, 4096, 21504), (37, 100, 64),
                                    (300, 130, 272), (17, 4096, 4096), (513, 2688, 1856)])
-def test_gemm_w8a8_bit_exact(ctx, m, n, k):
-    note(f"gemm_w8a8 m={m} n={n} k={k}")
+@pytest.mark.parametrize("a_layout", ["row-major", "tiled"])
+def test_gemm_w8a8_bit_exact(ctx, m, n, k, a_layout):
+    note(f"gemm_w8a8 m={m} n={n} k={k} A {a_layout}")
     _, wq, sw = quantized_weights(n, k)
     x = activations_bf16(m, k)
     _, xq, sx, _ = O.quantize_rows_bf16(x)
-    dxq, dsx, dw, dsw = ctx.upload(xq), ctx.upload(sx), ctx.upload(tile_16x64(wq)), ctx.upload(sw)
+    dxq = ctx.upload(xq if a_layout == "row-major" else tile_16x64(xq))
+    dsx, dw, dsw = ctx.upload(sx), ctx.upload(tile_16x64(wq)), ctx.upload(sw)
     out = ctx.empty((m, n), np.uint16)
-    NH.call("nh_gemm_w8a8", ctx.handle, dxq.ptr, dsx.ptr, dw.ptr, dsw.ptr, None, m, n, k, out.ptr, NH.BF16, None)
+    fn = "nh_gemm_w8a8" if a_layout == "row-major" else "nh_gemm_w8a8_ta"
+    NH.call(fn, ctx.handle, dxq.ptr, dsx.ptr, dw.ptr, dsw.ptr, None, m, n, k, out.ptr, NH.BF16, None)
     ctx.synchronize()
     got = out.numpy()
     rows = np.arange(m) if m * n * k <= 2e9 else np.unique(np.concatenate(
