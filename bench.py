@@ -309,6 +309,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--only", choices=["moe", "gemm", "stack", "decode"], default=None,
+                    help="run one secondary workload only (for profiling) and print its figures")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (torch's copy kernel), the "
                          "calibration run for the FETCH_SIZE / WRITE_SIZE counters, and exit")
@@ -330,6 +332,24 @@ def main():
         sys.exit(2)
 
     b = Bench()
+    if args.only:
+        res = {}
+        if args.only == "moe":
+            t, mbytes, mops = b.moe(10, 2)
+            res = {"us": round(t * 1e3, 1), "GBps": round(mbytes / (t * 1e-3) / 1e9, 1)}
+        elif args.only == "gemm":
+            for (mm, nn, kk) in [(2048, 4096, 4096), (2048, 21504, 4096), (2048, 4096, 21504)]:
+                t, t_rm = b.gemm(mm, nn, kk, 20, 3)
+                res[f"m{mm}_n{nn}_k{kk}"] = {"us": round(t * 1e3, 1), "row_major_a_us": round(t_rm * 1e3, 1)}
+        elif args.only == "stack":
+            t, sbytes = b.decode_stack(20, 3)
+            res = {"ms": round(t, 4), "GBps": round(sbytes / (t * 1e-3) / 1e9, 1)}
+        else:
+            for (mm, nn, kk) in [(4, 16384, 4096), (8, 16384, 4096), (16, 16384, 4096), (8, 4096, 8192)]:
+                t, _, _, _ = b.decode(mm, nn, kk, 50, 5)
+                res[f"m{mm}_k{kk}_n{nn}"] = round(t * 1e3, 2)
+        print(json.dumps({"only": args.only, **res}), flush=True)
+        return
     m, n, k = 1, 16384, 4096
     log = lambda s: print(s, file=sys.stderr, flush=True)  # noqa: E731
     log("[bench] headline decode unit m=1 k=4096 n=16384")

@@ -161,12 +161,16 @@ extern "C" __global__ __launch_bounds__(1024) void nh_moe_permute_kernel(Permute
 // w + e * tiled_bytes(N, K); wave w owns K tiles w, w + waves, ... and issues
 // the loads of all of them (at most 16, one contiguous KiB each, streaming
 // policy) at once; the slab then stays in registers while the expert's
-// segment is walked in blocks of 16 routed rows (one block for a typical
+// segment is walked in blocks of 16 routed rows (two blocks for a typical
 // ~24-row segment), so each expert weight byte leaves HBM once.  A rows are
-// gathered per lane (token perm[slot] / top_k for the up projection, the slot
-// itself for the down projection).  Tiles past KT and rows past the segment
-// load from an out-of-range buffer offset, which returns zeros without
-// touching memory.
+// slots (the MoE layer quantizes the routes' tokens straight into slot
+// order), or gathered per lane (token perm[slot] / top_k) when the public
+// entry point is given token-major activations.  The first block's A loads
+// go out before the weight slab and each next block's under the current
+// block's reduction: behind an index load queued after the slab (the
+// gathered form), the A loads would wait for the whole slab first.
+// Tiles past KT and rows past the segment load from an out-of-range buffer
+// offset, which returns zeros without touching memory.
 constexpr int kGroupedSteps = 16;
 
 extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(GroupedGemmArgs a) {
@@ -183,26 +187,46 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(Gro
     const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.aq, (uint32_t)a.a_rows * (uint32_t)K);
     const int n = tile * 16 + r16;
     const float swn = n < N ? a.sw[(int64_t)e * N + n] : 0.0f;
-    v4i b[kGroupedSteps];
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int s = 0; s < kGroupedSteps; ++s) b[s] = buffer_load16_stream(wr, (wave + s * W) * 1024 + lane * 16);
-    __builtin_amdgcn_sched_barrier(0);
-    for (int m0 = seg0; m0 < seg1; m0 += 16) {
+    // A row of slot s (gathered rows: the public entry point's token-major
+    // activations; the MoE layer passes them already in slot order)
+    auto a_row = [&](int s) { return a.gather ? a.perm[s] / a.top_k : s; };
+    v4i x[kGroupedSteps];
+    float sa[4];
+    // one 16-slot chunk's A fragments and epilogue scales
+    auto load_chunk = [&](int m0) {
         const int slot = m0 + r16;
         const bool mok = slot < seg1;
-        const int arow = mok ? (a.gather ? a.perm[slot] / a.top_k : slot) : 0;
-        v4i x[kGroupedSteps];
-        __builtin_amdgcn_sched_barrier(0);
+        const int arow = mok ? a_row(slot) : 0;
 #pragma unroll
         for (int s = 0; s < kGroupedSteps; ++s) {
             const int k = (wave + s * W) * 64 + g * 16;
             x[s] = buffer_load16(ar, (mok && k < K) ? arow * K + k : kOutOfRange);
         }
-        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int srow = m0 + 4 * g + r;
+            sa[r] = srow < seg1 ? a.sa[a_row(srow)] : 0.0f;
+        }
+    };
+    // the first chunk's activations ahead of the weight slab: loads return
+    // in issue order, so the MFMAs wait for the slab only, not for an index
+    // load queued behind it
+    __builtin_amdgcn_sched_barrier(0);
+    load_chunk(seg0);
+    __builtin_amdgcn_sched_barrier(0);
+    v4i b[kGroupedSteps];
+#pragma unroll
+    for (int s = 0; s < kGroupedSteps; ++s) b[s] = buffer_load16_stream(wr, (wave + s * W) * 1024 + lane * 16);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int m0 = seg0; m0 < seg1; m0 += 16) {
         v4i acc = {0, 0, 0, 0};
 #pragma unroll
         for (int s = 0; s < kGroupedSteps; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[s], b[s], acc, 0, 0, 0);
+        float sa_cur[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sa_cur[r] = sa[r];
+        // the next chunk's loads run under this chunk's reduction and epilogue
+        if (m0 + 16 < seg1) load_chunk(m0 + 16);
         if (W > 1) {
             red[wave * 64 + lane] = acc;
             __syncthreads();
@@ -214,8 +238,7 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(Gro
             for (int r = 0; r < 4; ++r) {
                 const int srow = m0 + 4 * g + r;
                 if (srow < seg1) {
-                    const int ar_ = a.gather ? a.perm[srow] / a.top_k : srow;
-                    float y = epilogue_w8a8(acc[r], a.sa[ar_], swn);
+                    float y = epilogue_w8a8(acc[r], sa_cur[r], swn);
                     if (a.relu2) y = relu2(y);
                     a.out[(int64_t)srow * N + n] = y;
                 }

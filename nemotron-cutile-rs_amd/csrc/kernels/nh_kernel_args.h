@@ -24,7 +24,8 @@ struct QuantizeRowsArgs {
                           // ((m / P * KT + k / 64) * 4 + (k / 16) % 4) * P * 16 + (m % P) * 16 + k % 16,
                           // KT = ceil(cols / 64): P = rows (<= 16) gives the GEMV's [KT][4][rows][16],
                           // P = 16 the weights' tiled layout (the GEMM's A operand)
-    int32_t pad_;
+    int32_t gather_div;   // with gather: output row r quantizes input row gather[r] / gather_div
+    const int32_t* gather;  // or null (output row r = input row r)
 };
 
 // Q3: out[r][c] = (float)q[r][c] * scales[r]

@@ -27,10 +27,11 @@ template <int DT>
 __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, float* redf, int* redi) {
     constexpr int VPC = DT == DT_BF16 ? 8 : 4;  // values per 16-byte chunk
     const int64_t row = blockIdx.x;
+    const int64_t src = a.gather ? a.gather[row] / a.gather_div : row;
     const int cols = (int)a.cols;
     const int chunks = cols / VPC;
     const uint32_t rb = (uint32_t)cols * (DT == DT_BF16 ? 2u : 4u);
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc((const char*)a.x + row * (int64_t)rb, rb);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc((const char*)a.x + src * (int64_t)rb, rb);
     v4i xv[kRegChunks];
 #pragma unroll
     for (int r = 0; r < kRegChunks; ++r) {
@@ -93,7 +94,7 @@ __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, floa
 __device__ __forceinline__ void quantize_row_scalar(const QuantizeRowsArgs& a, float* redf, int* redi) {
     const int64_t row = blockIdx.x;
     const int64_t cols = a.cols;
-    const int64_t base = row * cols;
+    const int64_t base = (a.gather ? a.gather[row] / a.gather_div : row) * cols;  // input row
     float amax = 0.0f;
     int bad = 0x7fffffff;
     for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
@@ -111,7 +112,7 @@ __device__ __forceinline__ void quantize_row_scalar(const QuantizeRowsArgs& a, f
     const float r = s > 0.0f ? 1.0f / s : 0.0f;
     for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
         const int8_t code = (int8_t)quantize_i8_fast(load_as_f32(a.x, base + c, a.x_dtype), s, r);
-        if (a.q) a.q[base + c] = code;
+        if (a.q) a.q[row * cols + c] = code;
         if (a.q_act) a.q_act[act_tile_offset(row, c, a.act_p, (cols + 63) / 64)] = code;
     }
 }
@@ -119,7 +120,9 @@ __device__ __forceinline__ void quantize_row_scalar(const QuantizeRowsArgs& a, f
 }  // namespace
 
 // Q1/Q2: one workgroup per row; codes bit-identical to quantize_i8 (the
-// reference's division) without dividing (quantize_i8_fast).
+// reference's division) without dividing (quantize_i8_fast).  With a gather
+// list the output rows are input rows gather[r] / gather_div (the MoE's
+// routes in expert order: each route's codes and scale are its token's).
 extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_i8_kernel(QuantizeRowsArgs a) {
     __shared__ float redf[4];
     __shared__ int redi[4];

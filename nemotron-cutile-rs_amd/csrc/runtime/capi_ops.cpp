@@ -109,13 +109,13 @@ nh_status check_w8a8_shape(size_t m, size_t n, size_t k, nh_error* err) {
 // rows of whole 16-byte chunks and code stores aligned to a chunk's codes.
 nh_status launch_quantize(nh_context* ctx, const void* x, nh_dtype dtype, size_t rows, size_t cols, int8_t* q,
                           float* scales, int32_t* row_status, int8_t* q_act, nh_stream stream, nh_error* err,
-                          int act_p = 0) {
+                          int act_p = 0, const int32_t* gather = nullptr, int gather_div = 1) {
     const size_t esz = dtype == NH_BF16 ? 2 : 4;
     const size_t row_bytes = cols * esz;
     const bool vec = aligned16(x) && row_bytes % 16 == 0 && row_bytes < (1ull << 31) &&
                      ((uintptr_t)q % (16 / esz)) == 0 && aligned16(q_act);
     QuantizeRowsArgs a{x, q, scales, row_status, q_act, (int64_t)rows, (int64_t)cols, dtype, vec ? 1 : 0,
-                       act_p > 0 ? act_p : (int)rows, 0};
+                       act_p > 0 ? act_p : (int)rows, gather_div, gather};
     return launch(ctx, K_QUANTIZE_ROWS, (unsigned)rows, 256, 0, stream, a, err);
 }
 
@@ -549,8 +549,8 @@ static void moe_layout(size_t T, size_t H, size_t I, size_t E, size_t k, size_t 
     off[2] = take((E + 1) * 4);  // offsets
     off[3] = take(R * 4);        // perm
     off[4] = take(R * 4);        // pos
-    off[5] = take(T * H);        // xq
-    off[6] = take(T * 4);        // sx
+    off[5] = take(R * H);        // xq, one row per route in expert order
+    off[6] = take(R * 4);        // sx
     off[7] = take(R * I * 4);    // up output (f32, ReLU^2 applied)
     off[8] = take(R * I);        // requantized up output
     off[9] = take(R * 4);        // its scales
@@ -599,12 +599,18 @@ nh_status nh_moe_forward_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, 
     float* d = (float*)(ws + off[10]);
     const size_t R = tokens * top_k;
     nh_status st;
-    if ((st = nh_quantize_rows_i8(ctx, x, x_dtype, tokens, hidden, xq, sx, nullptr, stream, err))) return st;
+    if ((st = check_dtype(x_dtype, err))) return st;
     if ((st = nh_moe_route_sigmoid_topk(ctx, logits, tokens, experts, top_k, renormalize, scaling, idx, wts, stream,
                                         err)))
         return st;
     if ((st = nh_moe_permute(ctx, idx, tokens, top_k, experts, offsets, perm, pos, stream, err))) return st;
-    if ((st = nh_moe_grouped_gemm_w8a8(ctx, xq, sx, 1, top_k, offsets, perm, R, tokens, experts, w_up, s_up, inter,
+    // Q2 of each route's token, written in expert order (slot s = token
+    // perm[s] / top_k): the up projection then reads its rows contiguously,
+    // with no index load in front of its activation loads
+    if ((st = launch_quantize(ctx, x, x_dtype, R, hidden, xq, sx, nullptr, nullptr, stream, err, 0, perm,
+                              (int)top_k)))
+        return st;
+    if ((st = nh_moe_grouped_gemm_w8a8(ctx, xq, sx, 0, top_k, offsets, perm, R, R, experts, w_up, s_up, inter,
                                        hidden, 1, h, stream, err)))
         return st;
     if ((st = nh_quantize_rows_i8(ctx, h, NH_F32, R, inter, hq, sh, nullptr, stream, err))) return st;
