@@ -36,7 +36,6 @@ using namespace nh;
 
 namespace {
 
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Epilogue of a wave's WM x WN accumulator tile (16x16 fragments, lane l
 // holding D[4 (l / 16) + r][l % 16]): y = ((float)acc * sx[m]) * sw[n]

@@ -144,6 +144,9 @@ __device__ __forceinline__ uint32_t quantize4_f32(v4i xv, float s, float r, bool
     return pack_codes4(q[0], q[1], q[2], q[3]);
 }
 
+// LDS destination of the direct-to-LDS buffer loads.
+typedef __attribute__((address_space(3))) void lds_void_t;
+
 // s_waitcnt vmcnt(<= n) with the other counters left alone (gfx9 encoding:
 // vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] << 14).
 // The wait is an immediate, hence the switch over the counts in use.

@@ -173,6 +173,23 @@ struct GroupedGemmArgs {
     int32_t waves;
 };
 
+// R3, the MoE layer's form: A already in slot (expert) order.  grid =
+// (wgs_per_expert, experts); workgroup (nb, e) owns expert e's N tiles
+// [nb * tiles_per_wg, +tiles_per_wg) with `streams` tiles in flight, each
+// split over `waves` K waves (blockDim = 64 * waves * streams).
+struct ExpertGemmArgs {
+    const int8_t* aq;        // [R][K] codes in slot order
+    const float* sa;         // [R]
+    const int32_t* offsets;  // [E+1]
+    const int8_t* w;         // [E] x tiled [N][K], expert stride tiled_bytes(N, K)
+    const float* sw;         // [E][N]
+    float* out;              // [R][N]
+    int32_t N, K, kt;
+    int32_t a_rows;          // R
+    int32_t waves, streams, tiles_per_wg;
+    int32_t relu2;
+};
+
 // R4: scatter-combine.
 struct CombineArgs {
     const float* slot_out;   // [R][H]

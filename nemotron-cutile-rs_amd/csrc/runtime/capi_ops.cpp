@@ -500,6 +500,34 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
         return set_error(err, NH_UNSUPPORTED, "grouped GEMM envelope: experts <= 65535, k <= 8192, a_rows * k < 2^31");
     if ((st = bind_device(ctx, err))) return st;
     if (routes == 0) return NH_OK;
+    const int kt = (int)tiled_k_tiles(k);
+    const int w_k = (kt + 15) / 16;  // K waves per N tile: one 16-tile slab each
+    if (!gather) {
+        // slot-ordered A: the expert-block kernel (A staged once per expert
+        // in LDS, N tiles streamed), two workgroups per expert
+        const int streams = w_k <= 12 ? 12 / w_k : 0;  // up to 12 waves (the kernel's register budget)
+        const size_t lds = (size_t)2 * kt * 1024 + (size_t)streams * w_k * 2 * 1024;
+        if (streams > 0 && lds <= ctx->max_shared_per_block) {
+            ExpertGemmArgs e{};
+            e.aq = aq;
+            e.sa = sa;
+            e.offsets = offsets;
+            e.w = w;
+            e.sw = sw;
+            e.out = out;
+            e.N = (int)n;
+            e.K = (int)k;
+            e.kt = kt;
+            e.a_rows = (int)a_rows;
+            e.waves = w_k;
+            e.streams = streams;
+            const int ntiles = (int)((n + 15) / 16);
+            e.tiles_per_wg = (ntiles + 1) / 2;
+            e.relu2 = relu2 ? 1 : 0;
+            return launch(ctx, K_EXPERT_GEMM, 2u, (unsigned)(64 * e.waves * e.streams), lds, stream, e, err,
+                          (unsigned)experts);
+        }
+    }
     GroupedGemmArgs a{};
     a.aq = aq;
     a.sa = sa;
