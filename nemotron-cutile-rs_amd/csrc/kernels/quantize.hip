@@ -16,8 +16,9 @@ __device__ __forceinline__ int64_t act_tile_offset(int64_t m, int64_t k, int64_t
 
 // Vector path: one workgroup per row, 16-byte chunks (8 bf16 or 4 f32
 // values).  The first kRegChunks chunks of every thread stay in registers
-// between the absmax pass and the code pass, so rows up to 8192 bf16 / 4096
-// f32 values are read from memory once; longer rows read the rest again (L2).
+// between the absmax pass and the code pass, so rows up to 4 * 256 chunks
+// (8192 bf16 / 4096 f32 values) are read from memory once; longer rows read
+// the rest again (L2), four chunks in flight per thread.
 // Codes go to the row-major matrix and/or the A-operand tiles (act_p rows
 // per tile: the compact [KT][4][rows][16] of the M <= 16 GEMV, or 16, the
 // weights' tiled layout read by the GEMM).
@@ -32,10 +33,11 @@ __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, floa
     const int chunks = cols / VPC;
     const uint32_t rb = (uint32_t)cols * (DT == DT_BF16 ? 2u : 4u);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc((const char*)a.x + src * (int64_t)rb, rb);
+    const int T = blockDim.x;
     v4i xv[kRegChunks];
 #pragma unroll
     for (int r = 0; r < kRegChunks; ++r) {
-        const int c = threadIdx.x + r * 256;
+        const int c = threadIdx.x + r * T;
         xv[r] = buffer_load16(xr, c < chunks ? c * 16 : kOutOfRange);
     }
     float amax = 0.0f;
@@ -55,8 +57,14 @@ __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, floa
         }
     };
 #pragma unroll
-    for (int r = 0; r < kRegChunks; ++r) scan(xv[r], threadIdx.x + r * 256);  // chunks past the row read zeros
-    for (int c = threadIdx.x + kRegChunks * 256; c < chunks; c += 256) scan(buffer_load16(xr, c * 16), c);
+    for (int r = 0; r < kRegChunks; ++r) scan(xv[r], threadIdx.x + r * T);  // chunks past the row read zeros
+    for (int c0 = threadIdx.x + kRegChunks * T; c0 < chunks; c0 += 4 * T) {  // the tail, 4 loads at a time
+        v4i t[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t[j] = buffer_load16(xr, c0 + j * T < chunks ? (c0 + j * T) * 16 : kOutOfRange);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) scan(t[j], c0 + j * T);  // past the row: zeros
+    }
     amax = block_max(amax, redf);
     bad = block_min_i32(bad, redi);
     const float s = scale_from_amax(amax);
@@ -83,10 +91,17 @@ __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, floa
     };
 #pragma unroll
     for (int r = 0; r < kRegChunks; ++r) {
-        const int c = threadIdx.x + r * 256;
+        const int c = threadIdx.x + r * T;
         if (c < chunks) emit(xv[r], c);
     }
-    for (int c = threadIdx.x + kRegChunks * 256; c < chunks; c += 256) emit(buffer_load16(xr, c * 16), c);
+    for (int c0 = threadIdx.x + kRegChunks * T; c0 < chunks; c0 += 4 * T) {
+        v4i t[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) t[j] = buffer_load16(xr, c0 + j * T < chunks ? (c0 + j * T) * 16 : kOutOfRange);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (c0 + j * T < chunks) emit(t[j], c0 + j * T);
+    }
 }
 
 // Scalar path (any alignment, any column count): pass 1 = absmax + first
@@ -124,8 +139,8 @@ __device__ __forceinline__ void quantize_row_scalar(const QuantizeRowsArgs& a, f
 // list the output rows are input rows gather[r] / gather_div (the MoE's
 // routes in expert order: each route's codes and scale are its token's).
 extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_i8_kernel(QuantizeRowsArgs a) {
-    __shared__ float redf[4];
-    __shared__ int redi[4];
+    __shared__ float redf[16];
+    __shared__ int redi[16];
     if ((int64_t)blockIdx.x >= a.rows) return;
     if (!a.vec)
         quantize_row_scalar(a, redf, redi);

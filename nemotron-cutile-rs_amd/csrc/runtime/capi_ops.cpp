@@ -66,8 +66,13 @@ bool plan_decode(const nh_context* ctx, size_t m, size_t n, size_t k, DecodePlan
             *p = DecodePlan{kid, ntw, 64 * w * ntw, (size_t)kt * 64 * mm + (size_t)w * ntw * 1024 + (size_t)mm * 4};
             return true;
         };
+        const size_t cu = (size_t)ctx->cu_count;
         for (int ntw = 16 / w; ntw >= 1; ntw /= 2) {
-            if (ntw > 1 && (tiles + ntw - 1) / ntw < (size_t)ctx->cu_count) continue;
+            // one wide workgroup per CU at a time: whole rounds only (a
+            // partial second round costs a full one: 28.7 us at M = 8,
+            // 4096 -> 21504, 336 workgroups, against ~20 us in two launches)
+            const size_t wgs = (tiles + ntw - 1) / ntw;
+            if (ntw > 1 && (wgs < cu || (wgs % cu != 0 && wgs < 4 * cu))) continue;
             if (ntw == 1 && m <= 4) break;
             if (fits(ntw)) return wide(ntw);
         }
