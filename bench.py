@@ -309,7 +309,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["moe", "gemm", "stack", "decode"], default=None,
+    ap.add_argument("--only", choices=["moe", "gemm", "stack", "decode", "w8a32"], default=None,
                     help="run one secondary workload only (for profiling) and print its figures")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (torch's copy kernel), the "
@@ -341,6 +341,8 @@ def main():
             for (mm, nn, kk) in [(2048, 4096, 4096), (2048, 21504, 4096), (2048, 4096, 21504)]:
                 t, t_rm = b.gemm(mm, nn, kk, 20, 3)
                 res[f"m{mm}_n{nn}_k{kk}"] = {"us": round(t * 1e3, 1), "row_major_a_us": round(t_rm * 1e3, 1)}
+        elif args.only == "w8a32":
+            res = {"us": round(b.w8a32(4096, 4096, 200, 20) * 1e3, 2)}
         elif args.only == "stack":
             t, sbytes = b.decode_stack(20, 3)
             res = {"ms": round(t, 4), "GBps": round(sbytes / (t * 1e-3) / 1e9, 1)}

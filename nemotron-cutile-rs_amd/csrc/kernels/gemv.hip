@@ -414,26 +414,49 @@ extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_w8a8_m8_kern
 // it agrees with that path to a few f64 ulps before the final f32 rounding.
 // grid = (N tiles, ceil(M / 4)): a workgroup owns 16 weight rows and 4
 // activation rows; lane (r, g) dequantizes 16 weights of row r per K tile
-// and the f64 partial sums meet through shuffles and LDS.
-extern "C" __global__ __launch_bounds__(512) void nh_gemv_w8a32_kernel(GemvW8A32Args a) {
-    __shared__ double redd[8][4][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = a.waves;
+// and the f64 partial sums meet through shuffles and LDS.  Waves hold 4 K
+// tiles each (16 waves at K = 4096, four per SIMD, overlap their loads with
+// each other's f64 work: 7.5 us against 10.4 at 4 waves).  When the 4
+// activation rows fit (x_lds), they are loaded into LDS ahead of the
+// weights, once per workgroup, instead of per K tile behind the weight
+// slab.
+constexpr int kSlab32 = 4;
+
+extern "C" __global__ __launch_bounds__(1024) void nh_gemv_w8a32_kernel(GemvW8A32Args a) {
+    __shared__ double redd[16][4][64];
+    extern __shared__ __align__(16) int8_t xlds[];  // [4][K] f32 when x_lds
+    const int lane = threadIdx.x & 63, W = a.waves;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
     const int M = a.M, N = a.N, K = a.K, kt = a.kt;
     const int tile = blockIdx.x, m0 = blockIdx.y * 4;
     const __amdgpu_buffer_rsrc_t wr = row_tile_rsrc(a.wq, tile, kt);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)M * (uint32_t)K * 4u);
+    const float* xs = (const float*)xlds;
+    if (a.x_lds) {  // the 4 rows are contiguous: 1 KiB per direct-to-LDS load, ahead of the weights
+        const int bytes = 4 * K * 4;
+        for (int i = wave; i * 1024 < bytes; i += W)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t*)(xlds + i * 1024), 16,
+                                                     (uint32_t)m0 * (uint32_t)K * 4u + (uint32_t)(i * 1024 + lane * 16),
+                                                     0, 0, 0);
+    }
     const int n = tile * 16 + r16;
     const float s = n < N ? a.sw[n] : 0.0f;
     const int steps = (kt + W - 1) / W;
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    for (int s0 = 0; s0 < steps; s0 += kSlab) {
-        v4i b[kSlab];
-        __builtin_amdgcn_sched_barrier(0);
-        load_slab(b, wr, wave + s0 * W, W, lane);
+    for (int s0 = 0; s0 < steps; s0 += kSlab32) {
+        v4i b[kSlab32];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int st = 0; st < kSlab; ++st) {
+        for (int st = 0; st < kSlab32; ++st)
+            b[st] = buffer_load16_stream(wr, (wave + (s0 + st) * W) * 1024 + lane * 16);
+        __builtin_amdgcn_sched_barrier(0);
+        if (a.x_lds && s0 == 0) {
+            wait_vmcnt_le(kSlab32);  // this wave's activation loads are in (the slab stays in flight)
+            lds_barrier();           // ... and every wave's
+        }
+#pragma unroll
+        for (int st = 0; st < kSlab32; ++st) {
             const int k = (wave + (s0 + st) * W) * 64 + g * 16;
             if (k >= K) continue;
             float wv[16];
@@ -447,7 +470,8 @@ extern "C" __global__ __launch_bounds__(512) void nh_gemv_w8a32_kernel(GemvW8A32
                 if (m >= M) break;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const v4i xx = buffer_load16(xr, (m * K + k + 4 * q) * 4);
+                    const v4i xx = a.x_lds ? *(const v4i*)(xs + mm * K + k + 4 * q)
+                                           : buffer_load16(xr, (m * K + k + 4 * q) * 4);
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         // the f64 product of two f32 values is exact, so the fused

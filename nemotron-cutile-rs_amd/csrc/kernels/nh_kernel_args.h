@@ -97,7 +97,7 @@ struct GemvW8A32Args {
     int32_t M, N, K;
     int32_t kt;
     int32_t waves;
-    int32_t pad_;
+    int32_t x_lds;        // 1: the workgroup's 4 activation rows are staged in LDS (4 * K * 4 bytes)
 };
 
 // Row-major int8 [N][K] -> tiled, one 16-byte tile chunk per thread.

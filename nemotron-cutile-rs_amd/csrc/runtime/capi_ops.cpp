@@ -457,8 +457,11 @@ nh_status nh_gemv_w8a32(nh_context* ctx, const float* x, const int8_t* wq, const
         return set_error(err, NH_UNSUPPORTED, "device W8A32 GEMV needs m <= 262140 and m * k * 4 < 2^32");
     GemvW8A32Args a{x, wq, sw, y, (int)m, (int)n, (int)k, 0, 0, 0};
     a.kt = (int)tiled_k_tiles(k);
-    a.waves = gemv_waves(a.kt);
-    return launch(ctx, K_GEMV_W8A32, (unsigned)((n + 15) / 16), 64u * a.waves, 0, stream, a, err,
+    a.waves = std::max(1, std::min(16, (a.kt + 3) / 4));  // 4 K tiles per wave and slab
+    // activation rows in LDS when 4 of them fit in 64 KiB (x is 16-byte aligned and K % 16 == 0)
+    const size_t xbytes = (size_t)4 * k * 4;
+    a.x_lds = xbytes <= 65536 ? 1 : 0;
+    return launch(ctx, K_GEMV_W8A32, (unsigned)((n + 15) / 16), 64u * a.waves, a.x_lds ? xbytes : 0, stream, a, err,
                   (unsigned)((m + 3) / 4));
 }
 

@@ -398,7 +398,7 @@ def test_linear_decode_unit_rounding_ties(ctx, m):
 
 
 # ---- G2: W8A32 dequant GEMV ------------------------------------
-@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (2, 1000, 80)])
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (2, 1000, 80), (5, 300, 1040), (3, 64, 20480)])
 def test_gemv_w8a32_within_tolerance(ctx, m, n, k):
     note(f"gemv_w8a32 m={m} n={n} k={k}")
     _, wq, sw = quantized_weights(n, k)
