@@ -250,21 +250,24 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(Gro
 
 // R3 for the MoE layer (A in slot order).  One workgroup per (expert, half
 // of its N tiles): the chip runs one of them per CU in a single round.  The
-// expert's routed rows are staged once per pass of up to 32 slots into LDS
-// as 1 KiB MFMA A tiles (direct-to-LDS loads, lane l fetching row l % 16,
-// bytes 16 (l / 16) of its 64-byte K tile, so the fragment reads are linear),
-// and stay there while the workgroup streams its N tiles: `streams` tiles at
-// a time, each split over `waves` K waves that hold 16 K tiles of weights in
-// registers.  A wave issues the next tile's weights right after its MFMAs,
-// so its stream keeps going under the reduction and the epilogue (the
-// one-tile-per-workgroup kernel above streamed only between its start and
-// its first MFMA).  Measured per MoE layer: 406 vs 425 us.  12 waves with
-// one slab each beat 6-8 waves with two (double-buffered: 226 / 210 us per
-// projection against 172 us on average).  The K waves of a tile meet through LDS; the barriers are
-// bare (the next weights stay in flight).  A segment longer than 32 slots
-// takes several passes, each streaming the expert's tiles again (rare: the
-// mean is 24 slots).
+// expert's routed rows are staged once per pass of up to 16 * row_blocks
+// slots into LDS as 1 KiB MFMA A tiles (direct-to-LDS loads, lane l fetching
+// row l % 16, bytes 16 (l / 16) of its 64-byte K tile, so the fragment reads
+// are linear), and stay there while the workgroup streams its N tiles:
+// `streams` tiles at a time, each split over `waves` K waves that hold 16 K
+// tiles of weights in registers.  A wave issues the next tile's weights right
+// after its MFMAs, so its stream keeps going under the reduction and the
+// epilogue.  12 waves with one slab each beat 6-8 waves with two
+// (double-buffered: 226 / 210 us per projection).  The K waves of a tile meet
+// through LDS (only the waves past the first write partial sums); the
+// barriers are bare (the next weights stay in flight).
+// The host sizes row_blocks to fill the LDS (3 at K = 2688, 4 at K = 1856):
+// every pass re-streams the expert's weights, and since all workgroups run
+// in one round the layer waits for its longest segment.  With 32-slot
+// passes, the 6 of 128 experts holding 33-40 of the 3072 routes took two
+// passes and doubled the projection time.
 extern "C" __global__ __launch_bounds__(768) void nh_moe_expert_gemm_kernel(ExpertGemmArgs a) {
+    constexpr int kMaxRb = 4;
     extern __shared__ __align__(16) int8_t lds[];
     const int e = blockIdx.y;
     const int seg0 = a.offsets[e], seg1 = a.offsets[e + 1];
@@ -275,13 +278,15 @@ extern "C" __global__ __launch_bounds__(768) void nh_moe_expert_gemm_kernel(Expe
     const int st = wave / W, kw = wave - st * W;
     const int r16 = lane & 15, g = lane >> 4;
     const int N = a.N, K = a.K, kt = a.kt;
+    const int RB = a.row_blocks, cap = 16 * RB;
     const int ntiles = (N + 15) / 16;
     const int t_begin = blockIdx.x * a.tiles_per_wg;
     const int t_end = min(t_begin + a.tiles_per_wg, ntiles);
     if (t_begin >= t_end) return;  // uniform
     const int n_it = (t_end - t_begin + NS - 1) / NS;
-    int8_t* As = lds;                                  // [2][kt] A tiles
-    v4i* red = (v4i*)(lds + 2 * kt * 1024);            // [NW][2][64]
+    int8_t* As = lds;                                  // [RB][kt] A tiles
+    v4i* red = (v4i*)(lds + RB * kt * 1024);           // [NS][W - 1][RB][64] partial sums
+    float* sas = (float*)(red + NS * (W - 1) * RB * 64);  // [16 RB] the pass's row scales
     const int8_t* wexp = a.w + (int64_t)e * tiled_bytes(N, K);
     const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.aq, (uint32_t)a.a_rows * (uint32_t)K);
     auto tile_rsrc = [&](int t) {
@@ -293,8 +298,8 @@ extern "C" __global__ __launch_bounds__(768) void nh_moe_expert_gemm_kernel(Expe
 #pragma unroll
         for (int s = 0; s < kGroupedSteps; ++s) b[s] = buffer_load16_stream(wr, (kw + s * W) * 1024 + lane * 16);
     };
-    for (int p0 = seg0; p0 < seg1; p0 += 32) {
-        const int nrb = min(32, seg1 - p0) > 16 ? 2 : 1;  // uniform
+    for (int p0 = seg0; p0 < seg1; p0 += cap) {
+        const int nrb = (min(cap, seg1 - p0) + 15) / 16;  // uniform
         // 1. the pass's A tiles, then the first tile's weights
         __builtin_amdgcn_sched_barrier(0);
         for (int i = wave; i < nrb * kt; i += NW) {
@@ -304,57 +309,58 @@ extern "C" __global__ __launch_bounds__(768) void nh_moe_expert_gemm_kernel(Expe
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_void_t*)(As + i * 1024), 16,
                                                      slot < seg1 ? off : (uint32_t)kOutOfRange, 0, 0, 0);
         }
-        float sa[2][4];
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int slot = p0 + rb * 16 + 4 * g + r;
-                sa[rb][r] = slot < seg1 ? a.sa[slot] : 0.0f;
-            }
+        float sav = 0.0f;
+        if ((int)threadIdx.x < cap && p0 + (int)threadIdx.x < seg1) sav = a.sa[p0 + threadIdx.x];
         __builtin_amdgcn_sched_barrier(0);
         load_weights(t_begin + st);
         __builtin_amdgcn_sched_barrier(0);
         wait_vmcnt_le(kGroupedSteps);  // this wave's A loads are in (the weights stay in flight)
-        lds_barrier();                 // ... and every wave's
+        if ((int)threadIdx.x < cap) sas[threadIdx.x] = sav;  // read after the first lds_publish below
+        lds_barrier();                 // every wave's A loads are in
         for (int it = 0; it < n_it; ++it) {
             const int t = t_begin + st + it * NS;
             const int n = t * 16 + r16;
             const float swn = (t < t_end && n < N) ? a.sw[(int64_t)e * N + n] : 0.0f;
             // 2. MFMAs of this tile (A from LDS; K tiles past kt meet zero weights)
-            v4i acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+            v4i acc[kMaxRb];
 #pragma unroll
-            for (int s = 0; s < kGroupedSteps; ++s) {
-                const int tt = kw + s * W;
-                const int8_t* at = As + (tt < kt ? tt : 0) * 1024 + lane * 16;
-                acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const v4i*)at, b[s], acc[0], 0, 0, 0);
-                if (nrb > 1)
-                    acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const v4i*)(at + kt * 1024), b[s], acc[1], 0, 0,
-                                                                   0);
+            for (int rb = 0; rb < kMaxRb; ++rb) acc[rb] = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int rb = 0; rb < kMaxRb; ++rb) {
+                if (rb >= nrb) break;
+#pragma unroll
+                for (int s = 0; s < kGroupedSteps; ++s) {
+                    const int tt = kw + s * W;
+                    acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        *(const v4i*)(As + (rb * kt + (tt < kt ? tt : 0)) * 1024 + lane * 16), b[s], acc[rb], 0, 0, 0);
+                }
             }
             // 3. the next tile's weights, then the reduction and the epilogue under them
             if (it + 1 < n_it) load_weights(t + NS);
+            if (kw > 0) {
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb) red[(wave * 2 + rb) * 64 + lane] = acc[rb];
+                for (int rb = 0; rb < kMaxRb; ++rb)
+                    if (rb < nrb) red[((st * (W - 1) + kw - 1) * RB + rb) * 64 + lane] = acc[rb];
+            }
             lds_publish();
             if (kw == 0 && t < t_end && n < N) {
 #pragma unroll
-                for (int rb = 0; rb < 2; ++rb) {
+                for (int rb = 0; rb < kMaxRb; ++rb) {
                     if (rb >= nrb) break;
                     v4i sum = acc[rb];
-                    for (int w = 1; w < W; ++w) sum += red[((wave + w) * 2 + rb) * 64 + lane];
+                    for (int w = 1; w < W; ++w) sum += red[((st * (W - 1) + w - 1) * RB + rb) * 64 + lane];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int slot = p0 + rb * 16 + 4 * g + r;
                         if (slot < seg1) {
-                            float y = epilogue_w8a8(sum[r], sa[rb][r], swn);
+                            float y = epilogue_w8a8(sum[r], sas[rb * 16 + 4 * g + r], swn);
                             if (a.relu2) y = relu2(y);
                             a.out[(int64_t)slot * N + n] = y;
                         }
                     }
                 }
             }
-            lds_publish();  // red is rewritten by the next tile
+            lds_publish();  // red and, after the last tile, As and sas are rewritten next
         }
     }
 }

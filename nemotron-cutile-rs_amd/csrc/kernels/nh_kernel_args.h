@@ -188,6 +188,7 @@ struct ExpertGemmArgs {
     int32_t a_rows;          // R
     int32_t waves, streams, tiles_per_wg;
     int32_t relu2;
+    int32_t row_blocks;      // 16-row blocks of A staged per pass (1..4)
 };
 
 // R4: scatter-combine.

@@ -551,6 +551,32 @@ def test_moe_stages_bit_exact(ctx, tokens, hidden, inter, experts, top_k):
     assert np.array_equal(out.numpy(), O.moe_combine(d_ref, pos, w, tokens, top_k, hidden, out_bf16=True))
 
 
+@pytest.mark.parametrize("n,k", [(1856, 2688), (2688, 1856), (40, 64)])
+def test_expert_gemm_long_segments_bit_exact(ctx, n, k):
+    """Slot-ordered grouped GEMM (the MoE layer's expert-block kernel) with
+    segments around every pass boundary: a pass stages 48 rows at K = 2688,
+    64 at K = 1856, 64 at K = 64, and longer segments take several passes."""
+    note(f"expert gemm long segments n={n} k={k}")
+    counts = [0, 1, 17, 33, 47, 48, 49, 64, 65, 100, 130, 0, 16]
+    experts = len(counts)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    R = int(offsets[-1])
+    rng = np.random.default_rng(n + k)
+    aq = rng.integers(-127, 128, size=(R, k), dtype=np.int8)
+    sa = rng.uniform(1e-3, 2e-2, size=R).astype(np.float32)
+    w = rng.integers(-127, 128, size=(experts, n, k), dtype=np.int8)
+    sw = rng.uniform(1e-4, 1e-3, size=(experts, n)).astype(np.float32)
+    perm = np.arange(R, dtype=np.int32)
+    for relu2 in (0, 1):
+        ref = O.moe_grouped(aq, sa, False, 1, offsets, perm, w, sw, relu2=relu2)
+        d = {nm: ctx.upload(a) for nm, a in dict(aq=aq, sa=sa, off=offsets, perm=perm, w=tile_experts(w), sw=sw).items()}
+        out = ctx.empty((R, n), np.float32)
+        NH.call("nh_moe_grouped_gemm_w8a8", ctx.handle, d["aq"].ptr, d["sa"].ptr, 0, 1, d["off"].ptr, d["perm"].ptr,
+                R, R, experts, d["w"].ptr, d["sw"].ptr, n, k, relu2, out.ptr, None)
+        ctx.synchronize()
+        assert np.array_equal(out.numpy(), ref)
+
+
 @pytest.mark.parametrize("tokens,hidden,inter,experts,top_k", [(64, 2688, 1856, 128, 6), (13, 64, 32, 8, 3)])
 def test_moe_forward_bit_exact(ctx, tokens, hidden, inter, experts, top_k):
     note(f"moe forward t={tokens} h={hidden} i={inter} e={experts} k={top_k}")
