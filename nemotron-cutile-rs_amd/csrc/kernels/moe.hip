@@ -253,14 +253,13 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(Gro
 // expert's routed rows are staged once per pass of up to 16 * row_blocks
 // slots into LDS as 1 KiB MFMA A tiles (direct-to-LDS loads, lane l fetching
 // row l % 16, bytes 16 (l / 16) of its 64-byte K tile, so the fragment reads
-// are linear), and stay there while the workgroup streams its N tiles:
-// `streams` tiles at a time, each split over `waves` K waves that hold 16 K
-// tiles of weights in registers.  A wave issues the next tile's weights right
-// after its MFMAs, so its stream keeps going under the reduction and the
-// epilogue.  12 waves with one slab each beat 6-8 waves with two
-// (double-buffered: 226 / 210 us per projection).  The K waves of a tile meet
-// through LDS (only the waves past the first write partial sums); the
-// barriers are bare (the next weights stay in flight).
+// are linear), and stay there while the waves stream the weights.  Every
+// wave owns whole N tiles (t_begin + wave, + waves, ...) and walks each
+// one's K range in chunks of 16 K tiles held in registers: after a chunk's
+// MFMAs it issues the next chunk (of the same tile or of its next one) and,
+// at a tile's end, writes the tile's outputs itself.  No partial sums cross
+// waves, so a pass has no barrier between its staging and its end, and the
+// waves drift apart like independent streams (12 x 16 KiB in flight per CU).
 // The host sizes row_blocks to fill the LDS (3 at K = 2688, 4 at K = 1856):
 // every pass re-streams the expert's weights, and since all workgroups run
 // in one round the layer waits for its longest segment.  With 32-slot
@@ -268,39 +267,39 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(Gro
 // passes and doubled the projection time.
 extern "C" __global__ __launch_bounds__(768) void nh_moe_expert_gemm_kernel(ExpertGemmArgs a) {
     constexpr int kMaxRb = 4;
+    constexpr int kChunk = 16;  // K tiles per register slab
     extern __shared__ __align__(16) int8_t lds[];
     const int e = blockIdx.y;
     const int seg0 = a.offsets[e], seg1 = a.offsets[e + 1];
     if (seg0 >= seg1) return;  // no routes: the expert's weights are never read
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int W = a.waves, NS = a.streams, NW = W * NS;
-    const int st = wave / W, kw = wave - st * W;
+    const int NW = a.streams;
     const int r16 = lane & 15, g = lane >> 4;
     const int N = a.N, K = a.K, kt = a.kt;
+    const int nch = (kt + kChunk - 1) / kChunk;
     const int RB = a.row_blocks, cap = 16 * RB;
     const int ntiles = (N + 15) / 16;
     const int t_begin = blockIdx.x * a.tiles_per_wg;
     const int t_end = min(t_begin + a.tiles_per_wg, ntiles);
     if (t_begin >= t_end) return;  // uniform
-    const int n_it = (t_end - t_begin + NS - 1) / NS;
-    int8_t* As = lds;                                  // [RB][kt] A tiles
-    v4i* red = (v4i*)(lds + RB * kt * 1024);           // [NS][W - 1][RB][64] partial sums
-    float* sas = (float*)(red + NS * (W - 1) * RB * 64);  // [16 RB] the pass's row scales
+    const int my_tiles = t_begin + wave < t_end ? (t_end - t_begin - wave + NW - 1) / NW : 0;
+    const int nj = my_tiles * nch;  // this wave's chunks
+    int8_t* As = lds;                                // [RB][kt] A tiles
+    float* sas = (float*)(lds + RB * kt * 1024);     // [16 RB] the pass's row scales
     const int8_t* wexp = a.w + (int64_t)e * tiled_bytes(N, K);
     const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.aq, (uint32_t)a.a_rows * (uint32_t)K);
-    auto tile_rsrc = [&](int t) {
-        return t < t_end ? make_rsrc(wexp + (int64_t)t * kt * 1024, (uint32_t)kt * 1024u) : make_rsrc(wexp, 0);
-    };
-    v4i b[kGroupedSteps];
-    auto load_weights = [&](int t) {
-        const __amdgpu_buffer_rsrc_t wr = tile_rsrc(t);
+    v4i b[kChunk];
+    auto load_chunk = [&](int j) {  // j < nj: tile t_begin + wave + (j / nch) NW < t_end
+        const int t = t_begin + wave + (j / nch) * NW, k0 = (j % nch) * kChunk;
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(wexp + (int64_t)t * kt * 1024, (uint32_t)kt * 1024u);
 #pragma unroll
-        for (int s = 0; s < kGroupedSteps; ++s) b[s] = buffer_load16_stream(wr, (kw + s * W) * 1024 + lane * 16);
+        for (int s = 0; s < kChunk; ++s)
+            b[s] = buffer_load16_stream(wr, k0 + s < kt ? (k0 + s) * 1024 + lane * 16 : (int)kOutOfRange);
     };
     for (int p0 = seg0; p0 < seg1; p0 += cap) {
         const int nrb = (min(cap, seg1 - p0) + 15) / 16;  // uniform
-        // 1. the pass's A tiles, then the first tile's weights
+        // 1. the pass's A tiles and row scales, then this wave's first chunk
         __builtin_amdgcn_sched_barrier(0);
         for (int i = wave; i < nrb * kt; i += NW) {
             const int rb = i / kt, t = i - rb * kt;
@@ -312,56 +311,53 @@ extern "C" __global__ __launch_bounds__(768) void nh_moe_expert_gemm_kernel(Expe
         float sav = 0.0f;
         if ((int)threadIdx.x < cap && p0 + (int)threadIdx.x < seg1) sav = a.sa[p0 + threadIdx.x];
         __builtin_amdgcn_sched_barrier(0);
-        load_weights(t_begin + st);
+        if (nj > 0) load_chunk(0);
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt_le(kGroupedSteps);  // this wave's A loads are in (the weights stay in flight)
-        if ((int)threadIdx.x < cap) sas[threadIdx.x] = sav;  // read after the first lds_publish below
-        lds_barrier();                 // every wave's A loads are in
-        for (int it = 0; it < n_it; ++it) {
-            const int t = t_begin + st + it * NS;
-            const int n = t * 16 + r16;
-            const float swn = (t < t_end && n < N) ? a.sw[(int64_t)e * N + n] : 0.0f;
-            // 2. MFMAs of this tile (A from LDS; K tiles past kt meet zero weights)
-            v4i acc[kMaxRb];
+        if (nj > 0) wait_vmcnt_le(kChunk); else wait_vmcnt_le(0);  // A and scale loads in, weights in flight
+        if ((int)threadIdx.x < cap) sas[threadIdx.x] = sav;
+        lds_publish();  // every wave's A tiles and the scales
+        v4i acc[kMaxRb];
+        float swn = 0.0f;
+        int n = 0;
+        for (int j = 0; j < nj; ++j) {
+            const int c = j % nch;
+            const int t = t_begin + wave + (j / nch) * NW;
+            if (c == 0) {
 #pragma unroll
-            for (int rb = 0; rb < kMaxRb; ++rb) acc[rb] = v4i{0, 0, 0, 0};
+                for (int rb = 0; rb < kMaxRb; ++rb) acc[rb] = v4i{0, 0, 0, 0};
+                n = t * 16 + r16;
+                swn = n < N ? a.sw[(int64_t)e * N + n] : 0.0f;
+            }
+            // 2. the chunk's MFMAs (K tiles past kt met zero weights and are skipped)
+            const int k0 = c * kChunk;
 #pragma unroll
             for (int rb = 0; rb < kMaxRb; ++rb) {
                 if (rb >= nrb) break;
 #pragma unroll
-                for (int s = 0; s < kGroupedSteps; ++s) {
-                    const int tt = kw + s * W;
-                    acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                        *(const v4i*)(As + (rb * kt + (tt < kt ? tt : 0)) * 1024 + lane * 16), b[s], acc[rb], 0, 0, 0);
-                }
+                for (int s = 0; s < kChunk; ++s)
+                    if (k0 + s < kt)
+                        acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            *(const v4i*)(As + (rb * kt + k0 + s) * 1024 + lane * 16), b[s], acc[rb], 0, 0, 0);
             }
-            // 3. the next tile's weights, then the reduction and the epilogue under them
-            if (it + 1 < n_it) load_weights(t + NS);
-            if (kw > 0) {
-#pragma unroll
-                for (int rb = 0; rb < kMaxRb; ++rb)
-                    if (rb < nrb) red[((st * (W - 1) + kw - 1) * RB + rb) * 64 + lane] = acc[rb];
-            }
-            lds_publish();
-            if (kw == 0 && t < t_end && n < N) {
+            // 3. the next chunk in flight, then the tile's outputs under it
+            if (j + 1 < nj) load_chunk(j + 1);
+            if (c == nch - 1 && n < N) {
 #pragma unroll
                 for (int rb = 0; rb < kMaxRb; ++rb) {
                     if (rb >= nrb) break;
-                    v4i sum = acc[rb];
-                    for (int w = 1; w < W; ++w) sum += red[((st * (W - 1) + w - 1) * RB + rb) * 64 + lane];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int slot = p0 + rb * 16 + 4 * g + r;
                         if (slot < seg1) {
-                            float y = epilogue_w8a8(sum[r], sas[rb * 16 + 4 * g + r], swn);
+                            float y = epilogue_w8a8(acc[rb][r], sas[rb * 16 + 4 * g + r], swn);
                             if (a.relu2) y = relu2(y);
                             a.out[(int64_t)slot * N + n] = y;
                         }
                     }
                 }
             }
-            lds_publish();  // red and, after the last tile, As and sas are rewritten next
         }
+        lds_publish();  // the pass's A and scale reads are done before the next pass restages them
     }
 }
 

@@ -175,8 +175,8 @@ struct GroupedGemmArgs {
 
 // R3, the MoE layer's form: A already in slot (expert) order.  grid =
 // (wgs_per_expert, experts); workgroup (nb, e) owns expert e's N tiles
-// [nb * tiles_per_wg, +tiles_per_wg) with `streams` tiles in flight, each
-// split over `waves` K waves (blockDim = 64 * waves * streams).
+// [nb * tiles_per_wg, +tiles_per_wg), dealt to its `streams` waves
+// (blockDim = 64 * streams), each wave computing whole tiles.
 struct ExpertGemmArgs {
     const int8_t* aq;        // [R][K] codes in slot order
     const float* sa;         // [R]
@@ -186,7 +186,9 @@ struct ExpertGemmArgs {
     float* out;              // [R][N]
     int32_t N, K, kt;
     int32_t a_rows;          // R
-    int32_t waves, streams, tiles_per_wg;
+    int32_t waves;           // unused (1)
+    int32_t streams;         // waves per workgroup, each streaming its own N tiles
+    int32_t tiles_per_wg;
     int32_t relu2;
     int32_t row_blocks;      // 16-row blocks of A staged per pass (1..4)
 };

@@ -509,21 +509,17 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
     if ((st = bind_device(ctx, err))) return st;
     if (routes == 0) return NH_OK;
     const int kt = (int)tiled_k_tiles(k);
-    const int w_k = (kt + 15) / 16;  // K waves per N tile: one 16-tile slab each
     if (!gather) {
         // slot-ordered A: the expert-block kernel (A staged once per pass in
-        // LDS, N tiles streamed), two workgroups per expert.  A pass stages as
-        // many 16-row blocks (up to 4) as the LDS holds next to the partial
-        // sums of the K waves past the first and the pass's row scales: every
-        // pass re-streams the expert's weights.
-        const int streams = w_k <= 12 ? 12 / w_k : 0;  // up to 12 waves (the kernel's register budget)
-        auto expert_lds = [&](int rb) {
-            return (size_t)rb * kt * 1024 + (size_t)streams * (w_k - 1) * rb * 1024 + (size_t)rb * 16 * 4;
-        };
+        // LDS, 12 waves streaming whole N tiles), two workgroups per expert.
+        // A pass stages as many 16-row blocks (up to 4) as the LDS holds next
+        // to the pass's row scales: every pass re-streams the expert's weights.
+        constexpr int kExpertWaves = 12;
+        auto expert_lds = [&](int rb) { return (size_t)rb * kt * 1024 + (size_t)rb * 16 * 4; };
         int row_blocks = 4;
         while (row_blocks > 1 && expert_lds(row_blocks) > ctx->max_shared_per_block) --row_blocks;
         const size_t lds = expert_lds(row_blocks);
-        if (streams > 0 && lds <= ctx->max_shared_per_block) {
+        if (lds <= ctx->max_shared_per_block) {
             ExpertGemmArgs e{};
             e.aq = aq;
             e.sa = sa;
@@ -535,13 +531,13 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
             e.K = (int)k;
             e.kt = kt;
             e.a_rows = (int)a_rows;
-            e.waves = w_k;
-            e.streams = streams;
+            e.waves = 1;
+            e.streams = kExpertWaves;
             const int ntiles = (int)((n + 15) / 16);
             e.tiles_per_wg = (ntiles + 1) / 2;
             e.relu2 = relu2 ? 1 : 0;
             e.row_blocks = row_blocks;
-            return launch(ctx, K_EXPERT_GEMM, 2u, (unsigned)(64 * e.waves * e.streams), lds, stream, e, err,
+            return launch(ctx, K_EXPERT_GEMM, 2u, (unsigned)(64 * kExpertWaves), lds, stream, e, err,
                           (unsigned)experts);
         }
     }
