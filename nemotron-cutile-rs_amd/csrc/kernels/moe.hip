@@ -253,21 +253,98 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(Gro
 // expert's routed rows are staged once per pass of up to 16 * row_blocks
 // slots into LDS as 1 KiB MFMA A tiles (direct-to-LDS loads, lane l fetching
 // row l % 16, bytes 16 (l / 16) of its 64-byte K tile, so the fragment reads
-// are linear), and stay there while the waves stream the weights.  Every
-// wave owns whole N tiles (t_begin + wave, + waves, ...) and walks each
-// one's K range in chunks of 16 K tiles held in registers: after a chunk's
-// MFMAs it issues the next chunk (of the same tile or of its next one) and,
-// at a tile's end, writes the tile's outputs itself.  No partial sums cross
-// waves, so a pass has no barrier between its staging and its end, and the
-// waves drift apart like independent streams (12 x 16 KiB in flight per CU).
+// are linear), and stay there while the 8 waves stream the weights.  Every
+// wave owns whole N tiles (t_begin + wave, + 8, ...) and walks each one's K
+// range in chunks of 8 K tiles held in two register slabs in ping-pong:
+// while one chunk's MFMAs run, the next chunk is in flight, and a slab is
+// refilled (with the chunk after next, of the same tile or of the wave's
+// next one) as soon as its MFMAs are issued.  At a tile's end the wave
+// writes the tile's outputs itself.  No partial sums cross waves, so a pass
+// has no barrier between its staging and its end, and the waves drift apart
+// like independent streams.  Measured per projection (bench routing): 120
+// us; the same loads alone stream the 638 MB in 91 us, and most of the rest
+// is the output rows' write-back mixed into the stream (stores aimed at a
+// few L2-resident rows instead: 102 us).  The weight scales sit in LDS: a
+// global load in the epilogue made every wave wait for its weights in
+// flight (the compiler cannot count that load's place in the queue).
 // The host sizes row_blocks to fill the LDS (3 at K = 2688, 4 at K = 1856):
 // every pass re-streams the expert's weights, and since all workgroups run
 // in one round the layer waits for its longest segment.  With 32-slot
 // passes, the 6 of 128 experts holding 33-40 of the 3072 routes took two
 // passes and doubled the projection time.
-extern "C" __global__ __launch_bounds__(768) void nh_moe_expert_gemm_kernel(ExpertGemmArgs a) {
-    constexpr int kMaxRb = 4;
-    constexpr int kChunk = 16;  // K tiles per register slab
+constexpr int kExpertSlab = 8;  // K tiles per register slab (two slabs in ping-pong)
+
+// The waves' tile streams of one pass over NRB row blocks.  Straight-line
+// per chunk (every load issued, past the wave's last chunk from an empty
+// buffer; K tiles past kt load zeros and meet a valid A tile), so the
+// compiler's wait counts see the slabs in flight and wait for one slab only.
+template <int NRB>
+__device__ __forceinline__ void expert_stream(const ExpertGemmArgs& a, v4i (&b0)[kExpertSlab],
+                                              v4i (&b1)[kExpertSlab], const int8_t* As, const float* sas,
+                                              const float* sws, const int8_t* wexp, int wave, int lane, int t_begin,
+                                              int nj, int nch, int p0, int seg1) {
+    const int N = a.N, kt = a.kt, NW = a.streams;
+    const int r16 = lane & 15, g = lane >> 4;
+    auto load_chunk = [&](v4i (&b)[kExpertSlab], int j) {
+        const int t = t_begin + wave + (j / nch) * NW, k0 = (j % nch) * kExpertSlab;
+        const __amdgpu_buffer_rsrc_t wr =
+            j < nj ? make_rsrc(wexp + (int64_t)t * kt * 1024, (uint32_t)kt * 1024u) : make_rsrc(wexp, 0);
+#pragma unroll
+        for (int s = 0; s < kExpertSlab; ++s) b[s] = buffer_load16_stream(wr, (k0 + s) * 1024 + lane * 16);
+    };
+    v4i acc[NRB];
+    auto process = [&](const v4i (&b)[kExpertSlab], int j) {
+        const int c = j % nch, k0 = c * kExpertSlab;
+        if (c == 0) {
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb) acc[rb] = v4i{0, 0, 0, 0};
+        }
+        // A fragments one K tile ahead of the MFMAs (the order pinned, so the
+        // fragment reads do not pile up in registers)
+        v4i af[2][NRB];
+        auto read_a = [&](v4i (&f)[NRB], int s) {
+            const int kk = k0 + s < kt ? k0 + s : 0;
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb) f[rb] = *(const v4i*)(As + (rb * kt + kk) * 1024 + lane * 16);
+        };
+        read_a(af[0], 0);
+#pragma unroll
+        for (int s = 0; s < kExpertSlab; ++s) {
+            if (s + 1 < kExpertSlab) read_a(af[(s + 1) & 1], s + 1);
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb)
+                acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[s & 1][rb], b[s], acc[rb], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        const int n = (t_begin + wave + (j / nch) * NW) * 16 + r16;
+        if (c == nch - 1 && n < N) {
+            const float swn = sws[n - t_begin * 16];
+            // one per-lane base (row p0 + 4 g, column n); rows rb * 16 + r are uniform offsets
+            float* ob = a.out + (int64_t)(p0 + 4 * g) * N + n;
+            const int rows = seg1 - p0 - 4 * g;  // rows of this lane's group in the pass
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (rb * 16 + r < rows) {
+                        float y = epilogue_w8a8(acc[rb][r], sas[rb * 16 + 4 * g + r], swn);
+                        if (a.relu2) y = relu2(y);
+                        ob[(rb * 16 + r) * N] = y;
+                    }
+        }
+    };
+    // chunks in pairs: while one slab's MFMAs run, the other is in flight
+    // (a chunk past nj has zero weights and writes nothing: its tile is past
+    // the wave's last)
+    for (int j = 0; j < nj; j += 2) {
+        process(b0, j);
+        load_chunk(b0, j + 2);
+        process(b1, j + 1);
+        load_chunk(b1, j + 3);
+    }
+}
+
+extern "C" __global__ __launch_bounds__(512) void nh_moe_expert_gemm_kernel(ExpertGemmArgs a) {
     extern __shared__ __align__(16) int8_t lds[];
     const int e = blockIdx.y;
     const int seg0 = a.offsets[e], seg1 = a.offsets[e + 1];
@@ -277,7 +354,7 @@ extern "C" __global__ __launch_bounds__(768) void nh_moe_expert_gemm_kernel(Expe
     const int NW = a.streams;
     const int r16 = lane & 15, g = lane >> 4;
     const int N = a.N, K = a.K, kt = a.kt;
-    const int nch = (kt + kChunk - 1) / kChunk;
+    const int nch = (kt + kExpertSlab - 1) / kExpertSlab;
     const int RB = a.row_blocks, cap = 16 * RB;
     const int ntiles = (N + 15) / 16;
     const int t_begin = blockIdx.x * a.tiles_per_wg;
@@ -285,21 +362,19 @@ extern "C" __global__ __launch_bounds__(768) void nh_moe_expert_gemm_kernel(Expe
     if (t_begin >= t_end) return;  // uniform
     const int my_tiles = t_begin + wave < t_end ? (t_end - t_begin - wave + NW - 1) / NW : 0;
     const int nj = my_tiles * nch;  // this wave's chunks
+    const int nw_cols = min(t_end * 16, N) - t_begin * 16;  // this workgroup's weight rows
     int8_t* As = lds;                                // [RB][kt] A tiles
     float* sas = (float*)(lds + RB * kt * 1024);     // [16 RB] the pass's row scales
+    float* sws = sas + 16 * RB;                      // [16 tiles_per_wg] the workgroup's weight scales
+    const __amdgpu_buffer_rsrc_t swr = make_rsrc(a.sw + (int64_t)e * N + t_begin * 16, (uint32_t)nw_cols * 4u);
     const int8_t* wexp = a.w + (int64_t)e * tiled_bytes(N, K);
     const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.aq, (uint32_t)a.a_rows * (uint32_t)K);
-    v4i b[kChunk];
-    auto load_chunk = [&](int j) {  // j < nj: tile t_begin + wave + (j / nch) NW < t_end
-        const int t = t_begin + wave + (j / nch) * NW, k0 = (j % nch) * kChunk;
-        const __amdgpu_buffer_rsrc_t wr = make_rsrc(wexp + (int64_t)t * kt * 1024, (uint32_t)kt * 1024u);
-#pragma unroll
-        for (int s = 0; s < kChunk; ++s)
-            b[s] = buffer_load16_stream(wr, k0 + s < kt ? (k0 + s) * 1024 + lane * 16 : (int)kOutOfRange);
-    };
+    v4i b0[kExpertSlab], b1[kExpertSlab];
     for (int p0 = seg0; p0 < seg1; p0 += cap) {
         const int nrb = (min(cap, seg1 - p0) + 15) / 16;  // uniform
-        // 1. the pass's A tiles and row scales, then this wave's first chunk
+        // 1. the pass's A tiles, the weight scales (straight to LDS: a global
+        //    load in the epilogue would make the wave wait for its weight
+        //    loads in flight) and the row scales, then this wave's first two chunks
         __builtin_amdgcn_sched_barrier(0);
         for (int i = wave; i < nrb * kt; i += NW) {
             const int rb = i / kt, t = i - rb * kt;
@@ -308,54 +383,32 @@ extern "C" __global__ __launch_bounds__(768) void nh_moe_expert_gemm_kernel(Expe
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_void_t*)(As + i * 1024), 16,
                                                      slot < seg1 ? off : (uint32_t)kOutOfRange, 0, 0, 0);
         }
+        for (int i = wave * 64; i < nw_cols; i += NW * 64)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(swr, (lds_void_t*)(sws + i), 4, (uint32_t)(i + lane) * 4u, 0, 0,
+                                                     0);
         float sav = 0.0f;
         if ((int)threadIdx.x < cap && p0 + (int)threadIdx.x < seg1) sav = a.sa[p0 + threadIdx.x];
         __builtin_amdgcn_sched_barrier(0);
-        if (nj > 0) load_chunk(0);
+        {
+            auto first = [&](v4i (&b)[kExpertSlab], int j) {
+                const int t = t_begin + wave + (j / nch) * NW, k0 = (j % nch) * kExpertSlab;
+                const __amdgpu_buffer_rsrc_t wr =
+                    j < nj ? make_rsrc(wexp + (int64_t)t * kt * 1024, (uint32_t)kt * 1024u) : make_rsrc(wexp, 0);
+#pragma unroll
+                for (int s = 0; s < kExpertSlab; ++s) b[s] = buffer_load16_stream(wr, (k0 + s) * 1024 + lane * 16);
+            };
+            first(b0, 0);
+            first(b1, 1);
+        }
         __builtin_amdgcn_sched_barrier(0);
-        if (nj > 0) wait_vmcnt_le(kChunk); else wait_vmcnt_le(0);  // A and scale loads in, weights in flight
+        wait_vmcnt_le(2 * kExpertSlab);  // A and scale loads in, weights in flight
         if ((int)threadIdx.x < cap) sas[threadIdx.x] = sav;
         lds_publish();  // every wave's A tiles and the scales
-        v4i acc[kMaxRb];
-        float swn = 0.0f;
-        int n = 0;
-        for (int j = 0; j < nj; ++j) {
-            const int c = j % nch;
-            const int t = t_begin + wave + (j / nch) * NW;
-            if (c == 0) {
-#pragma unroll
-                for (int rb = 0; rb < kMaxRb; ++rb) acc[rb] = v4i{0, 0, 0, 0};
-                n = t * 16 + r16;
-                swn = n < N ? a.sw[(int64_t)e * N + n] : 0.0f;
-            }
-            // 2. the chunk's MFMAs (K tiles past kt met zero weights and are skipped)
-            const int k0 = c * kChunk;
-#pragma unroll
-            for (int rb = 0; rb < kMaxRb; ++rb) {
-                if (rb >= nrb) break;
-#pragma unroll
-                for (int s = 0; s < kChunk; ++s)
-                    if (k0 + s < kt)
-                        acc[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                            *(const v4i*)(As + (rb * kt + k0 + s) * 1024 + lane * 16), b[s], acc[rb], 0, 0, 0);
-            }
-            // 3. the next chunk in flight, then the tile's outputs under it
-            if (j + 1 < nj) load_chunk(j + 1);
-            if (c == nch - 1 && n < N) {
-#pragma unroll
-                for (int rb = 0; rb < kMaxRb; ++rb) {
-                    if (rb >= nrb) break;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int slot = p0 + rb * 16 + 4 * g + r;
-                        if (slot < seg1) {
-                            float y = epilogue_w8a8(acc[rb][r], sas[rb * 16 + 4 * g + r], swn);
-                            if (a.relu2) y = relu2(y);
-                            a.out[(int64_t)slot * N + n] = y;
-                        }
-                    }
-                }
-            }
+        switch (nrb) {
+        case 1: expert_stream<1>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1); break;
+        case 2: expert_stream<2>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1); break;
+        case 3: expert_stream<3>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1); break;
+        default: expert_stream<4>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1); break;
         }
         lds_publish();  // the pass's A and scale reads are done before the next pass restages them
     }

@@ -511,11 +511,16 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
     const int kt = (int)tiled_k_tiles(k);
     if (!gather) {
         // slot-ordered A: the expert-block kernel (A staged once per pass in
-        // LDS, 12 waves streaming whole N tiles), two workgroups per expert.
+        // LDS, 8 waves streaming whole N tiles), two workgroups per expert.
         // A pass stages as many 16-row blocks (up to 4) as the LDS holds next
-        // to the pass's row scales: every pass re-streams the expert's weights.
-        constexpr int kExpertWaves = 12;
-        auto expert_lds = [&](int rb) { return (size_t)rb * kt * 1024 + (size_t)rb * 16 * 4; };
+        // to the pass's row scales and the workgroup's weight scales: every
+        // pass re-streams the expert's weights.
+        constexpr int kExpertWaves = 8;
+        const int ntiles = (int)((n + 15) / 16);
+        const int tiles_per_wg = (ntiles + 1) / 2;
+        auto expert_lds = [&](int rb) {
+            return (size_t)rb * kt * 1024 + (size_t)rb * 16 * 4 + (size_t)tiles_per_wg * 16 * 4;
+        };
         int row_blocks = 4;
         while (row_blocks > 1 && expert_lds(row_blocks) > ctx->max_shared_per_block) --row_blocks;
         const size_t lds = expert_lds(row_blocks);
@@ -533,8 +538,7 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
             e.a_rows = (int)a_rows;
             e.waves = 1;
             e.streams = kExpertWaves;
-            const int ntiles = (int)((n + 15) / 16);
-            e.tiles_per_wg = (ntiles + 1) / 2;
+            e.tiles_per_wg = tiles_per_wg;
             e.relu2 = relu2 ? 1 : 0;
             e.row_blocks = row_blocks;
             return launch(ctx, K_EXPERT_GEMM, 2u, (unsigned)(64 * kExpertWaves), lds, stream, e, err,
