@@ -104,6 +104,75 @@ __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, floa
     }
 }
 
+// Wave path: one wave per row, 4 rows per 256-thread workgroup.  A row of up
+// to 64 * NCH 16-byte chunks stays in registers between the absmax and the
+// code pass, and both reductions are wave reductions: no barrier, and a row
+// costs one round trip to memory.  Same codes and scales as the vector path
+// (max and min are exact in any order).
+template <int DT, int NCH>
+__device__ __forceinline__ void quantize_row_wave(const QuantizeRowsArgs& a) {
+    constexpr int VPC = DT == DT_BF16 ? 8 : 4;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= a.rows) return;  // the whole wave
+    const int64_t src = a.gather ? a.gather[row] / a.gather_div : row;
+    const int cols = (int)a.cols;
+    const int chunks = cols / VPC;
+    const uint32_t rb = (uint32_t)cols * (DT == DT_BF16 ? 2u : 4u);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc((const char*)a.x + src * (int64_t)rb, rb);
+    v4i xv[NCH];
+#pragma unroll
+    for (int r = 0; r < NCH; ++r) {
+        const int c = lane + r * 64;
+        xv[r] = buffer_load16(xr, c < chunks ? c * 16 : kOutOfRange);
+    }
+    float amax = 0.0f;
+    int bad = 0x7fffffff;
+#pragma unroll
+    for (int r = 0; r < NCH; ++r) {
+        float f[VPC];
+        if constexpr (DT == DT_BF16) {
+            unpack_bf16x8(xv[r], f);
+        } else {
+#pragma unroll
+            for (int j = 0; j < VPC; ++j) f[j] = f32_from_bits((uint32_t)xv[r][j]);
+        }
+        const int c = lane + r * 64;  // chunks past the row read zeros
+#pragma unroll
+        for (int j = 0; j < VPC; ++j) {
+            if (!is_finite_f32(f[j])) bad = min(bad, c * VPC + j);
+            else amax = fmaxf(amax, fabsf(f[j]));
+        }
+    }
+    amax = wave_max(amax);
+    bad = wave_min_i32(bad);
+    const float s = scale_from_amax(amax);
+    if (lane == 0) {
+        a.scales[row] = s;
+        if (a.row_status) a.row_status[row] = bad == 0x7fffffff ? -1 : bad;
+    }
+    const float rcp = s > 0.0f ? 1.0f / s : 0.0f;
+    const bool pow2 = scale_is_pow2(s);
+    const int64_t kt = (cols + 63) / 64;
+#pragma unroll
+    for (int r = 0; r < NCH; ++r) {
+        const int c = lane + r * 64;
+        if (c >= chunks) break;
+        const int k = c * VPC;
+        int8_t* tile = a.q_act ? a.q_act + act_tile_offset(row, k, a.act_p, kt) : nullptr;
+        if constexpr (DT == DT_BF16) {
+            uint32_t code[2];
+            quantize8_bf16(xv[r], s, rcp, pow2, code);
+            if (a.q) *(uint2*)(a.q + row * cols + k) = make_uint2(code[0], code[1]);
+            if (tile) *(uint2*)tile = make_uint2(code[0], code[1]);
+        } else {
+            const uint32_t code = quantize4_f32(xv[r], s, rcp, pow2);
+            if (a.q) *(uint32_t*)(a.q + row * cols + k) = code;
+            if (tile) *(uint32_t*)tile = code;
+        }
+    }
+}
+
 // Scalar path (any alignment, any column count): pass 1 = absmax + first
 // non-finite column, pass 2 = codes; the row stays in L2 between the passes.
 __device__ __forceinline__ void quantize_row_scalar(const QuantizeRowsArgs& a, float* redf, int* redi) {
@@ -148,6 +217,15 @@ extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_i8_kernel(Qua
         quantize_row_vec<DT_BF16>(a, redf, redi);
     else
         quantize_row_vec<DT_F32>(a, redf, redi);
+}
+
+// Q1/Q2 for vector-path rows of up to 512 16-byte chunks (4096 bf16 / 2048
+// f32 values): one wave per row (quantize_row_wave), grid = ceil(rows / 4).
+extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_wave_kernel(QuantizeRowsArgs a) {
+    if (a.x_dtype == DT_BF16)
+        quantize_row_wave<DT_BF16, 8>(a);
+    else
+        quantize_row_wave<DT_F32, 8>(a);
 }
 
 // Row-major int8 [rows][cols] -> the tiled layout (nh_numerics.h): thread c

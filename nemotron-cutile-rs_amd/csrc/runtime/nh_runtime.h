@@ -37,6 +37,7 @@ enum KernelId : int {
     K_LINEAR_DECODE_ROW2,  // M <= 2, one N tile per workgroup
     K_LINEAR_DECODE_ROW4,  // M <= 4, one N tile per workgroup
     K_EXPERT_GEMM,         // grouped GEMM on slot-ordered A
+    K_QUANTIZE_ROWS_WAVE,  // row quantizer, one wave per row
     K_COUNT
 };
 

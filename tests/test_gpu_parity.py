@@ -124,6 +124,42 @@ def test_quantize_rows_special_rows(ctx):
     assert dstat.numpy().tolist() == [-1, -1, -1, -1, 9]
 
 
+@pytest.mark.parametrize("cols,dtype", [(2688, "bf16"), (1856, "f32"), (4096, "bf16"), (2048, "f32"), (8, "bf16"),
+                                        (4, "f32")])
+def test_quantize_many_rows_bit_exact(ctx, cols, dtype):
+    """1100 rows: the one-wave-per-row quantizer (rows of up to 512 16-byte
+    chunks, 1024 rows or more), with tie, tiny, subnormal and non-finite rows
+    among them."""
+    rows = 1100
+    note(f"quantize_rows many {rows}x{cols} {dtype}")
+    x = O.normal_f32(11, rows * cols, 0.0, 0.02 if dtype == "f32" else 1.0).reshape(rows, cols)
+    n = min(cols, 7)
+    x[3, :n] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.49999988, -126.5][:n]
+    x[3, n:] = 0.0
+    x[500, :] = 0.0
+    x[500, 0] = np.float32(1e-45)
+    x[700] = np.linspace(-3e-39, 3e-39, cols, dtype=np.float32)
+    x[1099, :] = 1.0
+    x[1099, cols // 2] = np.nan
+    x[1099, cols - 1] = np.inf
+    if dtype == "bf16":
+        xs = O.to_bf16(x)
+        st, q_ref, s_ref, _ = O.quantize_rows_bf16(xs[:rows - 1])
+        dx, dt = ctx.upload(xs), NH.BF16
+    else:
+        st, q_ref, s_ref, _ = O.quantize_rows_f32(x[:rows - 1])
+        dx, dt = ctx.upload(x), NH.F32
+    dq = ctx.empty((rows, cols), np.int8)
+    ds = ctx.empty(rows, np.float32)
+    dstat = ctx.empty(rows, np.int32)
+    NH.call("nh_quantize_rows_i8", ctx.handle, dx.ptr, dt, rows, cols, dq.ptr, ds.ptr, dstat.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(dq.numpy()[:rows - 1], q_ref)
+    assert np.array_equal(ds.numpy()[:rows - 1].view(np.uint32), s_ref.view(np.uint32))
+    stat = dstat.numpy()
+    assert np.all(stat[:rows - 1] == -1) and stat[rows - 1] == cols // 2
+
+
 def test_dequantize_i8_bit_exact(ctx):
     note("dequantize_i8")
     _, q, s = quantized_weights(256, 1024)
@@ -577,7 +613,8 @@ def test_expert_gemm_long_segments_bit_exact(ctx, n, k):
         assert np.array_equal(out.numpy(), ref)
 
 
-@pytest.mark.parametrize("tokens,hidden,inter,experts,top_k", [(64, 2688, 1856, 128, 6), (13, 64, 32, 8, 3)])
+@pytest.mark.parametrize("tokens,hidden,inter,experts,top_k", [(64, 2688, 1856, 128, 6), (13, 64, 32, 8, 3),
+                                                                (256, 64, 32, 16, 6)])
 def test_moe_forward_bit_exact(ctx, tokens, hidden, inter, experts, top_k):
     note(f"moe forward t={tokens} h={hidden} i={inter} e={experts} k={top_k}")
     x, logits, up, su, down, sd = moe_case(tokens, hidden, inter, experts, top_k)
