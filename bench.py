@@ -42,13 +42,48 @@ class Bench:
         self.ctx = NH.Context(0)
         self.ev = NH.HipEvents()
         self.e0, self.e1 = self.ev.create(), self.ev.create()
+        self.graphs = NH.HipGraphs()
         s = ctypes.c_void_p()
         NH.call("nh_stream_create", self.ctx.handle, ctypes.byref(s))
         self.stream = s
 
-    def time_ms(self, fn, steps, warmup):
-        """Mean time per step of fn(i) on self.stream: `warmup` untimed calls,
-        then `steps` calls bracketed by HIP events recorded on that stream."""
+    def time_ms(self, fn, steps, warmup, per_graph=None, out=None):
+        """Mean time per step of fn(i) on self.stream.  `warmup` eager calls;
+        then the calls of steps warmup .. warmup + steps - 1 are captured from
+        the same entry points into HIP graphs of `per_graph` steps each,
+        replayed once untimed, and replayed again bracketed by HIP events on
+        that stream.  The replay issues exactly the captured launches, without
+        the ~12 us of Python/ctypes work per eager call (which bounded the eager
+        loop of the 12 us decode unit).  With `out`, the replayed result must
+        equal an eager call of the last step."""
+        for i in range(warmup):
+            fn(i)
+        fn(warmup + steps - 1)
+        self.ctx.synchronize(self.stream)
+        eager = out.numpy() if out is not None else None
+        per = per_graph or steps
+        graphs = []
+        for c0 in range(0, steps, per):
+            idx = range(warmup + c0, warmup + min(steps, c0 + per))
+            graphs.append(self.graphs.capture(self.stream, lambda idx=idx: [fn(i) for i in idx]))
+        for _, ex in graphs:
+            self.graphs.launch(ex, self.stream)
+        self.ctx.synchronize(self.stream)
+        self.ev.record(self.e0, self.stream)
+        for _, ex in graphs:
+            self.graphs.launch(ex, self.stream)
+        self.ev.record(self.e1, self.stream)
+        ms = self.ev.elapsed_ms(self.e0, self.e1)
+        self.ctx.synchronize(self.stream)
+        for g, ex in graphs:
+            self.graphs.destroy(g, ex)
+        if eager is not None and not np.array_equal(out.numpy(), eager):
+            raise AssertionError("graph replay differs from the eager call of the same step")
+        return ms / steps
+
+    def time_eager_ms(self, fn, steps, warmup):
+        """The same timing with eager calls from this Python loop (reported
+        beside the headline: it includes the per-call host overhead)."""
         for i in range(warmup):
             fn(i)
         self.ctx.synchronize(self.stream)
@@ -93,7 +128,8 @@ class Bench:
             if st:
                 NH.check(st, err)
 
-        ms = self.time_ms(step, steps, warmup)
+        ms = self.time_ms(step, steps, warmup, out=out)
+        self.last_step = step
         return ms, pool, x, out
 
     def gemm(self, m, n, k, steps, warmup):
@@ -114,7 +150,7 @@ class Bench:
                         ctypes.byref(err))
                 if st:
                     NH.check(st, err)
-            return self.time_ms(step, steps, warmup)
+            return self.time_ms(step, steps, warmup, out=out)
 
         return run(L.nh_gemm_w8a8_ta, xt), run(L.nh_gemm_w8a8, xq)
 
@@ -132,7 +168,7 @@ class Bench:
             if st:
                 NH.check(st, err)
 
-        return self.time_ms(step, steps, warmup)
+        return self.time_ms(step, steps, warmup, out=y)
 
     def moe(self, steps, warmup, tokens=512, hidden=2688, inter=1856, experts=128, top_k=6):
         L = NH.lib()
@@ -175,7 +211,7 @@ class Bench:
             if st:
                 NH.check(st, err)
 
-        ms = self.time_ms(step, steps, warmup)
+        ms = self.time_ms(step, steps, warmup, out=out)
         # weights of the experts that received routes + scales + activations
         wbytes = experts * (inter * hidden + hidden * inter) + experts * 4 * (inter + hidden)
         abytes = tokens * hidden * 2 + tokens * experts * 4 + tokens * hidden * 2
@@ -253,7 +289,7 @@ class Bench:
                     if st:
                         NH.check(st, err)
 
-        ms = self.time_ms(step, steps, warmup)
+        ms = self.time_ms(step, steps, warmup, per_graph=1, out=outs[4096])
         for bufs, s in layers.values():
             for d in bufs:
                 d.free()
@@ -356,6 +392,7 @@ def main():
     log = lambda s: print(s, file=sys.stderr, flush=True)  # noqa: E731
     log("[bench] headline decode unit m=1 k=4096 n=16384")
     ms, pool, x, out = b.decode(m, n, k, args.steps, args.warmup)
+    eager_ms = b.time_eager_ms(b.last_step, args.steps, args.warmup)
     nbytes = decode_bytes(m, n, k)
     gbs = nbytes / (ms * 1e-3) / 1e9
     extra = {}
@@ -420,7 +457,9 @@ def main():
         "data": "synthetic",
         "config": {"workload": "decode unit (per-token int8 quantization + W8A8 GEMV), M=1, K=4096 -> N=16384, "
                                "bf16 in/out, int8 per-row weights from N(0,0.02) (BASELINE configs[1])",
-                   "m": m, "k": k, "n": n, "weight_pool_MiB": POOL_BYTES >> 20},
+                   "m": m, "k": k, "n": n, "weight_pool_MiB": POOL_BYTES >> 20,
+                   "timing": "HIP-graph replay of the captured entry-point calls; eager Python-loop "
+                             f"figure {eager_ms * 1e3:.2f} us/step"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "nh_linear_decode_w8a8_m1_kernel", "bytes_per_launch": nbytes},

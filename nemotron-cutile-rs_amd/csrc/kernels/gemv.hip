@@ -31,8 +31,10 @@ constexpr int kSlab = 16;                // K tiles per wave in flight at once
 // The decode unit issues the first kSlabHead tiles of its slab, quantizes the
 // activations while they stream (the activation loads went first, so they
 // return first), then issues the rest: the quantizer's VALU work no longer
-// waits for the whole slab to have been issued (measured 0.1-0.2 us faster).
-constexpr int kSlabHead = 4;
+// waits for the whole slab to have been issued.  Measured at M = 1,
+// K = 4096 -> N = 16384: 2 / 4 / 6 / 8 / 12 / 16 head tiles take 12.98 /
+// 12.45 / 12.05 / 12.08 / 12.38 / 12.55 us (16 cost occupancy: 143 VGPRs).
+constexpr int kSlabHead = 8;
 
 // The KT KiB of 16-row N tile `tile`.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_tile_rsrc(const int8_t* wq, int tile, int kt) {

@@ -16,15 +16,13 @@ __device__ __forceinline__ int64_t act_tile_offset(int64_t m, int64_t k, int64_t
 
 // Vector path: one workgroup per row, 16-byte chunks (8 bf16 or 4 f32
 // values).  The first kRegChunks chunks of every thread stay in registers
-// between the absmax pass and the code pass, so rows up to 4 * 256 chunks
-// (8192 bf16 / 4096 f32 values) are read from memory once; longer rows read
-// the rest again (L2), four chunks in flight per thread.
+// between the absmax pass and the code pass, so rows up to kRegChunks *
+// blockDim.x chunks are read from memory once; longer rows read the rest
+// again (L2), four chunks in flight per thread.
 // Codes go to the row-major matrix and/or the A-operand tiles (act_p rows
 // per tile: the compact [KT][4][rows][16] of the M <= 16 GEMV, or 16, the
 // weights' tiled layout read by the GEMM).
-constexpr int kRegChunks = 4;
-
-template <int DT>
+template <int DT, int kRegChunks>
 __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, float* redf, int* redi) {
     constexpr int VPC = DT == DT_BF16 ? 8 : 4;  // values per 16-byte chunk
     const int64_t row = blockIdx.x;
@@ -214,9 +212,23 @@ extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_i8_kernel(Qua
     if (!a.vec)
         quantize_row_scalar(a, redf, redi);
     else if (a.x_dtype == DT_BF16)
-        quantize_row_vec<DT_BF16>(a, redf, redi);
+        quantize_row_vec<DT_BF16, 4>(a, redf, redi);
     else
-        quantize_row_vec<DT_F32>(a, redf, redi);
+        quantize_row_vec<DT_F32, 4>(a, redf, redi);
+}
+
+// The vector path for a few long rows (the decode batch's activations): 1024
+// threads per row, 8 chunks each in registers, so a row of up to 8192 chunks
+// (the MLP's 21504-wide f32 intermediate is 5376) costs one round trip to
+// memory instead of one per 1024 chunks.
+extern "C" __global__ __launch_bounds__(1024) void nh_quantize_rows_long_kernel(QuantizeRowsArgs a) {
+    __shared__ float redf[16];
+    __shared__ int redi[16];
+    if ((int64_t)blockIdx.x >= a.rows) return;
+    if (a.x_dtype == DT_BF16)
+        quantize_row_vec<DT_BF16, 8>(a, redf, redi);
+    else
+        quantize_row_vec<DT_F32, 8>(a, redf, redi);
 }
 
 // Q1/Q2 for vector-path rows of up to 512 16-byte chunks (4096 bf16 / 2048

@@ -127,6 +127,10 @@ nh_status launch_quantize(nh_context* ctx, const void* x, nh_dtype dtype, size_t
     // 2.26 vs 2.15 ms)
     if (vec && row_bytes <= 512 * 16 && rows >= 1024)
         return launch(ctx, K_QUANTIZE_ROWS_WAVE, (unsigned)((rows + 3) / 4), 256, 0, stream, a, err);
+    // a few rows longer than a 256-thread workgroup holds in registers
+    // (1024 chunks): 1024 threads per row, one round trip to memory
+    if (vec && row_bytes > 1024 * 16 && rows <= 256)
+        return launch(ctx, K_QUANTIZE_ROWS_LONG, (unsigned)rows, 1024, 0, stream, a, err);
     return launch(ctx, K_QUANTIZE_ROWS, (unsigned)rows, 256, 0, stream, a, err);
 }
 

@@ -36,6 +36,7 @@ const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
     "nh_linear_decode_w8a8_row4_kernel", // K_LINEAR_DECODE_ROW4
     "nh_moe_expert_gemm_kernel",         // K_EXPERT_GEMM
     "nh_quantize_rows_wave_kernel",      // K_QUANTIZE_ROWS_WAVE
+    "nh_quantize_rows_long_kernel",      // K_QUANTIZE_ROWS_LONG
 };
 
 void clear_error(nh_error* err) {

@@ -38,6 +38,7 @@ enum KernelId : int {
     K_LINEAR_DECODE_ROW4,  // M <= 4, one N tile per workgroup
     K_EXPERT_GEMM,         // grouped GEMM on slot-ordered A
     K_QUANTIZE_ROWS_WAVE,  // row quantizer, one wave per row
+    K_QUANTIZE_ROWS_LONG,  // row quantizer, 1024 threads per row
     K_COUNT
 };
 

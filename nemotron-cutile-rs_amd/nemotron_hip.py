@@ -268,6 +268,50 @@ class HipEvents:
         self.hip.hipEventDestroy(ev)
 
 
+class HipGraphs:
+    """Stream capture into HIP graphs and their replay (plumbing for the
+    benchmark: the library's calls are captured as issued, nothing else)."""
+
+    CAPTURE_RELAXED = 2
+
+    def __init__(self):
+        self.hip = C.CDLL("libamdhip64.so.7")
+        self.hip.hipStreamBeginCapture.argtypes = [P, C.c_int]
+        self.hip.hipStreamEndCapture.argtypes = [P, C.POINTER(P)]
+        self.hip.hipGraphInstantiate.argtypes = [C.POINTER(P), P, P, C.c_char_p, C.c_size_t]
+        self.hip.hipGraphLaunch.argtypes = [P, P]
+        self.hip.hipGraphExecDestroy.argtypes = [P]
+        self.hip.hipGraphDestroy.argtypes = [P]
+
+    def capture(self, stream, issue):
+        """Runs issue() under capture on `stream`; returns (graph, exec)."""
+        rc = self.hip.hipStreamBeginCapture(stream, self.CAPTURE_RELAXED)
+        if rc != 0:
+            raise RuntimeError(f"hipStreamBeginCapture failed ({rc})")
+        try:
+            issue()
+        finally:
+            g = P()
+            rc = self.hip.hipStreamEndCapture(stream, C.byref(g))
+        if rc != 0:
+            raise RuntimeError(f"hipStreamEndCapture failed ({rc})")
+        ex = P()
+        rc = self.hip.hipGraphInstantiate(C.byref(ex), g, None, None, 0)
+        if rc != 0:
+            self.hip.hipGraphDestroy(g)
+            raise RuntimeError(f"hipGraphInstantiate failed ({rc})")
+        return g, ex
+
+    def launch(self, ex, stream):
+        rc = self.hip.hipGraphLaunch(ex, stream)
+        if rc != 0:
+            raise RuntimeError(f"hipGraphLaunch failed ({rc})")
+
+    def destroy(self, g, ex):
+        self.hip.hipGraphExecDestroy(ex)
+        self.hip.hipGraphDestroy(g)
+
+
 def tile_weights(ctx, wq_dev, n, k, stream=None):
     """Device int8 [n][k] row-major -> a new device buffer in the tiled layout."""
     nbytes = lib().nh_tiled_weights_bytes(n, k)

@@ -58,7 +58,9 @@ def activations_bf16(m, k, seed=1):
 # ---- Q1/Q2/Q3 ----------------------------------------------------------------
 @pytest.mark.parametrize("rows,cols,dtype", [(1, 4096, "bf16"), (16, 8192, "bf16"), (3072, 1856, "f32"),
                                              (4096, 4096, "f32"), (7, 33, "f32"), (5, 1, "bf16"),
-                                             (3, 21504, "f32"), (2, 40000, "bf16"), (4, 12, "f32")])
+                                             (3, 21504, "f32"), (2, 40000, "bf16"), (4, 12, "f32"),
+                                             # past the 8192 chunks the 1024-thread kernel holds in registers
+                                             (2, 70000, "bf16")])
 def test_quantize_rows_bit_exact(ctx, rows, cols, dtype):
     note(f"quantize_rows {rows}x{cols} {dtype}")
     x = O.normal_f32(5, rows * cols, 0.0, 0.02 if dtype == "f32" else 1.0).reshape(rows, cols)
@@ -453,7 +455,11 @@ def test_gemv_w8a32_within_tolerance(ctx, m, n, k):
 
 # ---- G3: W8A8 GEMM (prefill) -----------------------------------------------------
 @pytest.mark.parametrize("m,n,k", [(2048, 4096, 4096), (2048, 21504, 4096), (2048, 4096, 21504), (37, 100, 64),
-                                   (300, 130, 272), (17, 4096, 4096), (513, 2688, 1856)])
+                                   (300, 130, 272), (17, 4096, 4096), (513, 2688, 1856),
+                                   # 256 x 128 tiles at their edges: one K step, fewer K steps than
+                                   # ring slots, an odd K-tile count with a partial last tile, ragged
+                                   # M and N (a half-valid last weight tile)
+                                   (512, 8192, 64), (1000, 2000, 192), (777, 8200, 1040)])
 @pytest.mark.parametrize("a_layout", ["row-major", "tiled"])
 def test_gemm_w8a8_bit_exact(ctx, m, n, k, a_layout):
     note(f"gemm_w8a8 m={m} n={n} k={k} A {a_layout}")
