@@ -170,7 +170,7 @@ class Bench:
 
         return self.time_ms(step, steps, warmup, out=y)
 
-    def moe(self, steps, warmup, tokens=512, hidden=2688, inter=1856, experts=128, top_k=6):
+    def moe(self, steps, warmup, tokens=512, hidden=2688, inter=1856, experts=128, top_k=6, shared_inter=0):
         L = NH.lib()
         tb_up, tb_down = L.nh_tiled_weights_bytes(inter, hidden), L.nh_tiled_weights_bytes(hidden, inter)
         up_q = self.ctx.empty(experts * tb_up, np.int8)
@@ -200,22 +200,38 @@ class Bench:
         x = self.ctx.upload(NH_bf16(NH.normal_f32(1, tokens * hidden)))
         logits = self.ctx.upload(NH.normal_f32(2, tokens * experts))
         out = self.ctx.empty((tokens, hidden), np.uint16)
-        ws_bytes = L.nh_moe_forward_w8a8_workspace_size(tokens, hidden, inter, experts, top_k)
-        ws = self.ctx.empty(ws_bytes, np.uint8)
         err = NH.NhError()
+        if shared_inter:
+            # the shared expert (the reference config's 3712-wide MLP), N(0, 0.02) seeds 120 / 121
+            sh = []
+            for seed, (n, k) in ((120, (shared_inter, hidden)), (121, (hidden, shared_inter))):
+                (q, s_), = self.quantized_pool(n, k, 1, seed=seed)
+                sh += [q, s_]
+            ws_bytes = L.nh_moe_forward_shared_w8a8_workspace_size(tokens, hidden, inter, experts, top_k,
+                                                                   shared_inter)
+        else:
+            ws_bytes = L.nh_moe_forward_w8a8_workspace_size(tokens, hidden, inter, experts, top_k)
+        ws = self.ctx.empty(ws_bytes, np.uint8)
 
         def step(i):
-            st = L.nh_moe_forward_w8a8(h, x.ptr, NH.BF16, logits.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
-                                       up_q.ptr, up_s.ptr, down_q.ptr, down_s.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes,
-                                       self.stream, ctypes.byref(err))
+            if shared_inter:
+                st = L.nh_moe_forward_shared_w8a8(h, x.ptr, NH.BF16, logits.ptr, tokens, hidden, inter, experts, top_k,
+                                                  1, 1.0, up_q.ptr, up_s.ptr, down_q.ptr, down_s.ptr, shared_inter,
+                                                  sh[0].ptr, sh[1].ptr, sh[2].ptr, sh[3].ptr, out.ptr, NH.BF16, ws.ptr,
+                                                  ws_bytes, self.stream, ctypes.byref(err))
+            else:
+                st = L.nh_moe_forward_w8a8(h, x.ptr, NH.BF16, logits.ptr, tokens, hidden, inter, experts, top_k, 1,
+                                           1.0, up_q.ptr, up_s.ptr, down_q.ptr, down_s.ptr, out.ptr, NH.BF16, ws.ptr,
+                                           ws_bytes, self.stream, ctypes.byref(err))
             if st:
                 NH.check(st, err)
 
         ms = self.time_ms(step, steps, warmup, out=out)
         # weights of the experts that received routes + scales + activations
         wbytes = experts * (inter * hidden + hidden * inter) + experts * 4 * (inter + hidden)
+        wbytes += 2 * shared_inter * hidden + 4 * (shared_inter + hidden) if shared_inter else 0
         abytes = tokens * hidden * 2 + tokens * experts * 4 + tokens * hidden * 2
-        return ms, wbytes + abytes, 2.0 * tokens * top_k * hidden * inter * 2
+        return ms, wbytes + abytes, 2.0 * tokens * (top_k * inter + shared_inter) * hidden * 2
 
 
     def decode_stack(self, steps, warmup, m=8):
@@ -432,6 +448,11 @@ def main():
         extra["moe_512tok_128exp_top6"] = {"us": round(t * 1e3, 1), "GBps": round(mbytes / (t * 1e-3) / 1e9, 1),
                                            "frac_hbm_peak": round(mbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                            "TOPS": round(mops / (t * 1e-3) / 1e12, 2)}
+        log("[bench] moe layer with its 3712-wide shared expert")
+        t, mbytes, mops = b.moe(10, 2, shared_inter=3712)
+        extra["moe_512tok_128exp_top6_shared3712"] = {
+            "us": round(t * 1e3, 1), "GBps": round(mbytes / (t * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(mbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "TOPS": round(mops / (t * 1e-3) / 1e12, 2)}
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline")

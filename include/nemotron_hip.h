@@ -246,6 +246,16 @@ nh_status nh_moe_combine(nh_context *ctx, const float *slot_out, const int32_t *
                          nh_stream stream, nh_error *err);
 nh_status nh_moe_combine_host(const float *slot_out, const int32_t *pos, const float *weights, size_t tokens,
                               size_t top_k, size_t hidden, void *out, nh_dtype out_dtype, nh_error *err);
+/* R4 with the shared expert (moe.rs:197-219): out[t] = 0 + shared[t] +
+ * sum_j w[t,j] * slot_out[pos[t*k+j]], each add in that order in f32 (the
+ * reference zeroes the output, adds the shared expert's row, then the routes).
+ * shared is f32 [tokens][hidden] or NULL (then exactly nh_moe_combine). */
+nh_status nh_moe_combine_shared(nh_context *ctx, const float *slot_out, const int32_t *pos, const float *weights,
+                                const float *shared, size_t tokens, size_t top_k, size_t hidden, void *out,
+                                nh_dtype out_dtype, nh_stream stream, nh_error *err);
+nh_status nh_moe_combine_shared_host(const float *slot_out, const int32_t *pos, const float *weights,
+                                     const float *shared, size_t tokens, size_t top_k, size_t hidden, void *out,
+                                     nh_dtype out_dtype, nh_error *err);
 /* Whole int8 MoE layer on the device: Q2(x) -> R1 -> R2 -> up (R3, gather,
  * ReLU^2) -> Q2 -> down (R3) -> R4.  Replaces MoeLayer::forward_into
  * (moe.rs:154-249) for routed experts with int8 per-row weights
@@ -264,6 +274,25 @@ nh_status nh_moe_forward_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, 
                               int renormalize, float scaling, const int8_t *w_up, const float *s_up,
                               const int8_t *w_down, const float *s_down, void *out, nh_dtype out_dtype,
                               void *workspace, size_t workspace_bytes, nh_stream stream, nh_error *err);
+/* The int8 MoE layer with its shared expert, MoeLayer::forward_into with
+ * shared_expert = Some(..) (moe.rs:197-219): the shared expert is an int8
+ * MLP over every token (nh_mlp_w8a8 on x, f32, no biases: w_up_shared tiled
+ * [shared_inter][hidden], w_down_shared tiled [hidden][shared_inter]), added
+ * to each output row before the routed experts (nh_moe_combine_shared).
+ * Routing, experts and errors as nh_moe_forward_w8a8; INVALID_PARAMS for a
+ * NULL w_up_shared, INVALID_SHAPE for shared_inter == 0 or a missing shared
+ * operand.  The workspace (nh_moe_forward_shared_w8a8_workspace_size) starts
+ * with nh_moe_workspace_layout's fields. */
+size_t nh_moe_forward_shared_w8a8_workspace_size(size_t tokens, size_t hidden, size_t inter, size_t experts,
+                                                 size_t top_k, size_t shared_inter);
+nh_status nh_moe_forward_shared_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const float *logits,
+                                     size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
+                                     int renormalize, float scaling, const int8_t *w_up, const float *s_up,
+                                     const int8_t *w_down, const float *s_down, size_t shared_inter,
+                                     const int8_t *w_up_shared, const float *s_up_shared,
+                                     const int8_t *w_down_shared, const float *s_down_shared, void *out,
+                                     nh_dtype out_dtype, void *workspace, size_t workspace_bytes, nh_stream stream,
+                                     nh_error *err);
 
 /* ---- synthetic inputs (build-defined seeded generator; the reference has
  *      no RNG): splitmix64 -> Box-Muller (f64) -> f32 ------------------- */

@@ -338,11 +338,18 @@ nh_status nh_moe_grouped_gemm_w8a8_host(const int8_t* aq, const float* sa, int g
 
 nh_status nh_moe_combine_host(const float* slot_out, const int32_t* pos, const float* weights, size_t tokens,
                               size_t top_k, size_t hidden, void* out, nh_dtype out_dtype, nh_error* err) {
+    return nh_moe_combine_shared_host(slot_out, pos, weights, nullptr, tokens, top_k, hidden, out, out_dtype, err);
+}
+
+nh_status nh_moe_combine_shared_host(const float* slot_out, const int32_t* pos, const float* weights,
+                                     const float* shared, size_t tokens, size_t top_k, size_t hidden, void* out,
+                                     nh_dtype out_dtype, nh_error* err) {
     clear_error(err);
     if (out_dtype != NH_F32 && out_dtype != NH_BF16) return set_error(err, NH_INVALID_PARAMS, "unknown dtype");
     for (size_t t = 0; t < tokens; ++t)
         for (size_t h = 0; h < hidden; ++h) {
             float v = 0.0f;
+            if (shared) v = v + shared[t * hidden + h];  // the shared expert first (moe.rs:212-219)
             for (size_t j = 0; j < top_k; ++j) {
                 const size_t r = t * top_k + j;
                 const float p = weights[r] * slot_out[(size_t)pos[r] * hidden + h];

@@ -52,7 +52,8 @@ __device__ __forceinline__ void store_tile_through_lds(const GemmW8A8Args& a, co
     const int lpr = WN * esz / 16;           // lanes per output row
     const int rows_per_pass = 64 / lpr;
     const int rl = lane / lpr, cl = (lane % lpr) * 16;
-    const bool full_n = gn0 + WN <= N && ((N * esz) & 15) == 0;
+    const int64_t ldo = a.ldo;
+    const bool full_n = gn0 + WN <= N && ((ldo * esz) & 15) == 0;
     constexpr int kPassFrags = 4;            // 64 rows = 4 fragment rows per pass
     float bnv[FN];
 #pragma unroll
@@ -82,7 +83,7 @@ __device__ __forceinline__ void store_tile_through_lds(const GemmW8A8Args& a, co
             const int m = gm0 + i0 * 16 + ml;
             if (m >= M) break;
             const v4i v = *(const v4i*)(et + ml * pitch + cl);
-            int8_t* dst = (int8_t*)a.out + ((int64_t)m * N + gn0) * esz + cl;
+            int8_t* dst = (int8_t*)a.out + ((int64_t)m * ldo + gn0) * esz + cl;
             if (full_n) {
                 *(v4i*)dst = v;
             } else {

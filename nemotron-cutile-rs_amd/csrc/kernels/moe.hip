@@ -421,6 +421,7 @@ extern "C" __global__ __launch_bounds__(256) void nh_moe_combine_kernel(CombineA
     const int h = blockIdx.x * blockDim.x + threadIdx.x;
     if (h >= a.hidden) return;
     float v = 0.0f;
+    if (a.shared) v = v + a.shared[(int64_t)t * a.hidden + h];  // the shared expert first (moe.rs:212-219)
     for (int j = 0; j < a.top_k; ++j) {
         const int r = t * a.top_k + j;
         const float w = a.weights[r];

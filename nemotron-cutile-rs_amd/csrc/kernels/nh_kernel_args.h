@@ -132,6 +132,8 @@ struct GemmW8A8Args {
     int32_t out_dtype;
     int32_t relu2;
     int32_t kt;           // ceil(K / 64)
+    int32_t ldo;          // elements between output rows (>= N: a launch may cover a column range)
+    int32_t pad_;
 };
 
 // R1: sigmoid top-k routing, one wave per token.
@@ -199,6 +201,7 @@ struct CombineArgs {
     const int32_t* pos;      // [T*k]
     const float* weights;    // [T*k]
     void* out;               // [T][H]
+    const float* shared;     // [T][H] shared-expert output, added first; or null
     int32_t tokens, top_k, hidden;
     int32_t out_dtype;
 };

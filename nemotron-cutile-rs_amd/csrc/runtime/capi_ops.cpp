@@ -178,6 +178,7 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
     a.out_dtype = out_dtype;
     a.relu2 = relu2;
     a.kt = (int)tiled_k_tiles(K);
+    a.ldo = N;
     // Tile choice: 256x128 (8 compute + 8 loader waves) unless that leaves
     // most CUs idle, then 128x128 (more, smaller tiles).
     struct Cfg {
@@ -208,6 +209,37 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
     }
     a.tiles_m = (M + cfg->bm - 1) / cfg->bm;
     a.tiles_n = (N + cfg->bn - 1) / cfg->bn;
+    // Every workgroup runs in one of ceil(tiles / CUs) rounds.  When the last
+    // round of 256x128 tiles would be at most half full, the columns of the
+    // whole rounds take the big tiles and the rest takes 128x128 tiles (half
+    // the work each, twice as many): 2048 x 21504 x 4096 is 5 rounds + about
+    // half a round instead of 6.
+    const int64_t cu = ctx->cu_count;
+    const int64_t nbig = (int64_t)a.tiles_m * a.tiles_n;
+    if (cfg == &big && small.lds <= ctx->max_shared_per_block && nbig > cu && nbig % cu != 0 &&
+        nbig % cu <= cu / 2) {
+        const int tn_main = (int)(nbig / cu * cu / a.tiles_m);  // N tiles of whole rounds
+        const int n_main = tn_main * big.bn;
+        if (tn_main > 0 && n_main < N) {
+            GemmW8A8Args r = a;
+            a.N = n_main;
+            a.tiles_n = tn_main;
+            nh_status st =
+                launch(ctx, big.id, (unsigned)(a.tiles_m * a.tiles_n), (unsigned)big.threads, big.lds, stream, a, err);
+            if (st) return st;
+            // columns n_main .. N: weights, scales, bias and outputs from there, rows still N apart
+            const size_t esz = out_dtype == NH_BF16 ? 2 : 4;
+            r.wq = wq + (size_t)(n_main / 16) * (size_t)r.kt * 1024;
+            r.sw = sw + n_main;
+            r.bias = bias ? bias + n_main : nullptr;
+            r.out = (char*)out + (size_t)n_main * esz;
+            r.N = N - n_main;
+            r.tiles_m = (M + small.bm - 1) / small.bm;
+            r.tiles_n = (r.N + small.bn - 1) / small.bn;
+            return launch(ctx, small.id, (unsigned)(r.tiles_m * r.tiles_n), (unsigned)small.threads, small.lds, stream,
+                          r, err);
+        }
+    }
     return launch(ctx, cfg->id, (unsigned)(a.tiles_m * a.tiles_n), (unsigned)cfg->threads, cfg->lds, stream, a, err);
 }
 
@@ -579,6 +611,13 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
 nh_status nh_moe_combine(nh_context* ctx, const float* slot_out, const int32_t* pos, const float* weights,
                          size_t tokens, size_t top_k, size_t hidden, void* out, nh_dtype out_dtype, nh_stream stream,
                          nh_error* err) {
+    return nh_moe_combine_shared(ctx, slot_out, pos, weights, nullptr, tokens, top_k, hidden, out, out_dtype, stream,
+                                 err);
+}
+
+nh_status nh_moe_combine_shared(nh_context* ctx, const float* slot_out, const int32_t* pos, const float* weights,
+                                const float* shared, size_t tokens, size_t top_k, size_t hidden, void* out,
+                                nh_dtype out_dtype, nh_stream stream, nh_error* err) {
     clear_error(err);
     nh_status st;
     if ((st = check_dtype(out_dtype, err))) return st;
@@ -586,7 +625,7 @@ nh_status nh_moe_combine(nh_context* ctx, const float* slot_out, const int32_t* 
         return set_error(err, NH_INVALID_SHAPE, "invalid combine shape");
     if ((st = bind_device(ctx, err))) return st;
     if (tokens == 0 || hidden == 0) return NH_OK;
-    CombineArgs a{slot_out, pos, weights, out, (int)tokens, (int)top_k, (int)hidden, out_dtype};
+    CombineArgs a{slot_out, pos, weights, out, shared, (int)tokens, (int)top_k, (int)hidden, out_dtype};
     return launch(ctx, K_COMBINE, (unsigned)((hidden + 255) / 256), 256, 0, stream, a, err, (unsigned)tokens);
 }
 
@@ -627,18 +666,28 @@ void nh_moe_workspace_layout(size_t tokens, size_t hidden, size_t inter, size_t 
     for (int i = 0; i < 5; ++i) offsets_out[i] = off[i];
 }
 
-nh_status nh_moe_forward_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const float* logits, size_t tokens,
-                              size_t hidden, size_t inter, size_t experts, size_t top_k, int renormalize,
-                              float scaling, const int8_t* w_up, const float* s_up, const int8_t* w_down,
-                              const float* s_down, void* out, nh_dtype out_dtype, void* workspace,
-                              size_t workspace_bytes, nh_stream stream, nh_error* err) {
+// The routed MoE layer, with the shared expert when w_up_sh is not null:
+// shared = the int8 MLP of x (nh_mlp_w8a8, f32), added first by the combine.
+static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, const float* logits, size_t tokens,
+                             size_t hidden, size_t inter, size_t experts, size_t top_k, int renormalize, float scaling,
+                             const int8_t* w_up, const float* s_up, const int8_t* w_down, const float* s_down,
+                             size_t inter_sh, const int8_t* w_up_sh, const float* s_up_sh, const int8_t* w_down_sh,
+                             const float* s_down_sh, void* out, nh_dtype out_dtype, void* workspace,
+                             size_t workspace_bytes, nh_stream stream, nh_error* err) {
     clear_error(err);
     if (tokens == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
     if (hidden == 0 || experts == 0 || top_k == 0 || top_k > experts || inter == 0)
         return set_error(err, NH_INVALID_SHAPE, "invalid MoE shape");
+    const bool has_shared = w_up_sh != nullptr;
+    if (has_shared && (inter_sh == 0 || !s_up_sh || !w_down_sh || !s_down_sh))
+        return set_error(err, NH_INVALID_SHAPE, "shared expert needs intermediate_dim > 0 and all four operands");
     size_t off[12];
     moe_layout(tokens, hidden, inter, experts, top_k, off);
-    if (!workspace || workspace_bytes < off[11]) return mismatch(err, "workspace", off[11], workspace_bytes);
+    const size_t shared_at = off[11];
+    const size_t shared_bytes = has_shared ? align256(tokens * hidden * sizeof(float)) : 0;
+    const size_t need =
+        off[11] + (has_shared ? shared_bytes + nh_mlp_w8a8_workspace_size(tokens, hidden, inter_sh) : 0);
+    if (!workspace || workspace_bytes < need) return mismatch(err, "workspace", need, workspace_bytes);
     if (!aligned16(workspace)) return set_error(err, NH_UNSUPPORTED, "workspace must be 16-byte aligned");
     char* ws = (char*)workspace;
     int32_t* idx = (int32_t*)(ws + off[0]);
@@ -652,9 +701,15 @@ nh_status nh_moe_forward_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, 
     int8_t* hq = (int8_t*)(ws + off[8]);
     float* sh = (float*)(ws + off[9]);
     float* d = (float*)(ws + off[10]);
+    float* shared = has_shared ? (float*)(ws + shared_at) : nullptr;
     const size_t R = tokens * top_k;
     nh_status st;
     if ((st = check_dtype(x_dtype, err))) return st;
+    if (has_shared &&
+        (st = nh_mlp_w8a8(ctx, x, x_dtype, w_up_sh, s_up_sh, nullptr, w_down_sh, s_down_sh, nullptr, tokens, hidden,
+                          inter_sh, shared, NH_F32, ws + shared_at + shared_bytes, workspace_bytes - shared_at -
+                          shared_bytes, stream, err)))
+        return st;
     if ((st = nh_moe_route_sigmoid_topk(ctx, logits, tokens, experts, top_k, renormalize, scaling, idx, wts, stream,
                                         err)))
         return st;
@@ -672,7 +727,42 @@ nh_status nh_moe_forward_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, 
     if ((st = nh_moe_grouped_gemm_w8a8(ctx, hq, sh, 0, top_k, offsets, perm, R, R, experts, w_down, s_down, hidden,
                                        inter, 0, d, stream, err)))
         return st;
-    return nh_moe_combine(ctx, d, pos, wts, tokens, top_k, hidden, out, out_dtype, stream, err);
+    return nh_moe_combine_shared(ctx, d, pos, wts, shared, tokens, top_k, hidden, out, out_dtype, stream, err);
+}
+
+nh_status nh_moe_forward_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const float* logits, size_t tokens,
+                              size_t hidden, size_t inter, size_t experts, size_t top_k, int renormalize,
+                              float scaling, const int8_t* w_up, const float* s_up, const int8_t* w_down,
+                              const float* s_down, void* out, nh_dtype out_dtype, void* workspace,
+                              size_t workspace_bytes, nh_stream stream, nh_error* err) {
+    return moe_forward(ctx, x, x_dtype, logits, tokens, hidden, inter, experts, top_k, renormalize, scaling, w_up,
+                       s_up, w_down, s_down, 0, nullptr, nullptr, nullptr, nullptr, out, out_dtype, workspace,
+                       workspace_bytes, stream, err);
+}
+
+size_t nh_moe_forward_shared_w8a8_workspace_size(size_t tokens, size_t hidden, size_t inter, size_t experts,
+                                                 size_t top_k, size_t shared_inter) {
+    size_t off[12];
+    moe_layout(tokens, hidden, inter, experts, top_k, off);
+    return off[11] + align256(tokens * hidden * sizeof(float)) +
+           nh_mlp_w8a8_workspace_size(tokens, hidden, shared_inter);
+}
+
+nh_status nh_moe_forward_shared_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const float* logits,
+                                     size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
+                                     int renormalize, float scaling, const int8_t* w_up, const float* s_up,
+                                     const int8_t* w_down, const float* s_down, size_t shared_inter,
+                                     const int8_t* w_up_shared, const float* s_up_shared,
+                                     const int8_t* w_down_shared, const float* s_down_shared, void* out,
+                                     nh_dtype out_dtype, void* workspace, size_t workspace_bytes, nh_stream stream,
+                                     nh_error* err) {
+    if (!w_up_shared) {
+        clear_error(err);
+        return set_error(err, NH_INVALID_PARAMS, "w_up_shared must not be null (nh_moe_forward_w8a8 has no shared expert)");
+    }
+    return moe_forward(ctx, x, x_dtype, logits, tokens, hidden, inter, experts, top_k, renormalize, scaling, w_up,
+                       s_up, w_down, s_down, shared_inter, w_up_shared, s_up_shared, w_down_shared, s_down_shared,
+                       out, out_dtype, workspace, workspace_bytes, stream, err);
 }
 
 }  // extern "C"

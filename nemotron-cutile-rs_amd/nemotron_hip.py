@@ -115,6 +115,11 @@ _SIGNATURES = {
     "nh_moe_workspace_layout": (None, [SZ, SZ, SZ, SZ, SZ, C.POINTER(SZ)]),
     "nh_moe_forward_w8a8": (ST, [P, P, C.c_int, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, P,
                                  C.c_int, P, SZ, P, E]),
+    "nh_moe_combine_shared": (ST, [P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, P, E]),
+    "nh_moe_combine_shared_host": (ST, [P, P, P, P, SZ, SZ, SZ, P, C.c_int, E]),
+    "nh_moe_forward_shared_w8a8_workspace_size": (SZ, [SZ, SZ, SZ, SZ, SZ, SZ]),
+    "nh_moe_forward_shared_w8a8": (ST, [P, P, C.c_int, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, SZ,
+                                        P, P, P, P, P, C.c_int, P, SZ, P, E]),
     "nh_fill_normal_f32_host": (None, [C.c_uint64, C.c_float, C.c_float, P, SZ]),
 }
 

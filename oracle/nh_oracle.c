@@ -515,9 +515,17 @@ void or_moe_grouped_w8a8(const int8_t *aq, const float *sa, int gather_tokens, s
  * expert row from its slot. */
 void or_moe_combine(const float *slot_out, const int32_t *pos, const float *weights, size_t tokens,
                     size_t top_k, size_t hidden, int out_bf16, void *out) {
+    or_moe_combine_shared(slot_out, pos, weights, NULL, tokens, top_k, hidden, out_bf16, out);
+}
+
+/* moe.rs:195-244: the output row starts at 0.0, the shared expert's row is
+ * added (moe.rs:212-219), then each route's weighted output in route order. */
+void or_moe_combine_shared(const float *slot_out, const int32_t *pos, const float *weights, const float *shared,
+                           size_t tokens, size_t top_k, size_t hidden, int out_bf16, void *out) {
     for (size_t t = 0; t < tokens; ++t) {
         for (size_t h = 0; h < hidden; ++h) {
             float v = 0.0f;
+            if (shared) v = v + shared[t * hidden + h];
             for (size_t j = 0; j < top_k; ++j) {
                 size_t r = t * top_k + j;
                 v = v + weights[r] * slot_out[(size_t)pos[r] * hidden + h];
@@ -530,6 +538,36 @@ void or_moe_combine(const float *slot_out, const int32_t *pos, const float *weig
     }
 }
 
+/* int8 MLP of bf16 rows (spec composition, L2 with int8 weights, no biases):
+ * Q2(x) -> W8A8 up with ReLU^2 (f32) -> Q2 -> W8A8 down (f32). */
+int or_mlp_w8a8(const uint16_t *x_bf16, size_t rows, size_t hidden, size_t inter, const int8_t *w_up,
+                const float *s_up, const int8_t *w_down, const float *s_down, float *out) {
+    int8_t *xq = (int8_t *)malloc(rows * hidden + 1);
+    float *sx = (float *)malloc((rows + 1) * sizeof(float));
+    int32_t *acc = (int32_t *)malloc((rows * (inter > hidden ? inter : hidden) + 1) * sizeof(int32_t));
+    float *h = (float *)malloc((rows * inter + 1) * sizeof(float));
+    int8_t *hq = (int8_t *)malloc(rows * inter + 1);
+    float *sh = (float *)malloc((rows + 1) * sizeof(float));
+    or_error err;
+    int st = or_quantize_rows_i8_bf16(x_bf16, rows, hidden, xq, sx, &err);
+    if (st == OR_OK) {
+        or_gemm_i8_i32(xq, w_up, rows, inter, hidden, acc);
+        or_epilogue_w8a8(acc, sx, s_up, NULL, rows, inter, 1, 0, h);
+        st = or_quantize_rows_i8_f32(h, rows, inter, hq, sh, &err);
+    }
+    if (st == OR_OK) {
+        or_gemm_i8_i32(hq, w_down, rows, hidden, inter, acc);
+        or_epilogue_w8a8(acc, sh, s_down, NULL, rows, hidden, 0, 0, out);
+    }
+    free(xq);
+    free(sx);
+    free(acc);
+    free(h);
+    free(hq);
+    free(sh);
+    return st;
+}
+
 /* Full int8 MoE pipeline (spec composition of Q2, R1, R2, R3, R4):
  * x(bf16) -> Q2 -> route -> permute -> up (gather, ReLU^2, f32) -> Q2 ->
  * down (f32 per slot) -> combine -> bf16. */
@@ -538,6 +576,20 @@ int or_moe_forward_w8a8(const uint16_t *x_bf16, const float *logits, size_t toke
                         const int8_t *w_up, const float *s_up, const int8_t *w_down,
                         const float *s_down, uint16_t *out_bf16, int32_t *idx_out, float *w_out,
                         int32_t *offsets_out, int32_t *perm_out, int32_t *pos_out) {
+    return or_moe_forward_shared_w8a8(x_bf16, logits, tokens, hidden, inter, experts, top_k, renormalize, scaling,
+                                      w_up, s_up, w_down, s_down, 0, NULL, NULL, NULL, NULL, out_bf16, idx_out,
+                                      w_out, offsets_out, perm_out, pos_out);
+}
+
+/* The same with a shared expert (w_up_sh not NULL): or_mlp_w8a8 of x, added
+ * by the combine ahead of the routes (moe.rs:197-219). */
+int or_moe_forward_shared_w8a8(const uint16_t *x_bf16, const float *logits, size_t tokens, size_t hidden,
+                               size_t inter, size_t experts, size_t top_k, int renormalize, float scaling,
+                               const int8_t *w_up, const float *s_up, const int8_t *w_down,
+                               const float *s_down, size_t inter_sh, const int8_t *w_up_sh,
+                               const float *s_up_sh, const int8_t *w_down_sh, const float *s_down_sh,
+                               uint16_t *out_bf16, int32_t *idx_out, float *w_out, int32_t *offsets_out,
+                               int32_t *perm_out, int32_t *pos_out) {
     size_t routes = tokens * top_k;
     int8_t *xq = (int8_t *)malloc(tokens * hidden + 1);
     float *sx = (float *)malloc((tokens + 1) * sizeof(float));
@@ -556,11 +608,17 @@ int or_moe_forward_w8a8(const uint16_t *x_bf16, const float *logits, size_t toke
                             h);
         st = or_quantize_rows_i8_f32(h, routes, inter, hq, sh, &err);
     }
+    float *shared = NULL;
+    if (st == OR_OK && w_up_sh) {
+        shared = (float *)malloc((tokens * hidden + 1) * sizeof(float));
+        st = or_mlp_w8a8(x_bf16, tokens, hidden, inter_sh, w_up_sh, s_up_sh, w_down_sh, s_down_sh, shared);
+    }
     if (st == OR_OK) {
         or_moe_grouped_w8a8(hq, sh, 0, top_k, offsets_out, perm_out, experts, w_down, s_down, hidden, inter,
                             0, d);
-        or_moe_combine(d, pos_out, w_out, tokens, top_k, hidden, 1, out_bf16);
+        or_moe_combine_shared(d, pos_out, w_out, shared, tokens, top_k, hidden, 1, out_bf16);
     }
+    free(shared);
     free(xq);
     free(sx);
     free(h);

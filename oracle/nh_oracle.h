@@ -112,6 +112,17 @@ int or_moe_forward_w8a8(const uint16_t *x_bf16, const float *logits, size_t toke
                         const int8_t *w_up, const float *s_up, const int8_t *w_down,
                         const float *s_down, uint16_t *out_bf16, int32_t *idx_out, float *w_out,
                         int32_t *offsets_out, int32_t *perm_out, int32_t *pos_out);
+void or_moe_combine_shared(const float *slot_out, const int32_t *pos, const float *weights, const float *shared,
+                           size_t tokens, size_t top_k, size_t hidden, int out_bf16, void *out);
+int or_mlp_w8a8(const uint16_t *x_bf16, size_t rows, size_t hidden, size_t inter, const int8_t *w_up,
+                const float *s_up, const int8_t *w_down, const float *s_down, float *out);
+int or_moe_forward_shared_w8a8(const uint16_t *x_bf16, const float *logits, size_t tokens, size_t hidden,
+                               size_t inter, size_t experts, size_t top_k, int renormalize, float scaling,
+                               const int8_t *w_up, const float *s_up, const int8_t *w_down,
+                               const float *s_down, size_t inter_sh, const int8_t *w_up_sh,
+                               const float *s_up_sh, const int8_t *w_down_sh, const float *s_down_sh,
+                               uint16_t *out_bf16, int32_t *idx_out, float *w_out, int32_t *offsets_out,
+                               int32_t *perm_out, int32_t *pos_out);
 
 /* ---- L1/L2 and the reference MoE layer (linear.rs, mlp.rs, moe.rs) ------- */
 int or_linear_project(const float *input, size_t input_len, size_t rows, const float *weights,

@@ -79,6 +79,10 @@ def _declare(L):
     L.or_linear_project.argtypes = [P, SZ, SZ, P, SZ, SZ, P, P, SZ, C.POINTER(OrError)]
     L.or_mlp_forward.argtypes = [P, SZ, SZ, SZ, P, P, P, P, P]
     L.or_moe_forward_dense.argtypes = [P, SZ, SZ, SZ, SZ, P, P, SZ, P, P, SZ, P, P, P]
+    L.or_moe_combine_shared.argtypes = [P, P, P, P, SZ, SZ, SZ, C.c_int, P]
+    L.or_mlp_w8a8.argtypes = [P, SZ, SZ, SZ, P, P, P, P, P]
+    L.or_moe_forward_shared_w8a8.argtypes = [P, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, SZ, P, P, P,
+                                             P, P, P, P, P, P, P]
 
 
 def ptr(a):
@@ -257,6 +261,52 @@ def moe_forward_w8a8(x_bf16, logits, w_up, s_up, w_down, s_down, top_k, renormal
                                    tokens, hidden, inter, experts, top_k, int(renormalize), scaling,
                                    ptr(w_up), ptr(s_up), ptr(w_down), ptr(s_down), ptr(out), ptr(idx), ptr(w),
                                    ptr(offsets), ptr(perm), ptr(pos))
+    return st, out, idx, w, offsets, perm, pos
+
+
+def moe_combine_shared(slot_out, pos, weights, shared, tokens, top_k, hidden, out_bf16=False):
+    out = np.zeros((tokens, hidden), dtype=np.uint16 if out_bf16 else np.float32)
+    slot_out = np.ascontiguousarray(slot_out, dtype=np.float32)
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    weights = np.ascontiguousarray(weights, dtype=np.float32)
+    shared = None if shared is None else np.ascontiguousarray(shared, dtype=np.float32)
+    lib().or_moe_combine_shared(ptr(slot_out), ptr(pos), ptr(weights), ptr(shared), tokens, top_k, hidden,
+                                int(out_bf16), ptr(out))
+    return out
+
+
+def mlp_w8a8(x_bf16, w_up, s_up, w_down, s_down):
+    """int8 MLP of bf16 rows: Q2 -> up (ReLU^2, f32) -> Q2 -> down (f32)."""
+    x_bf16 = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    rows, hidden = x_bf16.shape
+    inter = w_up.shape[0]
+    out = np.zeros((rows, hidden), dtype=np.float32)
+    st = lib().or_mlp_w8a8(ptr(x_bf16), rows, hidden, inter, ptr(np.ascontiguousarray(w_up, dtype=np.int8)),
+                           ptr(np.ascontiguousarray(s_up, dtype=np.float32)),
+                           ptr(np.ascontiguousarray(w_down, dtype=np.int8)),
+                           ptr(np.ascontiguousarray(s_down, dtype=np.float32)), ptr(out))
+    return st, out
+
+
+def moe_forward_shared_w8a8(x_bf16, logits, w_up, s_up, w_down, s_down, top_k, sh_up, sh_su, sh_down, sh_sd,
+                            renormalize=True, scaling=1.0):
+    tokens, hidden = x_bf16.shape
+    experts, inter, _ = w_up.shape
+    routes = tokens * top_k
+    out = np.zeros((tokens, hidden), dtype=np.uint16)
+    idx = np.zeros(routes, dtype=np.int32)
+    w = np.zeros(routes, dtype=np.float32)
+    offsets = np.zeros(experts + 1, dtype=np.int32)
+    perm = np.zeros(routes, dtype=np.int32)
+    pos = np.zeros(routes, dtype=np.int32)
+    keep = [np.ascontiguousarray(a, dtype=d) for a, d in ((x_bf16, np.uint16), (logits, np.float32), (w_up, np.int8),
+                                                           (s_up, np.float32), (w_down, np.int8), (s_down, np.float32),
+                                                           (sh_up, np.int8), (sh_su, np.float32), (sh_down, np.int8),
+                                                           (sh_sd, np.float32))]
+    st = lib().or_moe_forward_shared_w8a8(ptr(keep[0]), ptr(keep[1]), tokens, hidden, inter, experts, top_k,
+                                          int(renormalize), scaling, ptr(keep[2]), ptr(keep[3]), ptr(keep[4]),
+                                          ptr(keep[5]), sh_up.shape[0], ptr(keep[6]), ptr(keep[7]), ptr(keep[8]),
+                                          ptr(keep[9]), ptr(out), ptr(idx), ptr(w), ptr(offsets), ptr(perm), ptr(pos))
     return st, out, idx, w, offsets, perm, pos
 
 

@@ -397,3 +397,31 @@ def test_moe_host_twins_match_oracle():
     NH.call("nh_moe_combine_host", out.ctypes.data, pos.ctypes.data, weights.ctypes.data, tokens, k_top, inter,
             comb.ctypes.data, NH.BF16)
     assert np.array_equal(comb, O.moe_combine(out, pos, weights, tokens, k_top, inter, out_bf16=True))
+
+    # with a shared expert's rows, added ahead of the routes
+    shared = rng.standard_normal((tokens, inter)).astype(np.float32)
+    comb_sh = np.zeros((tokens, inter), dtype=np.float32)
+    NH.call("nh_moe_combine_shared_host", out.ctypes.data, pos.ctypes.data, weights.ctypes.data, shared.ctypes.data,
+            tokens, k_top, inter, comb_sh.ctypes.data, NH.F32)
+    assert np.array_equal(comb_sh, O.moe_combine_shared(out, pos, weights, shared, tokens, k_top, inter))
+
+
+def test_moe_forward_shared_validation_before_any_launch():
+    """nh_moe_forward_shared_w8a8 rejects a missing shared expert, an empty
+    shared intermediate and a short workspace before touching the device
+    (NULL context)."""
+    T, H, I, E, K, SI = 4, 64, 32, 8, 2, 48
+    need = NH.lib().nh_moe_forward_shared_w8a8_workspace_size(T, H, I, E, K, SI)
+    assert need > NH.lib().nh_moe_forward_w8a8_workspace_size(T, H, I, E, K)
+
+    def call(si, up_sh, ws_bytes, tokens=T):
+        dummy = 16
+        return NH.call_status("nh_moe_forward_shared_w8a8", None, dummy, NH.BF16, dummy, tokens, H, I, E, K, 1, 1.0,
+                              dummy, dummy, dummy, dummy, si, up_sh, dummy, dummy, dummy, dummy, NH.BF16,
+                              dummy if ws_bytes else None, ws_bytes, None)
+
+    assert call(SI, None, need)[0] == NH.INVALID_PARAMS
+    assert call(0, 16, need)[0] == NH.INVALID_SHAPE
+    assert call(SI, 16, need, tokens=0)[0] == NH.INVALID_ROW_COUNT
+    st, err = call(SI, 16, need - 1)
+    assert st == NH.LENGTH_MISMATCH and err.argument.decode() == "workspace" and err.expected == need

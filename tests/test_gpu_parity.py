@@ -459,7 +459,10 @@ def test_gemv_w8a32_within_tolerance(ctx, m, n, k):
                                    # 256 x 128 tiles at their edges: one K step, fewer K steps than
                                    # ring slots, an odd K-tile count with a partial last tile, ragged
                                    # M and N (a half-valid last weight tile)
-                                   (512, 8192, 64), (1000, 2000, 192), (777, 8200, 1040)])
+                                   (512, 8192, 64), (1000, 2000, 192), (777, 8200, 1040),
+                                   # a sparse last round of 256 x 128 tiles: whole rounds, then the
+                                   # remaining columns as 128 x 128 tiles (also at 2048 x 21504 and 777 x 8200)
+                                   (1100, 9000, 128)])
 @pytest.mark.parametrize("a_layout", ["row-major", "tiled"])
 def test_gemm_w8a8_bit_exact(ctx, m, n, k, a_layout):
     note(f"gemm_w8a8 m={m} n={n} k={k} A {a_layout}")
@@ -617,6 +620,31 @@ def test_expert_gemm_long_segments_bit_exact(ctx, n, k):
                 R, R, experts, d["w"].ptr, d["sw"].ptr, n, k, relu2, out.ptr, None)
         ctx.synchronize()
         assert np.array_equal(out.numpy(), ref)
+
+
+@pytest.mark.parametrize("tokens,hidden,inter,experts,top_k,sh_inter", [(64, 2688, 1856, 128, 6, 3712),
+                                                                         (13, 64, 32, 8, 3, 48)])
+def test_moe_forward_shared_expert_bit_exact(ctx, tokens, hidden, inter, experts, top_k, sh_inter):
+    """The layer with its shared expert (moe.rs:197-219; 3712 wide in the
+    reference config, config.rs:227): the int8 MLP of every token, added to
+    the output row ahead of the routed experts."""
+    note(f"moe forward + shared t={tokens} h={hidden} i={inter} e={experts} k={top_k} si={sh_inter}")
+    x, logits, up, su, down, sd = moe_case(tokens, hidden, inter, experts, top_k)
+    _, hu, hsu = quantized_weights(sh_inter, hidden, seed=30)
+    _, hd, hsd = quantized_weights(hidden, sh_inter, seed=31)
+    st, ref, *_ = O.moe_forward_shared_w8a8(x, logits, up, su, down, sd, top_k, hu, hsu, hd, hsd)
+    assert st == O.OK
+    ws_bytes = NH.lib().nh_moe_forward_shared_w8a8_workspace_size(tokens, hidden, inter, experts, top_k, sh_inter)
+    ws = ctx.empty(ws_bytes, np.uint8)
+    dx, dl = ctx.upload(x), ctx.upload(logits)
+    dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
+    dhu, dhsu, dhd, dhsd = ctx.upload(tile_16x64(hu)), ctx.upload(hsu), ctx.upload(tile_16x64(hd)), ctx.upload(hsd)
+    out = ctx.empty((tokens, hidden), np.uint16)
+    NH.call("nh_moe_forward_shared_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k,
+            1, 1.0, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, sh_inter, dhu.ptr, dhsu.ptr, dhd.ptr, dhsd.ptr, out.ptr,
+            NH.BF16, ws.ptr, ws_bytes, None)
+    ctx.synchronize()
+    assert np.array_equal(out.numpy(), ref)
 
 
 @pytest.mark.parametrize("tokens,hidden,inter,experts,top_k", [(64, 2688, 1856, 128, 6), (13, 64, 32, 8, 3),

@@ -608,3 +608,75 @@ def test_moe_int8_pipeline_equals_dense_reference_when_lossless():
         t, e = r // top_k, idx[r]
         dense = np.maximum(x[t] @ wu[e].T, 0) ** 2
         assert np.array_equal(h[pos[r]], dense.astype(np.float32))
+
+
+# --------------------------------------------------------------------------
+# Shared expert (moe.rs:195-244): the output row starts at 0.0, the shared
+# expert's row is added first, then each route's weighted output in route
+# order.  The values make the order visible in f32: shared first gives
+# (1e8 - 1e8) + 3 = 3; the routes first would give (-1e8 + 3) + 1e8 = 0
+# (f32 spacing at 1e8 is 8).
+def test_moe_combine_shared_adds_the_shared_row_first():
+    slot_out = np.array([[-1e8], [3.0]], dtype=np.float32)
+    pos = np.array([0, 1], dtype=np.int32)
+    w = np.array([1.0, 1.0], dtype=np.float32)
+    shared = np.array([[1e8]], dtype=np.float32)
+    assert O.moe_combine_shared(slot_out, pos, w, shared, 1, 2, 1)[0, 0] == 3.0
+    # without the shared row: exactly or_moe_combine (0 + (-1e8) + 3 = -1e8 in f32)
+    no_sh = O.moe_combine_shared(slot_out, pos, w, None, 1, 2, 1)
+    assert np.array_equal(no_sh, O.moe_combine(slot_out, pos, w, 1, 2, 1))
+    assert no_sh[0, 0] == np.float32(-1e8)
+    # 0.0 + (-0.0) = +0.0: the output starts at +0.0 as output.fill(0.0) does
+    z = O.moe_combine_shared(np.zeros((1, 1), np.float32), np.zeros(1, np.int32), np.zeros(1, np.float32),
+                             np.array([[-0.0]], dtype=np.float32), 1, 1, 1)
+    assert np.signbit(z[0, 0]) == False  # noqa: E712
+
+
+def test_moe_combine_shared_matches_the_dense_reference_layer_kat():
+    # moe.rs:417-435 (pinned through or_moe_forward_dense above): 0.5*4 +
+    # 0.880797*8 + 0.7310586*12 with the shared row first
+    kat = [k for k in KATS["moe"] if k["shared_scale"] is not None][0]
+    x = kat["input"][0]
+    shared = np.array([[kat["shared_scale"] * max(x, 0.0) ** 2]], dtype=np.float32)
+    scores = np.array([O.sigmoid(b) for b in kat["router_b"]], dtype=np.float32)
+    order = sorted(range(kat["experts"]), key=lambda e: (-scores[e], e))[:kat["top_k"]]
+    slot_out = np.array([[kat["expert_scales"][e] * x * x] for e in order], dtype=np.float32)
+    w = scores[order]
+    got = O.moe_combine_shared(slot_out, np.arange(len(order), dtype=np.int32), w, shared, 1, len(order), 1)
+    assert_close(got.ravel(), kat["out"], kat["tol"])
+
+
+def test_mlp_w8a8_composes_its_parts():
+    rows, hidden, inter = 9, 96, 40
+    x = O.to_bf16(O.normal_f32(7, rows * hidden)).reshape(rows, hidden)
+    _, wu, su, _ = O.quantize_rows_f32(O.normal_f32(8, inter * hidden, 0, 0.02).reshape(inter, hidden))
+    _, wd, sd, _ = O.quantize_rows_f32(O.normal_f32(9, hidden * inter, 0, 0.02).reshape(hidden, inter))
+    st, out = O.mlp_w8a8(x, wu, su, wd, sd)
+    assert st == O.OK
+    _, xq, sx, _ = O.quantize_rows_bf16(x)
+    h = O.epilogue(O.gemm_i8_i32(xq, wu), sx, su, relu2=True)
+    _, hq, sh, _ = O.quantize_rows_f32(h)
+    assert np.array_equal(out, O.linear_w8a8(hq, sh, wd, sd))
+
+
+def test_moe_forward_shared_composes_its_parts():
+    tokens, hidden, inter, experts, top_k, sh_inter = 12, 64, 32, 8, 3, 48
+    x = O.to_bf16(O.normal_f32(1, tokens * hidden)).reshape(tokens, hidden)
+    logits = O.normal_f32(2, tokens * experts)
+    _, qu, su, _ = O.quantize_rows_f32(O.normal_f32(3, experts * inter * hidden, 0, 0.02).reshape(-1, hidden))
+    _, qd, sd, _ = O.quantize_rows_f32(O.normal_f32(4, experts * hidden * inter, 0, 0.02).reshape(-1, inter))
+    _, hu, hsu, _ = O.quantize_rows_f32(O.normal_f32(5, sh_inter * hidden, 0, 0.02).reshape(sh_inter, hidden))
+    _, hd, hsd, _ = O.quantize_rows_f32(O.normal_f32(6, hidden * sh_inter, 0, 0.02).reshape(hidden, sh_inter))
+    qu, su = qu.reshape(experts, inter, hidden), su.reshape(experts, inter)
+    qd, sd = qd.reshape(experts, hidden, inter), sd.reshape(experts, hidden)
+    st, out, idx, w, offsets, perm, pos = O.moe_forward_shared_w8a8(x, logits, qu, su, qd, sd, top_k, hu, hsu, hd, hsd)
+    assert st == O.OK
+    st0, out0, idx0, w0, off0, perm0, pos0 = O.moe_forward_w8a8(x, logits, qu, su, qd, sd, top_k)
+    assert np.array_equal(idx, idx0) and np.array_equal(w, w0) and np.array_equal(pos, pos0)
+    _, xq, sx, _ = O.quantize_rows_bf16(x)
+    h = O.moe_grouped(xq, sx, True, top_k, offsets, perm, qu, su, relu2=True)
+    _, hq, sh, _ = O.quantize_rows_f32(h)
+    d = O.moe_grouped(hq, sh, False, top_k, offsets, perm, qd, sd, relu2=False)
+    _, shared = O.mlp_w8a8(x, hu, hsu, hd, hsd)
+    assert np.array_equal(out, O.moe_combine_shared(d, pos, w, shared, tokens, top_k, hidden, out_bf16=True))
+    assert not np.array_equal(out, out0)  # the shared expert contributes
