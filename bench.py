@@ -132,6 +132,34 @@ class Bench:
         self.last_step = step
         return ms, pool, x, out
 
+    def w4a8(self, m, n, k, steps, warmup):
+        """The W4A8 decode unit (nh_linear_w4a8): bf16 rows quantized per token
+        in the GEMV over tiled INT4 weights (per-tensor scale 0.01, zero point
+        8), rotating through a > 512 MiB pool of random codes."""
+        copies = max(2, -(-POOL_BYTES // (n * k // 2)))
+        L, h = NH.lib(), self.ctx.handle
+        packed = np.random.default_rng(7).integers(0, 256, size=(k * n + 1) // 2, dtype=np.uint8)
+        dp = self.ctx.upload(packed)
+        need = L.nh_tiled_int4_weights_bytes(n, k)
+        pool = []
+        for _ in range(copies):
+            t = self.ctx.empty(need, np.uint8)
+            NH.call("nh_tile_weights_int4", h, dp.ptr, packed.size, k, n, 8, t.ptr, need, None)
+            pool.append(t)
+        self.ctx.synchronize()
+        dp.free()
+        x = self.ctx.upload(NH_bf16(NH.normal_f32(1, m * k)).reshape(m, k))
+        out = self.ctx.empty((m, n), np.uint16)
+        err = NH.NhError()
+
+        def step(i):
+            st = L.nh_linear_w4a8(h, x.ptr, NH.BF16, pool[i % len(pool)].ptr, 0.01, 8, None, m, n, k, out.ptr,
+                                  NH.BF16, self.stream, ctypes.byref(err))
+            if st:
+                NH.check(st, err)
+
+        return self.time_ms(step, steps, warmup, out=out)
+
     def gemm(self, m, n, k, steps, warmup):
         """G3 on pre-quantized activations: nh_gemm_w8a8_ta (A in the tiled
         layout, as the linear entry point feeds it) and nh_gemm_w8a8 (row-major
@@ -361,7 +389,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["moe", "gemm", "stack", "decode", "w8a32"], default=None,
+    ap.add_argument("--only", choices=["moe", "gemm", "stack", "decode", "w8a32", "w4a8"], default=None,
                     help="run one secondary workload only (for profiling) and print its figures")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (torch's copy kernel), the "
@@ -393,6 +421,9 @@ def main():
             for (mm, nn, kk) in [(2048, 4096, 4096), (2048, 21504, 4096), (2048, 4096, 21504)]:
                 t, t_rm = b.gemm(mm, nn, kk, 20, 3)
                 res[f"m{mm}_n{nn}_k{kk}"] = {"us": round(t * 1e3, 1), "row_major_a_us": round(t_rm * 1e3, 1)}
+        elif args.only == "w4a8":
+            for (mm, nn, kk) in [(1, 16384, 4096), (4, 16384, 4096), (1, 4096, 8192)]:
+                res[f"m{mm}_k{kk}_n{nn}"] = round(b.w4a8(mm, nn, kk, 50, 5) * 1e3, 2)
         elif args.only == "w8a32":
             res = {"us": round(b.w8a32(4096, 4096, 200, 20) * 1e3, 2)}
         elif args.only == "stack":
@@ -423,6 +454,15 @@ def main():
                                           "GBps": round(decode_bytes(mm, nn, kk) / (t * 1e-3) / 1e9, 1)}
         extra["decode_sweep"] = sweep
         del pool
+        w4 = {}
+        for (mm, nn, kk) in [(1, 16384, 4096), (4, 16384, 4096), (1, 4096, 8192)]:
+            log(f"[bench] w4a8 decode m={mm} k={kk} n={nn}")
+            t = b.w4a8(mm, nn, kk, max(20, args.steps // 4), 5)
+            # int4 codes + bf16 x + bf16 y + f32 token scales (one scale and zero point per tensor)
+            wbytes = nn * kk // 2 + 2 * mm * kk + 2 * mm * nn + 4 * mm + 8
+            w4[f"m{mm}_k{kk}_n{nn}"] = {"us": round(t * 1e3, 2), "GBps": round(wbytes / (t * 1e-3) / 1e9, 1),
+                                        "frac_hbm_peak": round(wbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        extra["w4a8_decode_int4_weights"] = w4
         log("[bench] w8a32 gemv k=4096 n=4096")
         t = b.w8a32(4096, 4096, max(20, args.steps // 4), 5)
         w32_bytes = 4096 * 4096 + 4 * 4096 + 4 * 4096 + 4 * 4096

@@ -294,6 +294,42 @@ nh_status nh_moe_forward_shared_w8a8(nh_context *ctx, const void *x, nh_dtype x_
                                      nh_dtype out_dtype, void *workspace, size_t workspace_bytes, nh_stream stream,
                                      nh_error *err);
 
+/* ---- INT4 affine weights on the device (W4A8), SURVEY §8(f) 3 --------------
+ * The reference's INT4 linear weights (Int4LinearWeights, linear.rs:99-131)
+ * are the [input_dim = K][output_dim = N] matrix of affine codes packed two
+ * per byte, low nibble first (quantize.rs:75-77), with one per-tensor scale
+ * and zero point; the reference materialises them as (code - zp) * scale
+ * (quantize.rs:202-204) and rejects projecting with them
+ * (linear.rs:316-321).  On the device the codes stay 4-bit: code - zp is
+ * exact in int8 (both 0..15), so the layer is the W8A8 linear with weights
+ * (code - zp) and every row scale equal to `scale`, bit-exact with it, at half
+ * the weight bytes. */
+size_t nh_tiled_int4_weights_bytes(size_t n, size_t k);
+/* Offline repack of the reference's packed [k][n] codes into the tiled INT4
+ * layout.  Errors: INVALID_SHAPE (k or n == 0), LENGTH_MISMATCH
+ * "packed_weights" (Int4LinearWeights::validate, linear.rs:113-121) or
+ * "tiled", INVALID_PARAMS (zero_point > 15). */
+nh_status nh_tile_weights_int4(nh_context *ctx, const uint8_t *packed, size_t packed_len, size_t k, size_t n,
+                               uint32_t zero_point, uint8_t *tiled, size_t tiled_len, nh_stream stream,
+                               nh_error *err);
+nh_status nh_tile_weights_int4_host(const uint8_t *packed, size_t packed_len, size_t k, size_t n,
+                                    uint32_t zero_point, uint8_t *tiled, size_t tiled_len, nh_error *err);
+/* W4A8 linear: per-token Q2 of bf16 x fused with the GEMV over tiled INT4
+ * weights, acc = sum_k xq * (code - zp) (int32, exact), y = ((float)acc * sx)
+ * * scale [+ bias].  Device envelope (nh_supports_linear_w4a8): bf16 x, m <=
+ * 16 (groups of 4 rows, each streaming the weights once), k <= 8192, k % 16
+ * == 0; otherwise UNSUPPORTED and the caller takes nh_linear_w4a8_host.
+ * Errors in the reference's order: INVALID_SHAPE, INVALID_PARAMS
+ * (validate_int4_params, quantize.rs:180-186), INVALID_ROW_COUNT. */
+int nh_supports_linear_w4a8(size_t m, size_t n, size_t k);
+nh_status nh_linear_w4a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const uint8_t *w4_tiled, float scale,
+                         uint32_t zero_point, const float *bias, size_t m, size_t n, size_t k, void *out,
+                         nh_dtype out_dtype, nh_stream stream, nh_error *err);
+/* The host twin on the reference's packed layout (f32 or bf16 x, any shape). */
+nh_status nh_linear_w4a8_host(const void *x, nh_dtype x_dtype, const uint8_t *packed, size_t packed_len,
+                              float scale, uint32_t zero_point, const float *bias, size_t m, size_t n, size_t k,
+                              void *out, nh_dtype out_dtype, nh_error *err);
+
 /* ---- synthetic inputs (build-defined seeded generator; the reference has
  *      no RNG): splitmix64 -> Box-Muller (f64) -> f32 ------------------- */
 void nh_fill_normal_f32_host(uint64_t seed, float mean, float stddev, float *out, size_t n);

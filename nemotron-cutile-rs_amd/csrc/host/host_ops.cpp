@@ -217,6 +217,71 @@ nh_status nh_gemm_w8a8_host(const int8_t* xq, const float* sx, const int8_t* wq,
     return NH_OK;
 }
 
+// INT4 [K][N] packed codes -> tiled INT4 (nh_numerics.h), same bytes as the
+// device repack.
+nh_status nh_tile_weights_int4_host(const uint8_t* packed, size_t packed_len, size_t k, size_t n, uint32_t zero_point,
+                                    uint8_t* tiled, size_t tiled_len, nh_error* err) {
+    clear_error(err);
+    size_t kn;
+    if (k == 0 || n == 0 || !mul_ok(k, n, &kn)) return set_error(err, NH_INVALID_SHAPE, "invalid INT4 weight shape");
+    if (packed_len != nh_packed_int4_len(kn)) return mismatch(err, "packed_weights", nh_packed_int4_len(kn), packed_len);
+    if (zero_point > 0x0F) return set_error(err, NH_INVALID_PARAMS, "zero_point %u > 15", zero_point);
+    const size_t need = (size_t)tiled_int4_bytes(n, k);
+    if (tiled_len != need) return mismatch(err, "tiled", need, tiled_len);
+    const size_t kt = (size_t)tiled_k_tiles(k), lanes = need / 8;
+    for (size_t c = 0; c < lanes; ++c) {
+        const size_t t = c >> 6, lane = c & 63;
+        const size_t row = (t / kt) * 16 + (lane & 15), k0 = (t % kt) * 64 + (lane >> 4) * 16;
+        uint8_t* dst = tiled + c * 8;
+        std::memset(dst, 0, 8);
+        for (size_t j = 0; j < 16; ++j) {
+            uint32_t code = zero_point;
+            if (row < n && k0 + j < k) {
+                const size_t i = (k0 + j) * n + row;
+                code = (packed[i >> 1] >> ((i & 1) * 4)) & 15u;
+            }
+            dst[j >> 1] |= (uint8_t)(code << ((j & 1) * 4));
+        }
+    }
+    return NH_OK;
+}
+
+// W4A8 linear on the reference's packed [K][N] INT4 weights: per-token Q2 of
+// x, acc = sum_k xq * (code - zero_point) exactly in int32, y = ((float)acc *
+// sx) * scale [+ bias].
+nh_status nh_linear_w4a8_host(const void* x, nh_dtype x_dtype, const uint8_t* packed, size_t packed_len, float scale,
+                              uint32_t zero_point, const float* bias, size_t m, size_t n, size_t k, void* out,
+                              nh_dtype out_dtype, nh_error* err) {
+    clear_error(err);
+    size_t kn, mk;
+    if (k == 0 || n == 0 || !mul_ok(k, n, &kn)) return set_error(err, NH_INVALID_SHAPE, "invalid linear shape");
+    if (packed_len != nh_packed_int4_len(kn)) return mismatch(err, "packed_weights", nh_packed_int4_len(kn), packed_len);
+    if (!int4_params_ok(scale, zero_point))
+        return set_error(err, NH_INVALID_PARAMS, "invalid INT4 params scale=%g zero_point=%u", (double)scale, zero_point);
+    if (m == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
+    if (out_dtype != NH_F32 && out_dtype != NH_BF16) return set_error(err, NH_INVALID_PARAMS, "unknown dtype");
+    if (!mul_ok(m, k, &mk)) return set_error(err, NH_INVALID_SHAPE, "m*k overflows");
+    std::vector<int8_t> xq(mk);
+    std::vector<float> sx(m);
+    nh_status st = nh_quantize_rows_i8_host(x, x_dtype, m, k, xq.data(), sx.data(), err);
+    if (st) return st;
+    std::vector<int8_t> col(k);
+    for (size_t c = 0; c < n; ++c) {
+        for (size_t d = 0; d < k; ++d) {
+            const size_t i = d * n + c;
+            col[d] = (int8_t)((int)((packed[i >> 1] >> ((i & 1) * 4)) & 15u) - (int)zero_point);
+        }
+        for (size_t r = 0; r < m; ++r) {
+            int32_t acc = 0;
+            for (size_t d = 0; d < k; ++d) acc += (int32_t)xq[r * k + d] * (int32_t)col[d];
+            float y = epilogue_w8a8(acc, sx[r], scale);
+            if (bias) y = y + bias[c];
+            store_f32(out, r * n + c, y, out_dtype);
+        }
+    }
+    return NH_OK;
+}
+
 nh_status nh_gemv_w8a32_host(const float* x, const int8_t* wq, const float* sw, size_t m, size_t n, size_t k,
                              float* y, nh_error* err) {
     clear_error(err);

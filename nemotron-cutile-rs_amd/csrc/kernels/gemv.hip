@@ -146,6 +146,22 @@ extern "C" __global__ __launch_bounds__(512) void nh_gemv_w8a8_xt_kernel(GemvW8A
     gemv_w8a8<true>(a, red);
 }
 
+// int8 B operand from 8 bytes of tiled INT4 codes (16 codes of one lane):
+// the low nibbles and the high nibbles of each word as bytes, i.e. K order
+// 0 2 4 6 1 3 5 7 | 8 10 12 14 9 11 13 15.  The activation codes are stored
+// in the same order (act_order_int4), so the MFMA pairs them correctly, and
+// the zero point is folded out of the sum afterwards.
+__device__ __forceinline__ v4i expand_int4(uint2 q) {
+    return v4i{(int)(q.x & 0x0F0F0F0Fu), (int)((q.x >> 4) & 0x0F0F0F0Fu), (int)(q.y & 0x0F0F0F0Fu),
+               (int)((q.y >> 4) & 0x0F0F0F0Fu)};
+}
+
+// 8 activation codes k0..k7 (little-endian in c0, c1) in the order of
+// expand_int4: k0 k2 k4 k6 | k1 k3 k5 k7.
+__device__ __forceinline__ uint2 act_order_int4(uint32_t c0, uint32_t c1) {
+    return make_uint2(__builtin_amdgcn_perm(c1, c0, 0x06040200u), __builtin_amdgcn_perm(c1, c0, 0x07050301u));
+}
+
 // Decode unit for M <= MM <= 4 rows, K <= 8192: per-token quantization of
 // the bf16 activation rows (Q2) fused in front of the GEMV, one N tile per
 // workgroup (used for one row, and for 2..4 rows when K = 8192).  Every workgroup quantizes the row into LDS itself while its
@@ -158,10 +174,16 @@ extern "C" __global__ __launch_bounds__(512) void nh_gemv_w8a8_xt_kernel(GemvW8A
 // tie decision for the rare value next to a rounding tie, so codes and scales
 // are bit-identical to quantize_i8 in every workgroup; workgroup 0 also
 // writes them out when asked.
-template <int MM>
+// W4: tiled INT4 weights, half the bytes.  Each lane's 8-byte load becomes
+// its MFMA operand with four bitwise ops (expand_int4) against activation
+// codes stored in the matching order; the MFMA sums xq * code, and the zero
+// point comes off as acc - zp * sum_k xq (exact in int32, the row sums from
+// the quantizer); the per-tensor scale replaces the row scales.
+template <int MM, bool W4 = false>
 __device__ __forceinline__ void linear_decode_row(const LinearDecodeArgs& a, int8_t* xs) {
     __shared__ v4i red[8 * 64];
     __shared__ float redf[8][MM];
+    __shared__ int redi[W4 ? 8 : 1][MM];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = a.waves;
     const int T = 64 * W;
     const int M = a.M, N = a.N, K = a.K, kt = a.kt;
@@ -184,11 +206,23 @@ __device__ __forceinline__ void linear_decode_row(const LinearDecodeArgs& a, int
             xv[m][v] = buffer_load16(xrs, (m < M && c < K) ? (m * K + c) * 2 : kOutOfRange);
         }
     const int n = tile * 16 + (lane & 15);
-    const float swn = n < N ? a.sw[n] : 0.0f;
+    const float swn = W4 ? a.w4_scale : n < N ? a.sw[n] : 0.0f;
     const float bn = (a.bias && n < N) ? a.bias[n] : 0.0f;
-    const __amdgpu_buffer_rsrc_t wr = row_tile_rsrc(a.wq, tile, kt);
+    constexpr int kTile = W4 ? 512 : 1024;  // bytes per weight tile
+    // W4 tiles are half the bytes: the whole slab (32 VGPRs) goes out ahead
+    // of the quantizer, twice the int8 head's bytes in flight
+    constexpr int KH = kSlabHead;
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wq + (int64_t)tile * kt * kTile, (uint32_t)kt * kTile);
+    uint2 bq[W4 ? kSlab : 1];
+    auto load_tile = [&](int s) {
+        if constexpr (W4)
+            bq[s] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wr, (wave + s * W) * 512 + lane * 8,
+                                                                                  0, 2));
+        else
+            b[s] = buffer_load16_stream(wr, (wave + s * W) * 1024 + lane * 16);
+    };
 #pragma unroll
-    for (int s = 0; s < kSlabHead; ++s) b[s] = buffer_load16_stream(wr, (wave + s * W) * 1024 + lane * 16);
+    for (int s = 0; s < KH; ++s) load_tile(s);
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. row absmax over the workgroup; every thread derives the scales
@@ -213,7 +247,11 @@ __device__ __forceinline__ void linear_decode_row(const LinearDecodeArgs& a, int
         for (int i = 1; i < W; ++i) r = fmaxf(r, redf[i][m]);
         sx[m] = scale_from_amax(r);
     }
-    // 3. codes into LDS (zeros past K and for rows >= M)
+    // 3. codes into LDS (zeros past K and for rows >= M); W4: each thread's
+    //    share of the row sums of the codes
+    int rsum[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) rsum[m] = 0;
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
         const float rcp = 1.0f / sx[m];
@@ -226,27 +264,55 @@ __device__ __forceinline__ void linear_decode_row(const LinearDecodeArgs& a, int
                 quantize8_bf16(xv[m][v], sx[m], rcp, pow2, code);
                 if (blockIdx.x == 0 && a.xq_out) *(uint2*)(a.xq_out + (int64_t)m * K + c) = make_uint2(code[0], code[1]);
             }
-            *(uint2*)(xs + m * ldx + c) = make_uint2(code[0], code[1]);
+            if constexpr (W4) {
+                rsum[m] = __builtin_amdgcn_sdot4((int)code[0], 0x01010101, rsum[m], false);
+                rsum[m] = __builtin_amdgcn_sdot4((int)code[1], 0x01010101, rsum[m], false);
+                *(uint2*)(xs + m * ldx + c) = act_order_int4(code[0], code[1]);
+            } else {
+                *(uint2*)(xs + m * ldx + c) = make_uint2(code[0], code[1]);
+            }
         }
         if (blockIdx.x == 0 && threadIdx.x == 0 && a.sx_out && m < M) a.sx_out[m] = sx[m];
+    }
+    if constexpr (W4) {
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+            int v = rsum[m];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+            if (lane == 0) redi[wave][m] = v;
+        }
     }
     // the rest of the slab: its loads queue behind the head's while the MFMAs wait
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int s = kSlabHead; s < kSlab; ++s) b[s] = buffer_load16_stream(wr, (wave + s * W) * 1024 + lane * 16);
+    for (int s = KH; s < kSlab; ++s) load_tile(s);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
+    if constexpr (W4) {
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+            int v = redi[0][m];
+            for (int i = 1; i < W; ++i) v += redi[i][m];
+            rsum[m] = v;
+        }
+    }
 
     // 4. MFMAs with A from LDS (lanes of rows >= MM read row 0: discarded outputs)
     const int8_t* xrow = xs + ((lane & 15) < MM ? (lane & 15) : 0) * ldx + (lane >> 4) * 16;
     v4i acc = {0, 0, 0, 0};
 #pragma unroll
-    for (int s = 0; s < kSlab; ++s)
+    for (int s = 0; s < kSlab; ++s) {
+        if constexpr (W4) b[s] = expand_int4(bq[s]);
         acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(*(const v4i*)(xrow + (wave + s * W) * 64), b[s], acc, 0, 0, 0);
+    }
     if (reduce_waves(acc, red, W) && n < N && (lane >> 4) == 0) {
 #pragma unroll
         for (int r = 0; r < MM; ++r)
-            if (r < M) store_y(a.out, a.out_dtype, (int64_t)r * N + n, acc[r], sx[r], swn, a.bias, bn, a.relu2);
+            if (r < M) {
+                const int32_t v = W4 ? acc[r] - a.w4_zp * rsum[r] : acc[r];  // sum xq * (code - zp)
+                store_y(a.out, a.out_dtype, (int64_t)r * N + n, v, sx[r], swn, a.bias, bn, a.relu2);
+            }
     }
 }
 
@@ -392,6 +458,23 @@ extern "C" __global__ __launch_bounds__(512) void nh_linear_decode_w8a8_row2_ker
 extern "C" __global__ __launch_bounds__(512) void nh_linear_decode_w8a8_row4_kernel(LinearDecodeArgs a) {
     extern __shared__ __align__(16) int8_t xs[];  // [4][W * 1024 + 16] codes
     linear_decode_row<4>(a, xs);
+}
+
+// The same decode unit on tiled INT4 weights (W4A8): 1, 2 or 4 rows.
+extern "C" __global__ __launch_bounds__(512) void nh_linear_decode_w4a8_m1_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t xs[];
+    linear_decode_row<1, true>(a, xs);
+}
+
+extern "C" __global__ __launch_bounds__(512) void nh_linear_decode_w4a8_row2_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t xs[];
+    linear_decode_row<2, true>(a, xs);
+}
+
+extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void
+nh_linear_decode_w4a8_row4_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t xs[];
+    linear_decode_row<4, true>(a, xs);
 }
 
 extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_w8a8_m2_kernel(LinearDecodeArgs a) {

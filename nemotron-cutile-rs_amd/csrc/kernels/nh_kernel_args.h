@@ -85,6 +85,8 @@ struct LinearDecodeArgs {
     int32_t out_dtype;
     int32_t ntw;          // N tiles per workgroup
     int32_t relu2;        // ReLU^2 after the bias (the MLP up projection)
+    int32_t w4_zp;        // INT4 weights (tiled_int4): the per-tensor zero point
+    float w4_scale;       //   and scale, used in place of sw
     int32_t pad_;
 };
 
@@ -101,6 +103,16 @@ struct GemvW8A32Args {
 };
 
 // Row-major int8 [N][K] -> tiled, one 16-byte tile chunk per thread.
+// INT4 [K][N] packed codes (the reference's layout) -> tiled_int4.
+struct TileInt4Args {
+    const uint8_t* packed;  // ceil(K * N / 2) bytes
+    uint8_t* tiled;         // tiled_int4_bytes(N, K)
+    int64_t n, k;
+    int64_t lanes;          // tiled_int4_bytes / 8
+    int32_t kt;
+    int32_t zp;
+};
+
 struct TileWeightsArgs {
     const int8_t* w;      // [rows][cols] row-major
     int8_t* tiled;        // tiled_bytes(rows, cols)

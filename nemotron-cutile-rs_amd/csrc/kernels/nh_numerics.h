@@ -115,6 +115,18 @@ NH_HD uint64_t tiled_offset(uint64_t n, uint64_t k, uint64_t kt_count) {
     return (((n >> 4) * kt_count + (k >> 6)) << 10) + (((((k >> 4) & 3) << 4) | (n & 15)) << 4) + (k & 15);
 }
 
+// Tiled INT4 weight layout: the same tiles at half the bytes.  The
+// reference stores INT4 linear weights as the [K][N] matrix (input_dim x
+// output_dim, linear.rs:324) packed two codes per byte, low nibble first, in
+// flat order (quantize.rs:75-77).  Tiled, the logical [N][K] matrix is
+// ceil(N/16) x KT tiles of 512 bytes at (nt * KT + kt) * 512; lane l = 16 g + r
+// of a tile owns bytes [8 l, 8 l + 8), byte j holding W[16 nt + r][64 kt +
+// 16 g + 2 j] in its low nibble and W[..][.. + 2 j + 1] in its high nibble,
+// and the zero point outside the matrix.  One 64-lane 8-byte load of a tile
+// expands (code - zero point) into exactly the int8 B operand of one MFMA K
+// step.
+NH_HD uint64_t tiled_int4_bytes(uint64_t n, uint64_t k) { return (n + 15) / 16 * tiled_k_tiles(k) * 512; }
+
 // Row scale from the row's absolute maximum: one RN division by 127.
 NH_HD float scale_from_amax(float amax) { return amax / 127.0f; }
 

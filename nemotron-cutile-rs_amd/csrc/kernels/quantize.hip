@@ -240,6 +240,30 @@ extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_wave_kernel(Q
         quantize_row_wave<DT_F32, 8>(a);
 }
 
+// INT4 [K][N] codes, low nibble first (the reference's packed layout) -> the
+// tiled INT4 layout (nh_numerics.h): thread c writes the 8 bytes of lane
+// c % 64 of tile c / 64, the zero point outside the matrix.  A one-off
+// repack: the reads gather nibbles N apart.
+extern "C" __global__ __launch_bounds__(256) void nh_tile_weights_int4_kernel(TileInt4Args a) {
+    for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < a.lanes;
+         c += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = c >> 6;
+        const int lane = (int)(c & 63);
+        const int64_t n = (t / a.kt) * 16 + (lane & 15);
+        const int64_t k0 = (t % a.kt) * 64 + (lane >> 4) * 16;
+        uint32_t w[2] = {0, 0};
+        for (int j = 0; j < 16; ++j) {
+            uint32_t code = (uint32_t)a.zp;
+            if (n < a.n && k0 + j < a.k) {
+                const int64_t i = (k0 + j) * a.n + n;
+                code = (a.packed[i >> 1] >> ((i & 1) * 4)) & 15u;
+            }
+            w[j >> 3] |= code << ((j & 7) * 4);
+        }
+        *(uint2*)(a.tiled + c * 8) = make_uint2(w[0], w[1]);
+    }
+}
+
 // Row-major int8 [rows][cols] -> the tiled layout (nh_numerics.h): thread c
 // writes 16-byte chunk c of the tiled buffer (lane c % 64 of tile c / 64),
 // zeros outside the matrix.

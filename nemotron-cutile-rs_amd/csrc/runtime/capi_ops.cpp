@@ -287,6 +287,80 @@ nh_status nh_tile_weights_i8(nh_context* ctx, const int8_t* wq, size_t n, size_t
     return launch(ctx, K_TILE_WEIGHTS, grid_for(a.chunks, 256), 256, 0, stream, a, err);
 }
 
+size_t nh_tiled_int4_weights_bytes(size_t n, size_t k) {
+    if (n == 0 || k == 0 || n > (1ull << 40) || k > (1ull << 40)) return 0;
+    return (size_t)tiled_int4_bytes(n, k);
+}
+
+nh_status nh_tile_weights_int4(nh_context* ctx, const uint8_t* packed, size_t packed_len, size_t k, size_t n,
+                               uint32_t zero_point, uint8_t* tiled, size_t tiled_len, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    size_t kn;
+    if (k == 0 || n == 0 || !mul_ok(k, n, &kn)) return set_error(err, NH_INVALID_SHAPE, "invalid INT4 weight shape");
+    if (packed_len != nh_packed_int4_len(kn)) return mismatch(err, "packed_weights", nh_packed_int4_len(kn), packed_len);
+    if (zero_point > 0x0F) return set_error(err, NH_INVALID_PARAMS, "zero_point %u > 15", zero_point);
+    if (n >= (1u << 31) || k >= (1u << 31)) return set_error(err, NH_UNSUPPORTED, "n and k must be < 2^31");
+    const size_t need = nh_tiled_int4_weights_bytes(n, k);
+    if (tiled_len != need) return mismatch(err, "tiled", need, tiled_len);
+    if (((uintptr_t)tiled & 7u) != 0) return set_error(err, NH_UNSUPPORTED, "tiled must be 8-byte aligned");
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    TileInt4Args a{packed, tiled, (int64_t)n, (int64_t)k, (int64_t)(need / 8), (int)tiled_k_tiles(k), (int)zero_point};
+    return launch(ctx, K_TILE_INT4, grid_for(a.lanes, 256), 256, 0, stream, a, err);
+}
+
+int nh_supports_linear_w4a8(size_t m, size_t n, size_t k) {
+    // the fused decode unit: bf16 rows, K tiles of one slab per wave (k <= 8192), whole 16-byte chunks
+    return m > 0 && m <= 16 && n > 0 && n < (1u << 31) && k > 0 && k <= 8192 && (k % 16) == 0;
+}
+
+nh_status nh_linear_w4a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const uint8_t* w4_tiled, float scale,
+                         uint32_t zero_point, const float* bias, size_t m, size_t n, size_t k, void* out,
+                         nh_dtype out_dtype, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    nh_status st;
+    // the checks of Int4LinearWeights::validate and project_into (linear.rs:113-124, 290-311)
+    if (k == 0 || n == 0) return set_error(err, NH_INVALID_SHAPE, "invalid linear shape k=%zu n=%zu", k, n);
+    if (!std::isfinite(scale) || scale <= 0.0f || zero_point > 0x0F)
+        return set_error(err, NH_INVALID_PARAMS, "invalid INT4 params scale=%g zero_point=%u", (double)scale,
+                         zero_point);
+    if (m == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
+    if ((st = check_dtype(x_dtype, err)) || (st = check_dtype(out_dtype, err))) return st;
+    if (!nh_supports_linear_w4a8(m, n, k) || x_dtype != NH_BF16)
+        return set_error(err, NH_UNSUPPORTED, "W4A8 device path: bf16 x, m <= 16, k <= 8192, k %% 16 == 0 "
+                         "(m=%zu n=%zu k=%zu)", m, n, k);
+    if (!aligned16(x) || ((uintptr_t)w4_tiled & 7u) != 0)
+        return set_error(err, NH_UNSUPPORTED, "x must be 16-byte and w4_tiled 8-byte aligned");
+    if ((st = bind_device(ctx, err))) return st;
+    const int kt = (int)tiled_k_tiles(k), w = gemv_waves(kt);
+    const size_t esz = out_dtype == NH_BF16 ? 2 : 4;
+    // groups of up to 4 rows, each a launch that streams the weights once
+    for (size_t r0 = 0; r0 < m; r0 += 4) {
+        const size_t rows = std::min<size_t>(4, m - r0);
+        const size_t mm = rows == 1 ? 1 : rows <= 2 ? 2 : 4;
+        const KernelId kid = mm == 1 ? K_LINEAR_DECODE_W4_M1 : mm == 2 ? K_LINEAR_DECODE_W4_ROW2 : K_LINEAR_DECODE_W4_ROW4;
+        LinearDecodeArgs a{};
+        a.x = (const uint16_t*)x + r0 * k;
+        a.wq = (const int8_t*)w4_tiled;
+        a.bias = bias;
+        a.out = (char*)out + r0 * n * esz;
+        a.M = (int)rows;
+        a.N = (int)n;
+        a.K = (int)k;
+        a.kt = kt;
+        a.waves = w;
+        a.x_dtype = x_dtype;
+        a.out_dtype = out_dtype;
+        a.ntw = 1;
+        a.w4_zp = (int)zero_point;
+        a.w4_scale = scale;
+        const size_t lds = mm * ((size_t)w * 1024 + 16);
+        if (lds > ctx->max_shared_per_block) return set_error(err, NH_UNSUPPORTED, "LDS too small");
+        if ((st = launch(ctx, kid, (unsigned)((n + 15) / 16), (unsigned)(64 * w), lds, stream, a, err))) return st;
+    }
+    return NH_OK;
+}
+
 nh_status nh_dequantize_i8(nh_context* ctx, const int8_t* q, const float* scales, size_t rows, size_t cols,
                            float* out, nh_stream stream, nh_error* err) {
     clear_error(err);

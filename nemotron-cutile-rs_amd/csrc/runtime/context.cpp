@@ -37,6 +37,10 @@ const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
     "nh_moe_expert_gemm_kernel",         // K_EXPERT_GEMM
     "nh_quantize_rows_wave_kernel",      // K_QUANTIZE_ROWS_WAVE
     "nh_quantize_rows_long_kernel",      // K_QUANTIZE_ROWS_LONG
+    "nh_tile_weights_int4_kernel",       // K_TILE_INT4
+    "nh_linear_decode_w4a8_m1_kernel",   // K_LINEAR_DECODE_W4_M1
+    "nh_linear_decode_w4a8_row2_kernel", // K_LINEAR_DECODE_W4_ROW2
+    "nh_linear_decode_w4a8_row4_kernel", // K_LINEAR_DECODE_W4_ROW4
 };
 
 void clear_error(nh_error* err) {

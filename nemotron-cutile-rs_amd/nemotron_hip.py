@@ -120,6 +120,12 @@ _SIGNATURES = {
     "nh_moe_forward_shared_w8a8_workspace_size": (SZ, [SZ, SZ, SZ, SZ, SZ, SZ]),
     "nh_moe_forward_shared_w8a8": (ST, [P, P, C.c_int, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, SZ,
                                         P, P, P, P, P, C.c_int, P, SZ, P, E]),
+    "nh_tiled_int4_weights_bytes": (SZ, [SZ, SZ]),
+    "nh_tile_weights_int4": (ST, [P, P, SZ, SZ, SZ, C.c_uint32, P, SZ, P, E]),
+    "nh_tile_weights_int4_host": (ST, [P, SZ, SZ, SZ, C.c_uint32, P, SZ, E]),
+    "nh_supports_linear_w4a8": (C.c_int, [SZ, SZ, SZ]),
+    "nh_linear_w4a8": (ST, [P, P, C.c_int, P, C.c_float, C.c_uint32, P, SZ, SZ, SZ, P, C.c_int, P, E]),
+    "nh_linear_w4a8_host": (ST, [P, C.c_int, P, SZ, C.c_float, C.c_uint32, P, SZ, SZ, SZ, P, C.c_int, E]),
     "nh_fill_normal_f32_host": (None, [C.c_uint64, C.c_float, C.c_float, P, SZ]),
 }
 

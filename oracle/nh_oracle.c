@@ -628,6 +628,39 @@ int or_moe_forward_shared_w8a8(const uint16_t *x_bf16, const float *logits, size
     return st;
 }
 
+/* W4A8 linear (spec): the reference's INT4 linear weights
+ * (packed [K][N] affine codes, low nibble first, quantize.rs:75-77; one scale
+ * and zero point, linear.rs:99-131) with per-token Q2 of bf16 x:
+ * acc[m][n] = sum_k xq[m][k] * (code[k][n] - zp), exact in int32, then the
+ * W8A8 epilogue with sw[n] = scale. */
+int or_linear_w4a8(const uint16_t *x_bf16, size_t m, size_t k, const uint8_t *packed, size_t n, float scale,
+                   uint32_t zp, const float *bias, int out_bf16, void *out) {
+    int8_t *xq = (int8_t *)malloc(m * k + 1);
+    float *sx = (float *)malloc((m + 1) * sizeof(float));
+    int8_t *w = (int8_t *)malloc(n * k + 1); /* [N][K] = code - zp, transposed from [K][N] */
+    int32_t *acc = (int32_t *)malloc((m * n + 1) * sizeof(int32_t));
+    float *sw = (float *)malloc((n + 1) * sizeof(float));
+    or_error err;
+    int st = or_quantize_rows_i8_bf16(x_bf16, m, k, xq, sx, &err);
+    if (st == OR_OK) {
+        for (size_t kk = 0; kk < k; ++kk)
+            for (size_t c = 0; c < n; ++c) {
+                size_t i = kk * n + c;
+                int code = (packed[i / 2] >> (4 * (i % 2))) & 15;
+                w[c * k + kk] = (int8_t)(code - (int)zp);
+            }
+        for (size_t c = 0; c < n; ++c) sw[c] = scale;
+        or_gemm_i8_i32(xq, w, m, n, k, acc);
+        or_epilogue_w8a8(acc, sx, sw, bias, m, n, 0, out_bf16, out);
+    }
+    free(xq);
+    free(sx);
+    free(w);
+    free(acc);
+    free(sw);
+    return st;
+}
+
 /* ------------------------------------------------------------------------ */
 /* L1: linear.rs:283-342 (project_into): row_count, input and output lengths
  * are checked, weights are [in_dim, out_dim] row-major (linear.rs:324), then

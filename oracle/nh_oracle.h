@@ -124,6 +124,10 @@ int or_moe_forward_shared_w8a8(const uint16_t *x_bf16, const float *logits, size
                                uint16_t *out_bf16, int32_t *idx_out, float *w_out, int32_t *offsets_out,
                                int32_t *perm_out, int32_t *pos_out);
 
+/* ---- W4A8: the reference's INT4 linear weights with int8 activations ---- */
+int or_linear_w4a8(const uint16_t *x_bf16, size_t m, size_t k, const uint8_t *packed, size_t n, float scale,
+                   uint32_t zp, const float *bias, int out_bf16, void *out);
+
 /* ---- L1/L2 and the reference MoE layer (linear.rs, mlp.rs, moe.rs) ------- */
 int or_linear_project(const float *input, size_t input_len, size_t rows, const float *weights,
                       size_t in_dim, size_t out_dim, const float *bias, float *out, size_t out_len,

@@ -80,6 +80,7 @@ def _declare(L):
     L.or_mlp_forward.argtypes = [P, SZ, SZ, SZ, P, P, P, P, P]
     L.or_moe_forward_dense.argtypes = [P, SZ, SZ, SZ, SZ, P, P, SZ, P, P, SZ, P, P, P]
     L.or_moe_combine_shared.argtypes = [P, P, P, P, SZ, SZ, SZ, C.c_int, P]
+    L.or_linear_w4a8.argtypes = [P, SZ, SZ, P, SZ, C.c_float, C.c_uint32, P, C.c_int, P]
     L.or_mlp_w8a8.argtypes = [P, SZ, SZ, SZ, P, P, P, P, P]
     L.or_moe_forward_shared_w8a8.argtypes = [P, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, SZ, P, P, P,
                                              P, P, P, P, P, P, P]
@@ -308,6 +309,33 @@ def moe_forward_shared_w8a8(x_bf16, logits, w_up, s_up, w_down, s_down, top_k, s
                                           ptr(keep[5]), sh_up.shape[0], ptr(keep[6]), ptr(keep[7]), ptr(keep[8]),
                                           ptr(keep[9]), ptr(out), ptr(idx), ptr(w), ptr(offsets), ptr(perm), ptr(pos))
     return st, out, idx, w, offsets, perm, pos
+
+
+def quantize_int4(values, scale, zp):
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    packed = np.zeros((values.size + 1) // 2, dtype=np.uint8)
+    err = OrError()
+    st = lib().or_quantize_int4(ptr(values), values.size, scale, zp, ptr(packed), packed.size, C.byref(err))
+    return st, packed, err
+
+
+def dequantize_int4(packed, count, scale, zp):
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    out = np.zeros(count, dtype=np.float32)
+    err = OrError()
+    st = lib().or_dequantize_int4(ptr(packed), packed.size, count, scale, zp, ptr(out), count, C.byref(err))
+    return st, out, err
+
+
+def linear_w4a8(x_bf16, packed, n, scale, zp, bias=None, out_bf16=False):
+    """W4A8 linear on the reference's packed [K][N] INT4 codes."""
+    x_bf16 = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    m, k = x_bf16.shape
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    bias = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    out = np.zeros((m, n), dtype=np.uint16 if out_bf16 else np.float32)
+    st = lib().or_linear_w4a8(ptr(x_bf16), m, k, ptr(packed), n, scale, zp, ptr(bias), int(out_bf16), ptr(out))
+    return st, out
 
 
 def sigmoid(x):

@@ -425,3 +425,55 @@ def test_moe_forward_shared_validation_before_any_launch():
     assert call(SI, 16, need, tokens=0)[0] == NH.INVALID_ROW_COUNT
     st, err = call(SI, 16, need - 1)
     assert st == NH.LENGTH_MISMATCH and err.argument.decode() == "workspace" and err.expected == need
+
+
+def test_int4_host_twins_match_oracle_and_layout():
+    from tiling import tile_int4
+    rng = np.random.default_rng(12)
+    for (m, k, n, zp) in [(1, 64, 16, 8), (3, 200, 33, 0), (5, 1040, 100, 15)]:
+        packed = rng.integers(0, 256, size=(k * n + 1) // 2, dtype=np.uint8)
+        need = NH.lib().nh_tiled_int4_weights_bytes(n, k)
+        assert need == (n + 15) // 16 * ((k + 63) // 64) * 512
+        tiled = np.zeros(need, dtype=np.uint8)
+        NH.call("nh_tile_weights_int4_host", packed.ctypes.data, packed.size, k, n, zp, tiled.ctypes.data, need)
+        assert np.array_equal(tiled, tile_int4(packed, k, n, zp))
+        x = O.to_bf16(O.normal_f32(7, m * k)).reshape(m, k)
+        bias = rng.standard_normal(n).astype(np.float32)
+        for out_dtype, bf in ((NH.BF16, True), (NH.F32, False)):
+            y = np.zeros((m, n), dtype=np.uint16 if bf else np.float32)
+            NH.call("nh_linear_w4a8_host", x.ctypes.data, NH.BF16, packed.ctypes.data, packed.size, 0.0123, zp,
+                    bias.ctypes.data, m, n, k, y.ctypes.data, out_dtype)
+            st, ref = O.linear_w4a8(x, packed, n, 0.0123, zp, bias=bias, out_bf16=bf)
+            assert st == O.OK and np.array_equal(y, ref)
+        # f32 rows holding bf16 values quantize exactly like the bf16 rows
+        xf = (x.astype(np.uint32) << 16).view(np.float32)
+        y = np.zeros((m, n), dtype=np.float32)
+        NH.call("nh_linear_w4a8_host", xf.ctypes.data, NH.F32, packed.ctypes.data, packed.size, 0.0123, zp,
+                None, m, n, k, y.ctypes.data, NH.F32)
+        assert np.array_equal(y, O.linear_w4a8(x, packed, n, 0.0123, zp)[1])
+
+
+def test_int4_validation_in_the_reference_order():
+    packed = np.zeros(2, dtype=np.uint8)
+    y = np.zeros(4, dtype=np.float32)
+    x = np.zeros(4, dtype=np.float32)
+
+    def host(k, n, plen, scale, zp, m):
+        return NH.call_status("nh_linear_w4a8_host", x.ctypes.data, NH.F32, packed.ctypes.data, plen, scale, zp,
+                              None, m, n, k, y.ctypes.data, NH.F32)
+    assert host(0, 2, 0, 0.5, 8, 1)[0] == NH.INVALID_SHAPE
+    st, err = host(2, 2, 1, 0.5, 8, 1)  # linear.rs:113-121
+    assert st == NH.LENGTH_MISMATCH and (err.argument.decode(), err.expected, err.actual) == ("packed_weights", 2, 1)
+    assert host(2, 2, 2, 0.0, 8, 1)[0] == NH.INVALID_PARAMS  # quantize.rs:180-186
+    assert host(2, 2, 2, float("nan"), 8, 1)[0] == NH.INVALID_PARAMS
+    assert host(2, 2, 2, 0.5, 16, 1)[0] == NH.INVALID_PARAMS
+    assert host(2, 2, 2, 0.5, 8, 0)[0] == NH.INVALID_ROW_COUNT
+    # the device entry point validates before touching the (NULL) context
+    dev = lambda m, n, k, scale=0.5, zp=8: NH.call_status(  # noqa: E731
+        "nh_linear_w4a8", None, 16, NH.BF16, 16, scale, zp, None, m, n, k, 16, NH.BF16, None)[0]
+    assert dev(1, 0, 64) == NH.INVALID_SHAPE
+    assert dev(1, 16, 64, scale=-1.0) == NH.INVALID_PARAMS
+    assert dev(0, 16, 64) == NH.INVALID_ROW_COUNT
+    assert dev(17, 16, 64) == NH.UNSUPPORTED and dev(1, 16, 8192 + 16) == NH.UNSUPPORTED and dev(1, 16, 72) == NH.UNSUPPORTED
+    st, err = NH.call_status("nh_tile_weights_int4", None, 16, 3, 2, 2, 8, 16, 512, None)
+    assert st == NH.LENGTH_MISMATCH and err.argument.decode() == "packed_weights"

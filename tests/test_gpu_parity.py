@@ -453,6 +453,34 @@ def test_gemv_w8a32_within_tolerance(ctx, m, n, k):
     assert ulps.max() <= 1
 
 
+# ---- W4A8: the reference's INT4 linear weights, tiled, with the fused quantizer ----
+@pytest.mark.parametrize("m,n,k,zp", [(1, 16384, 4096, 8), (1, 4096, 8192, 0), (2, 100, 1040, 15), (3, 4096, 4096, 7),
+                                      (4, 33, 64, 8), (7, 4096, 4096, 3), (16, 1000, 2048, 9)])
+def test_linear_w4a8_bit_exact(ctx, m, n, k, zp):
+    from tiling import tile_int4
+    note(f"linear_w4a8 m={m} n={n} k={k} zp={zp}")
+    rng = np.random.default_rng(m * 1000 + zp)
+    packed = rng.integers(0, 256, size=(k * n + 1) // 2, dtype=np.uint8)
+    scale = 0.0137
+    x = activations_bf16(m, k)
+    bias = rng.standard_normal(n).astype(np.float32) if m % 2 else None
+    need = NH.lib().nh_tiled_int4_weights_bytes(n, k)
+    dp, dt = ctx.upload(packed), ctx.empty(need, np.uint8)
+    NH.call("nh_tile_weights_int4", ctx.handle, dp.ptr, packed.size, k, n, zp, dt.ptr, need, None)
+    ctx.synchronize()
+    assert np.array_equal(dt.numpy(), tile_int4(packed, k, n, zp))
+    dx = ctx.upload(x)
+    db = ctx.upload(bias) if bias is not None else None
+    for out_dtype, bf in ((NH.BF16, True), (NH.F32, False)):
+        out = ctx.empty((m, n), np.uint16 if bf else np.float32)
+        NH.call("nh_linear_w4a8", ctx.handle, dx.ptr, NH.BF16, dt.ptr, scale, zp, db.ptr if db else None, m, n, k,
+                out.ptr, out_dtype, None)
+        ctx.synchronize()
+        st, ref = O.linear_w4a8(x, packed, n, scale, zp, bias=bias, out_bf16=bf)
+        assert st == O.OK
+        assert np.array_equal(out.numpy(), ref)
+
+
 # ---- G3: W8A8 GEMM (prefill) -----------------------------------------------------
 @pytest.mark.parametrize("m,n,k", [(2048, 4096, 4096), (2048, 21504, 4096), (2048, 4096, 21504), (37, 100, 64),
                                    (300, 130, 272), (17, 4096, 4096), (513, 2688, 1856),

@@ -680,3 +680,61 @@ def test_moe_forward_shared_composes_its_parts():
     _, shared = O.mlp_w8a8(x, hu, hsu, hd, hsd)
     assert np.array_equal(out, O.moe_combine_shared(d, pos, w, shared, tokens, top_k, hidden, out_bf16=True))
     assert not np.array_equal(out, out0)  # the shared expert contributes
+
+
+# --------------------------------------------------------------------------
+# W4A8: the reference's INT4 linear weights (packed [K][N] affine codes) with
+# per-token int8 activations.
+def _int4_codes(packed, k, n):
+    flat = np.empty(packed.size * 2, dtype=np.int64)
+    flat[0::2], flat[1::2] = packed & 15, packed >> 4
+    return flat[:k * n].reshape(k, n)
+
+
+def test_linear_w4a8_reference_int4_layer_kat():
+    # linear.rs:493-502: params (0.5, 8), values [0.5, 1.0, -0.5, 0.0] as a
+    # 2 x 2 [input][output] layer materialise to the same values; projected
+    # on the lossless row x = [127, -3] (scale 1): [127*0.5 + 3*0.5, 127*1.0]
+    st, packed, _ = O.quantize_int4(np.array([0.5, 1.0, -0.5, 0.0], dtype=np.float32), 0.5, 8)
+    assert st == O.OK
+    st, dense, _ = O.dequantize_int4(packed, 4, 0.5, 8)
+    assert st == O.OK and np.array_equal(dense, np.array([0.5, 1.0, -0.5, 0.0], dtype=np.float32))
+    x = O.to_bf16(np.array([[127.0, -3.0]], dtype=np.float32))
+    st, y = O.linear_w4a8(x, packed, 2, 0.5, 8)
+    assert st == O.OK
+    assert np.array_equal(y, np.array([[65.0, 127.0]], dtype=np.float32))
+
+
+def test_linear_w4a8_equals_reference_dense_path_when_lossless():
+    # Integer activations with a 127 in every row quantize with scale 1; a
+    # power-of-two weight scale makes every (code - zp) * s exact, and the
+    # sums are exact in f64: then W4A8 must equal materialize_dense +
+    # gemm_into_host + bias (linear.rs:126-131, 325-339) to the bit.
+    rng = np.random.default_rng(4)
+    m, k, n, zp, scale = 3, 96, 40, 6, 2.0 ** -6
+    packed = rng.integers(0, 256, size=k * n // 2, dtype=np.uint8)
+    x = rng.integers(-100, 101, size=(m, k)).astype(np.float32)
+    x[:, 5] = 127.0
+    bias = rng.integers(-8, 9, size=n).astype(np.float32)
+    st, y = O.linear_w4a8(O.to_bf16(x), packed, n, scale, zp, bias=bias)
+    assert st == O.OK
+    st, dense, _ = O.dequantize_int4(packed, k * n, scale, zp)
+    assert st == O.OK
+    ref = np.zeros(m * n, dtype=np.float32)
+    st = O.lib().or_linear_project(O.ptr(x), m * k, m, O.ptr(dense), k, n, O.ptr(bias), O.ptr(ref), m * n, None)
+    assert st == O.OK
+    assert np.array_equal(y.ravel(), ref)
+
+
+def test_linear_w4a8_brute_force():
+    rng = np.random.default_rng(5)
+    m, k, n, zp, scale = 4, 200, 33, 11, 0.0173
+    packed = rng.integers(0, 256, size=(k * n + 1) // 2, dtype=np.uint8)
+    x = O.to_bf16(O.normal_f32(6, m * k)).reshape(m, k)
+    st, y = O.linear_w4a8(x, packed, n, scale, zp)
+    assert st == O.OK
+    _, xq, sx, _ = O.quantize_rows_bf16(x)
+    acc = xq.astype(np.int64) @ (_int4_codes(packed, k, n) - zp)  # [m][n]
+    assert np.abs(acc).max() < 2 ** 31
+    ref = (acc.astype(np.float32) * sx[:, None]).astype(np.float32) * np.float32(scale)
+    assert np.array_equal(y, ref.astype(np.float32))

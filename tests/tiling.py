@@ -27,3 +27,20 @@ def tile_experts(w):
 
 def tiled_bytes(n, k):
     return -(-n // 16) * 16 * -(-k // 64) * 64
+
+
+def tile_int4(packed, k, n, zp):
+    """The reference's packed [k][n] INT4 codes (low nibble first) -> the
+    tiled INT4 layout: 512-byte tiles of 16 rows (n) x 64 codes (k); lane
+    l = 16 g + r holds bytes [8 l, 8 l + 8), byte j = codes k = 64 kt + 16 g
+    + 2 j (low nibble) and + 2 j + 1 (high); the zero point outside."""
+    packed = np.asarray(packed, dtype=np.uint8)
+    flat = np.empty(packed.size * 2, dtype=np.uint8)
+    flat[0::2], flat[1::2] = packed & 15, packed >> 4
+    codes = flat[:k * n].reshape(k, n).T  # [n][k]
+    nt, kt = (n + 15) // 16, (k + 63) // 64
+    full = np.full((nt * 16, kt * 64), zp, dtype=np.uint8)
+    full[:n, :k] = codes
+    t = full.reshape(nt, 16, kt, 4, 16).transpose(0, 2, 3, 1, 4)  # [nt][kt][g][r][16 codes]
+    t = t.reshape(nt, kt, 64, 8, 2)
+    return (t[..., 0] | (t[..., 1] << 4)).astype(np.uint8).ravel()
