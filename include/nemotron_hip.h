@@ -51,7 +51,10 @@ typedef enum nh_status {
     NH_OUT_OF_RANGE = 5,      /* QuantizeError::Int4OutOfRange(u8) */
     NH_INVALID_ROW_COUNT = 6, /* LinearError::InvalidRowCount */
     NH_UNSUPPORTED = 7,       /* shape outside the device envelope: use the *_host twin */
-    NH_DEVICE_ERROR = 8       /* *Error::DeviceError(String) */
+    NH_DEVICE_ERROR = 8,      /* *Error::DeviceError(String) */
+    NH_IO_ERROR = 9,          /* WeightError::Io */
+    NH_INVALID_HEADER = 10,   /* WeightError::InvalidHeaderLength / InvalidHeaderJson / InvalidTensorHeader */
+    NH_TENSOR_NOT_FOUND = 11  /* WeightError::TensorNotFound */
 } nh_status;
 
 typedef struct nh_error {
@@ -329,6 +332,36 @@ nh_status nh_linear_w4a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const
 nh_status nh_linear_w4a8_host(const void *x, nh_dtype x_dtype, const uint8_t *packed, size_t packed_len,
                               float scale, uint32_t zero_point, const float *bias, size_t m, size_t n, size_t k,
                               void *out, nh_dtype out_dtype, nh_error *err);
+
+/* ---- safetensors weights into device memory, SURVEY §8(f) 2 -------------
+ * One .safetensors file: the 8-byte little-endian header length, the JSON
+ * header, the data section (WeightManifest::load_tensor and
+ * read_safetensors_header, nemotron-model/src/weights.rs:161-267).  Every
+ * tensor entry is validated as RawTensorHeader::from_value does
+ * (weights.rs:276-358) before the lookup.  Errors: IO_ERROR (WeightError::Io),
+ * INVALID_HEADER (InvalidHeaderLength: expected = file length, actual = the
+ * header length; InvalidHeaderJson; InvalidTensorHeader with the reference's
+ * reason text), TENSOR_NOT_FOUND ("tensor not found: <name>"). */
+typedef struct nh_tensor_info {
+    char dtype[16];      /* the header's dtype string: "I8", "F32", "BF16", "U8", ... */
+    uint32_t ndim;
+    uint64_t shape[8];
+    uint64_t data_begin; /* absolute byte offset of the tensor's data in the file */
+    uint64_t data_bytes; /* data_offsets end - start */
+} nh_tensor_info;
+nh_status nh_safetensors_tensor_info(const char *path, const char *name, nh_tensor_info *info, nh_error *err);
+/* The tensor's raw bytes into dst (device memory of exactly data_bytes:
+ * LENGTH_MISMATCH "dst" otherwise); synchronous. */
+nh_status nh_safetensors_read(nh_context *ctx, const char *path, const char *name, void *dst, size_t dst_len,
+                              nh_error *err);
+/* An int8 per-row linear layer from a file: codes_name I8 [n][k] (output
+ * rows) and scales_name F32 [n], into the tiled layout (tiled_len =
+ * nh_tiled_weights_bytes(n, k)) and device scales, through a device staging
+ * buffer of at least n * k bytes; synchronous.  INVALID_SHAPE for a dtype or
+ * shape other than those. */
+nh_status nh_load_linear_i8(nh_context *ctx, const char *path, const char *codes_name, const char *scales_name,
+                            size_t n, size_t k, void *staging, size_t staging_len, int8_t *tiled, size_t tiled_len,
+                            float *scales, nh_error *err);
 
 /* ---- synthetic inputs (build-defined seeded generator; the reference has
  *      no RNG): splitmix64 -> Box-Muller (f64) -> f32 ------------------- */

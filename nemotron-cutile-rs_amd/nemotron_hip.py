@@ -24,8 +24,17 @@ OUT_OF_RANGE = 5
 INVALID_ROW_COUNT = 6
 UNSUPPORTED = 7
 DEVICE_ERROR = 8
+IO_ERROR = 9
+INVALID_HEADER = 10
+TENSOR_NOT_FOUND = 11
 STATUS_NAMES = {0: "Ok", 1: "InvalidShape", 2: "LengthMismatch", 3: "InvalidParams", 4: "NonFiniteInput",
-                5: "Int4OutOfRange", 6: "InvalidRowCount", 7: "Unsupported", 8: "DeviceError"}
+                5: "Int4OutOfRange", 6: "InvalidRowCount", 7: "Unsupported", 8: "DeviceError", 9: "Io",
+                10: "InvalidHeader", 11: "TensorNotFound"}
+
+
+class TensorInfo(C.Structure):
+    _fields_ = [("dtype", C.c_char * 16), ("ndim", C.c_uint32), ("shape", C.c_uint64 * 8),
+                ("data_begin", C.c_uint64), ("data_bytes", C.c_uint64)]
 
 F32 = 0
 BF16 = 1
@@ -126,6 +135,9 @@ _SIGNATURES = {
     "nh_supports_linear_w4a8": (C.c_int, [SZ, SZ, SZ]),
     "nh_linear_w4a8": (ST, [P, P, C.c_int, P, C.c_float, C.c_uint32, P, SZ, SZ, SZ, P, C.c_int, P, E]),
     "nh_linear_w4a8_host": (ST, [P, C.c_int, P, SZ, C.c_float, C.c_uint32, P, SZ, SZ, SZ, P, C.c_int, E]),
+    "nh_safetensors_tensor_info": (ST, [C.c_char_p, C.c_char_p, C.POINTER(TensorInfo), E]),
+    "nh_safetensors_read": (ST, [P, C.c_char_p, C.c_char_p, P, SZ, E]),
+    "nh_load_linear_i8": (ST, [P, C.c_char_p, C.c_char_p, C.c_char_p, SZ, SZ, P, SZ, P, SZ, P, E]),
     "nh_fill_normal_f32_host": (None, [C.c_uint64, C.c_float, C.c_float, P, SZ]),
 }
 
