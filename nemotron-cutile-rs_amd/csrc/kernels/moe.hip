@@ -80,6 +80,104 @@ extern "C" __global__ __launch_bounds__(256) void nh_moe_route_sigmoid_kernel(Ro
 // phase 3 walks the routes in order in rounds of 1024 and gives every route
 // its stable rank: inside a wave by ballot-matching equal experts, across
 // waves by handing a running per-expert base from wave to wave in order.
+// R2 in four barriers, for routes x experts that fit a table in LDS: the
+// same stable counting sort by (expert, route id) as nh_moe_permute_kernel.
+//  1. every wave matches the experts of its 64 routes (ballots over the
+//     expert's bits: the lanes holding the same expert) and its leaders
+//     write the per-(round, wave) count of each expert into the table;
+//  2. each expert scans its column of the table in (round, wave) order:
+//     the column entries become the slot bases within the expert, and the
+//     totals the expert counts;
+//  3. wave 0 scans the counts into the offsets;
+//  4. every route takes slot = offsets[e] + base[round][wave][e] + its rank
+//     among the earlier lanes of its wave holding the same expert.
+// Routes are visited in id order within each step, so the slots are the
+// stable order of the per-wave serial kernel.  Table: rounds * NW * E ints.
+extern "C" __global__ __launch_bounds__(1024) void nh_moe_permute_table_kernel(PermuteArgs a) {
+    extern __shared__ int sm[];  // table[rounds][NW][E], then offsets[E]
+    const int E = a.experts, R = a.routes;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NW = blockDim.x >> 6;
+    const int rounds = (R + (int)blockDim.x - 1) / (int)blockDim.x;
+    int* table = sm;
+    int* off = sm + rounds * NW * E;
+    for (int i = tid; i < rounds * NW * E; i += blockDim.x) table[i] = 0;
+    __syncthreads();
+    int nbits = 0;
+    while ((1 << nbits) < E) ++nbits;
+    // the lanes of this wave holding expert e (valid routes only), this lane's rank among them
+    auto match = [&](int r, int* e_out, int* rank, int* cnt, bool* leader) {
+        const int ein = r < R ? a.indices[r] : -1;
+        const bool valid = ein >= 0 && ein < E;
+        const int e = valid ? ein : -1;
+        uint64_t mask = __ballot(valid);
+        for (int b = 0; b < nbits; ++b) {
+            const uint64_t bal = __ballot(valid && ((e >> b) & 1));
+            mask &= ((e >> b) & 1) ? bal : ~bal;
+        }
+        const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        *e_out = e;
+        *rank = __popcll(mask & lt);
+        *cnt = __popcll(mask);
+        *leader = valid && (mask & lt) == 0;
+    };
+    // 1.
+    for (int rd = 0; rd < rounds; ++rd) {
+        int e, rank, cnt;
+        bool leader;
+        match(rd * (int)blockDim.x + tid, &e, &rank, &cnt, &leader);
+        if (leader) table[(rd * NW + wave) * E + e] = cnt;
+    }
+    __syncthreads();
+    // 2.
+    for (int e = tid; e < E; e += blockDim.x) {
+        int run = 0;
+        for (int i = 0; i < rounds * NW; ++i) {
+            const int c = table[i * E + e];
+            table[i * E + e] = run;
+            run += c;
+        }
+        off[e] = run;
+    }
+    __syncthreads();
+    // 3.
+    if (wave == 0) {
+        int carry = 0;
+        for (int base = 0; base < E; base += 64) {
+            const int e = base + lane;
+            const int c = e < E ? off[e] : 0;
+            int v = c;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int t = __shfl_up(v, o, kWave);
+                if (lane >= o) v += t;
+            }
+            if (e < E) {
+                off[e] = carry + v - c;
+                a.offsets[e] = carry + v - c;
+            }
+            carry += __shfl(v, 63, kWave);
+        }
+        if (lane == 0) a.offsets[E] = carry;
+    }
+    __syncthreads();
+    // 4.
+    for (int rd = 0; rd < rounds; ++rd) {
+        const int r = rd * (int)blockDim.x + tid;
+        int e, rank, cnt;
+        bool leader;
+        match(r, &e, &rank, &cnt, &leader);
+        if (r < R) {
+            if (e < 0) {
+                a.pos[r] = -1;  // an expert id outside [0, E) is not placed
+            } else {
+                const int slot = off[e] + table[(rd * NW + wave) * E + e] + rank;
+                a.perm[slot] = r;
+                a.pos[r] = slot;
+            }
+        }
+    }
+}
+
 extern "C" __global__ __launch_bounds__(1024) void nh_moe_permute_kernel(PermuteArgs a) {
     extern __shared__ int sm[];  // counts[E], base[E]
     const int E = a.experts, R = a.routes;

@@ -608,6 +608,11 @@ nh_status nh_moe_permute(nh_context* ctx, const int32_t* indices, size_t tokens,
     nh_status st = bind_device(ctx, err);
     if (st) return st;
     PermuteArgs a{indices, offsets, perm, pos, (int)routes, (int)experts};
+    // the table form when rounds x 16 waves x experts fits in 48 KiB of LDS
+    // (3072 routes x 128 experts: 24 KiB), else the per-wave serial form
+    const size_t rounds = (routes + 1023) / 1024;
+    const size_t table = (rounds * 16 * experts + experts) * sizeof(int);
+    if (table <= 48 * 1024) return launch(ctx, K_PERMUTE_TABLE, 1, 1024, table, stream, a, err);
     return launch(ctx, K_PERMUTE, 1, 1024, 2 * experts * sizeof(int), stream, a, err);
 }
 

@@ -43,6 +43,7 @@ enum KernelId : int {
     K_LINEAR_DECODE_W4_M1,    // W4A8 decode unit, 1 row
     K_LINEAR_DECODE_W4_ROW2,  // 2 rows
     K_LINEAR_DECODE_W4_ROW4,  // 4 rows
+    K_PERMUTE_TABLE,          // R2 in four barriers
     K_COUNT
 };
 

@@ -554,7 +554,8 @@ def test_route_reference_kats_on_device(ctx):
     assert np.array_equal(idx, ridx) and np.array_equal(w, rw)
 
 
-@pytest.mark.parametrize("t,k,e", [(512, 6, 128), (1, 1, 1), (1000, 8, 64), (3, 2, 1000), (2000, 6, 128)])
+@pytest.mark.parametrize("t,k,e", [(512, 6, 128), (1, 1, 1), (1000, 8, 64), (3, 2, 1000), (2000, 6, 128),
+                                   (300, 2, 3)])  # the last: long same-expert runs inside every wave
 def test_permute_bit_exact(ctx, t, k, e):
     note(f"permute t={t} k={k} e={e}")
     rng = np.random.default_rng(t + e)
