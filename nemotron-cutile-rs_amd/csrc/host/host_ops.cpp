@@ -417,6 +417,7 @@ nh_status nh_moe_combine_shared_host(const float* slot_out, const int32_t* pos, 
             if (shared) v = v + shared[t * hidden + h];  // the shared expert first (moe.rs:212-219)
             for (size_t j = 0; j < top_k; ++j) {
                 const size_t r = t * top_k + j;
+                if (pos[r] < 0 || (size_t)pos[r] >= tokens * top_k) continue;  // not placed: adds nothing
                 const float p = weights[r] * slot_out[(size_t)pos[r] * hidden + h];
                 v = v + p;
             }

@@ -514,18 +514,60 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_expert_gemm_kernel(Expe
 
 // R4: out[t][h] = sum_j w[t,j] * slot_out[pos[t*k+j]][h], j ascending, f32
 // multiply then add (moe.rs:239-244).  grid = (ceil(H/256), T).
+// A route whose slot is outside [0, routes) (an expert id the permutation
+// did not place: pos = -1) adds nothing.
 extern "C" __global__ __launch_bounds__(256) void nh_moe_combine_kernel(CombineArgs a) {
     const int t = blockIdx.y;
     const int h = blockIdx.x * blockDim.x + threadIdx.x;
     if (h >= a.hidden) return;
+    const int routes = a.tokens * a.top_k;
     float v = 0.0f;
     if (a.shared) v = v + a.shared[(int64_t)t * a.hidden + h];  // the shared expert first (moe.rs:212-219)
     for (int j = 0; j < a.top_k; ++j) {
         const int r = t * a.top_k + j;
+        const int slot = a.pos[r];
+        if (slot < 0 || slot >= routes) continue;
         const float w = a.weights[r];
-        const float x = a.slot_out[(int64_t)a.pos[r] * a.hidden + h];
+        const float x = a.slot_out[(int64_t)slot * a.hidden + h];
         const float p = w * x;
         v = v + p;
     }
     store_out(a.out, (int64_t)t * a.hidden + h, v, a.out_dtype);
+}
+
+// The same with four consecutive columns per thread (16-byte loads of the
+// slot rows; hidden % 4 == 0, 16-byte aligned rows): every element is
+// summed exactly as above.
+extern "C" __global__ __launch_bounds__(256) void nh_moe_combine4_kernel(CombineArgs a) {
+    const int t = blockIdx.y;
+    const int h = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+    if (h >= a.hidden) return;
+    const int routes = a.tokens * a.top_k;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (a.shared) {
+        const float4 sh = *(const float4*)(a.shared + (int64_t)t * a.hidden + h);
+        v[0] = v[0] + sh.x;
+        v[1] = v[1] + sh.y;
+        v[2] = v[2] + sh.z;
+        v[3] = v[3] + sh.w;
+    }
+    for (int j = 0; j < a.top_k; ++j) {
+        const int r = t * a.top_k + j;
+        const int slot = a.pos[r];
+        if (slot < 0 || slot >= routes) continue;
+        const float w = a.weights[r];
+        const float4 x = *(const float4*)(a.slot_out + (int64_t)slot * a.hidden + h);
+        v[0] = v[0] + w * x.x;
+        v[1] = v[1] + w * x.y;
+        v[2] = v[2] + w * x.z;
+        v[3] = v[3] + w * x.w;
+    }
+    const int64_t o = (int64_t)t * a.hidden + h;
+    if (a.out_dtype == DT_BF16) {
+        const uint32_t lo = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+        const uint32_t hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+        *(uint2*)((uint16_t*)a.out + o) = make_uint2(lo, hi);
+    } else {
+        *(float4*)((float*)a.out + o) = make_float4(v[0], v[1], v[2], v[3]);
+    }
 }

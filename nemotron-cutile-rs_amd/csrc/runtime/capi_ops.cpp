@@ -704,7 +704,16 @@ nh_status nh_moe_combine_shared(nh_context* ctx, const float* slot_out, const in
         return set_error(err, NH_INVALID_SHAPE, "invalid combine shape");
     if ((st = bind_device(ctx, err))) return st;
     if (tokens == 0 || hidden == 0) return NH_OK;
+    size_t routes;
+    if (!mul_ok(tokens, top_k, &routes) || routes > (size_t)kMaxGrid)
+        return set_error(err, NH_UNSUPPORTED, "tokens * top_k must be < 2^31");
     CombineArgs a{slot_out, pos, weights, out, shared, (int)tokens, (int)top_k, (int)hidden, out_dtype};
+    // four columns per thread when every row starts 16-byte aligned (8 bytes for bf16 out)
+    const bool vec4 = hidden % 4 == 0 && aligned16(slot_out) && aligned16(shared) &&
+                      ((uintptr_t)out % (out_dtype == NH_BF16 ? 8 : 16)) == 0;
+    if (vec4)
+        return launch(ctx, K_COMBINE4, (unsigned)((hidden / 4 + 255) / 256), 256, 0, stream, a, err,
+                      (unsigned)tokens);
     return launch(ctx, K_COMBINE, (unsigned)((hidden + 255) / 256), 256, 0, stream, a, err, (unsigned)tokens);
 }
 

@@ -44,6 +44,7 @@ enum KernelId : int {
     K_LINEAR_DECODE_W4_ROW2,  // 2 rows
     K_LINEAR_DECODE_W4_ROW4,  // 4 rows
     K_PERMUTE_TABLE,          // R2 in four barriers
+    K_COMBINE4,               // R4, four columns per thread
     K_COUNT
 };
 

@@ -528,6 +528,7 @@ void or_moe_combine_shared(const float *slot_out, const int32_t *pos, const floa
             if (shared) v = v + shared[t * hidden + h];
             for (size_t j = 0; j < top_k; ++j) {
                 size_t r = t * top_k + j;
+                if (pos[r] < 0 || (size_t)pos[r] >= tokens * top_k) continue; /* not placed (pos -1) */
                 v = v + weights[r] * slot_out[(size_t)pos[r] * hidden + h];
             }
             if (out_bf16)

@@ -477,3 +477,16 @@ def test_int4_validation_in_the_reference_order():
     assert dev(17, 16, 64) == NH.UNSUPPORTED and dev(1, 16, 8192 + 16) == NH.UNSUPPORTED and dev(1, 16, 72) == NH.UNSUPPORTED
     st, err = NH.call_status("nh_tile_weights_int4", None, 16, 3, 2, 2, 8, 16, 512, None)
     assert st == NH.LENGTH_MISMATCH and err.argument.decode() == "packed_weights"
+
+
+def test_combine_skips_routes_without_a_slot():
+    """A route the permutation did not place (pos -1) adds nothing, on the
+    host twin as in the oracle."""
+    slot_out = np.array([[1.0, 2.0], [3.0, 4.0]], dtype=np.float32)
+    pos = np.array([1, -1], dtype=np.int32)
+    w = np.array([0.5, 0.25], dtype=np.float32)
+    out = np.zeros((1, 2), dtype=np.float32)
+    NH.call("nh_moe_combine_host", slot_out.ctypes.data, pos.ctypes.data, w.ctypes.data, 1, 2, 2, out.ctypes.data,
+            NH.F32)
+    assert np.array_equal(out, np.array([[1.5, 2.0]], dtype=np.float32))
+    assert np.array_equal(out, O.moe_combine(slot_out, pos, w, 1, 2, 2))

@@ -572,6 +572,30 @@ def test_permute_bit_exact(ctx, t, k, e):
     assert np.array_equal(pos.numpy(), ref[2])
 
 
+@pytest.mark.parametrize("tokens,top_k,hidden", [(512, 6, 2688), (7, 3, 37), (5, 2, 8)])
+@pytest.mark.parametrize("with_shared", [False, True])
+def test_combine_bit_exact(ctx, tokens, top_k, hidden, with_shared):
+    """R4 on the device: the four-column kernel (hidden % 4 == 0) and the
+    scalar one (37), f32 and bf16 out, with an unplaced route (pos -1)."""
+    note(f"combine t={tokens} k={top_k} h={hidden} shared={with_shared}")
+    rng = np.random.default_rng(tokens + hidden)
+    R = tokens * top_k
+    slot_out = rng.standard_normal((R, hidden)).astype(np.float32)
+    pos = rng.permutation(R).astype(np.int32)
+    pos[R // 2] = -1
+    w = rng.random(R).astype(np.float32)
+    shared = rng.standard_normal((tokens, hidden)).astype(np.float32) if with_shared else None
+    d = [ctx.upload(a) for a in (slot_out, pos, w)]
+    dsh = ctx.upload(shared) if with_shared else None
+    for out_dtype, bf in ((NH.F32, False), (NH.BF16, True)):
+        out = ctx.empty((tokens, hidden), np.uint16 if bf else np.float32)
+        NH.call("nh_moe_combine_shared", ctx.handle, d[0].ptr, d[1].ptr, d[2].ptr, dsh.ptr if dsh else None, tokens,
+                top_k, hidden, out.ptr, out_dtype, None)
+        ctx.synchronize()
+        ref = O.moe_combine_shared(slot_out, pos, w, shared, tokens, top_k, hidden, out_bf16=bf)
+        assert np.array_equal(out.numpy(), ref)
+
+
 def moe_weights(experts, inter, hidden):
     up = np.empty((experts, inter, hidden), dtype=np.int8)
     down = np.empty((experts, hidden, inter), dtype=np.int8)
