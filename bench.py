@@ -42,6 +42,7 @@ class Bench:
         self.ctx = NH.Context(0)
         self.ev = NH.HipEvents()
         self.e0, self.e1 = self.ev.create(), self.ev.create()
+        self.last_timing = {}
         self.graphs = NH.HipGraphs()
         s = ctypes.c_void_p()
         NH.call("nh_stream_create", self.ctx.handle, ctypes.byref(s))
@@ -50,14 +51,17 @@ class Bench:
     def time_ms(self, fn, steps, warmup, per_graph=None, out=None):
         """Mean time per step of fn(i) on self.stream.  `warmup` eager calls;
         then the calls of steps warmup .. warmup + steps - 1 are captured from
-        the same entry points into HIP graphs of `per_graph` steps each,
-        replayed once untimed, and replayed again bracketed by HIP events on
-        that stream.  Each timed graph launch carries a fixed cost (~0.1 ms
-        measured: 1000 decode units took 11.5 us each against 11.9 us for 200),
-        so the defaults keep every timed region near 10 ms or more.  The replay issues exactly the captured launches, without
-        the ~12 us of Python/ctypes work per eager call (which bounded the eager
-        loop of the 12 us decode unit).  With `out`, the replayed result must
-        equal an eager call of the last step."""
+        the same entry points into HIP graphs of `per_graph` steps each (the
+        replay issues exactly the captured launches, without the ~12 us of
+        Python/ctypes work per eager call).  After a synchronize, the graphs
+        are replayed twice back to back on the stream: an untimed replay, then
+        the timed one between two events.  The first event fires when the
+        untimed replay's last step ends, and the timed graphs were dispatched
+        while it ran, so the interval holds exactly the `steps` timed steps
+        and not the fixed cost of dispatching a graph onto an idle stream
+        (~20 us per launch: 1 us per step at 20 steps).  That cold figure (the
+        same replay after a synchronize) is kept in self.last_timing.  With
+        `out`, the replayed result must equal an eager call of the last step."""
         for i in range(warmup):
             fn(i)
         fn(warmup + steps - 1)
@@ -68,20 +72,30 @@ class Bench:
         for c0 in range(0, steps, per):
             idx = range(warmup + c0, warmup + min(steps, c0 + per))
             graphs.append(self.graphs.capture(self.stream, lambda idx=idx: [fn(i) for i in idx]))
-        for _, ex in graphs:
-            self.graphs.launch(ex, self.stream)
+
+        def replay():
+            for _, ex in graphs:
+                self.graphs.launch(ex, self.stream)
+
+        replay()  # first replay: graph upload and warm-up
         self.ctx.synchronize(self.stream)
         self.ev.record(self.e0, self.stream)
-        for _, ex in graphs:
-            self.graphs.launch(ex, self.stream)
+        replay()
         self.ev.record(self.e1, self.stream)
-        ms = self.ev.elapsed_ms(self.e0, self.e1)
+        cold = self.ev.elapsed_ms(self.e0, self.e1)
+        self.ctx.synchronize(self.stream)
+        replay()  # untimed: the stream is busy while the timed replay is dispatched
+        self.ev.record(self.e0, self.stream)
+        replay()
+        self.ev.record(self.e1, self.stream)
+        hot = self.ev.elapsed_ms(self.e0, self.e1)
         self.ctx.synchronize(self.stream)
         for g, ex in graphs:
             self.graphs.destroy(g, ex)
         if eager is not None and not np.array_equal(out.numpy(), eager):
             raise AssertionError("graph replay differs from the eager call of the same step")
-        return ms / steps
+        self.last_timing = {"back_to_back_ms": hot, "after_sync_ms": cold}
+        return hot / steps
 
     def time_eager_ms(self, fn, steps, warmup):
         """The same timing with eager calls from this Python loop (reported
@@ -126,7 +140,7 @@ class Bench:
         def step(i):
             q, s = pool[i % len(pool)]
             st = L.nh_linear_w8a8(h, x.ptr, NH.BF16, q.ptr, s.ptr, None, m, n, k, out.ptr, NH.BF16, ws.ptr,
-                                  ws_bytes, None, None, self.stream, ctypes.byref(err))
+                                  ws_bytes, None, None, None, self.stream, ctypes.byref(err))
             if st:
                 NH.check(st, err)
 
@@ -156,7 +170,7 @@ class Bench:
 
         def step(i):
             st = L.nh_linear_w4a8(h, x.ptr, NH.BF16, pool[i % len(pool)].ptr, 0.01, 8, None, m, n, k, out.ptr,
-                                  NH.BF16, self.stream, ctypes.byref(err))
+                                  NH.BF16, None, self.stream, ctypes.byref(err))
             if st:
                 NH.check(st, err)
 
@@ -248,11 +262,11 @@ class Bench:
                 st = L.nh_moe_forward_shared_w8a8(h, x.ptr, NH.BF16, logits.ptr, tokens, hidden, inter, experts, top_k,
                                                   1, 1.0, up_q.ptr, up_s.ptr, down_q.ptr, down_s.ptr, shared_inter,
                                                   sh[0].ptr, sh[1].ptr, sh[2].ptr, sh[3].ptr, out.ptr, NH.BF16, ws.ptr,
-                                                  ws_bytes, self.stream, ctypes.byref(err))
+                                                  ws_bytes, None, self.stream, ctypes.byref(err))
             else:
                 st = L.nh_moe_forward_w8a8(h, x.ptr, NH.BF16, logits.ptr, tokens, hidden, inter, experts, top_k, 1,
                                            1.0, up_q.ptr, up_s.ptr, down_q.ptr, down_s.ptr, out.ptr, NH.BF16, ws.ptr,
-                                           ws_bytes, self.stream, ctypes.byref(err))
+                                           ws_bytes, None, self.stream, ctypes.byref(err))
             if st:
                 NH.check(st, err)
 
@@ -313,7 +327,7 @@ class Bench:
         def linear(name, idx, x):
             (n, k), (bufs, s) = shapes[name], layers[name]
             st = L.nh_linear_w8a8(h, x.ptr, NH.BF16, bufs[idx].ptr, s.ptr, None, m, n, k, outs[n].ptr, NH.BF16,
-                                  ws.ptr, ws.nbytes, None, None, self.stream, eb)
+                                  ws.ptr, ws.nbytes, None, None, None, self.stream, eb)
             if st:
                 NH.check(st, err)
 
@@ -331,7 +345,8 @@ class Bench:
                 else:
                     (bu, su), (bd, sd) = layers["up"], layers["down"]
                     st = L.nh_mlp_w8a8(h, acts[4096].ptr, NH.BF16, bu[i].ptr, su.ptr, None, bd[i].ptr, sd.ptr, None,
-                                       m, 4096, 21504, outs[4096].ptr, NH.BF16, ws.ptr, ws.nbytes, self.stream, eb)
+                                       m, 4096, 21504, outs[4096].ptr, NH.BF16, ws.ptr, ws.nbytes, None, self.stream,
+                                       eb)
                     if st:
                         NH.check(st, err)
 
@@ -441,6 +456,7 @@ def main():
     log = lambda s: print(s, file=sys.stderr, flush=True)  # noqa: E731
     log("[bench] headline decode unit m=1 k=4096 n=16384")
     ms, pool, x, out = b.decode(m, n, k, args.steps, args.warmup)
+    head_timing = dict(b.last_timing)
     eager_ms = b.time_eager_ms(b.last_step, args.steps, args.warmup)
     nbytes = decode_bytes(m, n, k)
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -521,8 +537,12 @@ def main():
         "config": {"workload": "decode unit (per-token int8 quantization + W8A8 GEMV), M=1, K=4096 -> N=16384, "
                                "bf16 in/out, int8 per-row weights from N(0,0.02) (BASELINE configs[1])",
                    "m": m, "k": k, "n": n, "weight_pool_MiB": POOL_BYTES >> 20,
-                   "timing": "HIP-graph replay of the captured entry-point calls; eager Python-loop "
-                             f"figure {eager_ms * 1e3:.2f} us/step"},
+                   "timing": (f"{args.steps} steps captured in a HIP graph; the timed replay follows an "
+                              f"untimed one back to back on the stream, events around it "
+                              f"({head_timing['back_to_back_ms'] * 1e3 / args.steps:.2f} us/step); the same "
+                              f"replay launched onto an idle stream after a synchronize "
+                              f"{head_timing['after_sync_ms'] * 1e3 / args.steps:.2f} us/step (graph dispatch "
+                              f"included); eager Python-loop {eager_ms * 1e3:.2f} us/step")},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "nh_linear_decode_w8a8_m1_kernel", "bytes_per_launch": nbytes},

@@ -171,6 +171,22 @@ nh_status nh_gemm_w8a8_ta(nh_context *ctx, const int8_t *xq_tiled, const float *
 nh_status nh_gemm_w8a8_host(const int8_t *xq, const float *sx, const int8_t *wq, const float *sw,
                             const float *bias, size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype,
                             nh_error *err);
+/* Non-finite inputs of the quantizing layers (the spec's Q2 error,
+ * QuantizeError::NonFiniteInput{index, value} in the style of
+ * quantize.rs:193-195).  Device launches cannot return it, so the layer entry
+ * points below take an optional device word `nonfinite` (uint64, zero before
+ * the first call, e.g. nh_memset_d8): a quantizer that meets a NaN or an
+ * infinity records the first one there (the layer's input ahead of its
+ * intermediate, then the lowest row-major index) and carries on; the codes of
+ * such a row, and the outputs that depend on them, are unspecified.
+ * nh_take_nonfinite synchronizes `stream`, returns NH_NON_FINITE_INPUT with
+ * err->argument "input" (index into x) or "intermediate" (index into the
+ * layer's f32 intermediate: the MLP's [m][inter] ReLU^2 output, the MoE's
+ * [routes][inter] up output in expert-sorted slot order), err->index and
+ * err->value, and clears the word; NH_OK when it is zero.  NULL skips the
+ * check at no cost. */
+nh_status nh_take_nonfinite(nh_context *ctx, uint64_t *nonfinite, nh_stream stream, nh_error *err);
+
 /* Quantized linear layer, the drop-in for LinearProjection::project_into
  * with int8 per-row weights (linear.rs:283-342): dynamic per-token
  * quantization of x (f32 or bf16) then G1/G3 + bias.  For bf16 x with
@@ -185,7 +201,7 @@ size_t nh_linear_w8a8_workspace_size(size_t m, size_t k);
 nh_status nh_linear_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const int8_t *wq, const float *sw,
                          const float *bias, size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype,
                          void *workspace, size_t workspace_bytes, int8_t *xq_out, float *sx_out,
-                         nh_stream stream, nh_error *err);
+                         uint64_t *nonfinite, nh_stream stream, nh_error *err);
 /* L2: int8 MLP layer, the drop-in for MlpLayer::forward_into with int8
  * per-row weights (mlp.rs:157-211): h = ReLU^2(x W_up^T + b_up) in f32
  * (ReLU^2 after the bias, mlp.rs:205), then out = h W_down^T + b_down, each
@@ -199,7 +215,7 @@ size_t nh_mlp_w8a8_workspace_size(size_t m, size_t hidden, size_t inter);
 nh_status nh_mlp_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const int8_t *w_up, const float *s_up,
                       const float *b_up, const int8_t *w_down, const float *s_down, const float *b_down, size_t m,
                       size_t hidden, size_t inter, void *out, nh_dtype out_dtype, void *workspace,
-                      size_t workspace_bytes, nh_stream stream, nh_error *err);
+                      size_t workspace_bytes, uint64_t *nonfinite, nh_stream stream, nh_error *err);
 /* G2: W8A32 dequant GEMV, y = x * ((float)q * s)^T with f64 accumulation,
  * the arithmetic of materialize_dense + gemm_into_host (linear.rs:126-131). */
 nh_status nh_gemv_w8a32(nh_context *ctx, const float *x, const int8_t *wq, const float *sw, size_t m, size_t n,
@@ -276,7 +292,8 @@ nh_status nh_moe_forward_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, 
                               size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
                               int renormalize, float scaling, const int8_t *w_up, const float *s_up,
                               const int8_t *w_down, const float *s_down, void *out, nh_dtype out_dtype,
-                              void *workspace, size_t workspace_bytes, nh_stream stream, nh_error *err);
+                              void *workspace, size_t workspace_bytes, uint64_t *nonfinite, nh_stream stream,
+                              nh_error *err);
 /* The int8 MoE layer with its shared expert, MoeLayer::forward_into with
  * shared_expert = Some(..) (moe.rs:197-219): the shared expert is an int8
  * MLP over every token (nh_mlp_w8a8 on x, f32, no biases: w_up_shared tiled
@@ -294,8 +311,8 @@ nh_status nh_moe_forward_shared_w8a8(nh_context *ctx, const void *x, nh_dtype x_
                                      const int8_t *w_down, const float *s_down, size_t shared_inter,
                                      const int8_t *w_up_shared, const float *s_up_shared,
                                      const int8_t *w_down_shared, const float *s_down_shared, void *out,
-                                     nh_dtype out_dtype, void *workspace, size_t workspace_bytes, nh_stream stream,
-                                     nh_error *err);
+                                     nh_dtype out_dtype, void *workspace, size_t workspace_bytes,
+                                     uint64_t *nonfinite, nh_stream stream, nh_error *err);
 
 /* ---- INT4 affine weights on the device (W4A8), SURVEY §8(f) 3 --------------
  * The reference's INT4 linear weights (Int4LinearWeights, linear.rs:99-131)
@@ -327,7 +344,7 @@ nh_status nh_tile_weights_int4_host(const uint8_t *packed, size_t packed_len, si
 int nh_supports_linear_w4a8(size_t m, size_t n, size_t k);
 nh_status nh_linear_w4a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const uint8_t *w4_tiled, float scale,
                          uint32_t zero_point, const float *bias, size_t m, size_t n, size_t k, void *out,
-                         nh_dtype out_dtype, nh_stream stream, nh_error *err);
+                         nh_dtype out_dtype, uint64_t *nonfinite, nh_stream stream, nh_error *err);
 /* The host twin on the reference's packed layout (f32 or bf16 x, any shape). */
 nh_status nh_linear_w4a8_host(const void *x, nh_dtype x_dtype, const uint8_t *packed, size_t packed_len,
                               float scale, uint32_t zero_point, const float *bias, size_t m, size_t n, size_t k,

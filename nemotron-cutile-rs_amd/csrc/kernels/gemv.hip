@@ -70,6 +70,44 @@ __device__ __forceinline__ void store_y(void* out, int out_dtype, int64_t i, int
     store_out(out, i, y, out_dtype);
 }
 
+// The first non-finite activation of rows that hold one (the row maxima
+// said so; a uniform, rare branch), from the workgroup's registers: xv[m][v]
+// holds the 8 values at column (threadIdx.x + v T) 8 of row m.
+template <int MM>
+__device__ __forceinline__ void report_decode_rows(const LinearDecodeArgs& a, const v4i (&xv)[MM][2], int T) {
+    __shared__ int red_nf[16];
+    int first = 0x7fffffff;
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const int c = (threadIdx.x + v * T) * 8;
+            const int e = bf16x8_first_nonfinite(xv[m][v]);
+            if (m < a.M && c < a.K && e < 8) first = min(first, m * a.K + c + e);
+        }
+    first = block_min_i32(first, red_nf);
+    if (threadIdx.x == 0 && first != 0x7fffffff)
+        report_nonfinite(a.nonfinite, 0, first, bf16_to_f32(((const uint16_t*)a.x)[first]));
+}
+
+// The same for the wide decode unit: xv[j] holds chunk j T + threadIdx.x of
+// the row-major [M][K] input, i.e. the values at flat index 8 chunk + e.
+template <int XR>
+__device__ __forceinline__ void report_decode_chunks(const LinearDecodeArgs& a, const v4i (&xv)[XR], int T) {
+    __shared__ int red_nf[16];
+    int first = 0x7fffffff;
+    const int chunks = a.M * (a.K >> 3);
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+        const int c = j * T + (int)threadIdx.x;
+        const int e = bf16x8_first_nonfinite(xv[j]);
+        if (c < chunks && e < 8) first = min(first, c * 8 + e);
+    }
+    first = block_min_i32(first, red_nf);
+    if (threadIdx.x == 0 && first != 0x7fffffff)
+        report_nonfinite(a.nonfinite, 0, first, bf16_to_f32(((const uint16_t*)a.x)[first]));
+}
+
 }  // namespace
 
 // G1: quantized activations already in memory, M <= 16, any K <= 131072
@@ -182,7 +220,7 @@ __device__ __forceinline__ uint2 act_order_int4(uint32_t c0, uint32_t c1) {
 template <int MM, bool W4 = false>
 __device__ __forceinline__ void linear_decode_row(const LinearDecodeArgs& a, int8_t* xs) {
     __shared__ v4i red[8 * 64];
-    __shared__ float redf[8][MM];
+    __shared__ uint32_t redu[8][MM];
     __shared__ int redi[W4 ? 8 : 1][MM];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = a.waves;
     const int T = 64 * W;
@@ -225,28 +263,25 @@ __device__ __forceinline__ void linear_decode_row(const LinearDecodeArgs& a, int
     for (int s = 0; s < KH; ++s) load_tile(s);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. row absmax over the workgroup; every thread derives the scales
+    // 2. row absmax over the workgroup, as the largest bf16 magnitude bit
+    //    pattern (a pattern of 0x7f80 or more is an infinity or a NaN);
+    //    every thread derives the scales
     float sx[MM];
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
-        float amax = 0.0f;
-#pragma unroll
-        for (int v = 0; v < 2; ++v)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t u = (uint32_t)xv[m][v][j];
-                amax = fmaxf(amax, fmaxf(fabsf(f32_from_bits(u << 16)), fabsf(f32_from_bits(u & 0xffff0000u))));
-            }
-        amax = wave_max(amax);
-        if (lane == 0) redf[wave][m] = amax;
+        const uint32_t mb = wave_max_u32(max(bf16x8_absmax_bits(xv[m][0]), bf16x8_absmax_bits(xv[m][1])));
+        if (lane == 0) redu[wave][m] = mb;
     }
     __syncthreads();
+    bool nonfinite = false;
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
-        float r = redf[0][m];
-        for (int i = 1; i < W; ++i) r = fmaxf(r, redf[i][m]);
-        sx[m] = scale_from_amax(r);
+        uint32_t r = redu[0][m];
+        for (int i = 1; i < W; ++i) r = max(r, redu[i][m]);
+        sx[m] = scale_from_amax(f32_from_bits(r << 16));
+        nonfinite |= r >= 0x7f80u;
     }
+    if (nonfinite && a.nonfinite && blockIdx.x == 0) report_decode_rows<MM>(a, xv, T);
     // 3. codes into LDS (zeros past K and for rows >= M); W4: each thread's
     //    share of the row sums of the codes
     int rsum[MM];
@@ -379,17 +414,18 @@ __device__ __forceinline__ void linear_decode_wide(const LinearDecodeArgs& a, in
     for (int j = 0; j < XR; ++j) {
         const int c0 = j * T + wave * 64;  // the wave's first chunk: uniform
         if (c0 < M * cpr) {
-            float m = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t u = (uint32_t)xv[j][q];
-                m = fmaxf(m, fmaxf(fabsf(f32_from_bits(u << 16)), fabsf(f32_from_bits(u & 0xffff0000u))));
-            }
-            m = wave_max(m);
-            if (lane == 0) atomicMax(&rowmax[c0 / cpr], (int)f32_bits(m));  // non-negative: int order = float order
+            // the largest magnitude as the f32 bits of the widened bf16
+            // (non-negative: int order = value order, non-finite on top)
+            const uint32_t mb = wave_max_u32(bf16x8_absmax_bits(xv[j]));
+            if (lane == 0) atomicMax(&rowmax[c0 / cpr], (int)(mb << 16));
         }
     }
     lds_publish();
+    if (blockIdx.x == 0 && a.nonfinite) {
+        bool nonfinite = false;
+        for (int r = 0; r < M; ++r) nonfinite |= (uint32_t)rowmax[r] >= 0x7f800000u;
+        if (nonfinite) report_decode_chunks<XR>(a, xv, T);
+    }
     // codes into LDS: chunk c = 8 values of row c / cpr at k = 8 (c % cpr)
 #pragma unroll
     for (int j = 0; j < XR; ++j) {

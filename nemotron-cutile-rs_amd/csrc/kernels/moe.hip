@@ -415,7 +415,10 @@ __device__ __forceinline__ void expert_stream(const ExpertGemmArgs& a, v4i (&b0)
             __builtin_amdgcn_sched_barrier(0);
         }
         const int n = (t_begin + wave + (j / nch) * NW) * 16 + r16;
-        if (c == nch - 1 && n < N) {
+        // j >= nj: the chunk after the wave's last (an odd chunk count runs
+        // one past it with zero weights); its tile may belong to the other
+        // workgroup of the expert, so it stores nothing
+        if (j < nj && c == nch - 1 && n < N) {
             const float swn = sws[n - t_begin * 16];
             // one per-lane base (row p0 + 4 g, column n); rows rb * 16 + r are uniform offsets
             float* ob = a.out + (int64_t)(p0 + 4 * g) * N + n;
@@ -432,8 +435,7 @@ __device__ __forceinline__ void expert_stream(const ExpertGemmArgs& a, v4i (&b0)
         }
     };
     // chunks in pairs: while one slab's MFMAs run, the other is in flight
-    // (a chunk past nj has zero weights and writes nothing: its tile is past
-    // the wave's last)
+    // (a chunk past nj has zero weights and writes nothing)
     for (int j = 0; j < nj; j += 2) {
         process(b0, j);
         load_chunk(b0, j + 2);
@@ -463,7 +465,7 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_expert_gemm_kernel(Expe
     const int nw_cols = min(t_end * 16, N) - t_begin * 16;  // this workgroup's weight rows
     int8_t* As = lds;                                // [RB][kt] A tiles
     float* sas = (float*)(lds + RB * kt * 1024);     // [16 RB] the pass's row scales
-    float* sws = sas + 16 * RB;                      // [16 tiles_per_wg] the workgroup's weight scales
+    float* sws = sas + 16 * RB;                      // [16 tiles_per_wg, rounded up to 64] weight scales
     const __amdgpu_buffer_rsrc_t swr = make_rsrc(a.sw + (int64_t)e * N + t_begin * 16, (uint32_t)nw_cols * 4u);
     const int8_t* wexp = a.w + (int64_t)e * tiled_bytes(N, K);
     const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.aq, (uint32_t)a.a_rows * (uint32_t)K);

@@ -74,6 +74,49 @@ __device__ __forceinline__ void store_out(void* p, int64_t i, float v, int dtype
 
 __device__ __forceinline__ bool is_finite_f32(float v) { return (f32_bits(v) & 0x7f800000u) != 0x7f800000u; }
 
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, kWave));
+    return v;
+}
+
+// NonFiniteInput (quantize.rs:193-195: the first offending element and its
+// value) from the device quantizers.  The key (stage << 63 | flat index << 32
+// | f32 bits of the value) goes into the caller's 64-bit word as its
+// complement through an atomic max, so the word keeps the smallest key (the
+// layer's input before an intermediate, then the lowest row-major index) and
+// a zeroed word means that nothing was found.  Flat indices are < 2^31 (the
+// device envelope).  Vector atomic only.
+__device__ __forceinline__ void report_nonfinite(uint64_t* word, int stage, int64_t index, float value) {
+    const uint64_t key = ((uint64_t)(stage & 1) << 63) | ((uint64_t)(index & 0x7fffffff) << 32) | f32_bits(value);
+    atomicMax((unsigned long long*)word, (unsigned long long)~key);
+}
+
+typedef unsigned short nh_u16x2 __attribute__((ext_vector_type(2)));
+
+// Largest bf16 magnitude of the 8 values of one 16-byte load, as its 15-bit
+// pattern (sign cleared).  Magnitude bit patterns order like the values, and
+// infinities and NaNs (0x7f80 and above) order above every finite value, so
+// a row's maximum pattern is its absmax and also shows a non-finite element.
+// Three packed 16-bit maxima per load.
+__device__ __forceinline__ uint32_t bf16x8_absmax_bits(v4i xv) {
+    nh_u16x2 m = __builtin_bit_cast(nh_u16x2, (uint32_t)xv[0] & 0x7fff7fffu);
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+        m = __builtin_elementwise_max(m, __builtin_bit_cast(nh_u16x2, (uint32_t)xv[j] & 0x7fff7fffu));
+    return max((uint32_t)m.x, (uint32_t)m.y);
+}
+
+// Index (0..7) of the first non-finite value of a 16-byte bf16 load, or 8.
+__device__ __forceinline__ int bf16x8_first_nonfinite(v4i xv) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t h = ((uint32_t)xv[e >> 1] >> (16 * (e & 1))) & 0x7fffu;
+        if (h >= 0x7f80u) return e;
+    }
+    return 8;
+}
+
 // Codes of NV values with row scale s and r = RN(1/s): quantize_i8_fast
 // (nh_numerics.h) vectorized, so bit-identical to quantize_i8; q[i]'s low
 // byte is the code.  pow2 = scale_is_pow2(s) and the zero/subnormal test are

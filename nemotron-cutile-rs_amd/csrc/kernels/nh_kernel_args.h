@@ -26,6 +26,9 @@ struct QuantizeRowsArgs {
                           // P = 16 the weights' tiled layout (the GEMM's A operand)
     int32_t gather_div;   // with gather: output row r quantizes input row gather[r] / gather_div
     const int32_t* gather;  // or null (output row r = input row r)
+    uint64_t* nonfinite;  // or null: the first non-finite element (report_nonfinite, nh_device.h)
+    int32_t nonfinite_stage;  // 0: x is the caller's input; 1: an intermediate of the layer
+    int32_t pad_;
 };
 
 // Q3: out[r][c] = (float)q[r][c] * scales[r]
@@ -88,6 +91,7 @@ struct LinearDecodeArgs {
     int32_t w4_zp;        // INT4 weights (tiled_int4): the per-tensor zero point
     float w4_scale;       //   and scale, used in place of sw
     int32_t pad_;
+    uint64_t* nonfinite;  // or null: the first non-finite activation (report_nonfinite, nh_device.h)
 };
 
 // G2: W8A32 dequant GEMV; grid = (N tiles, ceil(M / 4)).

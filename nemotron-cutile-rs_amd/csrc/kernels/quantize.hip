@@ -14,6 +14,15 @@ __device__ __forceinline__ int64_t act_tile_offset(int64_t m, int64_t k, int64_t
     return (((m / p) * kt + (k >> 6)) * 4 + ((k >> 4) & 3)) * p * 16 + (m % p) * 16 + (k & 15);
 }
 
+// The row's first non-finite column (bad < INT_MAX) into the caller's
+// non-finite word, as the flat index of the input element.
+__device__ __forceinline__ void report_row(const QuantizeRowsArgs& a, int64_t src, int bad) {
+    if (a.nonfinite && bad != 0x7fffffff) {
+        const int64_t i = src * a.cols + bad;
+        report_nonfinite(a.nonfinite, a.nonfinite_stage, i, load_as_f32(a.x, i, a.x_dtype));
+    }
+}
+
 // Vector path: one workgroup per row, 16-byte chunks (8 bf16 or 4 f32
 // values).  The first kRegChunks chunks of every thread stay in registers
 // between the absmax pass and the code pass, so rows up to kRegChunks *
@@ -69,6 +78,7 @@ __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, floa
     if (threadIdx.x == 0) {
         a.scales[row] = s;
         if (a.row_status) a.row_status[row] = bad == 0x7fffffff ? -1 : bad;
+        report_row(a, src, bad);
     }
     const float rcp = s > 0.0f ? 1.0f / s : 0.0f;
     const bool pow2 = scale_is_pow2(s);
@@ -148,6 +158,7 @@ __device__ __forceinline__ void quantize_row_wave(const QuantizeRowsArgs& a) {
     if (lane == 0) {
         a.scales[row] = s;
         if (a.row_status) a.row_status[row] = bad == 0x7fffffff ? -1 : bad;
+        report_row(a, src, bad);
     }
     const float rcp = s > 0.0f ? 1.0f / s : 0.0f;
     const bool pow2 = scale_is_pow2(s);
@@ -176,7 +187,8 @@ __device__ __forceinline__ void quantize_row_wave(const QuantizeRowsArgs& a) {
 __device__ __forceinline__ void quantize_row_scalar(const QuantizeRowsArgs& a, float* redf, int* redi) {
     const int64_t row = blockIdx.x;
     const int64_t cols = a.cols;
-    const int64_t base = (a.gather ? a.gather[row] / a.gather_div : row) * cols;  // input row
+    const int64_t src = a.gather ? a.gather[row] / a.gather_div : row;
+    const int64_t base = src * cols;  // input row
     float amax = 0.0f;
     int bad = 0x7fffffff;
     for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
@@ -190,6 +202,7 @@ __device__ __forceinline__ void quantize_row_scalar(const QuantizeRowsArgs& a, f
     if (threadIdx.x == 0) {
         a.scales[row] = s;
         if (a.row_status) a.row_status[row] = bad == 0x7fffffff ? -1 : bad;
+        report_row(a, src, bad);
     }
     const float r = s > 0.0f ? 1.0f / s : 0.0f;
     for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {

@@ -114,13 +114,14 @@ nh_status check_w8a8_shape(size_t m, size_t n, size_t k, nh_error* err) {
 // rows of whole 16-byte chunks and code stores aligned to a chunk's codes.
 nh_status launch_quantize(nh_context* ctx, const void* x, nh_dtype dtype, size_t rows, size_t cols, int8_t* q,
                           float* scales, int32_t* row_status, int8_t* q_act, nh_stream stream, nh_error* err,
-                          int act_p = 0, const int32_t* gather = nullptr, int gather_div = 1) {
+                          int act_p = 0, const int32_t* gather = nullptr, int gather_div = 1,
+                          uint64_t* nonfinite = nullptr, int nonfinite_stage = 0) {
     const size_t esz = dtype == NH_BF16 ? 2 : 4;
     const size_t row_bytes = cols * esz;
     const bool vec = aligned16(x) && row_bytes % 16 == 0 && row_bytes < (1ull << 31) &&
                      ((uintptr_t)q % (16 / esz)) == 0 && aligned16(q_act);
     QuantizeRowsArgs a{x, q, scales, row_status, q_act, (int64_t)rows, (int64_t)cols, dtype, vec ? 1 : 0,
-                       act_p > 0 ? act_p : (int)rows, gather_div, gather};
+                       act_p > 0 ? act_p : (int)rows, gather_div, gather, nonfinite, nonfinite_stage, 0};
     // many rows of up to 512 16-byte chunks: one wave per row, no barrier
     // (3072 MoE routes: 299.6 vs 304 us per layer; a few decode rows keep a
     // workgroup each: 8 rows of 4096 on 2 workgroups cost the 52-layer stack
@@ -316,7 +317,7 @@ int nh_supports_linear_w4a8(size_t m, size_t n, size_t k) {
 
 nh_status nh_linear_w4a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const uint8_t* w4_tiled, float scale,
                          uint32_t zero_point, const float* bias, size_t m, size_t n, size_t k, void* out,
-                         nh_dtype out_dtype, nh_stream stream, nh_error* err) {
+                         nh_dtype out_dtype, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
     clear_error(err);
     nh_status st;
     // the checks of Int4LinearWeights::validate and project_into (linear.rs:113-124, 290-311)
@@ -354,6 +355,7 @@ nh_status nh_linear_w4a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
         a.ntw = 1;
         a.w4_zp = (int)zero_point;
         a.w4_scale = scale;
+        a.nonfinite = nonfinite;
         const size_t lds = mm * ((size_t)w * 1024 + 16);
         if (lds > ctx->max_shared_per_block) return set_error(err, NH_UNSUPPORTED, "LDS too small");
         if ((st = launch(ctx, kid, (unsigned)((n + 15) / 16), (unsigned)(64 * w), lds, stream, a, err))) return st;
@@ -457,7 +459,7 @@ namespace {
 nh_status linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* wq, const float* sw,
                       const float* bias, size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype,
                       void* workspace, size_t workspace_bytes, int8_t* xq_out, float* sx_out, int relu2,
-                      nh_stream stream, nh_error* err) {
+                      uint64_t* nonfinite, int nonfinite_stage, nh_stream stream, nh_error* err) {
     nh_status st;
     // bf16 rows: the fused decode unit when it fits (one launch, no workspace)
     DecodePlan plan;
@@ -479,6 +481,7 @@ nh_status linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const in
         a.out_dtype = out_dtype;
         a.ntw = plan.ntw;
         a.relu2 = relu2;
+        a.nonfinite = nonfinite;  // the fused unit reads the caller's input only (stage 0)
         const size_t tiles = (n + 15) / 16;
         return launch(ctx, plan.kid, (unsigned)((tiles + plan.ntw - 1) / plan.ntw), (unsigned)plan.threads, plan.lds,
                       stream, a, err);
@@ -491,7 +494,9 @@ nh_status linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const in
         if (!aligned16(workspace)) return set_error(err, NH_UNSUPPORTED, "workspace must be 16-byte aligned");
         int8_t* tiles = (int8_t*)workspace;
         float* sx = sx_out ? sx_out : (float*)((char*)workspace + align256(act_tiles_bytes(m, k)));
-        if ((st = launch_quantize(ctx, x, x_dtype, m, k, xq_out, sx, nullptr, tiles, stream, err))) return st;
+        if ((st = launch_quantize(ctx, x, x_dtype, m, k, xq_out, sx, nullptr, tiles, stream, err, 0, nullptr, 1,
+                                  nonfinite, nonfinite_stage)))
+            return st;
         return launch_gemv(ctx, tiles, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, true, stream, err,
                            relu2);
     }
@@ -501,7 +506,9 @@ nh_status linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const in
     if (!aligned16(workspace)) return set_error(err, NH_UNSUPPORTED, "workspace must be 16-byte aligned");
     int8_t* atiles = (int8_t*)workspace;
     float* sx = sx_out ? sx_out : (float*)((char*)workspace + align256(tiled_bytes(m, k)));
-    if ((st = launch_quantize(ctx, x, x_dtype, m, k, xq_out, sx, nullptr, atiles, stream, err, 16))) return st;
+    if ((st = launch_quantize(ctx, x, x_dtype, m, k, xq_out, sx, nullptr, atiles, stream, err, 16, nullptr, 1,
+                              nonfinite, nonfinite_stage)))
+        return st;
     return launch_gemm(ctx, atiles, sx, wq, sw, bias, (int)m, (int)n, (int)k, out, out_dtype, relu2, stream, err,
                        true);
 }
@@ -512,8 +519,8 @@ extern "C" {
 
 nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* wq, const float* sw,
                          const float* bias, size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype,
-                         void* workspace, size_t workspace_bytes, int8_t* xq_out, float* sx_out, nh_stream stream,
-                         nh_error* err) {
+                         void* workspace, size_t workspace_bytes, int8_t* xq_out, float* sx_out, uint64_t* nonfinite,
+                         nh_stream stream, nh_error* err) {
     clear_error(err);
     if (m == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
     nh_status st;
@@ -523,7 +530,7 @@ nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
     if (!aligned16(wq)) return set_error(err, NH_UNSUPPORTED, "wq must be 16-byte aligned");
     if ((st = bind_device(ctx, err))) return st;
     return linear_w8a8(ctx, x, x_dtype, wq, sw, bias, m, n, k, out, out_dtype, workspace, workspace_bytes, xq_out,
-                       sx_out, 0, stream, err);
+                       sx_out, 0, nonfinite, 0, stream, err);
 }
 
 size_t nh_mlp_w8a8_workspace_size(size_t m, size_t hidden, size_t inter) {
@@ -535,7 +542,7 @@ size_t nh_mlp_w8a8_workspace_size(size_t m, size_t hidden, size_t inter) {
 nh_status nh_mlp_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* w_up, const float* s_up,
                       const float* b_up, const int8_t* w_down, const float* s_down, const float* b_down, size_t m,
                       size_t hidden, size_t inter, void* out, nh_dtype out_dtype, void* workspace,
-                      size_t workspace_bytes, nh_stream stream, nh_error* err) {
+                      size_t workspace_bytes, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
     clear_error(err);
     if (hidden == 0 || inter == 0)
         return set_error(err, NH_INVALID_SHAPE, "mlp shape must be non-zero, got hidden_dim=%zu, intermediate_dim=%zu",
@@ -556,10 +563,11 @@ nh_status nh_mlp_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const in
     void* lin_ws = (char*)workspace + align256(m * inter * sizeof(float));
     const size_t lin_bytes = workspace_bytes - align256(m * inter * sizeof(float));
     if ((st = linear_w8a8(ctx, x, x_dtype, w_up, s_up, b_up, m, inter, hidden, h, NH_F32, lin_ws, lin_bytes, nullptr,
-                          nullptr, 1, stream, err)))
+                          nullptr, 1, nonfinite, 0, stream, err)))
         return st;
+    // h: the layer's intermediate (stage 1 of the non-finite report)
     return linear_w8a8(ctx, h, NH_F32, w_down, s_down, b_down, m, hidden, inter, out, out_dtype, lin_ws, lin_bytes,
-                       nullptr, nullptr, 0, stream, err);
+                       nullptr, nullptr, 0, nonfinite, 1, stream, err);
 }
 
 nh_status nh_gemv_w8a32(nh_context* ctx, const float* x, const int8_t* wq, const float* sw, size_t m, size_t n,
@@ -639,8 +647,12 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
         constexpr int kExpertWaves = 8;
         const int ntiles = (int)((n + 15) / 16);
         const int tiles_per_wg = (ntiles + 1) / 2;
+        // the weight scales arrive by 64-float direct-to-LDS rows (256 bytes
+        // each, also past the workgroup's last column), so their region is a
+        // whole number of rows
         auto expert_lds = [&](int rb) {
-            return (size_t)rb * kt * 1024 + (size_t)rb * 16 * 4 + (size_t)tiles_per_wg * 16 * 4;
+            const size_t sws_floats = ((size_t)tiles_per_wg * 16 + 63) / 64 * 64;
+            return (size_t)rb * kt * 1024 + (size_t)rb * 16 * 4 + sws_floats * 4;
         };
         int row_blocks = 4;
         while (row_blocks > 1 && expert_lds(row_blocks) > ctx->max_shared_per_block) --row_blocks;
@@ -761,7 +773,7 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
                              const int8_t* w_up, const float* s_up, const int8_t* w_down, const float* s_down,
                              size_t inter_sh, const int8_t* w_up_sh, const float* s_up_sh, const int8_t* w_down_sh,
                              const float* s_down_sh, void* out, nh_dtype out_dtype, void* workspace,
-                             size_t workspace_bytes, nh_stream stream, nh_error* err) {
+                             size_t workspace_bytes, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
     clear_error(err);
     if (tokens == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
     if (hidden == 0 || experts == 0 || top_k == 0 || top_k > experts || inter == 0)
@@ -796,7 +808,7 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
     if (has_shared &&
         (st = nh_mlp_w8a8(ctx, x, x_dtype, w_up_sh, s_up_sh, nullptr, w_down_sh, s_down_sh, nullptr, tokens, hidden,
                           inter_sh, shared, NH_F32, ws + shared_at + shared_bytes, workspace_bytes - shared_at -
-                          shared_bytes, stream, err)))
+                          shared_bytes, nonfinite, stream, err)))
         return st;
     if ((st = nh_moe_route_sigmoid_topk(ctx, logits, tokens, experts, top_k, renormalize, scaling, idx, wts, stream,
                                         err)))
@@ -806,12 +818,15 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
     // perm[s] / top_k): the up projection then reads its rows contiguously,
     // with no index load in front of its activation loads
     if ((st = launch_quantize(ctx, x, x_dtype, R, hidden, xq, sx, nullptr, nullptr, stream, err, 0, perm,
-                              (int)top_k)))
+                              (int)top_k, nonfinite, 0)))
         return st;
     if ((st = nh_moe_grouped_gemm_w8a8(ctx, xq, sx, 0, top_k, offsets, perm, R, R, experts, w_up, s_up, inter,
                                        hidden, 1, h, stream, err)))
         return st;
-    if ((st = nh_quantize_rows_i8(ctx, h, NH_F32, R, inter, hq, sh, nullptr, stream, err))) return st;
+    // the up outputs per slot: the layer's intermediate (stage 1)
+    if ((st = launch_quantize(ctx, h, NH_F32, R, inter, hq, sh, nullptr, nullptr, stream, err, 0, nullptr, 1,
+                              nonfinite, 1)))
+        return st;
     if ((st = nh_moe_grouped_gemm_w8a8(ctx, hq, sh, 0, top_k, offsets, perm, R, R, experts, w_down, s_down, hidden,
                                        inter, 0, d, stream, err)))
         return st;
@@ -822,10 +837,10 @@ nh_status nh_moe_forward_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, 
                               size_t hidden, size_t inter, size_t experts, size_t top_k, int renormalize,
                               float scaling, const int8_t* w_up, const float* s_up, const int8_t* w_down,
                               const float* s_down, void* out, nh_dtype out_dtype, void* workspace,
-                              size_t workspace_bytes, nh_stream stream, nh_error* err) {
+                              size_t workspace_bytes, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
     return moe_forward(ctx, x, x_dtype, logits, tokens, hidden, inter, experts, top_k, renormalize, scaling, w_up,
                        s_up, w_down, s_down, 0, nullptr, nullptr, nullptr, nullptr, out, out_dtype, workspace,
-                       workspace_bytes, stream, err);
+                       workspace_bytes, nonfinite, stream, err);
 }
 
 size_t nh_moe_forward_shared_w8a8_workspace_size(size_t tokens, size_t hidden, size_t inter, size_t experts,
@@ -842,15 +857,42 @@ nh_status nh_moe_forward_shared_w8a8(nh_context* ctx, const void* x, nh_dtype x_
                                      const int8_t* w_down, const float* s_down, size_t shared_inter,
                                      const int8_t* w_up_shared, const float* s_up_shared,
                                      const int8_t* w_down_shared, const float* s_down_shared, void* out,
-                                     nh_dtype out_dtype, void* workspace, size_t workspace_bytes, nh_stream stream,
-                                     nh_error* err) {
+                                     nh_dtype out_dtype, void* workspace, size_t workspace_bytes,
+                                     uint64_t* nonfinite, nh_stream stream, nh_error* err) {
     if (!w_up_shared) {
         clear_error(err);
         return set_error(err, NH_INVALID_PARAMS, "w_up_shared must not be null (nh_moe_forward_w8a8 has no shared expert)");
     }
     return moe_forward(ctx, x, x_dtype, logits, tokens, hidden, inter, experts, top_k, renormalize, scaling, w_up,
                        s_up, w_down, s_down, shared_inter, w_up_shared, s_up_shared, w_down_shared, s_down_shared,
-                       out, out_dtype, workspace, workspace_bytes, stream, err);
+                       out, out_dtype, workspace, workspace_bytes, nonfinite, stream, err);
 }
 
 }  // extern "C"
+
+extern "C" nh_status nh_take_nonfinite(nh_context* ctx, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    if (!nonfinite) return set_error(err, NH_INVALID_PARAMS, "null non-finite word");
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) return device_error(err, e, "hipStreamSynchronize");
+    uint64_t word = 0;
+    e = hipMemcpy(&word, nonfinite, sizeof(word), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return device_error(err, e, "hipMemcpy(DtoH)");
+    if (word == 0) return NH_OK;
+    const uint64_t zero = 0;  // cleared for the next call
+    e = hipMemcpy(nonfinite, &zero, sizeof(zero), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return device_error(err, e, "hipMemcpy(HtoD)");
+    const uint64_t key = ~word;
+    const char* what = (key >> 63) ? "intermediate" : "input";
+    const uint64_t index = (key >> 32) & 0x7fffffffu;
+    const float value = f32_from_bits((uint32_t)key);
+    if (err) {
+        err->argument = what;
+        err->index = index;
+        err->value = value;
+    }
+    return set_error(err, NH_NON_FINITE_INPUT, "non-finite %s value %g at index %llu", what, (double)value,
+                     (unsigned long long)index);
+}

@@ -105,9 +105,10 @@ _SIGNATURES = {
     "nh_gemm_w8a8_ta": (ST, [P, P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, P, E]),
     "nh_gemm_w8a8_host": (ST, [P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, E]),
     "nh_linear_w8a8_workspace_size": (SZ, [SZ, SZ]),
-    "nh_linear_w8a8": (ST, [P, P, C.c_int, P, P, P, SZ, SZ, SZ, P, C.c_int, P, SZ, P, P, P, E]),
+    "nh_take_nonfinite": (ST, [P, P, P, E]),
+    "nh_linear_w8a8": (ST, [P, P, C.c_int, P, P, P, SZ, SZ, SZ, P, C.c_int, P, SZ, P, P, P, P, E]),
     "nh_mlp_w8a8_workspace_size": (SZ, [SZ, SZ, SZ]),
-    "nh_mlp_w8a8": (ST, [P, P, C.c_int, P, P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, P, SZ, P, E]),
+    "nh_mlp_w8a8": (ST, [P, P, C.c_int, P, P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, P, SZ, P, P, E]),
     "nh_gemv_w8a32": (ST, [P, P, P, P, SZ, SZ, SZ, P, P, E]),
     "nh_gemv_w8a32_host": (ST, [P, P, P, SZ, SZ, SZ, P, E]),
     "nh_sigmoid_f32_host": (C.c_float, [C.c_float]),
@@ -123,17 +124,17 @@ _SIGNATURES = {
     "nh_moe_forward_w8a8_workspace_size": (SZ, [SZ, SZ, SZ, SZ, SZ]),
     "nh_moe_workspace_layout": (None, [SZ, SZ, SZ, SZ, SZ, C.POINTER(SZ)]),
     "nh_moe_forward_w8a8": (ST, [P, P, C.c_int, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, P,
-                                 C.c_int, P, SZ, P, E]),
+                                 C.c_int, P, SZ, P, P, E]),
     "nh_moe_combine_shared": (ST, [P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, P, E]),
     "nh_moe_combine_shared_host": (ST, [P, P, P, P, SZ, SZ, SZ, P, C.c_int, E]),
     "nh_moe_forward_shared_w8a8_workspace_size": (SZ, [SZ, SZ, SZ, SZ, SZ, SZ]),
     "nh_moe_forward_shared_w8a8": (ST, [P, P, C.c_int, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, SZ,
-                                        P, P, P, P, P, C.c_int, P, SZ, P, E]),
+                                        P, P, P, P, P, C.c_int, P, SZ, P, P, E]),
     "nh_tiled_int4_weights_bytes": (SZ, [SZ, SZ]),
     "nh_tile_weights_int4": (ST, [P, P, SZ, SZ, SZ, C.c_uint32, P, SZ, P, E]),
     "nh_tile_weights_int4_host": (ST, [P, SZ, SZ, SZ, C.c_uint32, P, SZ, E]),
     "nh_supports_linear_w4a8": (C.c_int, [SZ, SZ, SZ]),
-    "nh_linear_w4a8": (ST, [P, P, C.c_int, P, C.c_float, C.c_uint32, P, SZ, SZ, SZ, P, C.c_int, P, E]),
+    "nh_linear_w4a8": (ST, [P, P, C.c_int, P, C.c_float, C.c_uint32, P, SZ, SZ, SZ, P, C.c_int, P, P, E]),
     "nh_linear_w4a8_host": (ST, [P, C.c_int, P, SZ, C.c_float, C.c_uint32, P, SZ, SZ, SZ, P, C.c_int, E]),
     "nh_safetensors_tensor_info": (ST, [C.c_char_p, C.c_char_p, C.POINTER(TensorInfo), E]),
     "nh_safetensors_read": (ST, [P, C.c_char_p, C.c_char_p, P, SZ, E]),

@@ -63,7 +63,7 @@ def test_mlp_validates_like_mlp_layer_before_touching_a_device():
     then the workspace, all before the (NULL) context is used."""
     mlp = lambda m, hidden, inter, ws, ws_bytes: NH.call_status(
         "nh_mlp_w8a8", None, None, NH.BF16, None, None, None, None, None, None, m, hidden, inter, None, NH.BF16,
-        ws, ws_bytes, None)
+        ws, ws_bytes, None, None)
     assert mlp(1, 0, 64, None, 0)[0] == NH.INVALID_SHAPE
     assert mlp(1, 64, 0, None, 0)[0] == NH.INVALID_SHAPE
     assert mlp(0, 64, 64, None, 0)[0] == NH.INVALID_ROW_COUNT
@@ -92,7 +92,7 @@ def test_device_entry_points_validate_before_touching_a_device():
     st, err = NH.call_status("nh_gemm_w8a8", None, None, None, None, None, None, 2, 4, 12, None, NH.F32, None)
     assert st == NH.UNSUPPORTED  # k % 16 != 0 -> caller uses the host twin
     st, err = NH.call_status("nh_linear_w8a8", None, None, NH.BF16, None, None, None, 0, 4, 16, None, NH.BF16,
-                             None, 0, None, None, None)
+                             None, 0, None, None, None, None)
     assert st == NH.INVALID_ROW_COUNT
     st, err = NH.call_status("nh_moe_route_sigmoid_topk", None, None, 1, 2, 3, 0, 1.0, None, None, None)
     assert st == NH.INVALID_SHAPE
@@ -418,7 +418,7 @@ def test_moe_forward_shared_validation_before_any_launch():
         dummy = 16
         return NH.call_status("nh_moe_forward_shared_w8a8", None, dummy, NH.BF16, dummy, tokens, H, I, E, K, 1, 1.0,
                               dummy, dummy, dummy, dummy, si, up_sh, dummy, dummy, dummy, dummy, NH.BF16,
-                              dummy if ws_bytes else None, ws_bytes, None)
+                              dummy if ws_bytes else None, ws_bytes, None, None)
 
     assert call(SI, None, need)[0] == NH.INVALID_PARAMS
     assert call(0, 16, need)[0] == NH.INVALID_SHAPE
@@ -470,7 +470,7 @@ def test_int4_validation_in_the_reference_order():
     assert host(2, 2, 2, 0.5, 8, 0)[0] == NH.INVALID_ROW_COUNT
     # the device entry point validates before touching the (NULL) context
     dev = lambda m, n, k, scale=0.5, zp=8: NH.call_status(  # noqa: E731
-        "nh_linear_w4a8", None, 16, NH.BF16, 16, scale, zp, None, m, n, k, 16, NH.BF16, None)[0]
+        "nh_linear_w4a8", None, 16, NH.BF16, 16, scale, zp, None, m, n, k, 16, NH.BF16, None, None)[0]
     assert dev(1, 0, 64) == NH.INVALID_SHAPE
     assert dev(1, 16, 64, scale=-1.0) == NH.INVALID_PARAMS
     assert dev(0, 16, 64) == NH.INVALID_ROW_COUNT

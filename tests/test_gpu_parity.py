@@ -19,6 +19,7 @@ import pytest
 
 import nemotron_hip as NH
 import oracle_ctypes as O
+from exact_int import linear_w8a8_exact, moe_forward_exact, moe_grouped_exact
 from tiling import tile_16x64, tile_experts
 
 pytestmark = pytest.mark.gpu
@@ -279,10 +280,12 @@ def test_gemv_w8a8_bit_exact(ctx, m, n, k):
         assert np.array_equal(got, ref), f"max diff {np.max(np.abs(got.astype(np.float64) - ref))}"
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 13, 16])
-def test_linear_decode_unit_bit_exact(ctx, m):
-    n, k = 16384, 4096
-    note(f"linear_w8a8 decode m={m}")
+@pytest.mark.parametrize("m,n,k", [(m, 16384, 4096) for m in (1, 2, 3, 4, 5, 8, 13, 16)] +
+                         # configs[1]'s out_proj-like shape: the one-tile decode unit with 8 K waves
+                         # (M = 1..4), the two-launch path beyond
+                         [(m, 4096, 8192) for m in (1, 2, 4, 8, 16)])
+def test_linear_decode_unit_bit_exact(ctx, m, n, k):
+    note(f"linear_w8a8 decode m={m} n={n} k={k}")
     _, wq, sw = quantized_weights(n, k)
     x = activations_bf16(m, k, seed=1 + m)
     _, xq_ref, sx_ref, _ = O.quantize_rows_bf16(x)
@@ -295,7 +298,7 @@ def test_linear_decode_unit_bit_exact(ctx, m):
     ws_bytes = NH.lib().nh_linear_w8a8_workspace_size(m, k)
     ws = ctx.empty(max(ws_bytes, 1), np.uint8)
     NH.call("nh_linear_w8a8", ctx.handle, dx.ptr, NH.BF16, dw.ptr, ds.ptr, None, m, n, k, out.ptr, NH.BF16,
-            ws.ptr, ws_bytes, xq.ptr, sx.ptr, None)
+            ws.ptr, ws_bytes, xq.ptr, sx.ptr, None, None)
     ctx.synchronize()
     assert np.array_equal(xq.numpy(), xq_ref)
     assert np.array_equal(sx.numpy().view(np.uint32), sx_ref.view(np.uint32))
@@ -303,7 +306,7 @@ def test_linear_decode_unit_bit_exact(ctx, m):
     # without the optional quantized outputs (workspace path for m > 4)
     out2 = ctx.empty((m, n), np.uint16)
     NH.call("nh_linear_w8a8", ctx.handle, dx.ptr, NH.BF16, dw.ptr, ds.ptr, None, m, n, k, out2.ptr, NH.BF16,
-            ws.ptr, ws_bytes, None, None, None)
+            ws.ptr, ws_bytes, None, None, None, None)
     ctx.synchronize()
     assert np.array_equal(out2.numpy(), ref)
 
@@ -341,7 +344,7 @@ def test_linear_small_m_shapes_bit_exact(ctx, m, n, k, dtype):
     xq = ctx.empty((m, k), np.int8)
     sx = ctx.empty(m, np.float32)
     NH.call("nh_linear_w8a8", ctx.handle, dx.ptr, dt, dw.ptr, ds.ptr, db.ptr, m, n, k, out.ptr, NH.F32,
-            ws.ptr, ws_bytes, xq.ptr, sx.ptr, None)
+            ws.ptr, ws_bytes, xq.ptr, sx.ptr, None, None)
     ctx.synchronize()
     assert np.array_equal(xq.numpy(), xq_ref)
     assert np.array_equal(sx.numpy().view(np.uint32), sx_ref.view(np.uint32))
@@ -385,7 +388,7 @@ def test_mlp_bit_exact(ctx, m, hidden, inter, dtype):
     ws = ctx.empty(ws_bytes, np.uint8)
     out = ctx.empty((m, hidden), np.uint16)
     NH.call("nh_mlp_w8a8", ctx.handle, dx.ptr, xdt, dwu.ptr, dsu.ptr, db_up.ptr, dwd.ptr, dsd.ptr, db_down.ptr,
-            m, hidden, inter, out.ptr, NH.BF16, ws.ptr, ws_bytes, None)
+            m, hidden, inter, out.ptr, NH.BF16, ws.ptr, ws_bytes, None, None)
     ctx.synchronize()
     assert np.array_equal(out.numpy(), ref)
 
@@ -428,7 +431,7 @@ def test_linear_decode_unit_rounding_ties(ctx, m):
     ws_bytes = NH.lib().nh_linear_w8a8_workspace_size(m, k)
     ws = ctx.empty(max(ws_bytes, 1), np.uint8)
     NH.call("nh_linear_w8a8", ctx.handle, dx.ptr, NH.BF16, dw.ptr, ds.ptr, None, m, n, k, out.ptr, NH.BF16,
-            ws.ptr, ws_bytes, xq.ptr, sx.ptr, None)
+            ws.ptr, ws_bytes, xq.ptr, sx.ptr, None, None)
     ctx.synchronize()
     assert np.array_equal(sx.numpy().view(np.uint32), sx_ref.view(np.uint32))
     assert np.array_equal(xq.numpy(), xq_ref)
@@ -474,7 +477,7 @@ def test_linear_w4a8_bit_exact(ctx, m, n, k, zp):
     for out_dtype, bf in ((NH.BF16, True), (NH.F32, False)):
         out = ctx.empty((m, n), np.uint16 if bf else np.float32)
         NH.call("nh_linear_w4a8", ctx.handle, dx.ptr, NH.BF16, dt.ptr, scale, zp, db.ptr if db else None, m, n, k,
-                out.ptr, out_dtype, None)
+                out.ptr, out_dtype, None, None)
         ctx.synchronize()
         st, ref = O.linear_w4a8(x, packed, n, scale, zp, bias=bias, out_bf16=bf)
         assert st == O.OK
@@ -504,11 +507,12 @@ def test_gemm_w8a8_bit_exact(ctx, m, n, k, a_layout):
     NH.call(fn, ctx.handle, dxq.ptr, dsx.ptr, dw.ptr, dsw.ptr, None, m, n, k, out.ptr, NH.BF16, None)
     ctx.synchronize()
     got = out.numpy()
-    rows = np.arange(m) if m * n * k <= 2e9 else np.unique(np.concatenate(
-        [np.arange(0, m, max(1, m // 24)), [m - 1, 255, 256, 1023, 1024]]))
-    rows = rows[rows < m]
-    ref = O.linear_w8a8(xq[rows], sx[rows], wq, sw, out_bf16=True)
-    assert np.array_equal(got[rows], ref)
+    # every row and column: the oracle's epilogue on exact accumulators (the
+    # oracle's own int32 loop for small shapes, exact float64 BLAS for the
+    # M = 2048 configs, pinned against it in test_exact_int.py)
+    ref = O.linear_w8a8(xq, sx, wq, sw, out_bf16=True) if m * n * k <= 2e9 else \
+        linear_w8a8_exact(xq, sx, wq, sw, out_bf16=True)
+    assert np.array_equal(got, ref)
 
 
 # ---- R1..R4: MoE -----------------------------------------------------------------
@@ -610,11 +614,16 @@ def moe_weights(experts, inter, hidden):
     return up, su, down, sd
 
 
+@functools.lru_cache(maxsize=1)
+def moe_weights_cached(experts, inter, hidden):
+    return moe_weights(experts, inter, hidden)
+
+
 @functools.lru_cache(maxsize=2)
 def moe_case(tokens, hidden, inter, experts, top_k):
     x = activations_bf16(tokens, hidden)
     logits = O.normal_f32(2, tokens * experts)
-    up, su, down, sd = moe_weights(experts, inter, hidden)
+    up, su, down, sd = moe_weights_cached(experts, inter, hidden)
     return x, logits, up, su, down, sd
 
 
@@ -695,7 +704,7 @@ def test_moe_forward_shared_expert_bit_exact(ctx, tokens, hidden, inter, experts
     out = ctx.empty((tokens, hidden), np.uint16)
     NH.call("nh_moe_forward_shared_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k,
             1, 1.0, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, sh_inter, dhu.ptr, dhsu.ptr, dhd.ptr, dhsd.ptr, out.ptr,
-            NH.BF16, ws.ptr, ws_bytes, None)
+            NH.BF16, ws.ptr, ws_bytes, None, None)
     ctx.synchronize()
     assert np.array_equal(out.numpy(), ref)
 
@@ -713,7 +722,7 @@ def test_moe_forward_bit_exact(ctx, tokens, hidden, inter, experts, top_k):
     dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
     out = ctx.empty((tokens, hidden), np.uint16)
     NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
-            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, None)
+            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, None, None)
     ctx.synchronize()
     lay = (ctypes.c_size_t * 5)()
     NH.lib().nh_moe_workspace_layout(tokens, hidden, inter, experts, top_k, lay)
@@ -723,3 +732,178 @@ def test_moe_forward_bit_exact(ctx, tokens, hidden, inter, experts, top_k):
     assert np.array_equal(wsh[lay[2]:lay[2] + 4 * (experts + 1)].view(np.int32), offsets)
     assert np.array_equal(wsh[lay[3]:lay[3] + 4 * R].view(np.int32), perm)
     assert np.array_equal(out.numpy(), ref)
+
+
+# ---- configs[3] at its full size: 512 tokens, 128 experts, top-6 ----------------
+CONFIG3 = (512, 2688, 1856, 128, 6)
+
+
+@functools.lru_cache(maxsize=1)
+def config3_reference():
+    """The oracle's composition at configs[3]: the stages are the oracle's,
+    the expert accumulations exact through float64 BLAS (exact_int.py)."""
+    tokens, hidden, inter, experts, top_k = CONFIG3
+    x, logits, up, su, down, sd = moe_case(*CONFIG3)
+    return moe_forward_exact(x, logits, up, su, down, sd, top_k)
+
+
+def test_moe_forward_config3_bit_exact(ctx):
+    """nh_moe_forward_w8a8 at configs[3] (the bench's layer): every routing
+    index and weight, the offsets, the permutation and its inverse from the
+    workspace, and every output element against the oracle."""
+    tokens, hidden, inter, experts, top_k = CONFIG3
+    note(f"moe forward configs[3] t={tokens} h={hidden} i={inter} e={experts} k={top_k}")
+    x, logits, up, su, down, sd = moe_case(*CONFIG3)
+    ref, idx, w, offsets, perm, pos, _, _ = config3_reference()
+    counts = np.diff(offsets)
+    note(f"routes per expert: min {counts.min()} max {counts.max()} (expert kernel passes: 48 rows at K=2688)")
+    ws_bytes = NH.lib().nh_moe_forward_w8a8_workspace_size(tokens, hidden, inter, experts, top_k)
+    ws = ctx.empty(ws_bytes, np.uint8)
+    ws.fill_bytes(0xa5)
+    dx, dl = ctx.upload(x), ctx.upload(logits)
+    dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
+    out = ctx.empty((tokens, hidden), np.uint16)
+    NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
+            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, None, None)
+    ctx.synchronize()
+    lay = (ctypes.c_size_t * 5)()
+    NH.lib().nh_moe_workspace_layout(tokens, hidden, inter, experts, top_k, lay)
+    wsh = ws.numpy()
+    R = tokens * top_k
+    assert np.array_equal(wsh[lay[0]:lay[0] + 4 * R].view(np.int32), idx)
+    assert np.array_equal(wsh[lay[1]:lay[1] + 4 * R].view(np.uint32), w.view(np.uint32))
+    assert np.array_equal(wsh[lay[2]:lay[2] + 4 * (experts + 1)].view(np.int32), offsets)
+    assert np.array_equal(wsh[lay[3]:lay[3] + 4 * R].view(np.int32), perm)
+    assert np.array_equal(wsh[lay[4]:lay[4] + 4 * R].view(np.int32), pos)
+    got = out.numpy()
+    assert np.array_equal(got, ref), f"{(got != ref).sum()} of {ref.size} outputs differ"
+
+
+def test_grouped_gemm_config3_routes_bit_exact(ctx):
+    """nh_moe_grouped_gemm_w8a8 on the 3072 routes of configs[3]: the up
+    projection gathered from token-major codes (the grouped kernel) and from
+    slot-ordered codes (the MoE layer's expert-block kernel), and the down
+    projection, every output against the oracle."""
+    tokens, hidden, inter, experts, top_k = CONFIG3
+    note(f"grouped gemm configs[3] routes={tokens * top_k}")
+    x, logits, up, su, down, sd = moe_case(*CONFIG3)
+    _, idx, w, offsets, perm, pos, h_ref, d_ref = config3_reference()
+    _, xq, sx, _ = O.quantize_rows_bf16(x)
+    R = tokens * top_k
+    d = {nm: ctx.upload(a) for nm, a in dict(xq=xq, sx=sx, xs=xq[perm // top_k], ss=sx[perm // top_k], off=offsets,
+                                               perm=perm, up=tile_experts(up), su=su, down=tile_experts(down),
+                                               sd=sd).items()}
+    h = ctx.empty((R, inter), np.float32)
+    NH.call("nh_moe_grouped_gemm_w8a8", ctx.handle, d["xq"].ptr, d["sx"].ptr, 1, top_k, d["off"].ptr, d["perm"].ptr,
+            R, tokens, experts, d["up"].ptr, d["su"].ptr, inter, hidden, 1, h.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(h.numpy(), h_ref)
+    h2 = ctx.empty((R, inter), np.float32)
+    NH.call("nh_moe_grouped_gemm_w8a8", ctx.handle, d["xs"].ptr, d["ss"].ptr, 0, top_k, d["off"].ptr, d["perm"].ptr,
+            R, R, experts, d["up"].ptr, d["su"].ptr, inter, hidden, 1, h2.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(h2.numpy(), h_ref)
+    _, hq, sh, _ = O.quantize_rows_f32(h_ref)
+    dhq, dsh = ctx.upload(hq), ctx.upload(sh)
+    dd = ctx.empty((R, hidden), np.float32)
+    NH.call("nh_moe_grouped_gemm_w8a8", ctx.handle, dhq.ptr, dsh.ptr, 0, top_k, d["off"].ptr, d["perm"].ptr, R, R,
+            experts, d["down"].ptr, d["sd"].ptr, hidden, inter, 0, dd.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(dd.numpy(), d_ref)
+
+
+# ---- NonFiniteInput from the device quantizers -----------------------------------
+def take_nonfinite(ctx, word):
+    return NH.call_status("nh_take_nonfinite", ctx.handle, word.ptr, None)
+
+
+@pytest.mark.parametrize("m,n,k,dtype", [(1, 4096, 4096, "bf16"),    # fused one-row unit
+                                         (3, 4096, 8192, "bf16"),    # fused 4-row unit, one N tile per workgroup
+                                         (6, 16384, 4096, "bf16"),   # fused wide unit
+                                         (12, 1024, 4096, "bf16"),   # quantizer into activation tiles + GEMV
+                                         (2, 1024, 4096, "f32"),     # f32 rows: the row quantizer
+                                         (40, 512, 1024, "bf16")])   # quantizer into A tiles + GEMM
+def test_linear_nonfinite_input_reported(ctx, m, n, k, dtype):
+    """A NaN or infinity in x: nh_take_nonfinite returns NonFiniteInput with
+    the oracle's first non-finite index (row-major) and value, then the word is
+    clear; a finite call leaves it clear."""
+    note(f"linear nonfinite m={m} n={n} k={k} {dtype}")
+    _, wq, sw = quantized_weights(n, k)
+    xf = O.normal_f32(60 + m, m * k).reshape(m, k)
+    xf[m - 1, 5] = np.inf
+    xf[m // 2, k - 3] = np.nan
+    xf[m // 2, k - 1] = -np.inf
+    x = O.to_bf16(xf) if dtype == "bf16" else xf
+    st, _, _, oerr = O.quantize_rows_bf16(x) if dtype == "bf16" else O.quantize_rows_f32(x)
+    assert st == O.NON_FINITE_INPUT
+    dx, dw, ds = ctx.upload(x), ctx.upload(tile_16x64(wq)), ctx.upload(sw)
+    word = ctx.upload(np.zeros(1, dtype=np.uint64))
+    ws_bytes = NH.lib().nh_linear_w8a8_workspace_size(m, k)
+    ws = ctx.empty(max(ws_bytes, 1), np.uint8)
+    out = ctx.empty((m, n), np.uint16)
+    dt = NH.BF16 if dtype == "bf16" else NH.F32
+    NH.call("nh_linear_w8a8", ctx.handle, dx.ptr, dt, dw.ptr, ds.ptr, None, m, n, k, out.ptr, NH.BF16, ws.ptr,
+            ws_bytes, None, None, word.ptr, None)
+    st, err = take_nonfinite(ctx, word)
+    assert st == NH.NON_FINITE_INPUT
+    first = int(np.flatnonzero(~np.isfinite(xf))[0])
+    assert err.argument == b"input" and err.index == oerr.index == first
+    want = xf.flat[first]
+    assert (np.isnan(err.value) and np.isnan(want)) or err.value == want
+    assert take_nonfinite(ctx, word)[0] == NH.OK  # cleared
+    xc = np.where(np.isfinite(xf), xf, 0.0).astype(np.float32)
+    dxc = ctx.upload(O.to_bf16(xc) if dtype == "bf16" else xc)
+    NH.call("nh_linear_w8a8", ctx.handle, dxc.ptr, dt, dw.ptr, ds.ptr, None, m, n, k, out.ptr, NH.BF16, ws.ptr,
+            ws_bytes, None, None, word.ptr, None)
+    assert take_nonfinite(ctx, word)[0] == NH.OK
+    assert np.array_equal(word.numpy(), np.zeros(1, dtype=np.uint64))
+
+
+def test_mlp_nonfinite_intermediate_and_input_reported(ctx):
+    """The MLP's f32 intermediate overflows (ReLU^2 of a 3e38 biased output is
+    +inf): reported as "intermediate" at its row-major index; a NaN in x takes
+    precedence as "input"."""
+    m, hidden, inter = 2, 512, 1024
+    note("mlp nonfinite")
+    w_up, s_up, w_down, s_down = mlp_weights(hidden, inter)
+    b_up = np.zeros(inter, dtype=np.float32)
+    b_up[3] = 3e38
+    x = activations_bf16(m, hidden, seed=70)
+    d = {nm: ctx.upload(a) for nm, a in dict(x=x, bu=b_up, wu=tile_16x64(w_up), su=s_up, wd=tile_16x64(w_down),
+                                               sd=s_down).items()}
+    ws_bytes = NH.lib().nh_mlp_w8a8_workspace_size(m, hidden, inter)
+    ws = ctx.empty(ws_bytes, np.uint8)
+    out = ctx.empty((m, hidden), np.uint16)
+    word = ctx.upload(np.zeros(1, dtype=np.uint64))
+
+    def run(dx):
+        NH.call("nh_mlp_w8a8", ctx.handle, dx.ptr, NH.BF16, d["wu"].ptr, d["su"].ptr, d["bu"].ptr, d["wd"].ptr,
+                d["sd"].ptr, None, m, hidden, inter, out.ptr, NH.BF16, ws.ptr, ws_bytes, word.ptr, None)
+        return take_nonfinite(ctx, word)
+
+    st, err = run(d["x"])
+    assert st == NH.NON_FINITE_INPUT and err.argument == b"intermediate" and err.index == 3
+    assert np.isinf(err.value) and err.value > 0
+    xb = x.copy()
+    xb[1, 17] = O.to_bf16(np.array([np.nan], dtype=np.float32))[0]
+    st, err = run(ctx.upload(xb))
+    assert st == NH.NON_FINITE_INPUT and err.argument == b"input" and err.index == hidden + 17
+
+
+def test_moe_nonfinite_input_reported(ctx):
+    tokens, hidden, inter, experts, top_k = 13, 64, 32, 8, 3
+    note("moe nonfinite")
+    x, logits, up, su, down, sd = moe_case(tokens, hidden, inter, experts, top_k)
+    xb = x.copy()
+    xb[5, 10] = O.to_bf16(np.array([-np.inf], dtype=np.float32))[0]
+    ws_bytes = NH.lib().nh_moe_forward_w8a8_workspace_size(tokens, hidden, inter, experts, top_k)
+    ws = ctx.empty(ws_bytes, np.uint8)
+    dx, dl = ctx.upload(xb), ctx.upload(logits)
+    dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
+    out = ctx.empty((tokens, hidden), np.uint16)
+    word = ctx.upload(np.zeros(1, dtype=np.uint64))
+    NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
+            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, word.ptr, None)
+    st, err = take_nonfinite(ctx, word)
+    assert st == NH.NON_FINITE_INPUT and err.argument == b"input" and err.index == 5 * hidden + 10
+    assert np.isinf(err.value) and err.value < 0

@@ -190,6 +190,6 @@ def test_load_linear_i8_then_project(ctx, tmp_path, n, k):
     _, xq, sx, _ = O.quantize_rows_bf16(x)
     dx, out = ctx.upload(x), ctx.empty((1, n), np.uint16)
     NH.call("nh_linear_w8a8", ctx.handle, dx.ptr, NH.BF16, tiled.ptr, scales.ptr, None, 1, n, k, out.ptr, NH.BF16,
-            None, 0, None, None, None)
+            None, 0, None, None, None, None)
     ctx.synchronize()
     assert np.array_equal(out.numpy(), O.linear_w8a8(xq, sx, q, s, out_bf16=True))
