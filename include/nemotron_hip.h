@@ -202,6 +202,21 @@ nh_status nh_linear_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const
                          const float *bias, size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype,
                          void *workspace, size_t workspace_bytes, int8_t *xq_out, float *sx_out,
                          uint64_t *nonfinite, nh_stream stream, nh_error *err);
+/* nh_linear_w8a8 without a workspace argument and without allocating, for
+ * callers that cannot call hipMalloc (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  No counterpart in the
+ * reference.  The workspace is a static device array of 64 MiB (67108864
+ * bytes) per GPU, placed by the HIP runtime and held until the process ends;
+ * shapes whose nh_linear_w8a8_workspace_size(m, k) exceeds it return
+ * NH_UNSUPPORTED before anything is launched (m = 2048 fits k <= 32704, the
+ * 21504-wide MLP down projection included).
+ * Results are those of nh_linear_w8a8.  Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU (concurrent streams or threads)
+ * race and must be serialized by the caller. */
+nh_status nh_linear_w8a8_noalloc(nh_context *ctx, const void *x, nh_dtype x_dtype, const int8_t *wq, const float *sw,
+                                 const float *bias, size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype,
+                                 int8_t *xq_out, float *sx_out, uint64_t *nonfinite, nh_stream stream,
+                                 nh_error *err);
 /* L2: int8 MLP layer, the drop-in for MlpLayer::forward_into with int8
  * per-row weights (mlp.rs:157-211): h = ReLU^2(x W_up^T + b_up) in f32
  * (ReLU^2 after the bias, mlp.rs:205), then out = h W_down^T + b_down, each

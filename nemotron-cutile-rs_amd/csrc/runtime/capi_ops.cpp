@@ -896,3 +896,30 @@ extern "C" nh_status nh_take_nonfinite(nh_context* ctx, uint64_t* nonfinite, nh_
     return set_error(err, NH_NON_FINITE_INPUT, "non-finite %s value %g at index %llu", what, (double)value,
                      (unsigned long long)index);
 }
+
+// nh_linear_w8a8 with the static device scratch (scratch.hip) as its
+// workspace: no allocation, for callers that cannot allocate.  Validation as
+// nh_linear_w8a8, then the workspace the shape needs is checked against the
+// scratch before anything else touches the device.
+extern "C" nh_status nh_linear_w8a8_noalloc(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* wq,
+                                            const float* sw, const float* bias, size_t m, size_t n, size_t k,
+                                            void* out, nh_dtype out_dtype, int8_t* xq_out, float* sx_out,
+                                            uint64_t* nonfinite, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    if (m == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
+    nh_status st;
+    if ((st = check_dtype(x_dtype, err)) || (st = check_dtype(out_dtype, err)) ||
+        (st = check_w8a8_shape(m, n, k, err)))
+        return st;
+    const size_t need = nh_linear_w8a8_workspace_size(m, k);
+    if (need > kScratchBytes)
+        return set_error(err, NH_UNSUPPORTED,
+                         "m=%zu k=%zu needs a %zu-byte workspace, above the %zu-byte static scratch of "
+                         "nh_linear_w8a8_noalloc (use nh_linear_w8a8 with a caller workspace)",
+                         m, k, need, kScratchBytes);
+    if (!aligned16(wq)) return set_error(err, NH_UNSUPPORTED, "wq must be 16-byte aligned");
+    if ((st = bind_device(ctx, err))) return st;
+    if (!ctx->scratch) return set_error(err, NH_DEVICE_ERROR, "static scratch unavailable: %s", ctx->scratch_error);
+    return linear_w8a8(ctx, x, x_dtype, wq, sw, bias, m, n, k, out, out_dtype, ctx->scratch, kScratchBytes, xq_out,
+                       sx_out, 0, nonfinite, 0, stream, err);
+}

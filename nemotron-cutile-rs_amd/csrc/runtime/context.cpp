@@ -120,6 +120,12 @@ nh_status nh_context_create(int device, const char* code_object_path, nh_context
     ctx->device = device;
     ctx->cu_count = prop.multiProcessorCount;
     ctx->max_shared_per_block = prop.sharedMemPerBlock;
+    // the static scratch's address on this device (the device is current);
+    // only nh_linear_w8a8_noalloc needs it, so a failure is kept for it to report
+    nh_error serr;
+    clear_error(&serr);
+    if (scratch_address(&ctx->scratch, &serr) != NH_OK)
+        std::snprintf(ctx->scratch_error, sizeof(ctx->scratch_error), "%.120s", serr.message);
     if (code_object_path)
         e = hipModuleLoad(&ctx->module, code_object_path);
     else

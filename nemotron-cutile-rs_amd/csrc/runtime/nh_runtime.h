@@ -50,6 +50,10 @@ enum KernelId : int {
 
 extern const char* const kKernelSymbols[K_COUNT];
 
+// Bytes of the static device scratch (scratch.hip) that nh_linear_w8a8_noalloc
+// uses as its workspace.
+constexpr size_t kScratchBytes = 64ull << 20;
+
 }  // namespace nh
 
 struct nh_context {
@@ -58,6 +62,8 @@ struct nh_context {
     hipFunction_t fn[nh::K_COUNT];
     int cu_count;
     size_t max_shared_per_block;
+    void* scratch;             // this device's address of the static scratch, or null
+    char scratch_error[128];   // why it is null
 };
 
 namespace nh {
@@ -69,6 +75,9 @@ void clear_error(nh_error* err);
 
 // Makes ctx->device current for the calling thread.
 nh_status bind_device(nh_context* ctx, nh_error* err);
+
+// Device address of the static scratch on the current device (scratch.hip).
+nh_status scratch_address(void** out, nh_error* err);
 
 template <class Args>
 nh_status launch(nh_context* ctx, KernelId id, unsigned gx, unsigned bx, size_t shmem, nh_stream stream,

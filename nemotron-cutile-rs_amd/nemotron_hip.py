@@ -107,6 +107,7 @@ _SIGNATURES = {
     "nh_linear_w8a8_workspace_size": (SZ, [SZ, SZ]),
     "nh_take_nonfinite": (ST, [P, P, P, E]),
     "nh_linear_w8a8": (ST, [P, P, C.c_int, P, P, P, SZ, SZ, SZ, P, C.c_int, P, SZ, P, P, P, P, E]),
+    "nh_linear_w8a8_noalloc": (ST, [P, P, C.c_int, P, P, P, SZ, SZ, SZ, P, C.c_int, P, P, P, P, E]),
     "nh_mlp_w8a8_workspace_size": (SZ, [SZ, SZ, SZ]),
     "nh_mlp_w8a8": (ST, [P, P, C.c_int, P, P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, P, SZ, P, P, E]),
     "nh_gemv_w8a32": (ST, [P, P, P, P, SZ, SZ, SZ, P, P, E]),

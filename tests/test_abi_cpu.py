@@ -490,3 +490,16 @@ def test_combine_skips_routes_without_a_slot():
             NH.F32)
     assert np.array_equal(out, np.array([[1.5, 2.0]], dtype=np.float32))
     assert np.array_equal(out, O.moe_combine(slot_out, pos, w, 1, 2, 2))
+
+
+def test_linear_noalloc_rejects_a_workspace_above_its_scratch_before_the_device():
+    # 2048 x 32768 needs 64 MiB of A tiles + 8 KiB of scales: above the 64 MiB
+    # static scratch, refused before the (null) context is touched
+    st, err = NH.call_status("nh_linear_w8a8_noalloc", None, None, NH.BF16, None, None, None, 2048, 64, 32768, None,
+                             NH.BF16, None, None, None, None)
+    assert st == NH.UNSUPPORTED and b"static scratch" in err.message
+    assert NH.lib().nh_linear_w8a8_workspace_size(2048, 32768) > 64 << 20
+    assert NH.lib().nh_linear_w8a8_workspace_size(2048, 32704) <= 64 << 20
+    # m == 0 and shape errors keep the order of nh_linear_w8a8
+    assert NH.call_status("nh_linear_w8a8_noalloc", None, None, NH.BF16, None, None, None, 0, 64, 64, None, NH.BF16,
+                          None, None, None, None)[0] == NH.INVALID_ROW_COUNT
