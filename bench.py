@@ -54,14 +54,14 @@ class Bench:
         the same entry points into HIP graphs of `per_graph` steps each (the
         replay issues exactly the captured launches, without the ~12 us of
         Python/ctypes work per eager call).  After a synchronize, the graphs
-        are replayed twice back to back on the stream: an untimed replay, then
-        the timed one between two events.  The first event fires when the
-        untimed replay's last step ends, and the timed graphs were dispatched
-        while it ran, so the interval holds exactly the `steps` timed steps
-        and not the fixed cost of dispatching a graph onto an idle stream
-        (~20 us per launch: 1 us per step at 20 steps).  That cold figure (the
-        same replay after a synchronize) is kept in self.last_timing.  With
-        `out`, the replayed result must equal an eager call of the last step."""
+        are replayed back to back on the stream: untimed replays for ~10 ms
+        (the warm-up of sustained use), then the timed one between two events.
+        The first event fires when the last untimed replay ends, and the timed
+        graphs were dispatched while it ran, so the interval holds exactly the
+        `steps` timed steps and not the fixed cost of dispatching a graph onto
+        an idle stream.  That cold figure (one replay right after a
+        synchronize) is kept in self.last_timing.  With `out`, the replayed
+        result must equal an eager call of the last step."""
         for i in range(warmup):
             fn(i)
         fn(warmup + steps - 1)
@@ -84,7 +84,11 @@ class Bench:
         self.ev.record(self.e1, self.stream)
         cold = self.ev.elapsed_ms(self.e0, self.e1)
         self.ctx.synchronize(self.stream)
-        replay()  # untimed: the stream is busy while the timed replay is dispatched
+        # untimed replays back to back for ~10 ms (clocks and power state
+        # settle as in sustained use); the last keeps the stream busy while
+        # the timed replay is dispatched
+        for _ in range(max(1, int(np.ceil(10.0 / max(cold, 1e-3))))):
+            replay()
         self.ev.record(self.e0, self.stream)
         replay()
         self.ev.record(self.e1, self.stream)
@@ -537,8 +541,8 @@ def main():
         "config": {"workload": "decode unit (per-token int8 quantization + W8A8 GEMV), M=1, K=4096 -> N=16384, "
                                "bf16 in/out, int8 per-row weights from N(0,0.02) (BASELINE configs[1])",
                    "m": m, "k": k, "n": n, "weight_pool_MiB": POOL_BYTES >> 20,
-                   "timing": (f"{args.steps} steps captured in a HIP graph; the timed replay follows an "
-                              f"untimed one back to back on the stream, events around it "
+                   "timing": (f"{args.steps} steps captured in a HIP graph; the timed replay follows ~10 ms "
+                              f"of untimed replays back to back on the stream, events around it "
                               f"({head_timing['back_to_back_ms'] * 1e3 / args.steps:.2f} us/step); the same "
                               f"replay launched onto an idle stream after a synchronize "
                               f"{head_timing['after_sync_ms'] * 1e3 / args.steps:.2f} us/step (graph dispatch "
