@@ -5,3 +5,4 @@
 #include "gemm.hip"
 #include "gemm_f32.hip"
 #include "moe.hip"
+#include "gemm_persistent.hip"

@@ -161,6 +161,28 @@ nh_status launch_gemv(nh_context* ctx, const int8_t* xq, const float* sx, const 
                   a, err);
 }
 
+// The persistent 256 x 224 GEMM (gemm_persistent.hip) when its contract
+// holds and its tiles fill whole rounds of CUs with less work per CU than the
+// loader-wave kernel's 256 x 128 tiles: rounds x tile area (the 21504-wide
+// up projection at M = 2048: 3 rounds of 256 x 224 against 5.5 of 256 x 128;
+// measured 201-203 against 231-236 us).
+constexpr int kP224Stages = 2;
+constexpr size_t kP224Lds = (size_t)kP224Stages * 8 * ((2 * (256 + 224) / 16 + 7) / 8) * 1024 + (kP224Stages + 1) * 3 * 1024 +
+                            1024;
+
+bool use_persistent_224(const nh_context* ctx, const void* xq, const float* sx, const float* sw, const float* bias,
+                        int M, int N, int kt, const void* out, nh_dtype out_dtype) {
+    const size_t esz = out_dtype == NH_BF16 ? 2 : 4;
+    if (kt % 2 != 0 || M % 4 != 0 || N % 4 != 0 || !aligned16(xq) || !aligned16(sx) || !aligned16(sw) ||
+        !aligned16(bias) || !aligned16(out) || (uint64_t)M * N * esz >= (1ull << 31) ||
+        kP224Lds > ctx->max_shared_per_block)
+        return false;
+    const int64_t cu = ctx->cu_count, tm = (M + 255) / 256;
+    const int64_t tiles_p = tm * ((N + 223) / 224), tiles_o = tm * ((N + 127) / 128);
+    const int64_t work_p = (tiles_p + cu - 1) / cu * 224, work_o = (tiles_o + cu - 1) / cu * 128;
+    return tiles_p >= cu && work_p < work_o;
+}
+
 // G3 launch.  a_tiled: xq holds A in the weights' tiled layout (written by
 // the row quantizer with 16 rows per tile), else row-major [M][K].
 nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
@@ -180,6 +202,13 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
     a.relu2 = relu2;
     a.kt = (int)tiled_k_tiles(K);
     a.ldo = N;
+    if (a_tiled && use_persistent_224(ctx, xq, sx, sw, bias, M, N, a.kt, out, out_dtype)) {
+        a.tiles_m = (M + 255) / 256;
+        a.tiles_n = (N + 223) / 224;
+        const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
+        const unsigned grid = (unsigned)std::min<int64_t>(tiles, ctx->cu_count);
+        return launch(ctx, K_GEMM_P224, grid, 512u, kP224Lds, stream, a, err);
+    }
     // Tile choice: 256x128 (8 compute + 8 loader waves) unless that leaves
     // most CUs idle, then 128x128 (more, smaller tiles).
     struct Cfg {

@@ -45,6 +45,7 @@ enum KernelId : int {
     K_LINEAR_DECODE_W4_ROW4,  // 4 rows
     K_PERMUTE_TABLE,          // R2 in four barriers
     K_COMBINE4,               // R4, four columns per thread
+    K_GEMM_P224,              // persistent G3, 256 x 224 tiles, tiled A
     K_COUNT
 };
 

@@ -315,7 +315,9 @@ def test_linear_decode_unit_bit_exact(ctx, m, n, k):
                                          (1, 4096, 16384, "bf16"), (16, 96, 64, "f32"), (2, 300, 8192, "f32"),
                                          (3, 4096, 8192, "bf16"), (2, 1000, 4112, "bf16"), (7, 4096, 8192, "bf16"),
                                          (6, 6144, 4096, "bf16"), (17, 300, 4160, "bf16"), (100, 2688, 1856, "f32"),
-                                         (257, 1024, 4096, "bf16")])
+                                         (257, 1024, 4096, "bf16"),
+                                         # the persistent 256 x 224 GEMM with a bias and f32 out
+                                         (1000, 14236, 384, "bf16"), (1024, 14336, 256, "f32")])
 def test_linear_small_m_shapes_bit_exact(ctx, m, n, k, dtype):
     """The linear path off the headline shape (and past 16 rows, the GEMM on
     A tiles written by the quantizer, M and K tails included): several K slabs per
@@ -335,7 +337,7 @@ def test_linear_small_m_shapes_bit_exact(ctx, m, n, k, dtype):
         x = O.normal_f32(40 + m, m * k).reshape(m, k)
         _, xq_ref, sx_ref, _ = O.quantize_rows_f32(x)
         dt = NH.F32
-    ref = O.linear_w8a8(xq_ref, sx_ref, wq, sw, bias=bias, out_bf16=False)
+    ref = linear_w8a8_exact(xq_ref, sx_ref, wq, sw, bias=bias, out_bf16=False)
     dx, dw, ds, db = ctx.upload(x), ctx.upload(tile_16x64(wq)), ctx.upload(sw), ctx.upload(bias)
     ws_bytes = NH.lib().nh_linear_w8a8_workspace_size(m, k)
     ws = ctx.empty(max(ws_bytes, 1), np.uint8)
@@ -356,10 +358,10 @@ def mlp_oracle(x, xdt, w_up, s_up, b_up, w_down, s_down, b_down, out_bf16):
     """Per-token Q2, up projection + bias, ReLU^2 (mlp.rs:205) in f32, Q2 of
     the f32 intermediate, down projection + bias: the oracle's parts."""
     _, xq, sx, _ = O.quantize_rows_bf16(x) if xdt == NH.BF16 else O.quantize_rows_f32(x)
-    h = O.epilogue(O.gemm_i8_i32(xq, w_up), sx, s_up, bias=b_up, relu2=True)
+    h = linear_w8a8_exact(xq, sx, w_up, s_up, bias=b_up, relu2=True)
     st, hq, sh, _ = O.quantize_rows_f32(h)
     assert st == O.OK
-    return h, O.epilogue(O.gemm_i8_i32(hq, w_down), sh, s_down, bias=b_down, out_bf16=out_bf16)
+    return h, linear_w8a8_exact(hq, sh, w_down, s_down, bias=b_down, out_bf16=out_bf16)
 
 
 @functools.lru_cache(maxsize=2)
@@ -370,7 +372,9 @@ def mlp_weights(hidden, inter):
 
 
 @pytest.mark.parametrize("m,hidden,inter,dtype", [(8, 4096, 21504, "bf16"), (1, 4096, 21504, "bf16"),
-                                                  (37, 1024, 2560, "bf16"), (5, 512, 1856, "f32")])
+                                                  (37, 1024, 2560, "bf16"), (5, 512, 1856, "f32"),
+                                                  # the up projection (bias, ReLU^2, f32 out) on the persistent GEMM
+                                                  (1024, 512, 14336, "bf16")])
 def test_mlp_bit_exact(ctx, m, hidden, inter, dtype):
     note(f"mlp_w8a8 m={m} hidden={hidden} inter={inter} {dtype}")
     w_up, s_up, w_down, s_down = mlp_weights(hidden, inter)
@@ -492,8 +496,11 @@ def test_linear_w4a8_bit_exact(ctx, m, n, k, zp):
                                    # M and N (a half-valid last weight tile)
                                    (512, 8192, 64), (1000, 2000, 192), (777, 8200, 1040),
                                    # a sparse last round of 256 x 128 tiles: whole rounds, then the
-                                   # remaining columns as 128 x 128 tiles (also at 2048 x 21504 and 777 x 8200)
-                                   (1100, 9000, 128)])
+                                   # remaining columns as 128 x 128 tiles (also at 777 x 8200)
+                                   (1100, 9000, 128),
+                                   # the persistent 256 x 224 kernel (tiled A; also 2048 x 21504): one tile
+                                   # per CU, and ragged last tiles in M and N with several tiles per CU
+                                   (1024, 14336, 256), (1000, 14236, 384), (2000, 21484, 128)])
 @pytest.mark.parametrize("a_layout", ["row-major", "tiled"])
 def test_gemm_w8a8_bit_exact(ctx, m, n, k, a_layout):
     note(f"gemm_w8a8 m={m} n={n} k={k} A {a_layout}")
