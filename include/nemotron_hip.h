@@ -231,8 +231,11 @@ nh_status nh_mlp_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const in
                       const float *b_up, const int8_t *w_down, const float *s_down, const float *b_down, size_t m,
                       size_t hidden, size_t inter, void *out, nh_dtype out_dtype, void *workspace,
                       size_t workspace_bytes, uint64_t *nonfinite, nh_stream stream, nh_error *err);
-/* G2: W8A32 dequant GEMV, y = x * ((float)q * s)^T with f64 accumulation,
- * the arithmetic of materialize_dense + gemm_into_host (linear.rs:126-131). */
+/* G2: W8A32 dequant GEMV, y = x * ((float)q * s)^T: the value of
+ * materialize_dense + gemm_into_host (linear.rs:126-131).  The device sums
+ * each 16-code group in f32 and the groups in f64, then scales by s, so
+ * |y - exact| <= 16 u sum_k |x q s| + u |y| (u = 2^-24); the _host form keeps
+ * the reference's f64 arithmetic exactly. */
 nh_status nh_gemv_w8a32(nh_context *ctx, const float *x, const int8_t *wq, const float *sw, size_t m, size_t n,
                         size_t k, float *y, nh_stream stream, nh_error *err);
 nh_status nh_gemv_w8a32_host(const float *x, const int8_t *wq, const float *sw, size_t m, size_t n, size_t k,

@@ -528,96 +528,123 @@ extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_w8a8_m8_kern
     linear_decode_wide<8, 8, 8>(a, lds);
 }
 
-// G2: W8A32 dequant GEMV.  The reference's quantized-weight path materialises
-// W' = (float)q * s in f32 and accumulates x * W' in f64 (linear.rs:126-131,
-// gemm.rs:99-109); this kernel does the same arithmetic per element (f32
-// multiply, exact f64 product, f64 sum) in a different summation order, so
-// it agrees with that path to a few f64 ulps before the final f32 rounding.
-// grid = (N tiles, ceil(M / 4)): a workgroup owns 16 weight rows and 4
-// activation rows; lane (r, g) dequantizes 16 weights of row r per K tile
-// and the f64 partial sums meet through shuffles and LDS.  Waves hold 4 K
-// tiles each (16 waves at K = 4096, four per SIMD, overlap their loads with
-// each other's f64 work: 7.5 us against 10.4 at 4 waves).  When the 4
-// activation rows fit (x_lds), they are loaded into LDS ahead of the
-// weights, once per workgroup, instead of per K tile behind the weight
-// slab.
+// G2: W8A32 dequant GEMV, y[m][n] = sum_k x[m][k] * q[n][k] * s[n].  The
+// reference materialises W' = (float)q * s and sums x * W' in f64
+// (linear.rs:126-131, gemm.rs:99-109).  Here each lane sums the 16 products
+// of one 16-code group in f32 (one convert and one FMA per weight), adds the
+// group sum to an f64 accumulator, and the row scale multiplies the f64 total
+// once: every group sum carries at most 16 f32 roundings, so
+// |y - exact| <= 16 u sum_k |x q s| + u |y| to first order (u = 2^-24).
+//
+// grid = (N tiles, ceil(M / MM)).  A workgroup owns one 16-row weight tile
+// over all of K and MM activation rows; wave w takes K tiles w, w + W, ...
+// in slabs of 4 whose loads are in flight together.  Lane (r, g) holds code
+// row r, codes 16g .. 16g + 15 of a tile, and ONE activation per row and
+// tile, x[64t + 16g + r]: the FMA for code e reads lane (e, g)'s activation
+// through DPP row_newbcast:e (a 16-lane row is one g), so activations need
+// no LDS, no barrier and no per-lane copies.  Loads are issued in the order
+// scale, activations, weights, so the compiler's in-order vmcnt accounting
+// releases each tile's FMAs as its weight load lands.
 constexpr int kSlab32 = 4;
 
-extern "C" __global__ __launch_bounds__(1024) void nh_gemv_w8a32_kernel(GemvW8A32Args a) {
-    __shared__ double redd[16][4][64];
-    extern __shared__ __align__(16) int8_t xlds[];  // [4][K] f32 when x_lds
+// acc += sum_e x(lane 16 g + e) * w[e] over e = 0..15 in order (f32 FMAs).
+// One block: its leading s_nop gives the DPP source the two wait states a
+// preceding VALU write would need, and nothing inside writes x.
+__device__ __forceinline__ void fma16_row_bcast(float& acc, float x, const float (&w)[16]) {
+    asm("s_nop 1\n\t"
+        "v_fmac_f32_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf"
+        : "+v"(acc)
+        : "v"(x), "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(w[4]), "v"(w[5]), "v"(w[6]), "v"(w[7]), "v"(w[8]),
+          "v"(w[9]), "v"(w[10]), "v"(w[11]), "v"(w[12]), "v"(w[13]), "v"(w[14]), "v"(w[15]));
+}
+
+template <int MM>
+__device__ __forceinline__ void gemv_w8a32(const GemvW8A32Args& a) {
+    __shared__ double red[16][MM][16];
     const int lane = threadIdx.x & 63, W = a.waves;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
     const int M = a.M, N = a.N, K = a.K, kt = a.kt;
-    const int tile = blockIdx.x, m0 = blockIdx.y * 4;
+    const int tile = blockIdx.x, m0 = blockIdx.y * MM;
+    const int mrows = min(MM, M - m0);
     const __amdgpu_buffer_rsrc_t wr = row_tile_rsrc(a.wq, tile, kt);
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)M * (uint32_t)K * 4u);
-    const float* xs = (const float*)xlds;
-    if (a.x_lds) {  // the 4 rows are contiguous: 1 KiB per direct-to-LDS load, ahead of the weights
-        const int bytes = 4 * K * 4;
-        for (int i = wave; i * 1024 < bytes; i += W)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t*)(xlds + i * 1024), 16,
-                                                     (uint32_t)m0 * (uint32_t)K * 4u + (uint32_t)(i * 1024 + lane * 16),
-                                                     0, 0, 0);
-    }
-    const int n = tile * 16 + r16;
-    const float s = n < N ? a.sw[n] : 0.0f;
-    const int steps = (kt + W - 1) / W;
-    double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    for (int s0 = 0; s0 < steps; s0 += kSlab32) {
+    // one resource per activation row: columns past K and rows past M load
+    // as zeros, so the padding of the last K tile and K tiles past kt
+    // contribute exact zeros and the tile loop needs no branch (a branch
+    // around a tile would cost the in-order vmcnt accounting its precision)
+    __amdgpu_buffer_rsrc_t xr[MM];
+#pragma unroll
+    for (int mm = 0; mm < MM; ++mm)
+        xr[mm] = make_rsrc(a.x + (int64_t)(m0 + mm) * K, mm < mrows ? (uint32_t)K * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.sw, (uint32_t)N * 4u);
+    float s = 0.0f;
+    double acc[MM];
+#pragma unroll
+    for (int mm = 0; mm < MM; ++mm) acc[mm] = 0.0;
+    for (int i = 0; i < a.slabs; ++i) {
+        float xv[kSlab32][MM];
         v4i b[kSlab32];
         __builtin_amdgcn_sched_barrier(0);
+        // the row scale (reloaded per slab: a load pending across the loop
+        // edge costs the accounting its precision)
+        s = f32_from_bits((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(sr, (tile * 16 + r16) * 4, 0, 0));
 #pragma unroll
         for (int st = 0; st < kSlab32; ++st)
-            b[st] = buffer_load16_stream(wr, (wave + (s0 + st) * W) * 1024 + lane * 16);
+#pragma unroll
+            for (int mm = 0; mm < MM; ++mm)
+                xv[st][mm] = f32_from_bits((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                    xr[mm], ((wave + (i * kSlab32 + st) * W) * 64 + lane) * 4, 0, 0));
+#pragma unroll
+        for (int st = 0; st < kSlab32; ++st)
+            b[st] = buffer_load16_stream(wr, (wave + (i * kSlab32 + st) * W) * 1024 + lane * 16);
         __builtin_amdgcn_sched_barrier(0);
-        if (a.x_lds && s0 == 0) {
-            wait_vmcnt_le(kSlab32);  // this wave's activation loads are in (the slab stays in flight)
-            lds_barrier();           // ... and every wave's
-        }
 #pragma unroll
         for (int st = 0; st < kSlab32; ++st) {
-            const int k = (wave + (s0 + st) * W) * 64 + g * 16;
-            if (k >= K) continue;
-            float wv[16];
+            float wf[16];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) wv[4 * j + e] = (float)(int8_t)(b[st][j] >> (8 * e)) * s;
+                for (int e = 0; e < 4; ++e) wf[4 * j + e] = (float)(int8_t)(b[st][j] >> (8 * e));
 #pragma unroll
-            for (int mm = 0; mm < 4; ++mm) {
-                const int m = m0 + mm;
-                if (m >= M) break;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const v4i xx = a.x_lds ? *(const v4i*)(xs + mm * K + k + 4 * q)
-                                           : buffer_load16(xr, (m * K + k + 4 * q) * 4);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        // the f64 product of two f32 values is exact, so the fused
-                        // form rounds exactly like the reference's acc += a * b
-                        acc[mm] = __builtin_fma((double)f32_from_bits((uint32_t)xx[e]), (double)wv[4 * q + e], acc[mm]);
-                }
+            for (int mm = 0; mm < MM; ++mm) {
+                if (mm >= mrows) break;
+                float t = 0.0f;
+                fma16_row_bcast(t, xv[st][mm], wf);
+                acc[mm] += (double)t;
             }
         }
     }
-    // the 4 lanes of a row (g = 0..3), then the waves
+    // the 4 lanes of a weight row (g = 0..3), then the waves in order
 #pragma unroll
-    for (int mm = 0; mm < 4; ++mm) {
+    for (int mm = 0; mm < MM; ++mm) {
         acc[mm] += __shfl_xor(acc[mm], 16, kWave);
         acc[mm] += __shfl_xor(acc[mm], 32, kWave);
-        redd[wave][mm][lane] = acc[mm];
+        if (g == 0) red[wave][mm][r16] = acc[mm];
     }
     __syncthreads();
-    if (wave == 0 && g == 0 && n < N) {
-#pragma unroll
-        for (int mm = 0; mm < 4; ++mm) {
-            const int m = m0 + mm;
-            if (m >= M) break;
-            double t = redd[0][mm][lane];
-            for (int w = 1; w < W; ++w) t += redd[w][mm][lane];
-            a.y[(int64_t)m * N + n] = (float)t;
-        }
+    const int n = tile * 16 + r16;
+    if (wave == 0 && g < mrows && n < N) {
+        double t = red[0][g][r16];
+        for (int w = 1; w < W; ++w) t += red[w][g][r16];
+        a.y[(int64_t)(m0 + g) * N + n] = (float)(t * (double)s);
     }
 }
+
+extern "C" __global__ __launch_bounds__(1024) void nh_gemv_w8a32_kernel(GemvW8A32Args a) { gemv_w8a32<4>(a); }
+
+extern "C" __global__ __launch_bounds__(1024) void nh_gemv_w8a32_m1_kernel(GemvW8A32Args a) { gemv_w8a32<1>(a); }

@@ -94,7 +94,7 @@ struct LinearDecodeArgs {
     uint64_t* nonfinite;  // or null: the first non-finite activation (report_nonfinite, nh_device.h)
 };
 
-// G2: W8A32 dequant GEMV; grid = (N tiles, ceil(M / 4)).
+// G2: W8A32 dequant GEMV; grid = (N tiles, ceil(M / rows per workgroup)).
 struct GemvW8A32Args {
     const float* x;       // [M][K]
     const int8_t* wq;     // tiled [N][K]
@@ -102,8 +102,8 @@ struct GemvW8A32Args {
     float* y;             // [M][N]
     int32_t M, N, K;
     int32_t kt;
-    int32_t waves;
-    int32_t x_lds;        // 1: the workgroup's 4 activation rows are staged in LDS (4 * K * 4 bytes)
+    int32_t waves;        // waves per workgroup; each takes K tiles wave, wave + waves, ...
+    int32_t slabs;        // ceil(ceil(kt / waves) / 4): slabs of 4 K tiles per wave
 };
 
 // Row-major int8 [N][K] -> tiled, one 16-byte tile chunk per thread.

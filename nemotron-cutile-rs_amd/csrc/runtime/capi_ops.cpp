@@ -606,16 +606,16 @@ nh_status nh_gemv_w8a32(nh_context* ctx, const float* x, const int8_t* wq, const
     if ((st = check_w8a8_shape(m, n, k, err))) return st;
     if (!aligned16(x) || !aligned16(wq)) return set_error(err, NH_UNSUPPORTED, "x and wq must be 16-byte aligned");
     if ((st = bind_device(ctx, err))) return st;
-    if ((m + 3) / 4 > 65535 || (uint64_t)m * k * 4 >= (1ull << 32))
-        return set_error(err, NH_UNSUPPORTED, "device W8A32 GEMV needs m <= 262140 and m * k * 4 < 2^32");
+    if ((m + 3) / 4 > 65535 || n >= (1u << 29))
+        return set_error(err, NH_UNSUPPORTED, "device W8A32 GEMV needs m <= 262140 and n < 2^29");
     GemvW8A32Args a{x, wq, sw, y, (int)m, (int)n, (int)k, 0, 0, 0};
     a.kt = (int)tiled_k_tiles(k);
     a.waves = std::max(1, std::min(16, (a.kt + 3) / 4));  // 4 K tiles per wave and slab
-    // activation rows in LDS when 4 of them fit in 64 KiB (x is 16-byte aligned and K % 16 == 0)
-    const size_t xbytes = (size_t)4 * k * 4;
-    a.x_lds = xbytes <= 65536 ? 1 : 0;
-    return launch(ctx, K_GEMV_W8A32, (unsigned)((n + 15) / 16), 64u * a.waves, a.x_lds ? xbytes : 0, stream, a, err,
-                  (unsigned)((m + 3) / 4));
+    a.slabs = ((a.kt + a.waves - 1) / a.waves + 3) / 4;
+    // one activation row per workgroup at m = 1, else 4
+    const unsigned rows = m == 1 ? 1u : 4u;
+    return launch(ctx, m == 1 ? K_GEMV_W8A32_M1 : K_GEMV_W8A32, (unsigned)((n + 15) / 16), 64u * a.waves, 0, stream,
+                  a, err, (unsigned)((m + rows - 1) / rows));
 }
 
 // ---- MoE ------------------------------------------------------------------

@@ -20,6 +20,7 @@ const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
     "nh_linear_decode_w8a8_m1_kernel",   // K_LINEAR_DECODE_M1
     "nh_linear_decode_w8a8_m2_kernel",   // K_LINEAR_DECODE_M2
     "nh_gemv_w8a32_kernel",              // K_GEMV_W8A32
+    "nh_gemv_w8a32_m1_kernel",           // K_GEMV_W8A32_M1
     "nh_gemm_w8a8_256x128_kernel",       // K_GEMM_W8A8
     "nh_gemm_w8a8_128x128_kernel",       // K_GEMM_W8A8_128
     "nh_moe_route_sigmoid_kernel",       // K_ROUTE_SIGMOID

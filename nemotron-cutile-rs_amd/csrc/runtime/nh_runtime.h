@@ -22,6 +22,7 @@ enum KernelId : int {
     K_LINEAR_DECODE_M1,  // M == 1
     K_LINEAR_DECODE_M2,  // M <= 2
     K_GEMV_W8A32,
+    K_GEMV_W8A32_M1,
     K_GEMM_W8A8,
     K_GEMM_W8A8_128,
     K_ROUTE_SIGMOID,
