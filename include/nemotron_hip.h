@@ -331,8 +331,29 @@ nh_status nh_moe_forward_shared_w8a8(nh_context *ctx, const void *x, nh_dtype x_
                                      const int8_t *w_down_shared, const float *s_down_shared, void *out,
                                      nh_dtype out_dtype, void *workspace, size_t workspace_bytes,
                                      uint64_t *nonfinite, nh_stream stream, nh_error *err);
+/* The whole MoeLayer::forward_into (moe.rs:154-249) from its input, router
+ * included: logits = x router_w (+ router_b), router_w f32 [hidden][experts]
+ * as the reference's dense router LinearProjection stores it (moe.rs:185-188,
+ * linear.rs:324), accumulated in f64 with k ascending and rounded to f32,
+ * then the bias added in f32 (gemm_into_host + project_into, bit-identical;
+ * bf16 x is widened exactly).  Then routing and experts as
+ * nh_moe_forward_w8a8, with the shared expert when shared_inter != 0 (its
+ * four operands as nh_moe_forward_shared_w8a8).  MoeLayer routes with
+ * moe_route_host: renormalize = 0, scaling = 1.  The workspace
+ * (nh_moe_layer_w8a8_workspace_size) starts with nh_moe_workspace_layout's
+ * fields.  Errors: INVALID_ROW_COUNT (tokens == 0), INVALID_SHAPE,
+ * INVALID_PARAMS (router_w NULL), LENGTH_MISMATCH "workspace". */
+size_t nh_moe_layer_w8a8_workspace_size(size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
+                                        size_t shared_inter);
+nh_status nh_moe_layer_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const float *router_w,
+                            const float *router_b, size_t tokens, size_t hidden, size_t inter, size_t experts,
+                            size_t top_k, int renormalize, float scaling, const int8_t *w_up, const float *s_up,
+                            const int8_t *w_down, const float *s_down, size_t shared_inter,
+                            const int8_t *w_up_shared, const float *s_up_shared, const int8_t *w_down_shared,
+                            const float *s_down_shared, void *out, nh_dtype out_dtype, void *workspace,
+                            size_t workspace_bytes, uint64_t *nonfinite, nh_stream stream, nh_error *err);
 
-/* ---- INT4 affine weights on the device (W4A8), SURVEY §8(f) 3 --------------
+/* ---- INT4 affine weights on the device (W4A8) ---------------------------
  * The reference's INT4 linear weights (Int4LinearWeights, linear.rs:99-131)
  * are the [input_dim = K][output_dim = N] matrix of affine codes packed two
  * per byte, low nibble first (quantize.rs:75-77), with one per-tensor scale
@@ -368,7 +389,7 @@ nh_status nh_linear_w4a8_host(const void *x, nh_dtype x_dtype, const uint8_t *pa
                               float scale, uint32_t zero_point, const float *bias, size_t m, size_t n, size_t k,
                               void *out, nh_dtype out_dtype, nh_error *err);
 
-/* ---- safetensors weights into device memory, SURVEY §8(f) 2 -------------
+/* ---- safetensors weights into device memory -----------------------------
  * One .safetensors file: the 8-byte little-endian header length, the JSON
  * header, the data section (WeightManifest::load_tensor and
  * read_safetensors_header, nemotron-model/src/weights.rs:161-267).  Every

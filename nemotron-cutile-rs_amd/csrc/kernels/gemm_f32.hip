@@ -10,6 +10,10 @@
 // block; K advances 16 at a time through LDS (A transposed to [k][m] so both
 // operand reads are 16-byte vectors).  The last K step accumulates only the
 // positions that exist, so every output sees exactly K fused multiply-adds.
+//
+// For the MoE router (moe.rs:185-188, a dense f32 LinearProjection) the lhs
+// may be bf16 (widened exactly to f32 on load) and a bias may follow the
+// rounding to f32, as project_into adds it (linear.rs:330-336).
 #include "nh_device.h"
 
 using namespace nh;
@@ -31,7 +35,11 @@ extern "C" __global__ __launch_bounds__(256) void nh_gemm_f32_kernel(GemmF32Args
             const int idx = threadIdx.x + 256 * i;
             const int r = idx >> 4, kk = idx & 15;
             const int64_t gm = m0 + r, gk = k0 + kk;
-            As[kk][r] = (gm < M && gk < K) ? a.lhs[gm * K + gk] : 0.0f;
+            float v = 0.0f;
+            if (gm < M && gk < K)
+                v = a.lhs_bf16 ? f32_from_bits((uint32_t)((const uint16_t*)a.lhs)[gm * K + gk] << 16)
+                               : ((const float*)a.lhs)[gm * K + gk];
+            As[kk][r] = v;
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -61,7 +69,7 @@ extern "C" __global__ __launch_bounds__(256) void nh_gemm_f32_kernel(GemmF32Args
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int64_t gn = n0 + tx * 4 + j;
-            if (gn < N) a.out[gm * N + gn] = (float)acc[i][j];
+            if (gn < N) a.out[gm * N + gn] = a.bias ? (float)acc[i][j] + a.bias[gn] : (float)acc[i][j];
         }
     }
 }

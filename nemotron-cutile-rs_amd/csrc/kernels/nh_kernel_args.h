@@ -129,10 +129,13 @@ struct TileWeightsArgs {
 
 // G0d: f32 GEMM with f64 accumulation (the reference's gemm_into order).
 struct GemmF32Args {
-    const float* lhs;     // [M][K]
+    const void* lhs;      // [M][K], f32 or (lhs_bf16) bf16
     const float* rhs;     // [K][N]
     float* out;           // [M][N]
     int64_t M, K, N;
+    const float* bias;    // [N] or null: out = (float)acc + bias[n] in f32
+    int32_t lhs_bf16;
+    int32_t pad_;
 };
 
 // G3: W8A8 GEMM on int8 MFMA with LDS-staged tiles.

@@ -443,7 +443,7 @@ nh_status nh_gemm_f32(nh_context* ctx, const float* lhs, size_t lhs_len, const f
     if (!aligned16(out)) return set_error(err, NH_UNSUPPORTED, "out must be 16-byte aligned");
     nh_status st = bind_device(ctx, err);
     if (st) return st;
-    GemmF32Args a{lhs, rhs, out, (int64_t)m, (int64_t)k, (int64_t)n};
+    GemmF32Args a{lhs, rhs, out, (int64_t)m, (int64_t)k, (int64_t)n, nullptr, 0, 0};
     return launch(ctx, K_GEMM_F32, (unsigned)((n + 63) / 64), 256, 0, stream, a, err, (unsigned)((m + 63) / 64));
 }
 
@@ -895,6 +895,59 @@ nh_status nh_moe_forward_shared_w8a8(nh_context* ctx, const void* x, nh_dtype x_
     return moe_forward(ctx, x, x_dtype, logits, tokens, hidden, inter, experts, top_k, renormalize, scaling, w_up,
                        s_up, w_down, s_down, shared_inter, w_up_shared, s_up_shared, w_down_shared, s_down_shared,
                        out, out_dtype, workspace, workspace_bytes, nonfinite, stream, err);
+}
+
+size_t nh_moe_layer_w8a8_workspace_size(size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
+                                        size_t shared_inter) {
+    const size_t inner = shared_inter
+                             ? nh_moe_forward_shared_w8a8_workspace_size(tokens, hidden, inter, experts, top_k,
+                                                                         shared_inter)
+                             : nh_moe_forward_w8a8_workspace_size(tokens, hidden, inter, experts, top_k);
+    return align256(inner) + align256(tokens * experts * sizeof(float));
+}
+
+// MoeLayer::forward_into (moe.rs:154-249) from its input: the dense f32
+// router (router.project, moe.rs:185-188) as the f64-accumulated device GEMM
+// of gemm_into_host with the bias added after the rounding to f32, its
+// logits after the inner layer's workspace (so nh_moe_workspace_layout's
+// offsets still hold), then the routed layer (and the shared expert) on them.
+nh_status nh_moe_layer_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const float* router_w,
+                            const float* router_b, size_t tokens, size_t hidden, size_t inter, size_t experts,
+                            size_t top_k, int renormalize, float scaling, const int8_t* w_up, const float* s_up,
+                            const int8_t* w_down, const float* s_down, size_t shared_inter,
+                            const int8_t* w_up_shared, const float* s_up_shared, const int8_t* w_down_shared,
+                            const float* s_down_shared, void* out, nh_dtype out_dtype, void* workspace,
+                            size_t workspace_bytes, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
+    clear_error(err);
+    if (tokens == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
+    if (hidden == 0 || experts == 0 || top_k == 0 || top_k > experts || inter == 0)
+        return set_error(err, NH_INVALID_SHAPE, "invalid MoE shape");
+    if (!router_w) return set_error(err, NH_INVALID_PARAMS, "router_w must not be null");
+    if ((shared_inter != 0) != (w_up_shared != nullptr))
+        return set_error(err, NH_INVALID_SHAPE, "shared_inter and w_up_shared must be given together");
+    nh_status st;
+    if ((st = check_dtype(x_dtype, err))) return st;
+    const size_t inner = shared_inter
+                             ? nh_moe_forward_shared_w8a8_workspace_size(tokens, hidden, inter, experts, top_k,
+                                                                         shared_inter)
+                             : nh_moe_forward_w8a8_workspace_size(tokens, hidden, inter, experts, top_k);
+    const size_t need = nh_moe_layer_w8a8_workspace_size(tokens, hidden, inter, experts, top_k, shared_inter);
+    if (!workspace || workspace_bytes < need) return mismatch(err, "workspace", need, workspace_bytes);
+    if (!aligned16(workspace)) return set_error(err, NH_UNSUPPORTED, "workspace must be 16-byte aligned");
+    size_t t;
+    if (!mul_ok(tokens, hidden, &t) || !nh_supports_gemm_f32(tokens, hidden, experts))
+        return set_error(err, NH_UNSUPPORTED, "router shape tokens=%zu hidden=%zu experts=%zu outside the device "
+                         "envelope", tokens, hidden, experts);
+    if ((st = bind_device(ctx, err))) return st;
+    float* logits = (float*)((char*)workspace + align256(inner));
+    GemmF32Args a{x, router_w, logits, (int64_t)tokens, (int64_t)hidden, (int64_t)experts, router_b,
+                  x_dtype == NH_BF16 ? 1 : 0, 0};
+    if ((st = launch(ctx, K_GEMM_F32, (unsigned)((experts + 63) / 64), 256, 0, stream, a, err,
+                     (unsigned)((tokens + 63) / 64))))
+        return st;
+    return moe_forward(ctx, x, x_dtype, logits, tokens, hidden, inter, experts, top_k, renormalize, scaling, w_up,
+                       s_up, w_down, s_down, shared_inter, w_up_shared, s_up_shared, w_down_shared, s_down_shared,
+                       out, out_dtype, workspace, align256(inner), nonfinite, stream, err);
 }
 
 }  // extern "C"

@@ -629,7 +629,7 @@ int or_moe_forward_shared_w8a8(const uint16_t *x_bf16, const float *logits, size
     return st;
 }
 
-/* W4A8 linear (spec): the reference's INT4 linear weights
+/* W4A8 linear: the reference's INT4 linear weights
  * (packed [K][N] affine codes, low nibble first, quantize.rs:75-77; one scale
  * and zero point, linear.rs:99-131) with per-token Q2 of bf16 x:
  * acc[m][n] = sum_k xq[m][k] * (code[k][n] - zp), exact in int32, then the

@@ -795,6 +795,91 @@ def test_moe_forward_config3_bit_exact(ctx):
     assert np.array_equal(got, ref), f"{(got != ref).sum()} of {ref.size} outputs differ"
 
 
+def router_case(tokens, hidden, experts, seed=40):
+    """The dense f32 router of MoeLayer ([hidden][experts] weights and a bias)
+    and the logits the reference computes from bf16 x: gemm_into_host on the
+    widened input (the oracle's f64-accumulated GEMM), then the bias added in
+    f32 (linear.rs:330-336)."""
+    rw = O.normal_f32(seed, hidden * experts, 0.0, 0.02).reshape(hidden, experts)
+    rb = O.normal_f32(seed + 1, experts, 0.0, 0.1)
+    return rw, rb
+
+
+def router_logits(x_bf16, rw, rb):
+    tokens, hidden = x_bf16.shape
+    experts = rw.shape[1]
+    xf = (x_bf16.astype(np.uint32) << 16).view(np.float32)
+    st, logits, _ = O.gemm_f32(xf, rw, tokens, hidden, experts)
+    assert st == O.OK
+    return (logits.reshape(tokens, experts) + rb[None, :]).astype(np.float32).ravel()
+
+
+@pytest.mark.parametrize("tokens,hidden,inter,experts,top_k,sh_inter", [(13, 64, 32, 8, 3, 0), (64, 2688, 1856, 128, 6, 3712),
+                                                                         (512, 2688, 1856, 128, 6, 0)])
+def test_moe_layer_with_router_bit_exact(ctx, tokens, hidden, inter, experts, top_k, sh_inter):
+    """nh_moe_layer_w8a8: MoeLayer::forward_into from its input (moe.rs:154-249),
+    the dense router on the device, routing as moe_route_host (no
+    renormalization, scale 1).  The logits in the workspace and every output
+    element against the oracle."""
+    note(f"moe layer + router t={tokens} h={hidden} i={inter} e={experts} k={top_k} si={sh_inter}")
+    x, _, up, su, down, sd = moe_case(tokens, hidden, inter, experts, top_k)
+    rw, rb = router_case(tokens, hidden, experts)
+    logits = router_logits(x, rw, rb)
+    if sh_inter:
+        _, hu, hsu = quantized_weights(sh_inter, hidden, seed=30)
+        _, hd, hsd = quantized_weights(hidden, sh_inter, seed=31)
+        st, ref, idx, *_ = O.moe_forward_shared_w8a8(x, logits, up, su, down, sd, top_k, hu, hsu, hd, hsd,
+                                                     renormalize=False)
+        assert st == O.OK
+    elif tokens > 64:
+        ref, idx, *_ = moe_forward_exact(x, logits, up, su, down, sd, top_k, renormalize=False)
+    else:
+        st, ref, idx, *_ = O.moe_forward_w8a8(x, logits, up, su, down, sd, top_k, renormalize=False)
+        assert st == O.OK
+    lib = NH.lib()
+    ws_bytes = lib.nh_moe_layer_w8a8_workspace_size(tokens, hidden, inter, experts, top_k, sh_inter)
+    inner = (lib.nh_moe_forward_shared_w8a8_workspace_size(tokens, hidden, inter, experts, top_k, sh_inter) if sh_inter
+             else lib.nh_moe_forward_w8a8_workspace_size(tokens, hidden, inter, experts, top_k))
+    ws = ctx.empty(ws_bytes, np.uint8)
+    ws.fill_bytes(0x5a)
+    dx, drw, drb = ctx.upload(x), ctx.upload(rw), ctx.upload(rb)
+    dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
+    sh = [None] * 4
+    if sh_inter:
+        dhu, dhsu, dhd, dhsd = (ctx.upload(tile_16x64(hu)), ctx.upload(hsu), ctx.upload(tile_16x64(hd)),
+                                ctx.upload(hsd))
+        sh = [dhu.ptr, dhsu.ptr, dhd.ptr, dhsd.ptr]
+    out = ctx.empty((tokens, hidden), np.uint16)
+    NH.call("nh_moe_layer_w8a8", ctx.handle, dx.ptr, NH.BF16, drw.ptr, drb.ptr, tokens, hidden, inter, experts,
+            top_k, 0, 1.0, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, sh_inter, *sh, out.ptr, NH.BF16, ws.ptr, ws_bytes,
+            None, None)
+    ctx.synchronize()
+    wsh = ws.numpy()
+    at = (inner + 255) // 256 * 256
+    assert np.array_equal(wsh[at:at + 4 * tokens * experts].view(np.uint32), logits.view(np.uint32))
+    lay = (ctypes.c_size_t * 5)()
+    lib.nh_moe_workspace_layout(tokens, hidden, inter, experts, top_k, lay)
+    assert np.array_equal(wsh[lay[0]:lay[0] + 4 * tokens * top_k].view(np.int32), idx)
+    got = out.numpy()
+    assert np.array_equal(got, ref), f"{(got != ref).sum()} of {ref.size} outputs differ"
+
+
+def test_moe_layer_rejects_before_the_device(ctx):
+    err = NH.NhError()
+    L = NH.lib()
+    st = L.nh_moe_layer_w8a8(ctx.handle, None, NH.BF16, None, None, 0, 64, 32, 8, 3, 0, 1.0, None, None, None, None,
+                             0, None, None, None, None, None, NH.BF16, None, 0, None, None, ctypes.byref(err))
+    assert st == NH.INVALID_ROW_COUNT
+    st = L.nh_moe_layer_w8a8(ctx.handle, None, NH.BF16, None, None, 4, 64, 32, 8, 3, 0, 1.0, None, None, None, None,
+                             0, None, None, None, None, None, NH.BF16, None, 0, None, None, ctypes.byref(err))
+    assert st == NH.INVALID_PARAMS
+    ws_need = L.nh_moe_layer_w8a8_workspace_size(4, 64, 32, 8, 3, 0)
+    st = L.nh_moe_layer_w8a8(ctx.handle, None, NH.BF16, ctypes.c_void_p(16), None, 4, 64, 32, 8, 3, 0, 1.0, None,
+                             None, None, None, 0, None, None, None, None, None, NH.BF16, None, 0, None, None,
+                             ctypes.byref(err))
+    assert st == NH.LENGTH_MISMATCH and err.argument == b"workspace" and err.expected == ws_need
+
+
 def test_grouped_gemm_config3_routes_bit_exact(ctx):
     """nh_moe_grouped_gemm_w8a8 on the 3072 routes of configs[3]: the up
     projection gathered from token-major codes (the grouped kernel) and from
