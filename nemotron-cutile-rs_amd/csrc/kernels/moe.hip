@@ -371,16 +371,17 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(Gro
 // passes, the 6 of 128 experts holding 33-40 of the 3072 routes took two
 // passes and doubled the projection time.
 constexpr int kExpertSlab = 8;  // K tiles per register slab (two slabs in ping-pong)
+constexpr int kExpertPlain = 0, kExpertOmax = 1, kExpertQuantA = 2;
 
 // The waves' tile streams of one pass over NRB row blocks.  Straight-line
 // per chunk (every load issued, past the wave's last chunk from an empty
 // buffer; K tiles past kt load zeros and meet a valid A tile), so the
 // compiler's wait counts see the slabs in flight and wait for one slab only.
-template <int NRB>
+template <int NRB, int MODE>
 __device__ __forceinline__ void expert_stream(const ExpertGemmArgs& a, v4i (&b0)[kExpertSlab],
                                               v4i (&b1)[kExpertSlab], const int8_t* As, const float* sas,
                                               const float* sws, const int8_t* wexp, int wave, int lane, int t_begin,
-                                              int nj, int nch, int p0, int seg1) {
+                                              int nj, int nch, int p0, int seg1, uint32_t* lmax) {
     const int N = a.N, kt = a.kt, NW = a.streams;
     const int r16 = lane & 15, g = lane >> 4;
     auto load_chunk = [&](v4i (&b)[kExpertSlab], int j) {
@@ -391,6 +392,13 @@ __device__ __forceinline__ void expert_stream(const ExpertGemmArgs& a, v4i (&b0)
         for (int s = 0; s < kExpertSlab; ++s) b[s] = buffer_load16_stream(wr, (k0 + s) * 1024 + lane * 16);
     };
     v4i acc[NRB];
+    // kExpertOmax: this lane's running max of the finite |out| of its rows
+    // (its own columns; the 16 lanes of a row group meet at the pass end)
+    float rmax[NRB][4];
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rmax[rb][r] = 0.0f;
     auto process = [&](const v4i (&b)[kExpertSlab], int j) {
         const int c = j % nch, k0 = c * kExpertSlab;
         if (c == 0) {
@@ -431,6 +439,13 @@ __device__ __forceinline__ void expert_stream(const ExpertGemmArgs& a, v4i (&b0)
                         float y = epilogue_w8a8(acc[rb][r], sas[rb * 16 + 4 * g + r], swn);
                         if (a.relu2) y = relu2(y);
                         ob[(rb * 16 + r) * N] = y;
+                        if constexpr (MODE == kExpertOmax) {
+                            if (is_finite_f32(y))
+                                rmax[rb][r] = fmaxf(rmax[rb][r], fabsf(y));
+                            else if (a.nonfinite)
+                                report_nonfinite(a.nonfinite, a.nonfinite_stage,
+                                                 (int64_t)(p0 + 4 * g + rb * 16 + r) * N + n, y);
+                        }
                     }
         }
     };
@@ -442,10 +457,38 @@ __device__ __forceinline__ void expert_stream(const ExpertGemmArgs& a, v4i (&b0)
         process(b1, j + 1);
         load_chunk(b1, j + 3);
     }
+    if constexpr (MODE == kExpertOmax) {
+        // the row group's 16 lanes (one column each), then the waves (LDS max
+        // of the bit patterns: non-negative floats order like their bits)
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float m = rmax[rb][r];
+#pragma unroll
+                for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+                if (r16 == 0) atomicMax(&lmax[rb * 16 + 4 * g + r], f32_bits(m));
+            }
+    }
 }
 
-extern "C" __global__ __launch_bounds__(512) void nh_moe_expert_gemm_kernel(ExpertGemmArgs a) {
-    extern __shared__ __align__(16) int8_t lds[];
+// The three forms of the expert-block kernel:
+//  kExpertPlain  A codes in slot order (aq, sa) staged by direct-to-LDS loads;
+//  kExpertOmax   the same, and each workgroup also writes, for every row of
+//                its segment, the largest finite |out| over its own columns
+//                (omax[row][blockIdx.x], f32 bits) and reports non-finite
+//                outputs: the up projection of the MoE layer, whose output
+//                the down projection requantizes per row;
+//  kExpertQuantA A rows in f32 (ah), quantized per row while staged, with
+//                the row scale RN(amax / 127) from amax = the larger of the
+//                row's two omax entries: the max of the finite |h| over the
+//                whole row, so the codes and scales are those of
+//                nh_quantize_rows_i8 on h (the down projection; K <= 2048:
+//                a wave stages 4 K tiles of each row block).  That fuses
+//                the intermediate requantization of mlp.rs:201-208 into the
+//                two projections instead of a launch and an int8 copy.
+template <int MODE>
+__device__ __forceinline__ void expert_gemm(const ExpertGemmArgs& a, int8_t* lds) {
     const int e = blockIdx.y;
     const int seg0 = a.offsets[e], seg1 = a.offsets[e + 1];
     if (seg0 >= seg1) return;  // no routes: the expert's weights are never read
@@ -459,59 +502,157 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_expert_gemm_kernel(Expe
     const int ntiles = (N + 15) / 16;
     const int t_begin = blockIdx.x * a.tiles_per_wg;
     const int t_end = min(t_begin + a.tiles_per_wg, ntiles);
-    if (t_begin >= t_end) return;  // uniform
+    if (t_begin >= t_end) {  // uniform: no columns here, so no output of this range is non-zero
+        if constexpr (MODE == kExpertOmax)
+            for (int row = seg0 + (int)threadIdx.x; row < seg1; row += blockDim.x) a.omax[row * 2 + blockIdx.x] = 0u;
+        return;
+    }
     const int my_tiles = t_begin + wave < t_end ? (t_end - t_begin - wave + NW - 1) / NW : 0;
     const int nj = my_tiles * nch;  // this wave's chunks
     const int nw_cols = min(t_end * 16, N) - t_begin * 16;  // this workgroup's weight rows
     int8_t* As = lds;                                // [RB][kt] A tiles
     float* sas = (float*)(lds + RB * kt * 1024);     // [16 RB] the pass's row scales
-    float* sws = sas + 16 * RB;                      // [16 tiles_per_wg, rounded up to 64] weight scales
+    uint32_t* lmax = (uint32_t*)(sas + 16 * RB);     // [64] kExpertOmax: the pass's row maxima
+    float* sws = (float*)(lmax + 64);                // [16 tiles_per_wg, rounded up to 64] weight scales
     const __amdgpu_buffer_rsrc_t swr = make_rsrc(a.sw + (int64_t)e * N + t_begin * 16, (uint32_t)nw_cols * 4u);
     const int8_t* wexp = a.w + (int64_t)e * tiled_bytes(N, K);
-    const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.aq, (uint32_t)a.a_rows * (uint32_t)K);
     v4i b0[kExpertSlab], b1[kExpertSlab];
+    auto first = [&](v4i (&b)[kExpertSlab], int j) {
+        const int t = t_begin + wave + (j / nch) * NW, k0 = (j % nch) * kExpertSlab;
+        const __amdgpu_buffer_rsrc_t wr =
+            j < nj ? make_rsrc(wexp + (int64_t)t * kt * 1024, (uint32_t)kt * 1024u) : make_rsrc(wexp, 0);
+#pragma unroll
+        for (int s = 0; s < kExpertSlab; ++s) b[s] = buffer_load16_stream(wr, (k0 + s) * 1024 + lane * 16);
+    };
     for (int p0 = seg0; p0 < seg1; p0 += cap) {
         const int nrb = (min(cap, seg1 - p0) + 15) / 16;  // uniform
-        // 1. the pass's A tiles, the weight scales (straight to LDS: a global
-        //    load in the epilogue would make the wave wait for its weight
-        //    loads in flight) and the row scales, then this wave's first two chunks
-        __builtin_amdgcn_sched_barrier(0);
-        for (int i = wave; i < nrb * kt; i += NW) {
-            const int rb = i / kt, t = i - rb * kt;
-            const int slot = p0 + rb * 16 + r16;
-            const uint32_t off = (uint32_t)slot * (uint32_t)K + (uint32_t)(t * 64 + g * 16);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_void_t*)(As + i * 1024), 16,
-                                                     slot < seg1 ? off : (uint32_t)kOutOfRange, 0, 0, 0);
-        }
-        for (int i = wave * 64; i < nw_cols; i += NW * 64)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(swr, (lds_void_t*)(sws + i), 4, (uint32_t)(i + lane) * 4u, 0, 0,
-                                                     0);
-        float sav = 0.0f;
-        if ((int)threadIdx.x < cap && p0 + (int)threadIdx.x < seg1) sav = a.sa[p0 + threadIdx.x];
-        __builtin_amdgcn_sched_barrier(0);
-        {
-            auto first = [&](v4i (&b)[kExpertSlab], int j) {
-                const int t = t_begin + wave + (j / nch) * NW, k0 = (j % nch) * kExpertSlab;
-                const __amdgpu_buffer_rsrc_t wr =
-                    j < nj ? make_rsrc(wexp + (int64_t)t * kt * 1024, (uint32_t)kt * 1024u) : make_rsrc(wexp, 0);
-#pragma unroll
-                for (int s = 0; s < kExpertSlab; ++s) b[s] = buffer_load16_stream(wr, (k0 + s) * 1024 + lane * 16);
-            };
+        if constexpr (MODE == kExpertOmax)
+            if (threadIdx.x < 64) lmax[threadIdx.x] = 0u;  // published by the barrier below
+        if constexpr (MODE != kExpertQuantA) {
+            // 1. the pass's A tiles, the weight scales (straight to LDS: a global
+            //    load in the epilogue would make the wave wait for its weight
+            //    loads in flight) and the row scales, then this wave's first two chunks
+            const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.aq, (uint32_t)a.a_rows * (uint32_t)K);
+            __builtin_amdgcn_sched_barrier(0);
+            for (int i = wave; i < nrb * kt; i += NW) {
+                const int rb = i / kt, t = i - rb * kt;
+                const int slot = p0 + rb * 16 + r16;
+                const uint32_t off = (uint32_t)slot * (uint32_t)K + (uint32_t)(t * 64 + g * 16);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_void_t*)(As + i * 1024), 16,
+                                                         slot < seg1 ? off : (uint32_t)kOutOfRange, 0, 0, 0);
+            }
+            for (int i = wave * 64; i < nw_cols; i += NW * 64)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(swr, (lds_void_t*)(sws + i), 4, (uint32_t)(i + lane) * 4u,
+                                                         0, 0, 0);
+            float sav = 0.0f;
+            if ((int)threadIdx.x < cap && p0 + (int)threadIdx.x < seg1) sav = a.sa[p0 + threadIdx.x];
+            __builtin_amdgcn_sched_barrier(0);
             first(b0, 0);
             first(b1, 1);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt_le(2 * kExpertSlab);  // A and scale loads in, weights in flight
+            if ((int)threadIdx.x < cap) sas[threadIdx.x] = sav;
+        } else {
+            // 1. the A rows: f32 from ah, quantized with the row's scale into
+            //    the MFMA tile layout of the DMA form (lane l: row l % 16 of
+            //    the block, 16 codes at 16 (l / 16)); the 4 row blocks in a
+            //    two-deep pipeline of 4 K tiles per lane, with this wave's
+            //    first two weight chunks issued behind the first two blocks
+            const __amdgpu_buffer_rsrc_t hr = make_rsrc(a.ah, (uint32_t)a.a_rows * (uint32_t)K * 4u);
+            uint32_t hm[4][2];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) {
+                const int row = p0 + rb * 16 + r16;
+                const bool ok = rb < nrb && row < seg1;
+                hm[rb][0] = ok ? a.ahmax[row * 2] : 0u;
+                hm[rb][1] = ok ? a.ahmax[row * 2 + 1] : 0u;
+            }
+            v4i hv[2][4][4];
+            auto issue = [&](int rb, v4i (&buf)[4][4]) {
+                const int row = p0 + rb * 16 + r16;
+                const bool ok = rb < nrb && row < seg1;
+                const uint32_t rowoff = (uint32_t)row * (uint32_t)K * 4u;
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int t = wave + u * NW;
+                        const uint32_t off = rowoff + (uint32_t)((t * 64 + g * 16 + 4 * q) * 4);
+                        buf[u][q] = buffer_load16(hr, ok && t < kt ? (int)off : kOutOfRange);
+                    }
+            };
+            auto consume = [&](int rb, const v4i (&buf)[4][4]) {
+                if (rb >= nrb) return;  // uniform
+                const float sc = scale_from_amax(fmaxf(f32_from_bits(hm[rb][0]), f32_from_bits(hm[rb][1])));
+                const float rcp = sc > 0.0f ? 1.0f / sc : 0.0f;
+                const bool pow2 = scale_is_pow2(sc);
+                if (g == 0) sas[rb * 16 + r16] = sc;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int t = wave + u * NW;
+                    if (t >= kt) break;
+                    float v[16];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int w4 = 0; w4 < 4; ++w4) v[4 * q + w4] = f32_from_bits((uint32_t)buf[u][q][w4]);
+                    uint32_t qc[16];
+                    quantize_values<16>(v, sc, rcp, pow2, qc);
+                    const v4i codes = {(int)pack_codes4(qc[0], qc[1], qc[2], qc[3]),
+                                       (int)pack_codes4(qc[4], qc[5], qc[6], qc[7]),
+                                       (int)pack_codes4(qc[8], qc[9], qc[10], qc[11]),
+                                       (int)pack_codes4(qc[12], qc[13], qc[14], qc[15])};
+                    *(v4i*)(As + (rb * kt + t) * 1024 + lane * 16) = codes;
+                }
+            };
+            issue(0, hv[0]);
+            issue(1, hv[1]);
+            __builtin_amdgcn_sched_barrier(0);
+            first(b0, 0);
+            for (int i = wave * 64; i < nw_cols; i += NW * 64)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(swr, (lds_void_t*)(sws + i), 4, (uint32_t)(i + lane) * 4u,
+                                                         0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            consume(0, hv[0]);
+            issue(2, hv[0]);
+            consume(1, hv[1]);
+            issue(3, hv[1]);
+            consume(2, hv[0]);
+            consume(3, hv[1]);
+            // the second chunk is not read before the first one's MFMAs
+            __builtin_amdgcn_sched_barrier(0);
+            first(b1, 1);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt_le(kExpertSlab);  // the weight scales' direct-to-LDS loads in, the second chunk in flight
         }
-        __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt_le(2 * kExpertSlab);  // A and scale loads in, weights in flight
-        if ((int)threadIdx.x < cap) sas[threadIdx.x] = sav;
         lds_publish();  // every wave's A tiles and the scales
         switch (nrb) {
-        case 1: expert_stream<1>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1); break;
-        case 2: expert_stream<2>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1); break;
-        case 3: expert_stream<3>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1); break;
-        default: expert_stream<4>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1); break;
+        case 1: expert_stream<1, MODE>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1, lmax); break;
+        case 2: expert_stream<2, MODE>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1, lmax); break;
+        case 3: expert_stream<3, MODE>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1, lmax); break;
+        default: expert_stream<4, MODE>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1, lmax); break;
         }
         lds_publish();  // the pass's A and scale reads are done before the next pass restages them
+        if constexpr (MODE == kExpertOmax)
+            if ((int)threadIdx.x < nrb * 16 && p0 + (int)threadIdx.x < seg1)
+                a.omax[(p0 + threadIdx.x) * 2 + blockIdx.x] = lmax[threadIdx.x];
     }
+}
+
+extern "C" __global__ __launch_bounds__(512) void nh_moe_expert_gemm_kernel(ExpertGemmArgs a) {
+    extern __shared__ __align__(16) int8_t lds[];
+    expert_gemm<kExpertPlain>(a, lds);
+}
+
+extern "C" __global__ __launch_bounds__(512) void nh_moe_expert_gemm_omax_kernel(ExpertGemmArgs a) {
+    extern __shared__ __align__(16) int8_t lds[];
+    expert_gemm<kExpertOmax>(a, lds);
+}
+
+extern "C" __global__ __launch_bounds__(512) void nh_moe_expert_gemm_qa_kernel(ExpertGemmArgs a) {
+    extern __shared__ __align__(16) int8_t lds[];
+    expert_gemm<kExpertQuantA>(a, lds);
 }
 
 // R4: out[t][h] = sum_j w[t,j] * slot_out[pos[t*k+j]][h], j ascending, f32

@@ -212,6 +212,13 @@ struct ExpertGemmArgs {
     int32_t tiles_per_wg;
     int32_t relu2;
     int32_t row_blocks;      // 16-row blocks of A staged per pass (1..4)
+    // fused forms of the MoE layer (null when unused):
+    uint32_t* omax;          // [R][2] per workgroup column range: max finite |out| of each row (f32 bits)
+    const float* ah;         // [R][K] f32 A rows, quantized per row while staged (aq unused)
+    const uint32_t* ahmax;   // [R][2] the omax of the launch that wrote ah
+    uint64_t* nonfinite;     // non-finite outputs of the omax form are reported here
+    int32_t nonfinite_stage;
+    int32_t pad_;
 };
 
 // R4: scatter-combine.

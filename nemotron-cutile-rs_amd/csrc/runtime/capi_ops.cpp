@@ -653,6 +653,66 @@ nh_status nh_moe_permute(nh_context* ctx, const int32_t* indices, size_t tokens,
     return launch(ctx, K_PERMUTE, 1, 1024, 2 * experts * sizeof(int), stream, a, err);
 }
 
+}  // extern "C"
+
+// The expert-block kernel (slot-ordered A, kernels/moe.hip) in one of its
+// three forms; e carries the operands, this fills the launch shape.  Two
+// workgroups per expert, each owning half of the N tiles; a pass stages as
+// many 16-row blocks (up to 4) as the LDS holds next to the pass's row
+// scales, 64 row maxima and the workgroup's weight scales: every pass
+// re-streams the expert's weights.  NH_UNSUPPORTED when even one block does
+// not fit (the caller takes the grouped kernel).
+static nh_status launch_expert_gemm(nh_context* ctx, KernelId id, ExpertGemmArgs e, size_t experts, size_t n,
+                                    size_t k, nh_stream stream, nh_error* err) {
+    constexpr int kExpertWaves = 8;
+    const int kt = (int)tiled_k_tiles(k);
+    const int ntiles = (int)((n + 15) / 16);
+    const int tiles_per_wg = (ntiles + 1) / 2;
+    // the weight scales arrive by 64-float direct-to-LDS rows (256 bytes
+    // each, also past the workgroup's last column), so their region is a
+    // whole number of rows
+    auto expert_lds = [&](int rb) {
+        const size_t sws_floats = ((size_t)tiles_per_wg * 16 + 63) / 64 * 64;
+        return (size_t)rb * kt * 1024 + (size_t)rb * 16 * 4 + 64 * 4 + sws_floats * 4;
+    };
+    int row_blocks = 4;
+    while (row_blocks > 1 && expert_lds(row_blocks) > ctx->max_shared_per_block) --row_blocks;
+    const size_t lds = expert_lds(row_blocks);
+    if (lds > ctx->max_shared_per_block) return set_error(err, NH_UNSUPPORTED, "expert tiles exceed the LDS");
+    e.N = (int)n;
+    e.K = (int)k;
+    e.kt = kt;
+    e.waves = 1;
+    e.streams = kExpertWaves;
+    e.tiles_per_wg = tiles_per_wg;
+    e.row_blocks = row_blocks;
+    return launch(ctx, id, 2u, (unsigned)(64 * kExpertWaves), lds, stream, e, err, (unsigned)experts);
+}
+
+// Whether the MoE layer's two projections run as the fused expert-block
+// pair: the envelope of nh_moe_grouped_gemm_w8a8 for both shapes, the f32
+// intermediate within 32-bit buffer offsets, and a 16-row block of A tiles
+// in the LDS for both (checked before anything is launched).
+static bool expert_fused_ok(nh_context* ctx, size_t routes, size_t experts, size_t hidden, size_t inter,
+                            const int8_t* w_up, const int8_t* w_down) {
+    if (!nh_supports_gemm_w8a8(routes, inter, hidden) || !nh_supports_gemm_w8a8(routes, hidden, inter)) return false;
+    if (experts > 65535 || hidden > 8192 || inter > 8192 || routes * inter * 4 >= (1ull << 31) ||
+        routes * hidden >= (1ull << 31))
+        return false;
+    if (!aligned16(w_up) || !aligned16(w_down)) return false;
+    // the down kernel stages each 16-row block as 4 K tiles per wave (8
+    // waves): inter <= 2048
+    if (tiled_k_tiles(inter) > 32) return false;
+    auto fits = [&](size_t n, size_t k) {
+        const size_t tiles_per_wg = ((n + 15) / 16 + 1) / 2;
+        const size_t sws_floats = (tiles_per_wg * 16 + 63) / 64 * 64;
+        return tiled_k_tiles(k) * 1024 + 16 * 4 + 64 * 4 + sws_floats * 4 <= ctx->max_shared_per_block;
+    };
+    return fits(inter, hidden) && fits(hidden, inter);
+}
+
+extern "C" {
+
 nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const float* sa, int gather, size_t top_k,
                                    const int32_t* offsets, const int32_t* perm, size_t routes, size_t a_rows,
                                    size_t experts, const int8_t* w, const float* sw, size_t n, size_t k, int relu2,
@@ -666,46 +726,19 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
         return set_error(err, NH_UNSUPPORTED, "grouped GEMM envelope: experts <= 65535, k <= 8192, a_rows * k < 2^31");
     if ((st = bind_device(ctx, err))) return st;
     if (routes == 0) return NH_OK;
-    const int kt = (int)tiled_k_tiles(k);
     if (!gather) {
-        // slot-ordered A: the expert-block kernel (A staged once per pass in
-        // LDS, 8 waves streaming whole N tiles), two workgroups per expert.
-        // A pass stages as many 16-row blocks (up to 4) as the LDS holds next
-        // to the pass's row scales and the workgroup's weight scales: every
-        // pass re-streams the expert's weights.
-        constexpr int kExpertWaves = 8;
-        const int ntiles = (int)((n + 15) / 16);
-        const int tiles_per_wg = (ntiles + 1) / 2;
-        // the weight scales arrive by 64-float direct-to-LDS rows (256 bytes
-        // each, also past the workgroup's last column), so their region is a
-        // whole number of rows
-        auto expert_lds = [&](int rb) {
-            const size_t sws_floats = ((size_t)tiles_per_wg * 16 + 63) / 64 * 64;
-            return (size_t)rb * kt * 1024 + (size_t)rb * 16 * 4 + sws_floats * 4;
-        };
-        int row_blocks = 4;
-        while (row_blocks > 1 && expert_lds(row_blocks) > ctx->max_shared_per_block) --row_blocks;
-        const size_t lds = expert_lds(row_blocks);
-        if (lds <= ctx->max_shared_per_block) {
-            ExpertGemmArgs e{};
-            e.aq = aq;
-            e.sa = sa;
-            e.offsets = offsets;
-            e.w = w;
-            e.sw = sw;
-            e.out = out;
-            e.N = (int)n;
-            e.K = (int)k;
-            e.kt = kt;
-            e.a_rows = (int)a_rows;
-            e.waves = 1;
-            e.streams = kExpertWaves;
-            e.tiles_per_wg = tiles_per_wg;
-            e.relu2 = relu2 ? 1 : 0;
-            e.row_blocks = row_blocks;
-            return launch(ctx, K_EXPERT_GEMM, 2u, (unsigned)(64 * kExpertWaves), lds, stream, e, err,
-                          (unsigned)experts);
-        }
+        ExpertGemmArgs e{};
+        e.aq = aq;
+        e.sa = sa;
+        e.offsets = offsets;
+        e.w = w;
+        e.sw = sw;
+        e.out = out;
+        e.a_rows = (int)a_rows;
+        e.relu2 = relu2 ? 1 : 0;
+        st = launch_expert_gemm(ctx, K_EXPERT_GEMM, e, experts, n, k, stream, err);
+        if (st != NH_UNSUPPORTED) return st;
+        clear_error(err);
     }
     GroupedGemmArgs a{};
     a.aq = aq;
@@ -849,16 +882,46 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
     if ((st = launch_quantize(ctx, x, x_dtype, R, hidden, xq, sx, nullptr, nullptr, stream, err, 0, perm,
                               (int)top_k, nonfinite, 0)))
         return st;
-    if ((st = nh_moe_grouped_gemm_w8a8(ctx, xq, sx, 0, top_k, offsets, perm, R, R, experts, w_up, s_up, inter,
-                                       hidden, 1, h, stream, err)))
-        return st;
-    // the up outputs per slot: the layer's intermediate (stage 1)
-    if ((st = launch_quantize(ctx, h, NH_F32, R, inter, hq, sh, nullptr, nullptr, stream, err, 0, nullptr, 1,
-                              nonfinite, 1)))
-        return st;
-    if ((st = nh_moe_grouped_gemm_w8a8(ctx, hq, sh, 0, top_k, offsets, perm, R, R, experts, w_down, s_down, hidden,
-                                       inter, 0, d, stream, err)))
-        return st;
+    if (expert_fused_ok(ctx, R, experts, hidden, inter, w_up, w_down)) {
+        // up with ReLU^2, h in f32 plus each row's max finite |h| per
+        // workgroup (stage 1 of the non-finite report: h is the layer's
+        // intermediate); the down projection requantizes h per row while it
+        // stages it (the codes and scales of nh_quantize_rows_i8 on h)
+        uint32_t* hmax = (uint32_t*)(ws + off[8]);  // [R][2]
+        ExpertGemmArgs up{};
+        up.aq = xq;
+        up.sa = sx;
+        up.offsets = offsets;
+        up.w = w_up;
+        up.sw = s_up;
+        up.out = h;
+        up.a_rows = (int)R;
+        up.relu2 = 1;
+        up.omax = hmax;
+        up.nonfinite = nonfinite;
+        up.nonfinite_stage = 1;
+        if ((st = launch_expert_gemm(ctx, K_EXPERT_GEMM_OMAX, up, experts, inter, hidden, stream, err))) return st;
+        ExpertGemmArgs down{};
+        down.ah = h;
+        down.ahmax = hmax;
+        down.offsets = offsets;
+        down.w = w_down;
+        down.sw = s_down;
+        down.out = d;
+        down.a_rows = (int)R;
+        if ((st = launch_expert_gemm(ctx, K_EXPERT_GEMM_QA, down, experts, hidden, inter, stream, err))) return st;
+    } else {
+        if ((st = nh_moe_grouped_gemm_w8a8(ctx, xq, sx, 0, top_k, offsets, perm, R, R, experts, w_up, s_up, inter,
+                                           hidden, 1, h, stream, err)))
+            return st;
+        // the up outputs per slot: the layer's intermediate (stage 1)
+        if ((st = launch_quantize(ctx, h, NH_F32, R, inter, hq, sh, nullptr, nullptr, stream, err, 0, nullptr, 1,
+                                  nonfinite, 1)))
+            return st;
+        if ((st = nh_moe_grouped_gemm_w8a8(ctx, hq, sh, 0, top_k, offsets, perm, R, R, experts, w_down, s_down,
+                                           hidden, inter, 0, d, stream, err)))
+            return st;
+    }
     return nh_moe_combine_shared(ctx, d, pos, wts, shared, tokens, top_k, hidden, out, out_dtype, stream, err);
 }
 

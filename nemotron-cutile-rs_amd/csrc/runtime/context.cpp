@@ -36,6 +36,8 @@ const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
     "nh_linear_decode_w8a8_row2_kernel", // K_LINEAR_DECODE_ROW2
     "nh_linear_decode_w8a8_row4_kernel", // K_LINEAR_DECODE_ROW4
     "nh_moe_expert_gemm_kernel",         // K_EXPERT_GEMM
+    "nh_moe_expert_gemm_omax_kernel",    // K_EXPERT_GEMM_OMAX
+    "nh_moe_expert_gemm_qa_kernel",      // K_EXPERT_GEMM_QA
     "nh_quantize_rows_wave_kernel",      // K_QUANTIZE_ROWS_WAVE
     "nh_quantize_rows_long_kernel",      // K_QUANTIZE_ROWS_LONG
     "nh_tile_weights_int4_kernel",       // K_TILE_INT4

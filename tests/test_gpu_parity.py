@@ -991,6 +991,42 @@ def test_mlp_nonfinite_intermediate_and_input_reported(ctx):
     assert st == NH.NON_FINITE_INPUT and err.argument == b"input" and err.index == hidden + 17
 
 
+def test_moe_nonfinite_intermediate_reported(ctx):
+    """An expert's up output overflows (a 3e38 weight scale): the fused up
+    epilogue reports it as "intermediate" at its index into the
+    [routes][inter] up output in slot order, the lowest such index; the down
+    projection requantizes the finite rows as before."""
+    tokens, hidden, inter, experts, top_k = 13, 64, 32, 8, 3
+    note("moe nonfinite intermediate")
+    x, logits, up, su, down, sd = moe_case(tokens, hidden, inter, experts, top_k)
+    _, idx, w, _ = O.route_sigmoid(logits, tokens, experts, top_k, renormalize=True)
+    offsets, perm, pos = O.moe_permute(idx, tokens, top_k, experts)
+    e = int(np.argmax(np.diff(offsets)))  # the busiest expert
+    su2 = su.copy()
+    su2[e, 5] = 3e38
+    _, xq, sx, _ = O.quantize_rows_bf16(x)
+    h = O.moe_grouped(xq, sx, True, top_k, offsets, perm, up, su2, relu2=True)
+    bad = np.flatnonzero(~np.isfinite(h.ravel()))
+    assert bad.size > 0
+    ws_bytes = NH.lib().nh_moe_forward_w8a8_workspace_size(tokens, hidden, inter, experts, top_k)
+    ws = ctx.empty(ws_bytes, np.uint8)
+    dx, dl = ctx.upload(x), ctx.upload(logits)
+    dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su2), ctx.upload(tile_experts(down)), ctx.upload(sd)
+    out = ctx.empty((tokens, hidden), np.uint16)
+    word = ctx.upload(np.zeros(1, dtype=np.uint64))
+    NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
+            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, word.ptr, None)
+    st, err = take_nonfinite(ctx, word)
+    assert st == NH.NON_FINITE_INPUT and err.argument == b"intermediate" and err.index == bad[0]
+    assert np.isinf(err.value) and err.value > 0
+    # the word was cleared: a clean call reports nothing
+    dsu_clean = ctx.upload(su)
+    NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
+            dup.ptr, dsu_clean.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, word.ptr, None)
+    st, _ = take_nonfinite(ctx, word)
+    assert st == NH.OK
+
+
 def test_moe_nonfinite_input_reported(ctx):
     tokens, hidden, inter, experts, top_k = 13, 64, 32, 8, 3
     note("moe nonfinite")
