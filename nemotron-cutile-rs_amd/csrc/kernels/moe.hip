@@ -31,16 +31,17 @@ constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
 
 }  // namespace
 
-// R1: one wave per token.  Expert e lives in lane e % 64, slot e / 64.
-extern "C" __global__ __launch_bounds__(256) void nh_moe_route_sigmoid_kernel(RouteArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int token = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (token >= a.tokens) return;
+// R1: one wave per token.  Expert e lives in lane e % 64, slot e / 64 of
+// S slots (S = 2, 4 or 16: the body is instantiated per slot count, so a
+// 128-expert router runs 2 inlined sigmoids per lane instead of fetching the
+// code of 16).
+template <int S>
+__device__ __forceinline__ void route_token(const RouteArgs& a, int token, int lane) {
     const int E = a.experts;
     const float* s = a.scores + (int64_t)token * E;
-    int64_t key[kMaxExpertsPerLane];
+    int64_t key[S];
 #pragma unroll
-    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
+    for (int i = 0; i < S; ++i) {
         const int e = lane + 64 * i;
         key[i] = e < E ? route_key(sigmoid_f32(s[e]), e) : INT64_MIN;
     }
@@ -49,13 +50,13 @@ extern "C" __global__ __launch_bounds__(256) void nh_moe_route_sigmoid_kernel(Ro
     for (int j = 0; j < a.top_k; ++j) {
         int64_t best = INT64_MIN;
 #pragma unroll
-        for (int i = 0; i < kMaxExpertsPerLane; ++i) best = key[i] > best ? key[i] : best;
+        for (int i = 0; i < S; ++i) best = key[i] > best ? key[i] : best;
         best = wave_max_i64(best);
         const int e = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFF));
         const int32_t k32 = (int32_t)(best >> 32);
         const float w = f32_from_bits((uint32_t)total_cmp_key(f32_from_bits((uint32_t)k32)));
 #pragma unroll
-        for (int i = 0; i < kMaxExpertsPerLane; ++i)  // the owner drops it
+        for (int i = 0; i < S; ++i)  // the owner drops it
             if (lane + 64 * i == e) key[i] = INT64_MIN;
         if (lane == j) {
             wsel = w;
@@ -73,6 +74,36 @@ extern "C" __global__ __launch_bounds__(256) void nh_moe_route_sigmoid_kernel(Ro
         a.indices[(int64_t)token * a.top_k + lane] = esel;
         a.weights[(int64_t)token * a.top_k + lane] = wsel;
     }
+}
+
+// With x, the same wave first quantizes the token's row (Q2, the wave form
+// of nh_quantize_rows_i8: same codes and scales), token-major: the up
+// projection gathers its A rows through the permutation.
+extern "C" __global__ __launch_bounds__(256) void nh_moe_route_sigmoid_kernel(RouteArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int token = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (token >= a.tokens) return;
+    if (a.x) {
+        QuantizeRowsArgs q{};
+        q.x = a.x;
+        q.q = a.xq;
+        q.scales = a.sx;
+        q.rows = a.tokens;
+        q.cols = a.hidden;
+        q.x_dtype = a.x_dtype;
+        q.nonfinite = a.nonfinite;
+        q.nonfinite_stage = 0;
+        if (a.x_dtype == DT_BF16)
+            quantize_row_wave<DT_BF16, 8>(q);
+        else
+            quantize_row_wave<DT_F32, 8>(q);
+    }
+    if (a.experts <= 128)
+        route_token<2>(a, token, lane);
+    else if (a.experts <= 256)
+        route_token<4>(a, token, lane);
+    else
+        route_token<kMaxExpertsPerLane>(a, token, lane);
 }
 
 // R2: one workgroup of 1024 threads.  Phase 1 histograms the experts (LDS
@@ -533,24 +564,63 @@ __device__ __forceinline__ void expert_gemm(const ExpertGemmArgs& a, int8_t* lds
             //    load in the epilogue would make the wave wait for its weight
             //    loads in flight) and the row scales, then this wave's first two chunks
             const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.aq, (uint32_t)a.a_rows * (uint32_t)K);
-            __builtin_amdgcn_sched_barrier(0);
-            for (int i = wave; i < nrb * kt; i += NW) {
-                const int rb = i / kt, t = i - rb * kt;
-                const int slot = p0 + rb * 16 + r16;
-                const uint32_t off = (uint32_t)slot * (uint32_t)K + (uint32_t)(t * 64 + g * 16);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_void_t*)(As + i * 1024), 16,
-                                                         slot < seg1 ? off : (uint32_t)kOutOfRange, 0, 0, 0);
-            }
-            for (int i = wave * 64; i < nw_cols; i += NW * 64)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(swr, (lds_void_t*)(sws + i), 4, (uint32_t)(i + lane) * 4u,
-                                                         0, 0, 0);
             float sav = 0.0f;
-            if ((int)threadIdx.x < cap && p0 + (int)threadIdx.x < seg1) sav = a.sa[p0 + threadIdx.x];
-            __builtin_amdgcn_sched_barrier(0);
-            first(b0, 0);
-            first(b1, 1);
-            __builtin_amdgcn_sched_barrier(0);
-            wait_vmcnt_le(2 * kExpertSlab);  // A and scale loads in, weights in flight
+            if (!a.perm) {
+                __builtin_amdgcn_sched_barrier(0);
+                for (int i = wave; i < nrb * kt; i += NW) {
+                    const int rb = i / kt, t = i - rb * kt;
+                    const int slot = p0 + rb * 16 + r16;
+                    const uint32_t off = (uint32_t)slot * (uint32_t)K + (uint32_t)(t * 64 + g * 16);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_void_t*)(As + i * 1024), 16,
+                                                             slot < seg1 ? off : (uint32_t)kOutOfRange, 0, 0, 0);
+                }
+                for (int i = wave * 64; i < nw_cols; i += NW * 64)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(swr, (lds_void_t*)(sws + i), 4,
+                                                             (uint32_t)(i + lane) * 4u, 0, 0, 0);
+                if ((int)threadIdx.x < cap && p0 + (int)threadIdx.x < seg1) sav = a.sa[p0 + threadIdx.x];
+                __builtin_amdgcn_sched_barrier(0);
+                first(b0, 0);
+                first(b1, 1);
+                __builtin_amdgcn_sched_barrier(0);
+                wait_vmcnt_le(2 * kExpertSlab);  // A and scale loads in, weights in flight
+            } else {
+                // gathered A: row (and scale) of slot s is perm[s] / gather_div.
+                // The permutation entries of this lane's rows go out ahead of
+                // the weights, so waiting for them leaves the weights in
+                // flight; the A rows (L2) then arrive under the weights'
+                // latency (HBM).
+                // (unconditional loads: entries past the segment read zeros and are masked)
+                const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.perm, (uint32_t)seg1 * 4u);
+                int tok[4];
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb)
+                    tok[rb] = __builtin_amdgcn_raw_buffer_load_b32(pr, (p0 + rb * 16 + r16) * 4, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                first(b0, 0);
+                first(b1, 1);
+                __builtin_amdgcn_sched_barrier(0);
+                wait_vmcnt_le(2 * kExpertSlab);  // the permutation entries in, weights in flight
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb)
+                    tok[rb] = rb < nrb && p0 + rb * 16 + r16 < seg1 ? tok[rb] / a.gather_div : -1;
+                for (int i = wave; i < nrb * kt; i += NW) {
+                    const int rb = i / kt, t = i - rb * kt;
+                    const int tr = rb == 0 ? tok[0] : rb == 1 ? tok[1] : rb == 2 ? tok[2] : tok[3];
+                    const uint32_t off = (uint32_t)tr * (uint32_t)K + (uint32_t)(t * 64 + g * 16);
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_void_t*)(As + i * 1024), 16,
+                                                             tr >= 0 ? off : (uint32_t)kOutOfRange, 0, 0, 0);
+                }
+                for (int i = wave * 64; i < nw_cols; i += NW * 64)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(swr, (lds_void_t*)(sws + i), 4,
+                                                             (uint32_t)(i + lane) * 4u, 0, 0, 0);
+                // thread t < cap holds slot p0 + t: row block t / 16 = g of its wave 0 lane
+                if ((int)threadIdx.x < cap) {
+                    const int tr = g == 0 ? tok[0] : g == 1 ? tok[1] : g == 2 ? tok[2] : tok[3];
+                    if (tr >= 0) sav = a.sa[tr];
+                }
+                wait_vmcnt_le(0);  // A, scales and the first chunks
+            }
             if ((int)threadIdx.x < cap) sas[threadIdx.x] = sav;
         } else {
             // 1. the A rows: f32 from ah, quantized with the row's scale into

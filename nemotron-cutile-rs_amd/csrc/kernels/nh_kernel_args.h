@@ -164,6 +164,15 @@ struct RouteArgs {
     int32_t renormalize;
     float scaling;
     int32_t pad_;
+    // when not null: the wave of each token also quantizes the token's row
+    // of x ([T][hidden], f32 or bf16, 16-byte rows of at most 512 chunks)
+    // into xq [T][hidden] and sx [T], non-finite values reported at stage 0
+    const void* x;
+    int8_t* xq;
+    float* sx;
+    uint64_t* nonfinite;
+    int32_t x_dtype;
+    int32_t hidden;
 };
 
 // R2: counting-sort permutation, one workgroup.
@@ -218,7 +227,8 @@ struct ExpertGemmArgs {
     const uint32_t* ahmax;   // [R][2] the omax of the launch that wrote ah
     uint64_t* nonfinite;     // non-finite outputs of the omax form are reported here
     int32_t nonfinite_stage;
-    int32_t pad_;
+    int32_t gather_div;      // with perm: A row (and sa entry) of slot s = perm[s] / gather_div
+    const int32_t* perm;     // [R] or null (A rows in slot order)
 };
 
 // R4: scatter-combine.

@@ -631,7 +631,8 @@ nh_status nh_moe_route_sigmoid_topk(nh_context* ctx, const float* scores, size_t
     nh_status st = bind_device(ctx, err);
     if (st) return st;
     if (tokens == 0) return NH_OK;
-    RouteArgs a{scores, indices, weights, (int)tokens, (int)experts, (int)top_k, renormalize ? 1 : 0, scaling, 0};
+    RouteArgs a{scores, indices, weights, (int)tokens, (int)experts, (int)top_k, renormalize ? 1 : 0, scaling, 0,
+                nullptr, nullptr, nullptr, nullptr, 0, 0};
     return launch(ctx, K_ROUTE_SIGMOID, (unsigned)((tokens + 3) / 4), 256, 0, stream, a, err);
 }
 
@@ -872,17 +873,28 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
                           inter_sh, shared, NH_F32, ws + shared_at + shared_bytes, workspace_bytes - shared_at -
                           shared_bytes, nonfinite, stream, err)))
         return st;
-    if ((st = nh_moe_route_sigmoid_topk(ctx, logits, tokens, experts, top_k, renormalize, scaling, idx, wts, stream,
-                                        err)))
+    const bool fused = expert_fused_ok(ctx, R, experts, hidden, inter, w_up, w_down);
+    const size_t esz = x_dtype == NH_BF16 ? 2 : 4;
+    // the routing wave of each token also quantizes its row (token-major)
+    // when the row fits the wave quantizer; the up projection then gathers
+    const bool route_q = fused && aligned16(x) && (hidden * esz) % 16 == 0 && hidden * esz <= 512 * 16 &&
+                         experts <= 1024 && top_k <= 64 && tokens <= (size_t)kMaxGrid / 4;
+    if (route_q) {
+        if ((st = bind_device(ctx, err))) return st;
+        RouteArgs ra{logits, idx, wts, (int)tokens, (int)experts, (int)top_k, renormalize ? 1 : 0, scaling, 0,
+                     x, xq, sx, nonfinite, x_dtype == NH_BF16 ? DT_BF16 : DT_F32, (int)hidden};
+        if ((st = launch(ctx, K_ROUTE_SIGMOID, (unsigned)((tokens + 3) / 4), 256, 0, stream, ra, err))) return st;
+    } else if ((st = nh_moe_route_sigmoid_topk(ctx, logits, tokens, experts, top_k, renormalize, scaling, idx, wts,
+                                               stream, err))) {
         return st;
+    }
     if ((st = nh_moe_permute(ctx, idx, tokens, top_k, experts, offsets, perm, pos, stream, err))) return st;
-    // Q2 of each route's token, written in expert order (slot s = token
-    // perm[s] / top_k): the up projection then reads its rows contiguously,
-    // with no index load in front of its activation loads
-    if ((st = launch_quantize(ctx, x, x_dtype, R, hidden, xq, sx, nullptr, nullptr, stream, err, 0, perm,
-                              (int)top_k, nonfinite, 0)))
+    // otherwise Q2 of each route's token, written in expert order (slot s =
+    // token perm[s] / top_k): the up projection reads its rows contiguously
+    if (!route_q && (st = launch_quantize(ctx, x, x_dtype, R, hidden, xq, sx, nullptr, nullptr, stream, err, 0, perm,
+                                          (int)top_k, nonfinite, 0)))
         return st;
-    if (expert_fused_ok(ctx, R, experts, hidden, inter, w_up, w_down)) {
+    if (fused) {
         // up with ReLU^2, h in f32 plus each row's max finite |h| per
         // workgroup (stage 1 of the non-finite report: h is the layer's
         // intermediate); the down projection requantizes h per row while it
@@ -891,11 +903,15 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
         ExpertGemmArgs up{};
         up.aq = xq;
         up.sa = sx;
+        if (route_q) {  // token-major codes: slot s reads token perm[s] / top_k
+            up.perm = perm;
+            up.gather_div = (int)top_k;
+        }
         up.offsets = offsets;
         up.w = w_up;
         up.sw = s_up;
         up.out = h;
-        up.a_rows = (int)R;
+        up.a_rows = route_q ? (int)tokens : (int)R;
         up.relu2 = 1;
         up.omax = hmax;
         up.nonfinite = nonfinite;

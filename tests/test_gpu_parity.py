@@ -542,7 +542,8 @@ def route_on_device(ctx, scores, t, e, k, renorm, scaling=1.0):
 
 
 @pytest.mark.parametrize("t,e,k,renorm,scaling", [(512, 128, 6, 1, 1.0), (512, 128, 6, 0, 1.0), (64, 128, 6, 1, 2.5),
-                                                  (3, 1000, 8, 1, 1.0), (5, 7, 7, 0, 1.0)])
+                                                  (3, 1000, 8, 1, 1.0), (5, 7, 7, 0, 1.0), (17, 129, 4, 0, 1.0),
+                                                  (40, 200, 6, 1, 1.0), (9, 256, 8, 1, 1.0), (6, 257, 3, 0, 1.0)])
 def test_route_sigmoid_bit_exact(ctx, t, e, k, renorm, scaling):
     note(f"route t={t} e={e} k={k} renorm={renorm}")
     scores = O.normal_f32(2, t * e)
