@@ -368,14 +368,53 @@ def NH_bf16(x):
     return r
 
 
-def cpu_baseline(budget_s=10.0):
-    """The reference's host path for this layer on this host: gemm_into_host
-    (f64 accumulation, gemm.rs:91-112) on the f32 weights materialised from
-    the int8 codes (linear.rs:126-131), one M=1 decode step of configs[1]
-    (K=4096 -> N=16384) per call, repeated for about budget_s seconds."""
+def cpu_model():
+    """The host CPU's model string (/proc/cpuinfo), else the platform's."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_threads():
+    """Threads for the all-cores baselines: the CPUs this process may use,
+    capped at 16 (a one-GPU box's share of the host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def _parallel(fn, items, threads):
+    """fn over items on `threads` host threads (the oracle's C calls release
+    the GIL), wall time in seconds."""
+    from concurrent.futures import ThreadPoolExecutor
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        list(ex.map(fn, items))
+    return time.perf_counter() - t0
+
+
+def cpu_baselines(budget_s=6.0):
+    """The reference's host path on this host, timed on bounded samples
+    (restated by the oracle, which is only the checker elsewhere):
+    gemm_into_host (f64 accumulation, gemm.rs:91-112) on f32 weights
+    materialised from the int8 codes (linear.rs:126-131), and MoeLayer's
+    dense experts (moe.rs:207-246: every selected expert's MlpLayer over all
+    rows).  Returns (the headline object, the list of all baselines)."""
+    import ctypes
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_ctypes as O
 
+    T = cpu_threads()
+    model = cpu_model()
+    out = []
+    # configs[1]: one M=1 decode step, K=4096 -> N=16384
     m, n, k = 1, 16384, 4096
     w = O.normal_f32(0, n * k, 0.0, 0.02).reshape(n, k)
     st, q, s, _ = O.quantize_rows_f32(w)
@@ -385,22 +424,92 @@ def cpu_baseline(budget_s=10.0):
     x = O.normal_f32(1, m * k)
     runs, t0 = 0, time.perf_counter()
     while True:
-        st, out, _ = O.gemm_f32(x, w_mat, m, k, n)
+        O.gemm_f32(x, w_mat, m, k, n)
         runs += 1
         elapsed = time.perf_counter() - t0
-        if elapsed >= budget_s or runs >= 50:
+        if elapsed >= budget_s or runs >= 20:
             break
-    per = elapsed / runs
-    return {
-        "value": round(decode_bytes(m, n, k) / per / 1e9, 4),
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"{runs} x one M=1 decode step K=4096->N=16384 through the oracle's restatement of "
-                  f"gemm_into_host (f64 accumulation) on materialised f32 weights, {per * 1e3:.1f} ms/step, "
-                  f"{elapsed:.1f} s total; GB/s counts the int8 unit's algorithmic bytes "
-                  f"({platform.processor() or platform.machine()}, nproc={os.cpu_count()})",
-    }
+    per1 = elapsed / runs
+    out.append({"workload": "decode_m1_k4096_n16384", "value": round(decode_bytes(m, n, k) / per1 / 1e9, 4),
+                "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{runs} full M=1 steps, {per1 * 1e3:.0f} ms/step"})
+    # the same step split by output columns over T threads
+    cols = np.array_split(np.arange(n), T)
+    blocks = [np.ascontiguousarray(w_mat[:, c[0]:c[-1] + 1]) for c in cols]
+    del w_mat
+    reps, tt = 0, 0.0
+    while tt < budget_s / 2 and reps < 20:
+        tt += _parallel(lambda b: O.gemm_f32(x, b, 1, k, b.shape[1]), blocks, T)
+        reps += 1
+    perT = tt / reps
+    out.append({"workload": "decode_m1_k4096_n16384", "value": round(decode_bytes(m, n, k) / perT / 1e9, 4),
+                "unit": "GB/s", "cores": T, "kind": "port",
+                "sample": f"{reps} full M=1 steps, output columns split over {T} threads, {perT * 1e3:.0f} ms/step"})
+    del blocks
+    # configs[2] first shape: M=2048, K=4096 -> N=4096, timed on T rows (one per thread)
+    M2, N2, K2 = 2048, 4096, 4096
+    w2 = np.ascontiguousarray(O.normal_f32(3, K2 * N2, 0.0, 0.02).reshape(K2, N2))
+    rows = [O.normal_f32(100 + i, K2) for i in range(T)]
+    t_rows, nrows = 0.0, 0
+    while t_rows < 1.0 and nrows < M2:
+        t_rows += _parallel(lambda r: O.gemm_f32(r, w2, 1, K2, N2), rows, T)
+        nrows += T
+    t_full = t_rows * M2 / nrows
+    out.append({"workload": "gemm_m2048_n4096_k4096", "value": round(2 * M2 * N2 * K2 / t_full / 1e12, 6),
+                "unit": "TOPS", "cores": T, "kind": "port",
+                "sample": f"{nrows} of {M2} rows ({t_rows:.2f} s), extrapolated linearly to all rows: {t_full:.0f} s"})
+    del w2, rows
+    # MoeLayer::forward_into runs every selected expert's dense
+    # f32 MLP over all 512 rows (moe.rs:226-233); timed on T (expert, row)
+    # pairs of one expert's weights, extrapolated to 128 experts x 512 rows
+    H, I, E, TOK = 2688, 1856, 128, 512
+    wu = np.ascontiguousarray(O.normal_f32(4, H * I, 0.0, 0.02))  # [H][I]
+    wd = np.ascontiguousarray(O.normal_f32(5, I * H, 0.0, 0.02))  # [I][H]
+    lib = O.lib()
+    lib.or_mlp_forward.restype = ctypes.c_int
+    P = ctypes.c_void_p
+
+    def mlp_row(r):
+        o = np.empty(H, dtype=np.float32)
+        lib.or_mlp_forward(P(r.ctypes.data), ctypes.c_size_t(1), ctypes.c_size_t(H), ctypes.c_size_t(I),
+                           P(wu.ctypes.data), None, P(wd.ctypes.data), None, P(o.ctypes.data))
+    rows = [O.normal_f32(200 + i, H) for i in range(T)]
+    t_pairs, npairs = 0.0, 0
+    while t_pairs < 1.0 and npairs < E * TOK:
+        t_pairs += _parallel(mlp_row, rows, T)
+        npairs += T
+    t_layer = t_pairs * E * TOK / npairs
+    moe_bytes = 2 * E * H * I  # the int8 layer's expert weight bytes, the device line's GB/s basis
+    out.append({"workload": "moe_512tok_2688h_1856i_128e_top6", "value": round(moe_bytes / t_layer / 1e9, 6),
+                "unit": "GB/s", "cores": T, "kind": "port",
+                "sample": f"{npairs} (expert, row) dense MLPs ({t_pairs:.2f} s), extrapolated to {E} experts x {TOK} "
+                          f"rows (the reference's dense experts; all {E} are selected at top-6 of 512 tokens): "
+                          f"{t_layer:.0f} s per layer"})
+    # the W8A32 dequant GEMV, K=4096 -> N=4096, one core: the
+    # reference's path, materialize_dense then gemm_into_host on [K][N]
+    wq = O.normal_f32(6, 4096 * 4096, 0.0, 0.02).reshape(4096, 4096)
+    _, q0, s0, _ = O.quantize_rows_f32(wq)
+    w0 = np.ascontiguousarray((q0.astype(np.float32) * s0[:, None]).T)
+    del wq, q0
+    x0 = O.normal_f32(7, 4096)
+    runs0, t0 = 0, time.perf_counter()
+    while True:
+        O.gemm_f32(x0, w0, 1, 4096, 4096)
+        runs0 += 1
+        t_w32 = (time.perf_counter() - t0) / runs0
+        if t_w32 * runs0 >= 1.0 or runs0 >= 20:
+            break
+    out.append({"workload": "w8a32_gemv_k4096_n4096", "value": round((4096 * 4096 + 3 * 4 * 4096) / t_w32 / 1e9, 4),
+                "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{runs0} full GEMVs (materialised f32 weights, gemm_into_host), {t_w32 * 1e3:.0f} ms each"})
+    for b in out:
+        b["sample"] += f" ({model})"
+    head = dict(out[1])
+    head.pop("workload")
+    head["sample"] = ("configs[1] decode step K=4096->N=16384 through the oracle's restatement of gemm_into_host "
+                      "(f64 accumulation) on materialised f32 weights; GB/s counts the int8 unit's algorithmic "
+                      "bytes; " + head["sample"] + f"; one core: {out[0]['value']} GB/s")
+    return head, out
 
 
 def main():
@@ -515,10 +624,10 @@ def main():
         extra["moe_512tok_128exp_top6_shared3712"] = {
             "us": round(t * 1e3, 1), "GBps": round(mbytes / (t * 1e-3) / 1e9, 1),
             "frac_hbm_peak": round(mbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "TOPS": round(mops / (t * 1e-3) / 1e12, 2)}
-    cpu = None
+    cpu, cpu_all = None, None
     if not args.no_cpu:
-        log("[bench] cpu baseline")
-        cpu = cpu_baseline()
+        log("[bench] cpu baselines")
+        cpu, cpu_all = cpu_baselines()
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "decode_unit_m1_k4096_n16384_traffic.json")
@@ -552,6 +661,8 @@ def main():
                      "kernel": "nh_linear_decode_w8a8_m1_kernel", "bytes_per_launch": nbytes},
         "cpu_baseline": cpu,
     }
+    if cpu_all is not None:
+        line["cpu_baselines"] = cpu_all
     line.update(extra)
     print(json.dumps(line), flush=True)
 
