@@ -444,7 +444,10 @@ def cpu_baselines(budget_s=6.0):
     perT = tt / reps
     out.append({"workload": "decode_m1_k4096_n16384", "value": round(decode_bytes(m, n, k) / perT / 1e9, 4),
                 "unit": "GB/s", "cores": T, "kind": "port",
-                "sample": f"{reps} full M=1 steps, output columns split over {T} threads, {perT * 1e3:.0f} ms/step"})
+                "sample": f"{reps} full M=1 steps, output columns split over {T} threads, {perT * 1e3:.0f} ms/step "
+                          f"(each thread's [K][N/{T}] block is its own contiguous array: besides the threads, the "
+                          f"gain over one core includes the shorter stride of the depth loop, which on the "
+                          f"reference's one [K][N] matrix is N floats)"})
     del blocks
     # configs[2] first shape: M=2048, K=4096 -> N=4096, timed on T rows (one per thread)
     M2, N2, K2 = 2048, 4096, 4096
