@@ -527,7 +527,34 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (torch's copy kernel), the "
                          "calibration run for the FETCH_SIZE / WRITE_SIZE counters, and exit")
+    ap.add_argument("--stream", type=int, nargs="+", default=None, metavar="MIB",
+                    help="only time one read of MIB MiB with nh_stream_read (the weight streams' load pattern) "
+                         "over a 640 MiB pool, the HBM floor of the bandwidth-bound kernels, and exit")
     args = ap.parse_args()
+    if args.stream:
+        b = Bench()
+        L, h = NH.lib(), b.ctx.handle
+        err = NH.NhError()
+        sink = b.ctx.empty(256, np.int32)
+        res = {}
+        for mib in args.stream:
+            nbytes = mib << 20
+            copies = max(2, -(-POOL_BYTES // nbytes))
+            pool = b.ctx.empty(copies * nbytes, np.uint8)
+            pool.fill_bytes(1)
+
+            def step(i, pool=pool, nbytes=nbytes, copies=copies):
+                st = L.nh_stream_read(h, pool.ptr + (i % copies) * nbytes, nbytes, sink.ptr,
+                                      b.stream, ctypes.byref(err))
+                if st:
+                    NH.check(st, err)
+
+            t = b.time_ms(step, max(40, 4 * copies), 5)
+            res[f"{mib}MiB"] = {"us": round(t * 1e3, 2), "GBps": round(nbytes / (t * 1e-3) / 1e9, 1),
+                                "frac_hbm_peak": round(nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            pool.free()
+        print(json.dumps({"stream": res}), flush=True)
+        return
     if args.copy_probe:
         import torch
 

@@ -419,6 +419,16 @@ nh_status nh_load_linear_i8(nh_context *ctx, const char *path, const char *codes
                             size_t n, size_t k, void *staging, size_t staging_len, int8_t *tiled, size_t tiled_len,
                             float *scales, nh_error *err);
 
+/* ---- diagnostics ----------------------------------------------------------
+ * One read of `bytes` (a multiple of 16, < 2^31) from 16-byte aligned device
+ * memory, in the weight streams' load pattern (16-byte non-temporal loads,
+ * one contiguous KiB per wave instruction, 1024 workgroups of 256 threads):
+ * the HBM floor the bandwidth-bound kernels are compared with.  `sink` is
+ * 256 device ints, written only when the data's XOR is one magic value.  No
+ * counterpart in the reference. */
+nh_status nh_stream_read(nh_context *ctx, const void *src, size_t bytes, int32_t *sink, nh_stream stream,
+                         nh_error *err);
+
 /* ---- synthetic inputs (build-defined seeded generator; the reference has
  *      no RNG): splitmix64 -> Box-Muller (f64) -> f32 ------------------- */
 void nh_fill_normal_f32_host(uint64_t seed, float mean, float stddev, float *out, size_t n);

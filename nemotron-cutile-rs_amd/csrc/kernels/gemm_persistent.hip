@@ -2,7 +2,8 @@
 // tiles with 8 waves, each owning a (BM / WGM) x (BN / WGN) block of every
 // tile, all of them streaming both operands into LDS.  Used where its tile
 // fills whole rounds of CUs better than the loader-wave kernel of gemm.hip
-// (the 21504-wide up projection at M = 2048: 201-203 us against 231-236).
+// (the 21504-wide up projection at M = 2048: 162-164 us back to back against
+// 212-236 us for the loader-wave kernel).
 //
 //  * 64 x 112 wave tiles on a 256 x 224 tile read 98 B/clk of LDS per CU at
 //    the MFMA rate (the 64 x 64 tiles of gemm.hip: 128), and the tile needs

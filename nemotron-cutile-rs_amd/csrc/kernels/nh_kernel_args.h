@@ -106,6 +106,14 @@ struct GemvW8A32Args {
     int32_t slabs;        // ceil(ceil(kt / waves) / 4): slabs of 4 K tiles per wave
 };
 
+// Diagnostic read stream.
+struct StreamReadArgs {
+    const void* src;
+    int32_t* sink;        // [256], written only when the XOR of the data is a magic value
+    uint32_t bytes;       // < 2^31, a multiple of 16
+    uint32_t pad_;
+};
+
 // Row-major int8 [N][K] -> tiled, one 16-byte tile chunk per thread.
 // INT4 [K][N] packed codes (the reference's layout) -> tiled_int4.
 struct TileInt4Args {

@@ -253,6 +253,26 @@ extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_wave_kernel(Q
         quantize_row_wave<DT_F32, 8>(a);
 }
 
+// Diagnostic: one read of [src, src + bytes) in 16-byte non-temporal loads,
+// four per thread in flight, the contiguous KiB per wave instruction of the
+// weight streams; the XOR of everything read decides a store that never
+// happens for real data (it keeps the loads).  The floor the HBM-bound
+// kernels are compared with.
+extern "C" __global__ __launch_bounds__(256) void nh_stream_read_kernel(StreamReadArgs a) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(a.src, a.bytes);
+    const uint32_t per = gridDim.x * blockDim.x * 16u;  // bytes per round of one load per thread
+    const uint32_t base = blockIdx.x * blockDim.x * 16u + threadIdx.x * 16u;
+    int acc = 0;
+    for (uint32_t o = base; o < a.bytes; o += 4 * per) {
+        v4i v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = buffer_load16_stream(r, (int)(o + i * per < a.bytes ? o + i * per : kOutOfRange));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
+    }
+    if (acc == 0x5a17c0de) a.sink[threadIdx.x] = acc;
+}
+
 // INT4 [K][N] codes, low nibble first (the reference's packed layout) -> the
 // tiled INT4 layout (nh_numerics.h): thread c writes the 8 bytes of lane
 // c % 64 of tile c / 64, the zero point outside the matrix.  A one-off

@@ -1031,6 +1031,23 @@ nh_status nh_moe_layer_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, co
 
 }  // extern "C"
 
+// One read of bytes from src (device memory, 16-byte aligned, a multiple of
+// 16, < 2^31): 1024 workgroups of 256 threads, four 16-byte loads per thread
+// in flight.  sink: 256 device ints, normally never written.
+extern "C" nh_status nh_stream_read(nh_context* ctx, const void* src, size_t bytes, int32_t* sink, nh_stream stream,
+                                    nh_error* err) {
+    clear_error(err);
+    if (bytes == 0 || bytes % 16 != 0 || bytes >= (1ull << 31))
+        return set_error(err, NH_INVALID_SHAPE, "stream of %zu bytes: a multiple of 16 below 2^31", bytes);
+    if (!aligned16(src)) return set_error(err, NH_UNSUPPORTED, "src must be 16-byte aligned");
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    StreamReadArgs a{src, sink, (uint32_t)bytes, 0};
+    const size_t chunks = bytes / 16;
+    const unsigned grid = (unsigned)std::min<size_t>(1024, (chunks + 256 * 4 - 1) / (256 * 4));
+    return launch(ctx, K_STREAM_READ, grid, 256, 0, stream, a, err);
+}
+
 extern "C" nh_status nh_take_nonfinite(nh_context* ctx, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
     clear_error(err);
     if (!nonfinite) return set_error(err, NH_INVALID_PARAMS, "null non-finite word");

@@ -38,6 +38,7 @@ const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
     "nh_moe_expert_gemm_kernel",         // K_EXPERT_GEMM
     "nh_moe_expert_gemm_omax_kernel",    // K_EXPERT_GEMM_OMAX
     "nh_moe_expert_gemm_qa_kernel",      // K_EXPERT_GEMM_QA
+    "nh_stream_read_kernel",             // K_STREAM_READ
     "nh_quantize_rows_wave_kernel",      // K_QUANTIZE_ROWS_WAVE
     "nh_quantize_rows_long_kernel",      // K_QUANTIZE_ROWS_LONG
     "nh_tile_weights_int4_kernel",       // K_TILE_INT4

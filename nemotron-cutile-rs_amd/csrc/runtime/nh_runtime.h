@@ -40,6 +40,7 @@ enum KernelId : int {
     K_EXPERT_GEMM,         // grouped GEMM on slot-ordered A
     K_EXPERT_GEMM_OMAX,    // ... also writing per-row output maxima (MoE up projection)
     K_EXPERT_GEMM_QA,      // ... quantizing f32 A rows while staging them (MoE down projection)
+    K_STREAM_READ,         // diagnostic read stream
     K_QUANTIZE_ROWS_WAVE,  // row quantizer, one wave per row
     K_QUANTIZE_ROWS_LONG,  // row quantizer, 1024 threads per row
     K_TILE_INT4,           // INT4 [K][N] packed -> tiled INT4

@@ -1034,6 +1034,20 @@ extern "C" {
         err: *mut nh_error,
     ) -> nh_status;
 
+    /// diagnostics. One read of `bytes` (a multiple of 16, < 2^31) from 16-byte aligned device memory,
+    /// in the weight streams' load pattern (16-byte non-temporal loads, one contiguous KiB per wave
+    /// instruction, 1024 workgroups of 256 threads): the HBM floor the bandwidth-bound kernels are
+    /// compared with.  `sink` is 256 device ints, written only when the data's XOR is one magic value.
+    /// No counterpart in the reference.
+    pub fn nh_stream_read(
+        ctx: *mut nh_context,
+        src: *const c_void,
+        bytes: usize,
+        sink: *mut i32,
+        stream: nh_stream,
+        err: *mut nh_error,
+    ) -> nh_status;
+
     /// synthetic inputs (build-defined seeded generator; the reference has no RNG): splitmix64 ->
     /// Box-Muller (f64) -> f32
     pub fn nh_fill_normal_f32_host(seed: u64, mean: f32, stddev: f32, out: *mut f32, n: usize);
