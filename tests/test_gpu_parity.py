@@ -675,7 +675,7 @@ def test_moe_stages_bit_exact(ctx, tokens, hidden, inter, experts, top_k):
     assert np.array_equal(out.numpy(), O.moe_combine(d_ref, pos, w, tokens, top_k, hidden, out_bf16=True))
 
 
-@pytest.mark.parametrize("n,k", [(1856, 2688), (2688, 1856), (40, 64)])
+@pytest.mark.parametrize("n,k", [(1856, 2688), (2688, 1856), (40, 64), (256, 64), (160, 512)])
 def test_expert_gemm_long_segments_bit_exact(ctx, n, k):
     """Slot-ordered grouped GEMM (the MoE layer's expert-block kernel) with
     segments around every pass boundary: a pass stages 48 rows at K = 2688,
@@ -727,7 +727,8 @@ def test_moe_forward_shared_expert_bit_exact(ctx, tokens, hidden, inter, experts
 
 
 @pytest.mark.parametrize("tokens,hidden,inter,experts,top_k", [(64, 2688, 1856, 128, 6), (13, 64, 32, 8, 3),
-                                                                (256, 64, 32, 16, 6)])
+                                                                (256, 64, 32, 16, 6), (40, 256, 160, 8, 3),
+                                                                (24, 512, 256, 4, 2)])
 def test_moe_forward_bit_exact(ctx, tokens, hidden, inter, experts, top_k):
     note(f"moe forward t={tokens} h={hidden} i={inter} e={experts} k={top_k}")
     x, logits, up, su, down, sd = moe_case(tokens, hidden, inter, experts, top_k)
@@ -990,6 +991,19 @@ def test_mlp_nonfinite_intermediate_and_input_reported(ctx):
     xb[1, 17] = O.to_bf16(np.array([np.nan], dtype=np.float32))[0]
     st, err = run(ctx.upload(xb))
     assert st == NH.NON_FINITE_INPUT and err.argument == b"input" and err.index == hidden + 17
+
+
+def test_stream_read_diagnostic_reads_and_leaves_the_sink(ctx):
+    """nh_stream_read over a buffer of ones: returns OK, writes nothing
+    (the data's XOR is not the magic value), rejects unaligned sizes."""
+    note("stream read diagnostic")
+    src = ctx.upload(np.ones(1 << 22, dtype=np.int32))
+    sink = ctx.upload(np.zeros(256, dtype=np.int32))
+    NH.call("nh_stream_read", ctx.handle, src.ptr, 16 << 20, sink.ptr, None)
+    ctx.synchronize()
+    assert not sink.numpy().any()
+    err = NH.NhError()
+    assert NH.lib().nh_stream_read(ctx.handle, src.ptr, 17, sink.ptr, None, ctypes.byref(err)) == NH.INVALID_SHAPE
 
 
 def test_moe_nonfinite_intermediate_reported(ctx):
