@@ -90,16 +90,17 @@ __device__ __forceinline__ void report_decode_rows(const LinearDecodeArgs& a, co
         report_nonfinite(a.nonfinite, 0, first, bf16_to_f32(((const uint16_t*)a.x)[first]));
 }
 
-// The same for the wide decode unit: xv[j] holds chunk j T + threadIdx.x of
+// The same for the wide decode units: xv[j] holds chunk c0 + j stride of
 // the row-major [M][K] input, i.e. the values at flat index 8 chunk + e.
 template <int XR>
-__device__ __forceinline__ void report_decode_chunks(const LinearDecodeArgs& a, const v4i (&xv)[XR], int T) {
+__device__ __forceinline__ void report_decode_chunks(const LinearDecodeArgs& a, const v4i (&xv)[XR], int c0,
+                                                     int stride) {
     __shared__ int red_nf[16];
     int first = 0x7fffffff;
     const int chunks = a.M * (a.K >> 3);
 #pragma unroll
     for (int j = 0; j < XR; ++j) {
-        const int c = j * T + (int)threadIdx.x;
+        const int c = c0 + j * stride;
         const int e = bf16x8_first_nonfinite(xv[j]);
         if (c < chunks && e < 8) first = min(first, c * 8 + e);
     }
@@ -424,7 +425,7 @@ __device__ __forceinline__ void linear_decode_wide(const LinearDecodeArgs& a, in
     if (blockIdx.x == 0 && a.nonfinite) {
         bool nonfinite = false;
         for (int r = 0; r < M; ++r) nonfinite |= (uint32_t)rowmax[r] >= 0x7f800000u;
-        if (nonfinite) report_decode_chunks<XR>(a, xv, T);
+        if (nonfinite) report_decode_chunks<XR>(a, xv, (int)threadIdx.x, T);
     }
     // codes into LDS: chunk c = 8 values of row c / cpr at k = 8 (c % cpr)
 #pragma unroll
@@ -478,6 +479,179 @@ __device__ __forceinline__ void linear_decode_wide(const LinearDecodeArgs& a, in
     }
 }
 
+// Streaming decode unit: up to MM bf16 rows, any N.  Each of G workgroups
+// (16 waves, G <= the CU count) owns a contiguous run of N tiles (runs differ
+// by at most one tile) and quantizes the activations once for all of them:
+//  1. every thread loads its XR chunks of 8 activations (a wave's 64 XR
+//     chunks are consecutive, so each of its 64-chunk groups lies in one
+//     row), the weight scale and bias of one column of the run, then the
+//     first NB rounds of weights: wave w takes K tiles [w KS, w KS + KS) of
+//     the round's N tile;
+//  2. it waits for the activations only, takes each row's absmax (one DPP
+//     wave maximum per row the wave holds, one LDS max), derives the row
+//     scales in lanes 0..MM-1 (two divisions per wave), writes the codes into
+//     LDS in the A operand order [KT][4][MM][16] and moves the A operands of
+//     its K tiles into registers;
+//  3. per N tile of the run (a round): KS MFMAs on the landed weights, the
+//     partial tile into LDS, the loads of the round two ahead, one barrier,
+//     then 16 MM threads sum the 16 partials (int32: exact in any order) and
+//     apply the epilogue.  NB rounds of weights stay in flight, under which
+//     the quantizer runs: ~6 VALU per value, after activation loads that
+//     wait behind the other CUs' weight reads in L2 (2-4 us at 64 KiB per
+//     CU, 1.7 us with no weight traffic).
+// Every load is unconditional (rounds past the run and K tiles past kt read
+// out of range: zeros, no memory traffic), so each wait is a fixed count.
+// Codes and scales are bit-identical to quantize_i8 (quantize8_bf16).
+template <int MM, int XR, int KS, int NB>
+__device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, int8_t* lds) {
+    constexpr int NW = 16;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tid = threadIdx.x;
+    const int M = a.M, N = a.N, K = a.K, kt = a.kt;
+    const int cpr = K >> 3;  // 16-byte chunks per row
+    const int tiles = (N + 15) >> 4;
+    const int G = gridDim.x;
+    const int t0 = (int)(((int64_t)blockIdx.x * tiles) / G);
+    const int ntl = (int)(((int64_t)(blockIdx.x + 1) * tiles) / G) - t0;
+    const int r16 = lane & 15, g = lane >> 4;
+    int8_t* xs = lds;                          // codes, kt * 64 * MM bytes
+    v4i* red = (v4i*)(lds + kt * 64 * MM);     // [2][NW][64] partial tiles
+    float* swl = (float*)(red + 2 * NW * 64);  // [1024] weight scales of the run
+    float* bl = swl + 1024;                    // [1024] bias of the run
+    int* rowmax = (int*)(bl + 1024);           // [MM] row absmax (f32 bits)
+    float* srow = (float*)(rowmax + MM);       // [MM] row scales
+    if (tid < MM) rowmax[tid] = 0;
+
+    // 1. activations, epilogue operands, the first PRE rounds of weights
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)M * (uint32_t)K * 2u);
+    const int cbase = wave * XR * 64;  // the wave's first chunk
+    v4i xv[XR];
+    v4i b0[KS], b1[KS], b2[KS];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+        const int c = cbase + j * 64 + lane;
+        xv[j] = buffer_load16(xrs, c < M * cpr ? c * 16 : kOutOfRange);
+    }
+    const uint32_t run_bytes = (uint32_t)min(ntl * 16, N - t0 * 16) * 4u;
+    const float swv = f32_from_bits(
+        (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.sw + t0 * 16, run_bytes), tid * 4, 0, 0));
+    const float bv = f32_from_bits((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+        make_rsrc(a.bias ? a.bias + t0 * 16 : a.sw, a.bias ? run_bytes : 0u), tid * 4, 0, 0));
+    auto issue = [&](v4i (&b)[KS], int r) {
+        const bool in_run = r < ntl;
+        const __amdgpu_buffer_rsrc_t wr =
+            make_rsrc(a.wq + (int64_t)(t0 + (in_run ? r : 0)) * kt * 1024, in_run ? (uint32_t)kt * 1024u : 0u);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) b[s] = buffer_load16_stream(wr, (wave * KS + s) * 1024 + lane * 16);
+    };
+    issue(b0, 0);
+    issue(b1, 1);
+    if (NB > 2) issue(b2, 2);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. activations in (weights in flight): row absmax, one reduction per
+    //    row the wave holds (rows change only where a 64-chunk group starts)
+    wait_vmcnt_le(2 + NB * KS);
+    lds_publish();  // rowmax zeroed
+    {
+        uint32_t m = 0;
+        int cur = cbase / cpr;
+#pragma unroll
+        for (int j = 0; j < XR; ++j) {
+            const int c0 = cbase + j * 64;  // uniform
+            if (c0 < M * cpr) {
+                const int row = c0 / cpr;
+                if (row != cur) {
+                    const uint32_t mb = wave_max_dpp_u32(m);
+                    if (lane == 0) atomicMax(&rowmax[cur], (int)(mb << 16));
+                    m = 0;
+                    cur = row;
+                }
+                // the largest magnitude as the bits of the widened bf16
+                // (non-negative: int order = value order, non-finite on top)
+                m = max(m, bf16x8_absmax_bits(xv[j]));
+            }
+        }
+        if (cbase < M * cpr) {
+            const uint32_t mb = wave_max_dpp_u32(m);
+            if (lane == 0) atomicMax(&rowmax[cur], (int)(mb << 16));
+        }
+    }
+    wait_vmcnt_le(NB * KS);  // weight scales and bias in
+    swl[tid] = swv;
+    bl[tid] = bv;
+    lds_publish();  // row maxima complete
+    // row scales in lanes 0..MM-1 of every wave
+    const float sx_l = scale_from_amax(f32_from_bits((uint32_t)rowmax[lane < MM ? lane : 0]));
+    const float rcp_l = 1.0f / sx_l;
+    if (wave == 0 && lane < MM) srow[lane] = sx_l;
+    if (blockIdx.x == 0 && a.nonfinite) {
+        bool nonfinite = false;
+        for (int r = 0; r < M; ++r) nonfinite |= (uint32_t)rowmax[r] >= 0x7f800000u;
+        if (nonfinite) report_decode_chunks<XR>(a, xv, cbase + lane, 64);
+    }
+    // codes into LDS: chunk c = 8 values of row c / cpr at k = 8 (c % cpr)
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+        const int c0 = cbase + j * 64;
+        if (c0 < M * cpr) {
+            const int row = c0 / cpr;
+            const float sx = f32_from_bits((uint32_t)__builtin_amdgcn_readlane((int)f32_bits(sx_l), row));
+            const float rcp = f32_from_bits((uint32_t)__builtin_amdgcn_readlane((int)f32_bits(rcp_l), row));
+            uint32_t code[2];
+            quantize8_bf16(xv[j], sx, rcp, scale_is_pow2(sx), code);
+            const int k = (c0 + lane - row * cpr) * 8;
+            *(uint2*)(xs + (((k >> 6) * 4 + ((k >> 4) & 3)) * MM + row) * 16 + (k & 15)) = make_uint2(code[0], code[1]);
+            if (blockIdx.x == 0 && a.xq_out) *(uint2*)(a.xq_out + (int64_t)row * K + k) = make_uint2(code[0], code[1]);
+        }
+    }
+    if (blockIdx.x == 0 && a.sx_out && tid < M) a.sx_out[tid] = sx_l;
+    lds_publish();  // codes and row scales complete
+
+    // A operands of the wave's K tiles (lanes of rows >= MM read row 0:
+    // their outputs are discarded; K tiles past kt meet zero weights)
+    const int arow = r16 < MM ? r16 : 0;
+    v4i xa[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        const int t = wave * KS + s;
+        xa[s] = *(const v4i*)(xs + (((t < kt ? t : 0) * 4 + g) * MM + arow) * 16);
+    }
+    // the epilogue output of thread tid < 16 MM: row tid / 16, column tid % 16
+    const int em = tid >> 4, en = tid & 15;
+    const float sxe = srow[em < MM ? em : 0];
+    auto round = [&](v4i (&b)[KS], int r) {
+        const int buf = r & 1;
+        wait_vmcnt_le((NB - 1) * KS);  // this round's weights in, the next NB - 1 rounds' in flight
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[s], b[s], acc, 0, 0, 0);
+        red[(buf * NW + wave) * 64 + lane] = acc;
+        issue(b, r + NB);
+        lds_publish();
+        if (tid < 16 * MM && r < ntl) {
+            const int n = (t0 + r) * 16 + en;
+            if (em < M && n < N) {
+                // C[m][n] sits in element m % 4 of lane 16 (m / 4) + n % 16
+                const int32_t* rp = (const int32_t*)(red + buf * NW * 64) + (16 * (em >> 2) + en) * 4 + (em & 3);
+                int32_t sum = 0;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) sum += rp[w * 64 * 4];
+                store_y(a.out, a.out_dtype, (int64_t)em * N + n, sum, sxe, swl[r * 16 + en], a.bias,
+                        bl[r * 16 + en], a.relu2);
+            }
+        }
+    };
+    for (int r = 0; r < ntl; r += NB) {
+        round(b0, r);
+        round(b1, r + 1);
+        if (NB > 2) round(b2, r + 2);
+    }
+    wait_vmcnt_le(0);
+}
+
 extern "C" __global__ __launch_bounds__(512) void nh_linear_decode_w8a8_m1_kernel(LinearDecodeArgs a) {
     extern __shared__ __align__(16) int8_t xs[];  // [W * 1024 + 16] codes
     linear_decode_row<1>(a, xs);
@@ -526,6 +700,14 @@ extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_w8a8_kernel(
 extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_w8a8_m8_kernel(LinearDecodeArgs a) {
     extern __shared__ __align__(16) int8_t lds[];
     linear_decode_wide<8, 8, 8>(a, lds);
+}
+
+// The streaming unit for 5..8 rows, K <= 4096 (4 K tiles per wave), two
+// rounds of weights in flight (three: 16.9 vs 15.6 us at 4096 -> 16384, the
+// extra weight reads queue ahead of the activations' in L2).
+extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_stream_m8_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t lds[];
+    linear_decode_stream<8, 4, 4, 2>(a, lds);
 }
 
 // G2: W8A32 dequant GEMV, y[m][n] = sum_k x[m][k] * q[n][k] * s[n].  The

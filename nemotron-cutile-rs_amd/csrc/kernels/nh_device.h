@@ -80,6 +80,21 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return v;
 }
 
+// The same maximum through DPP lane moves (no LDS round trips): within rows
+// of 16 lanes by quad permutes and row rotates, then across rows by the
+// row broadcasts of lanes 15 and 31; lane 63 ends with the wave's maximum,
+// which readlane hands to every lane.  Lanes a DPP move leaves out keep
+// their own value, which a maximum absorbs.
+__device__ __forceinline__ uint32_t wave_max_dpp_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xb1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4e, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x124, 0xf, 0xf, false));  // row_ror 4
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x128, 0xf, 0xf, false));  // row_ror 8
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xa, 0xf, false));  // row_bcast 15
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xc, 0xf, false));  // row_bcast 31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // NonFiniteInput (quantize.rs:193-195: the first offending element and its
 // value) from the device quantizers.  The key (stage << 63 | flat index << 32
 // | f32 bits of the value) goes into the caller's 64-bit word as its
@@ -192,24 +207,20 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 
 // s_waitcnt vmcnt(<= n) with the other counters left alone (gfx9 encoding:
 // vmcnt[3:0] | expcnt[6:4] = 7 | lgkmcnt[11:8] = 15 | vmcnt[5:4] << 14).
-// The wait is an immediate, hence the switch over the counts in use.
+// The wait is an immediate, hence the switch over every count (0..63).
 __device__ __forceinline__ void wait_vmcnt_le(int n) {
 #define NH_VMCNT(n) ((((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14)))
+#define NH_VMCNT_CASE(n) \
+    case n: __builtin_amdgcn_s_waitcnt(NH_VMCNT(n)); break;
+#define NH_VMCNT_CASE8(n) NH_VMCNT_CASE(n) NH_VMCNT_CASE(n + 1) NH_VMCNT_CASE(n + 2) NH_VMCNT_CASE(n + 3) \
+    NH_VMCNT_CASE(n + 4) NH_VMCNT_CASE(n + 5) NH_VMCNT_CASE(n + 6) NH_VMCNT_CASE(n + 7)
     switch (n) {
-        case 0: __builtin_amdgcn_s_waitcnt(NH_VMCNT(0)); break;
-        case 1: __builtin_amdgcn_s_waitcnt(NH_VMCNT(1)); break;
-        case 2: __builtin_amdgcn_s_waitcnt(NH_VMCNT(2)); break;
-        case 3: __builtin_amdgcn_s_waitcnt(NH_VMCNT(3)); break;
-        case 4: __builtin_amdgcn_s_waitcnt(NH_VMCNT(4)); break;
-        case 6: __builtin_amdgcn_s_waitcnt(NH_VMCNT(6)); break;
-        case 8: __builtin_amdgcn_s_waitcnt(NH_VMCNT(8)); break;
-        case 9: __builtin_amdgcn_s_waitcnt(NH_VMCNT(9)); break;
-        case 12: __builtin_amdgcn_s_waitcnt(NH_VMCNT(12)); break;
-        case 16: __builtin_amdgcn_s_waitcnt(NH_VMCNT(16)); break;
-        case 18: __builtin_amdgcn_s_waitcnt(NH_VMCNT(18)); break;
-        case 24: __builtin_amdgcn_s_waitcnt(NH_VMCNT(24)); break;
+        NH_VMCNT_CASE8(0) NH_VMCNT_CASE8(8) NH_VMCNT_CASE8(16) NH_VMCNT_CASE8(24)
+        NH_VMCNT_CASE8(32) NH_VMCNT_CASE8(40) NH_VMCNT_CASE8(48) NH_VMCNT_CASE8(56)
         default: __builtin_amdgcn_s_waitcnt(NH_VMCNT(0)); break;
     }
+#undef NH_VMCNT_CASE8
+#undef NH_VMCNT_CASE
 #undef NH_VMCNT
 }
 

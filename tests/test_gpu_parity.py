@@ -316,6 +316,11 @@ def test_linear_decode_unit_bit_exact(ctx, m, n, k):
                                          (3, 4096, 8192, "bf16"), (2, 1000, 4112, "bf16"), (7, 4096, 8192, "bf16"),
                                          (6, 6144, 4096, "bf16"), (17, 300, 4160, "bf16"), (100, 2688, 1856, "f32"),
                                          (257, 1024, 4096, "bf16"),
+                                         # the streaming decode unit (5..8 rows): a ragged last N tile
+                                         # in runs of 5 and 6 tiles, fewer N tiles than CUs, K = 512
+                                         # (most waves past kt), K = 6144 on the 8-tile form, 17 rounds
+                                         (8, 21512, 4096, "bf16"), (8, 100, 4096, "bf16"), (5, 4000, 512, "bf16"),
+                                         (8, 3000, 6144, "bf16"), (6, 65544, 512, "bf16"),
                                          # the persistent 256 x 224 GEMM with a bias and f32 out
                                          (1000, 14236, 384, "bf16"), (1024, 14336, 256, "f32")])
 def test_linear_small_m_shapes_bit_exact(ctx, m, n, k, dtype):
@@ -325,7 +330,8 @@ def test_linear_small_m_shapes_bit_exact(ctx, m, n, k, dtype):
     (K = 4112, 4160: the activation tiles hold stale bytes there and meet
     zero weight padding), N not a multiple of 16, f32 activations, the
     one-tile-per-workgroup decode kernels for 2..4 rows (K = 8192 or
-    K % 512 != 0) and the wide one at N = 6144."""
+    K % 512 != 0) and the streaming one for 5..8 rows (runs of N tiles per
+    workgroup, odd and even run lengths, a ragged last tile)."""
     note(f"linear_w8a8 m={m} n={n} k={k} {dtype}")
     _, wq, sw = quantized_weights(n, k)
     bias = O.normal_f32(3, n, 0.0, 0.1)
@@ -397,7 +403,7 @@ def test_mlp_bit_exact(ctx, m, hidden, inter, dtype):
     assert np.array_equal(out.numpy(), ref)
 
 
-@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("m", [1, 3, 7])
 def test_linear_decode_unit_rounding_ties(ctx, m):
     """Rows whose scale is a power of two carry exact half-integer quotients
     (x/s = j + 0.5): round-half-away-from-zero and round-half-even disagree on
@@ -922,7 +928,8 @@ def take_nonfinite(ctx, word):
 
 @pytest.mark.parametrize("m,n,k,dtype", [(1, 4096, 4096, "bf16"),    # fused one-row unit
                                          (3, 4096, 8192, "bf16"),    # fused 4-row unit, one N tile per workgroup
-                                         (6, 16384, 4096, "bf16"),   # fused wide unit
+                                         (6, 16384, 4096, "bf16"),   # fused streaming unit
+                                         (8, 4096, 8192, "bf16"),    # streaming unit, 8 K tiles per wave
                                          (12, 1024, 4096, "bf16"),   # quantizer into activation tiles + GEMV
                                          (2, 1024, 4096, "f32"),     # f32 rows: the row quantizer
                                          (40, 512, 1024, "bf16")])   # quantizer into A tiles + GEMM
