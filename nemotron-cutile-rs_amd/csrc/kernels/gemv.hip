@@ -499,6 +499,9 @@ __device__ __forceinline__ void linear_decode_wide(const LinearDecodeArgs& a, in
 //     the quantizer runs: ~6 VALU per value, after activation loads that
 //     wait behind the other CUs' weight reads in L2 (2-4 us at 64 KiB per
 //     CU, 1.7 us with no weight traffic).
+// With row_max (f32 out), each workgroup also leaves the largest finite |y|
+// of its outputs per row, from which a consumer derives the rows' scales
+// without another pass over y (the MLP's intermediate).
 // Every load is unconditional (rounds past the run and K tiles past kt read
 // out of range: zeros, no memory traffic), so each wait is a fixed count.
 // Codes and scales are bit-identical to quantize_i8 (quantize8_bf16).
@@ -622,6 +625,7 @@ __device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, 
     // the epilogue output of thread tid < 16 MM: row tid / 16, column tid % 16
     const int em = tid >> 4, en = tid & 15;
     const float sxe = srow[em < MM ? em : 0];
+    uint32_t ymax = 0;  // largest finite |y| of the thread's outputs (f32 bits)
     auto round = [&](v4i (&b)[KS], int r) {
         const int buf = r & 1;
         wait_vmcnt_le((NB - 1) * KS);  // this round's weights in, the next NB - 1 rounds' in flight
@@ -639,8 +643,12 @@ __device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, 
                 int32_t sum = 0;
 #pragma unroll
                 for (int w = 0; w < NW; ++w) sum += rp[w * 64 * 4];
-                store_y(a.out, a.out_dtype, (int64_t)em * N + n, sum, sxe, swl[r * 16 + en], a.bias,
-                        bl[r * 16 + en], a.relu2);
+                // store_y's steps, keeping y for the row maxima
+                float y = epilogue_w8a8(sum, sxe, swl[r * 16 + en]);
+                if (a.bias) y = y + bl[r * 16 + en];
+                if (a.relu2) y = relu2(y);
+                store_out(a.out, (int64_t)em * N + n, y, a.out_dtype);
+                if (is_finite_f32(y)) ymax = max(ymax, f32_bits(y) & 0x7fffffffu);
             }
         }
     };
@@ -648,6 +656,11 @@ __device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, 
         round(b0, r);
         round(b1, r + 1);
         if (NB > 2) round(b2, r + 2);
+    }
+    // the workgroup's row maxima: the 16 threads of a row are one DPP row
+    if (a.row_max && tid < 16 * MM) {
+        ymax = row16_max_u32(ymax);
+        if (en == 0 && em < M) a.row_max[(int64_t)blockIdx.x * M + em] = ymax;
     }
     wait_vmcnt_le(0);
 }

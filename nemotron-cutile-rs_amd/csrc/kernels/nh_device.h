@@ -95,6 +95,15 @@ __device__ __forceinline__ uint32_t wave_max_dpp_u32(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
+// Maximum over each row of 16 lanes (every lane of the row gets it).
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x128, 0xf, 0xf, false));  // row_ror 8
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x124, 0xf, 0xf, false));  // row_ror 4
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x122, 0xf, 0xf, false));  // row_ror 2
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x121, 0xf, 0xf, false));  // row_ror 1
+    return v;
+}
+
 // NonFiniteInput (quantize.rs:193-195: the first offending element and its
 // value) from the device quantizers.  The key (stage << 63 | flat index << 32
 // | f32 bits of the value) goes into the caller's 64-bit word as its

@@ -31,6 +31,20 @@ struct QuantizeRowsArgs {
     int32_t pad_;
 };
 
+// Q2 of f32 rows whose absolute maxima a producer left as per-workgroup
+// partial maxima (LinearDecodeArgs::row_max): codes into the A-operand tiles
+// [KT][4][rows][16] of the M <= 16 GEMV.  grid = (slices of 256 four-value
+// chunks, rows).
+struct QuantizePmaxArgs {
+    const float* x;          // [rows][cols], 16-byte aligned rows, cols % 4 == 0
+    const uint32_t* pmax;    // [groups][rows] f32 bits of finite |x| maxima
+    int8_t* q_act;           // A-operand tiles
+    float* scales;           // [rows]
+    uint64_t* nonfinite;     // or null
+    int32_t rows, cols, groups;
+    int32_t nonfinite_stage;
+};
+
 // Q3: out[r][c] = (float)q[r][c] * scales[r]
 struct DequantizeI8Args {
     const int8_t* q;
@@ -92,6 +106,8 @@ struct LinearDecodeArgs {
     float w4_scale;       //   and scale, used in place of sw
     int32_t pad_;
     uint64_t* nonfinite;  // or null: the first non-finite activation (report_nonfinite, nh_device.h)
+    uint32_t* row_max;    // or null (streaming unit, f32 out): [gridDim.x][M] largest finite |y| of the
+                          // workgroup's outputs per row, as f32 bits (each workgroup writes its own slots)
 };
 
 // G2: W8A32 dequant GEMV; grid = (N tiles, ceil(M / rows per workgroup)).

@@ -244,6 +244,42 @@ extern "C" __global__ __launch_bounds__(1024) void nh_quantize_rows_long_kernel(
         quantize_row_vec<DT_F32, 8>(a, redf, redi);
 }
 
+// Q2 of f32 rows whose finite absolute maxima a producer already reduced
+// per workgroup (the streaming decode unit's row_max): every wave takes the
+// row's maximum over the `groups` partial maxima (max is exact in any order,
+// so the scale is quantize_rows' scale), then each thread quantizes one
+// 16-byte chunk into the A-operand tiles.  No block-wide reduction, so a row
+// spreads over many workgroups: grid = (ceil(cols / 1024), rows), 256
+// threads.  Non-finite values are reported as by the row quantizer (the
+// smallest flat index wins).
+extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_pmax_kernel(QuantizePmaxArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.y;
+    uint32_t m = 0;
+    for (int g = lane; g < a.groups; g += 64) m = max(m, a.pmax[(int64_t)g * a.rows + row]);
+    m = wave_max_dpp_u32(m);
+    const float s = scale_from_amax(f32_from_bits(m));
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.scales[row] = s;
+    const float rcp = s > 0.0f ? 1.0f / s : 0.0f;
+    const bool pow2 = scale_is_pow2(s);
+    const int chunks = a.cols >> 2;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= chunks) return;
+    const v4i v = __builtin_bit_cast(v4i, *(const int4*)(a.x + (int64_t)row * a.cols + c * 4));
+    if (a.nonfinite) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float f = f32_from_bits((uint32_t)v[j]);
+            if (!is_finite_f32(f)) {
+                report_nonfinite(a.nonfinite, a.nonfinite_stage, (int64_t)row * a.cols + c * 4 + j, f);
+                break;
+            }
+        }
+    }
+    const int64_t kt = (a.cols + 63) / 64;
+    *(uint32_t*)(a.q_act + act_tile_offset(row, c * 4, a.rows, kt)) = quantize4_f32(v, s, rcp, pow2);
+}
+
 // Q1/Q2 for vector-path rows of up to 512 16-byte chunks (4096 bf16 / 2048
 // f32 values): one wave per row (quantize_row_wave), grid = ceil(rows / 4).
 extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_wave_kernel(QuantizeRowsArgs a) {

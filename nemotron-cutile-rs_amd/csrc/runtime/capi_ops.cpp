@@ -508,7 +508,8 @@ namespace {
 nh_status linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* wq, const float* sw,
                       const float* bias, size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype,
                       void* workspace, size_t workspace_bytes, int8_t* xq_out, float* sx_out, int relu2,
-                      uint64_t* nonfinite, int nonfinite_stage, nh_stream stream, nh_error* err) {
+                      uint64_t* nonfinite, int nonfinite_stage, nh_stream stream, nh_error* err,
+                      uint32_t* row_max = nullptr) {
     nh_status st;
     // bf16 rows: the fused decode unit when it fits (one launch, no workspace)
     DecodePlan plan;
@@ -534,6 +535,7 @@ nh_status linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const in
         a.ntw = plan.ntw;
         a.relu2 = relu2;
         a.nonfinite = nonfinite;  // the fused unit reads the caller's input only (stage 0)
+        a.row_max = streaming ? row_max : nullptr;
         const size_t tiles = (n + 15) / 16;
         if (!streaming) grid = (unsigned)((tiles + plan.ntw - 1) / plan.ntw);
         return launch(ctx, plan.kid, grid, (unsigned)plan.threads, plan.lds, stream, a, err);
@@ -585,10 +587,15 @@ nh_status nh_linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
                        sx_out, 0, nonfinite, 0, stream, err);
 }
 
+// The MLP's workspace: the f32 intermediate h, the up projection's
+// per-workgroup row maxima of h (streaming unit: at most kMaxStreamGroups
+// workgroups x 8 rows), then the linear workspace of either projection.
+constexpr size_t kMaxStreamGroups = 1024;
+
 size_t nh_mlp_w8a8_workspace_size(size_t m, size_t hidden, size_t inter) {
     if (m == 0 || hidden == 0 || inter == 0 || m > (1ull << 31) || inter > (1ull << 31)) return 0;
     const size_t a = nh_linear_w8a8_workspace_size(m, hidden), b = nh_linear_w8a8_workspace_size(m, inter);
-    return align256(m * inter * sizeof(float)) + (a > b ? a : b);
+    return align256(m * inter * sizeof(float)) + align256(kMaxStreamGroups * 8 * sizeof(uint32_t)) + (a > b ? a : b);
 }
 
 nh_status nh_mlp_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* w_up, const float* s_up,
@@ -612,8 +619,29 @@ nh_status nh_mlp_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const in
     // h = ReLU^2(x W_up^T + b_up) in f32 (the reference's intermediate), then
     // out = h W_down^T + b_down with h quantized per row
     float* h = (float*)workspace;
-    void* lin_ws = (char*)workspace + align256(m * inter * sizeof(float));
-    const size_t lin_bytes = workspace_bytes - align256(m * inter * sizeof(float));
+    uint32_t* hmax = (uint32_t*)((char*)workspace + align256(m * inter * sizeof(float)));
+    void* lin_ws = (char*)hmax + align256(kMaxStreamGroups * 8 * sizeof(uint32_t));
+    const size_t lin_bytes = workspace_bytes - (size_t)((char*)lin_ws - (char*)workspace);
+    DecodePlan plan;
+    unsigned groups = 0;
+    if (x_dtype == NH_BF16 && aligned16(x) && inter % 4 == 0 && plan_stream(ctx, m, inter, hidden, &plan, &groups) &&
+        groups <= kMaxStreamGroups) {
+        // 5..8 rows: the streaming unit leaves each workgroup's row maxima of
+        // h, so h's quantizer needs no reduction pass over the 4 * inter-byte
+        // rows and spreads each row over many workgroups (K = 21504: 8.9 us
+        // as one workgroup per row)
+        if ((st = linear_w8a8(ctx, x, x_dtype, w_up, s_up, b_up, m, inter, hidden, h, NH_F32, lin_ws, lin_bytes,
+                              nullptr, nullptr, 1, nonfinite, 0, stream, err, hmax)))
+            return st;
+        int8_t* tiles = (int8_t*)lin_ws;
+        float* sh = (float*)((char*)lin_ws + align256(act_tiles_bytes(m, inter)));
+        QuantizePmaxArgs q{h, hmax, tiles, sh, nonfinite, (int)m, (int)inter, (int)groups, 1};
+        if ((st = launch(ctx, K_QUANTIZE_ROWS_PMAX, (unsigned)((inter / 4 + 255) / 256), 256, 0, stream, q, err,
+                         (unsigned)m)))
+            return st;
+        return launch_gemv(ctx, tiles, sh, w_down, s_down, b_down, (int)m, (int)hidden, (int)inter, out, out_dtype,
+                           true, stream, err);
+    }
     if ((st = linear_w8a8(ctx, x, x_dtype, w_up, s_up, b_up, m, inter, hidden, h, NH_F32, lin_ws, lin_bytes, nullptr,
                           nullptr, 1, nonfinite, 0, stream, err)))
         return st;

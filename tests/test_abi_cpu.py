@@ -69,8 +69,9 @@ def test_mlp_validates_like_mlp_layer_before_touching_a_device():
     assert mlp(0, 64, 64, None, 0)[0] == NH.INVALID_ROW_COUNT
     assert mlp(2, 64, 40, None, 0)[0] == NH.UNSUPPORTED  # inter % 16 != 0: the host path's job
     need = NH.lib().nh_mlp_w8a8_workspace_size(8, 4096, 21504)
-    # h (f32 [8][21504]) + the larger projection workspace (activation tiles + scales)
-    assert need == 8 * 21504 * 4 + (8 * 21504 + 255) // 256 * 256 + 256
+    # h (f32 [8][21504]) + the up projection's per-workgroup row maxima (1024
+    # workgroups x 8 rows) + the larger projection workspace (activation tiles + scales)
+    assert need == 8 * 21504 * 4 + 1024 * 8 * 4 + (8 * 21504 + 255) // 256 * 256 + 256
     st, err = mlp(8, 4096, 21504, None, need - 1)
     assert st == NH.LENGTH_MISMATCH and err.argument == b"workspace" and (err.expected, err.actual) == (need, need - 1)
     assert NH.lib().nh_mlp_w8a8_workspace_size(0, 4096, 21504) == 0

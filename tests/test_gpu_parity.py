@@ -379,6 +379,10 @@ def mlp_weights(hidden, inter):
 
 @pytest.mark.parametrize("m,hidden,inter,dtype", [(8, 4096, 21504, "bf16"), (1, 4096, 21504, "bf16"),
                                                   (37, 1024, 2560, "bf16"), (5, 512, 1856, "f32"),
+                                                  # the streaming up projection's row maxima feeding h's
+                                                  # quantizer: a last K tile partly past inter = 1872, one
+                                                  # N tile per workgroup
+                                                  (6, 512, 1872, "bf16"), (7, 1024, 4096, "bf16"),
                                                   # the up projection (bias, ReLU^2, f32 out) on the persistent GEMM
                                                   (1024, 512, 14336, "bf16")])
 def test_mlp_bit_exact(ctx, m, hidden, inter, dtype):
@@ -969,12 +973,14 @@ def test_linear_nonfinite_input_reported(ctx, m, n, k, dtype):
     assert np.array_equal(word.numpy(), np.zeros(1, dtype=np.uint64))
 
 
-def test_mlp_nonfinite_intermediate_and_input_reported(ctx):
+@pytest.mark.parametrize("m", [2, 6])
+def test_mlp_nonfinite_intermediate_and_input_reported(ctx, m):
     """The MLP's f32 intermediate overflows (ReLU^2 of a 3e38 biased output is
     +inf): reported as "intermediate" at its row-major index; a NaN in x takes
-    precedence as "input"."""
-    m, hidden, inter = 2, 512, 1024
-    note("mlp nonfinite")
+    precedence as "input".  m = 6: the intermediate's quantizer works from the
+    up projection's per-workgroup row maxima."""
+    hidden, inter = 512, 1024
+    note(f"mlp nonfinite m={m}")
     w_up, s_up, w_down, s_down = mlp_weights(hidden, inter)
     b_up = np.zeros(inter, dtype=np.float32)
     b_up[3] = 3e38
