@@ -174,7 +174,7 @@ class Bench:
 
         def step(i):
             st = L.nh_linear_w4a8(h, x.ptr, NH.BF16, pool[i % len(pool)].ptr, 0.01, 8, None, m, n, k, out.ptr,
-                                  NH.BF16, None, self.stream, ctypes.byref(err))
+                                  NH.BF16, None, 0, None, self.stream, ctypes.byref(err))
             if st:
                 NH.check(st, err)
 

@@ -373,17 +373,26 @@ nh_status nh_tile_weights_int4(nh_context *ctx, const uint8_t *packed, size_t pa
                                nh_error *err);
 nh_status nh_tile_weights_int4_host(const uint8_t *packed, size_t packed_len, size_t k, size_t n,
                                     uint32_t zero_point, uint8_t *tiled, size_t tiled_len, nh_error *err);
-/* W4A8 linear: per-token Q2 of bf16 x fused with the GEMV over tiled INT4
- * weights, acc = sum_k xq * (code - zp) (int32, exact), y = ((float)acc * sx)
- * * scale [+ bias].  Device envelope (nh_supports_linear_w4a8): bf16 x, m <=
- * 16 (groups of 4 rows, each streaming the weights once), k <= 8192, k % 16
- * == 0; otherwise UNSUPPORTED and the caller takes nh_linear_w4a8_host.
- * Errors in the reference's order: INVALID_SHAPE, INVALID_PARAMS
- * (validate_int4_params, quantize.rs:180-186), INVALID_ROW_COUNT. */
+/* W4A8 linear over tiled INT4 weights: acc = sum_k xq * (code - zp) (int32,
+ * exact) on per-token Q2 codes of x, y = ((float)acc * sx) * scale [+ bias].
+ * Two device forms:
+ *  * bf16 x with nh_supports_linear_w4a8(m, n, k) (m <= 16, k <= 8192,
+ *    k % 16 == 0): the fused decode unit streams the 4-bit weights (groups of
+ *    4 rows, each streaming them once); workspace may be NULL;
+ *  * otherwise (f32 x, prefill-sized m, longer K; k % 16 == 0 and the W8A8
+ *    GEMM envelope): the weights are expanded into int8 tiles of code - zp
+ *    in the workspace (nh_linear_w4a8_workspace_size(m, n, k) bytes, 16-byte
+ *    aligned; LENGTH_MISMATCH "workspace" when smaller) and nh_linear_w8a8's
+ *    path runs on them with every row scale equal to `scale`.
+ * Both are bit-identical to the layer's definition.  Errors in the
+ * reference's order: INVALID_SHAPE, INVALID_PARAMS (validate_int4_params,
+ * quantize.rs:180-186), INVALID_ROW_COUNT. */
 int nh_supports_linear_w4a8(size_t m, size_t n, size_t k);
+size_t nh_linear_w4a8_workspace_size(size_t m, size_t n, size_t k);
 nh_status nh_linear_w4a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const uint8_t *w4_tiled, float scale,
                          uint32_t zero_point, const float *bias, size_t m, size_t n, size_t k, void *out,
-                         nh_dtype out_dtype, uint64_t *nonfinite, nh_stream stream, nh_error *err);
+                         nh_dtype out_dtype, void *workspace, size_t workspace_bytes, uint64_t *nonfinite,
+                         nh_stream stream, nh_error *err);
 /* The host twin on the reference's packed layout (f32 or bf16 x, any shape). */
 nh_status nh_linear_w4a8_host(const void *x, nh_dtype x_dtype, const uint8_t *packed, size_t packed_len,
                               float scale, uint32_t zero_point, const float *bias, size_t m, size_t n, size_t k,

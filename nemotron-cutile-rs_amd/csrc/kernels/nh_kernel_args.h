@@ -45,6 +45,19 @@ struct QuantizePmaxArgs {
     int32_t nonfinite_stage;
 };
 
+// Tiled INT4 weights -> tiled int8 weights holding code - zero point (the
+// W8A8 operand the reference's INT4 layer is defined by), plus the per-tensor
+// scale as a per-column scale vector.  Grid-stride over the INT4 lanes.
+struct ExpandInt4Args {
+    const uint8_t* w4;  // tiled INT4 ([ceil(N/16)][KT][512 B])
+    int8_t* w8;         // tiled int8 ([ceil(N/16)][KT][1 KiB])
+    float* sw;          // [n] <- scale
+    int64_t lanes;      // 8-byte INT4 lanes
+    int64_t n;
+    float scale;
+    int32_t zp;
+};
+
 // Q3: out[r][c] = (float)q[r][c] * scales[r]
 struct DequantizeI8Args {
     const int8_t* q;

@@ -280,6 +280,30 @@ extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_pmax_kernel(Q
     *(uint32_t*)(a.q_act + act_tile_offset(row, c * 4, a.rows, kt)) = quantize4_f32(v, s, rcp, pow2);
 }
 
+// Tiled INT4 -> tiled int8 (code - zp).  INT4 lane l's 8 bytes hold the 16
+// codes of int8 lane l in nibble pairs (byte j: column 2 j low, 2 j + 1
+// high), so each lane expands in place of layout: two byte permutes
+// interleave the low and high nibbles, and code - zp is formed per byte
+// without borrows as ((v | 0x80) - zp) ^ 0x80 (v, zp in 0..15).  Padding
+// nibbles hold the zero point, so they expand to the int8 layout's zeros.
+extern "C" __global__ __launch_bounds__(256) void nh_expand_int4_tiles_kernel(ExpandInt4Args a) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const uint32_t zpw = (uint32_t)a.zp * 0x01010101u;
+    auto expand = [&](uint32_t w, uint32_t& w0, uint32_t& w1) {
+        const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        w0 = ((__builtin_amdgcn_perm(hi, lo, 0x05010400u) | 0x80808080u) - zpw) ^ 0x80808080u;
+        w1 = ((__builtin_amdgcn_perm(hi, lo, 0x07030602u) | 0x80808080u) - zpw) ^ 0x80808080u;
+    };
+    for (int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; l < a.lanes; l += stride) {
+        const uint2 q = ((const uint2*)a.w4)[l];
+        uint4 o;
+        expand(q.x, o.x, o.y);
+        expand(q.y, o.z, o.w);
+        ((uint4*)a.w8)[l] = o;
+    }
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride) a.sw[i] = a.scale;
+}
+
 // Q1/Q2 for vector-path rows of up to 512 16-byte chunks (4096 bf16 / 2048
 // f32 values): one wave per row (quantize_row_wave), grid = ceil(rows / 4).
 extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_wave_kernel(QuantizeRowsArgs a) {

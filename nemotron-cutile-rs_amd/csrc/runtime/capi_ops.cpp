@@ -364,9 +364,27 @@ int nh_supports_linear_w4a8(size_t m, size_t n, size_t k) {
     return m > 0 && m <= 16 && n > 0 && n < (1u << 31) && k > 0 && k <= 8192 && (k % 16) == 0;
 }
 
+size_t nh_linear_w4a8_workspace_size(size_t m, size_t n, size_t k) {
+    if (m == 0 || n == 0 || k == 0 || m > (1ull << 31) || n > (1ull << 31) || k > (1ull << 31)) return 0;
+    return align256((size_t)tiled_bytes(n, k)) + align256(n * sizeof(float)) + nh_linear_w8a8_workspace_size(m, k);
+}
+
+}  // extern "C"
+
+namespace {
+nh_status linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* wq, const float* sw,
+                      const float* bias, size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype,
+                      void* workspace, size_t workspace_bytes, int8_t* xq_out, float* sx_out, int relu2,
+                      uint64_t* nonfinite, int nonfinite_stage, nh_stream stream, nh_error* err,
+                      uint32_t* row_max = nullptr);
+}  // namespace
+
+extern "C" {
+
 nh_status nh_linear_w4a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const uint8_t* w4_tiled, float scale,
                          uint32_t zero_point, const float* bias, size_t m, size_t n, size_t k, void* out,
-                         nh_dtype out_dtype, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
+                         nh_dtype out_dtype, void* workspace, size_t workspace_bytes, uint64_t* nonfinite,
+                         nh_stream stream, nh_error* err) {
     clear_error(err);
     nh_status st;
     // the checks of Int4LinearWeights::validate and project_into (linear.rs:113-124, 290-311)
@@ -376,11 +394,25 @@ nh_status nh_linear_w4a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
                          zero_point);
     if (m == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
     if ((st = check_dtype(x_dtype, err)) || (st = check_dtype(out_dtype, err))) return st;
-    if (!nh_supports_linear_w4a8(m, n, k) || x_dtype != NH_BF16)
-        return set_error(err, NH_UNSUPPORTED, "W4A8 device path: bf16 x, m <= 16, k <= 8192, k %% 16 == 0 "
-                         "(m=%zu n=%zu k=%zu)", m, n, k);
-    if (!aligned16(x) || ((uintptr_t)w4_tiled & 7u) != 0)
-        return set_error(err, NH_UNSUPPORTED, "x must be 16-byte and w4_tiled 8-byte aligned");
+    if (((uintptr_t)w4_tiled & 7u) != 0) return set_error(err, NH_UNSUPPORTED, "w4_tiled must be 8-byte aligned");
+    if (x_dtype != NH_BF16 || !nh_supports_linear_w4a8(m, n, k) || !aligned16(x)) {
+        // any other shape or f32 rows: the weights expanded into int8 tiles of
+        // code - zp (the layer's definition) and the W8A8 linear path on them
+        if ((st = check_w8a8_shape(m, n, k, err))) return st;
+        const size_t need = nh_linear_w4a8_workspace_size(m, n, k);
+        if (!workspace || workspace_bytes < need) return mismatch(err, "workspace", need, workspace_bytes);
+        if (!aligned16(workspace)) return set_error(err, NH_UNSUPPORTED, "workspace must be 16-byte aligned");
+        if ((st = bind_device(ctx, err))) return st;
+        int8_t* w8 = (int8_t*)workspace;
+        float* sw = (float*)(w8 + align256((size_t)tiled_bytes(n, k)));
+        void* lin = (char*)sw + align256(n * sizeof(float));
+        const size_t lin_bytes = workspace_bytes - (size_t)((char*)lin - (char*)workspace);
+        ExpandInt4Args e{w4_tiled, w8, sw, (int64_t)(tiled_int4_bytes(n, k) / 8), (int64_t)n, scale,
+                         (int32_t)zero_point};
+        if ((st = launch(ctx, K_EXPAND_INT4, grid_for(e.lanes, 256), 256, 0, stream, e, err))) return st;
+        return linear_w8a8(ctx, x, x_dtype, w8, sw, bias, m, n, k, out, out_dtype, lin, lin_bytes, nullptr, nullptr,
+                           0, nonfinite, 0, stream, err);
+    }
     if ((st = bind_device(ctx, err))) return st;
     const int kt = (int)tiled_k_tiles(k), w = gemv_waves(kt);
     const size_t esz = out_dtype == NH_BF16 ? 2 : 4;
@@ -509,7 +541,7 @@ nh_status linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const in
                       const float* bias, size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype,
                       void* workspace, size_t workspace_bytes, int8_t* xq_out, float* sx_out, int relu2,
                       uint64_t* nonfinite, int nonfinite_stage, nh_stream stream, nh_error* err,
-                      uint32_t* row_max = nullptr) {
+                      uint32_t* row_max) {
     nh_status st;
     // bf16 rows: the fused decode unit when it fits (one launch, no workspace)
     DecodePlan plan;

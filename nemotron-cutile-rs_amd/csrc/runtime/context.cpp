@@ -43,6 +43,7 @@ const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
     "nh_quantize_rows_wave_kernel",      // K_QUANTIZE_ROWS_WAVE
     "nh_quantize_rows_long_kernel",      // K_QUANTIZE_ROWS_LONG
     "nh_quantize_rows_pmax_kernel",      // K_QUANTIZE_ROWS_PMAX
+    "nh_expand_int4_tiles_kernel",       // K_EXPAND_INT4
     "nh_tile_weights_int4_kernel",       // K_TILE_INT4
     "nh_linear_decode_w4a8_m1_kernel",   // K_LINEAR_DECODE_W4_M1
     "nh_linear_decode_w4a8_row2_kernel", // K_LINEAR_DECODE_W4_ROW2

@@ -45,6 +45,7 @@ enum KernelId : int {
     K_QUANTIZE_ROWS_WAVE,  // row quantizer, one wave per row
     K_QUANTIZE_ROWS_LONG,  // row quantizer, 1024 threads per row
     K_QUANTIZE_ROWS_PMAX,  // f32 rows with producer-reduced maxima, many workgroups per row
+    K_EXPAND_INT4,         // tiled INT4 -> tiled int8 code - zp
     K_TILE_INT4,           // INT4 [K][N] packed -> tiled INT4
     K_LINEAR_DECODE_W4_M1,    // W4A8 decode unit, 1 row
     K_LINEAR_DECODE_W4_ROW2,  // 2 rows

@@ -139,7 +139,8 @@ _SIGNATURES = {
     "nh_tile_weights_int4": (ST, [P, P, SZ, SZ, SZ, C.c_uint32, P, SZ, P, E]),
     "nh_tile_weights_int4_host": (ST, [P, SZ, SZ, SZ, C.c_uint32, P, SZ, E]),
     "nh_supports_linear_w4a8": (C.c_int, [SZ, SZ, SZ]),
-    "nh_linear_w4a8": (ST, [P, P, C.c_int, P, C.c_float, C.c_uint32, P, SZ, SZ, SZ, P, C.c_int, P, P, E]),
+    "nh_linear_w4a8_workspace_size": (SZ, [SZ, SZ, SZ]),
+    "nh_linear_w4a8": (ST, [P, P, C.c_int, P, C.c_float, C.c_uint32, P, SZ, SZ, SZ, P, C.c_int, P, SZ, P, P, E]),
     "nh_linear_w4a8_host": (ST, [P, C.c_int, P, SZ, C.c_float, C.c_uint32, P, SZ, SZ, SZ, P, C.c_int, E]),
     "nh_safetensors_tensor_info": (ST, [C.c_char_p, C.c_char_p, C.POINTER(TensorInfo), E]),
     "nh_safetensors_read": (ST, [P, C.c_char_p, C.c_char_p, P, SZ, E]),

@@ -954,13 +954,19 @@ extern "C" {
         err: *mut nh_error,
     ) -> nh_status;
 
-    /// W4A8 linear: per-token Q2 of bf16 x fused with the GEMV over tiled INT4 weights, acc = sum_k xq
-    /// * (code - zp) (int32, exact), y = ((float)acc * sx) * scale [+ bias].  Device envelope
-    /// (nh_supports_linear_w4a8): bf16 x, m <= 16 (groups of 4 rows, each streaming the weights once),
-    /// k <= 8192, k % 16 == 0; otherwise UNSUPPORTED and the caller takes nh_linear_w4a8_host. Errors
-    /// in the reference's order: INVALID_SHAPE, INVALID_PARAMS (validate_int4_params,
-    /// quantize.rs:180-186), INVALID_ROW_COUNT.
+    /// W4A8 linear over tiled INT4 weights: acc = sum_k xq * (code - zp) (int32, exact) on per-token Q2
+    /// codes of x, y = ((float)acc * sx) * scale [+ bias]. Two device forms: * bf16 x with
+    /// nh_supports_linear_w4a8(m, n, k) (m <= 16, k <= 8192, k % 16 == 0): the fused decode unit
+    /// streams the 4-bit weights (groups of 4 rows, each streaming them once); workspace may be NULL; *
+    /// otherwise (f32 x, prefill-sized m, longer K; k % 16 == 0 and the W8A8 GEMM envelope): the
+    /// weights are expanded into int8 tiles of code - zp in the workspace
+    /// (nh_linear_w4a8_workspace_size(m, n, k) bytes, 16-byte aligned; LENGTH_MISMATCH "workspace" when
+    /// smaller) and nh_linear_w8a8's path runs on them with every row scale equal to `scale`. Both are
+    /// bit-identical to the layer's definition.  Errors in the reference's order: INVALID_SHAPE,
+    /// INVALID_PARAMS (validate_int4_params, quantize.rs:180-186), INVALID_ROW_COUNT.
     pub fn nh_supports_linear_w4a8(m: usize, n: usize, k: usize) -> c_int;
+
+    pub fn nh_linear_w4a8_workspace_size(m: usize, n: usize, k: usize) -> usize;
 
     pub fn nh_linear_w4a8(
         ctx: *mut nh_context,
@@ -975,6 +981,8 @@ extern "C" {
         k: usize,
         out: *mut c_void,
         out_dtype: nh_dtype,
+        workspace: *mut c_void,
+        workspace_bytes: usize,
         nonfinite: *mut u64,
         stream: nh_stream,
         err: *mut nh_error,

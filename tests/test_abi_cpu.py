@@ -470,12 +470,19 @@ def test_int4_validation_in_the_reference_order():
     assert host(2, 2, 2, 0.5, 16, 1)[0] == NH.INVALID_PARAMS
     assert host(2, 2, 2, 0.5, 8, 0)[0] == NH.INVALID_ROW_COUNT
     # the device entry point validates before touching the (NULL) context
-    dev = lambda m, n, k, scale=0.5, zp=8: NH.call_status(  # noqa: E731
-        "nh_linear_w4a8", None, 16, NH.BF16, 16, scale, zp, None, m, n, k, 16, NH.BF16, None, None)[0]
-    assert dev(1, 0, 64) == NH.INVALID_SHAPE
-    assert dev(1, 16, 64, scale=-1.0) == NH.INVALID_PARAMS
-    assert dev(0, 16, 64) == NH.INVALID_ROW_COUNT
-    assert dev(17, 16, 64) == NH.UNSUPPORTED and dev(1, 16, 8192 + 16) == NH.UNSUPPORTED and dev(1, 16, 72) == NH.UNSUPPORTED
+    dev = lambda m, n, k, scale=0.5, zp=8, dt=NH.BF16: NH.call_status(  # noqa: E731
+        "nh_linear_w4a8", None, 16, dt, 16, scale, zp, None, m, n, k, 16, NH.BF16, None, 0, None, None)
+    assert dev(1, 0, 64)[0] == NH.INVALID_SHAPE
+    assert dev(1, 16, 64, scale=-1.0)[0] == NH.INVALID_PARAMS
+    assert dev(0, 16, 64)[0] == NH.INVALID_ROW_COUNT
+    # past the fused unit (m > 16, k > 8192, f32 rows): the expanded form needs its workspace
+    for st, err in (dev(17, 16, 64), dev(1, 16, 8192 + 16), dev(1, 16, 64, dt=NH.F32)):
+        assert st == NH.LENGTH_MISMATCH and err.argument == b"workspace" and err.actual == 0
+    assert dev(1, 16, 72)[0] == NH.UNSUPPORTED  # k % 16 != 0: the W8A8 envelope
+    L = NH.lib()
+    assert L.nh_linear_w4a8_workspace_size(2048, 4096, 4096) == (
+        4096 * 4096 + 4096 * 4 + L.nh_linear_w8a8_workspace_size(2048, 4096))
+    assert L.nh_linear_w4a8_workspace_size(0, 4096, 4096) == 0
     st, err = NH.call_status("nh_tile_weights_int4", None, 16, 3, 2, 2, 8, 16, 512, None)
     assert st == NH.LENGTH_MISMATCH and err.argument.decode() == "packed_weights"
 

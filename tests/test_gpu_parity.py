@@ -480,30 +480,55 @@ def test_gemv_w8a32_within_tolerance(ctx, m, n, k):
 
 
 # ---- W4A8: the reference's INT4 linear weights, tiled, with the fused quantizer ----
-@pytest.mark.parametrize("m,n,k,zp", [(1, 16384, 4096, 8), (1, 4096, 8192, 0), (2, 100, 1040, 15), (3, 4096, 4096, 7),
-                                      (4, 33, 64, 8), (7, 4096, 4096, 3), (16, 1000, 2048, 9)])
-def test_linear_w4a8_bit_exact(ctx, m, n, k, zp):
+@pytest.mark.parametrize("m,n,k,zp,dtype", [(1, 16384, 4096, 8, "bf16"), (1, 4096, 8192, 0, "bf16"),
+                                            (2, 100, 1040, 15, "bf16"), (3, 4096, 4096, 7, "bf16"),
+                                            (4, 33, 64, 8, "bf16"), (7, 4096, 4096, 3, "bf16"),
+                                            (16, 1000, 2048, 9, "bf16"),
+                                            # the expanded form: f32 rows, K past the fused unit's 8192,
+                                            # prefill-sized M on the GEMM (M and N tails)
+                                            (3, 1000, 2048, 6, "f32"), (1, 600, 16384, 5, "bf16"),
+                                            (17, 300, 1024, 11, "bf16"), (300, 2050, 1024, 8, "bf16"),
+                                            (129, 520, 4096, 2, "f32")])
+def test_linear_w4a8_bit_exact(ctx, m, n, k, zp, dtype):
+    """nh_linear_w4a8 against the layer's definition: or_linear_w4a8 for bf16
+    rows; for f32 rows the oracle's parts (quantize_rows_f32, then the W8A8
+    product with weights code - zp and every row scale = scale)."""
     from tiling import tile_int4
-    note(f"linear_w4a8 m={m} n={n} k={k} zp={zp}")
+    note(f"linear_w4a8 m={m} n={n} k={k} zp={zp} {dtype}")
     rng = np.random.default_rng(m * 1000 + zp)
     packed = rng.integers(0, 256, size=(k * n + 1) // 2, dtype=np.uint8)
     scale = 0.0137
-    x = activations_bf16(m, k)
+    if dtype == "bf16":
+        x, xdt = activations_bf16(m, k), NH.BF16
+    else:
+        x, xdt = O.normal_f32(90 + m, m * k).reshape(m, k), NH.F32
     bias = rng.standard_normal(n).astype(np.float32) if m % 2 else None
     need = NH.lib().nh_tiled_int4_weights_bytes(n, k)
     dp, dt = ctx.upload(packed), ctx.empty(need, np.uint8)
     NH.call("nh_tile_weights_int4", ctx.handle, dp.ptr, packed.size, k, n, zp, dt.ptr, need, None)
     ctx.synchronize()
     assert np.array_equal(dt.numpy(), tile_int4(packed, k, n, zp))
+    fused = dtype == "bf16" and NH.lib().nh_supports_linear_w4a8(m, n, k)
+    ws_bytes = NH.lib().nh_linear_w4a8_workspace_size(m, n, k)
+    ws = ctx.empty(ws_bytes, np.uint8)
     dx = ctx.upload(x)
     db = ctx.upload(bias) if bias is not None else None
+    if dtype == "f32":
+        st, xq, sx, _ = O.quantize_rows_f32(x)
+        assert st == O.OK
+        codes = np.stack([packed & 15, packed >> 4], axis=1).reshape(-1)[:k * n].reshape(k, n)
+        w = (codes.astype(np.int16) - zp).astype(np.int8).T.copy()  # [N][K] = code - zp
     for out_dtype, bf in ((NH.BF16, True), (NH.F32, False)):
         out = ctx.empty((m, n), np.uint16 if bf else np.float32)
-        NH.call("nh_linear_w4a8", ctx.handle, dx.ptr, NH.BF16, dt.ptr, scale, zp, db.ptr if db else None, m, n, k,
-                out.ptr, out_dtype, None, None)
+        # the fused unit needs no workspace
+        NH.call("nh_linear_w4a8", ctx.handle, dx.ptr, xdt, dt.ptr, scale, zp, db.ptr if db else None, m, n, k,
+                out.ptr, out_dtype, None if fused else ws.ptr, 0 if fused else ws_bytes, None, None)
         ctx.synchronize()
-        st, ref = O.linear_w4a8(x, packed, n, scale, zp, bias=bias, out_bf16=bf)
-        assert st == O.OK
+        if dtype == "bf16":
+            st, ref = O.linear_w4a8(x, packed, n, scale, zp, bias=bias, out_bf16=bf)
+            assert st == O.OK
+        else:
+            ref = linear_w8a8_exact(xq, sx, w, np.full(n, scale, np.float32), bias=bias, out_bf16=bf)
         assert np.array_equal(out.numpy(), ref)
 
 
