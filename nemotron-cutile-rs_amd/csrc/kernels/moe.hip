@@ -18,13 +18,30 @@ __device__ __forceinline__ int64_t route_key(float w, int e) {
     return ((int64_t)total_cmp_key(w) << 32) | (int64_t)(uint32_t)(0xFFFFFFFFu - (uint32_t)e);
 }
 
+// Wave maximum of a 64-bit key through DPP lane moves (no LDS round trips):
+// both halves move together each step (quad permutes and row rotates within
+// rows of 16, then the row broadcasts of lanes 15 and 31), lanes a move
+// leaves out keep their own key, and lane 63 ends with the maximum, which
+// readlane hands to every lane.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int64_t dpp_max_step_i64(int64_t v) {
+    const int lo = (int)(uint32_t)v, hi = (int)(v >> 32);
+    const int olo = __builtin_amdgcn_update_dpp(lo, lo, CTRL, ROWS, 0xf, false);
+    const int ohi = __builtin_amdgcn_update_dpp(hi, hi, CTRL, ROWS, 0xf, false);
+    const int64_t o = ((int64_t)ohi << 32) | (int64_t)(uint32_t)olo;
+    return o > v ? o : v;
+}
+
 __device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const int64_t o = __shfl_xor(v, off, kWave);
-        v = o > v ? o : v;
-    }
-    return v;
+    v = dpp_max_step_i64<0xb1, 0xf>(v);   // quad_perm 1,0,3,2
+    v = dpp_max_step_i64<0x4e, 0xf>(v);   // quad_perm 2,3,0,1
+    v = dpp_max_step_i64<0x124, 0xf>(v);  // row_ror 4
+    v = dpp_max_step_i64<0x128, 0xf>(v);  // row_ror 8
+    v = dpp_max_step_i64<0x142, 0xa>(v);  // row_bcast 15
+    v = dpp_max_step_i64<0x143, 0xc>(v);  // row_bcast 31
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), 63);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
@@ -66,7 +83,8 @@ __device__ __forceinline__ void route_token(const RouteArgs& a, int token, int l
     if (a.renormalize) {
         // sum in route order, as selected_total (moe_routing.rs:207-211)
         float total = 0.0f;
-        for (int j = 0; j < a.top_k; ++j) total = total + __shfl(wsel, j, kWave);
+        for (int j = 0; j < a.top_k; ++j)
+            total = total + f32_from_bits((uint32_t)__builtin_amdgcn_readlane((int)f32_bits(wsel), j));
         wsel = wsel / total;
     }
     if (a.scaling != 1.0f) wsel = wsel * a.scaling;
