@@ -723,6 +723,12 @@ extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_stream_m8_ke
     linear_decode_stream<8, 4, 4, 2>(a, lds);
 }
 
+// The same for 3..4 rows (two activation chunks per thread).
+extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_stream_m4_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t lds[];
+    linear_decode_stream<4, 2, 4, 2>(a, lds);
+}
+
 // G2: W8A32 dequant GEMV, y[m][n] = sum_k x[m][k] * q[n][k] * s[n].  The
 // reference materialises W' = (float)q * s and sums x * W' in f64
 // (linear.rs:126-131, gemm.rs:99-109).  Here each lane sums the 16 products

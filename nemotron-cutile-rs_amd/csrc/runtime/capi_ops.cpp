@@ -89,15 +89,16 @@ bool plan_decode(const nh_context* ctx, size_t m, size_t n, size_t k, DecodePlan
 // each CU would load 128 KiB of activations, as much as its share of a
 // 4096-wide output's weights: 16.4 us against 14.7 in two launches.)
 bool plan_stream(const nh_context* ctx, size_t m, size_t n, size_t k, DecodePlan* p, unsigned* grid) {
-    if (m < 5 || m > 8 || k % 512 != 0 || k > 4096) return false;
+    if (m < 3 || m > 8 || k % 512 != 0 || k > 4096) return false;
+    const size_t mm = m <= 4 ? 4 : 8;
     const size_t tiles = (n + 15) / 16, cu = (size_t)ctx->cu_count;
     const size_t rounds = (tiles + cu - 1) / cu;
     if (rounds > 64) return false;  // a run's scales and bias: at most 1024 LDS floats each
     // codes [KT][4][8][16], two sets of 16 partial tiles, the run's scales
     // and bias, row maxima and row scales
-    const size_t lds = (k / 64) * 64 * 8 + 2 * 16 * 64 * 16 + 2 * 1024 * 4 + 2 * 8 * 4;
+    const size_t lds = (k / 64) * 64 * mm + 2 * 16 * 64 * 16 + 2 * 1024 * 4 + 2 * mm * 4;
     if (lds > ctx->max_shared_per_block) return false;
-    *p = DecodePlan{K_LINEAR_DECODE_STREAM_M8, 0, 1024, lds};
+    *p = DecodePlan{mm == 4 ? K_LINEAR_DECODE_STREAM_M4 : K_LINEAR_DECODE_STREAM_M8, 0, 1024, lds};
     *grid = (unsigned)((tiles + rounds - 1) / rounds);
     return true;
 }

@@ -36,6 +36,7 @@ enum KernelId : int {
     K_GEMV_W8A8_XT,      // activation tiles
     K_LINEAR_DECODE_M8,  // M <= 8
     K_LINEAR_DECODE_STREAM_M8,  // 5..8 rows, any N, K <= 4096
+    K_LINEAR_DECODE_STREAM_M4,  // 3..4 rows
     K_LINEAR_DECODE_ROW2,  // M <= 2, one N tile per workgroup
     K_LINEAR_DECODE_ROW4,  // M <= 4, one N tile per workgroup
     K_EXPERT_GEMM,         // grouped GEMM on slot-ordered A
