@@ -505,7 +505,7 @@ __device__ __forceinline__ void linear_decode_wide(const LinearDecodeArgs& a, in
 // Every load is unconditional (rounds past the run and K tiles past kt read
 // out of range: zeros, no memory traffic), so each wait is a fixed count.
 // Codes and scales are bit-identical to quantize_i8 (quantize8_bf16).
-template <int MM, int XR, int KS, int NB>
+template <int MM, int XR, int KS, int NB, bool W4 = false>
 __device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, int8_t* lds) {
     constexpr int NW = 16;
     const int lane = threadIdx.x & 63;
@@ -524,13 +524,17 @@ __device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, 
     float* bl = swl + 1024;                    // [1024] bias of the run
     int* rowmax = (int*)(bl + 1024);           // [MM] row absmax (f32 bits)
     float* srow = (float*)(rowmax + MM);       // [MM] row scales
+    int* rowsum = (int*)(srow + MM);           // [MM] W4: the rows' code sums
     if (tid < MM) rowmax[tid] = 0;
+    if (W4 && tid < MM) rowsum[tid] = 0;
+    constexpr int kTile = W4 ? 512 : 1024;  // bytes per weight tile (K tile x 16 columns)
 
     // 1. activations, epilogue operands, the first PRE rounds of weights
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)M * (uint32_t)K * 2u);
     const int cbase = wave * XR * 64;  // the wave's first chunk
     v4i xv[XR];
-    v4i b0[KS], b1[KS], b2[KS];
+    using WB = std::conditional_t<W4, uint2, v4i>;  // one lane's share of a weight tile
+    WB b0[KS], b1[KS], b2[KS];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < XR; ++j) {
@@ -538,16 +542,23 @@ __device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, 
         xv[j] = buffer_load16(xrs, c < M * cpr ? c * 16 : kOutOfRange);
     }
     const uint32_t run_bytes = (uint32_t)min(ntl * 16, N - t0 * 16) * 4u;
-    const float swv = f32_from_bits(
-        (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(make_rsrc(a.sw + t0 * 16, run_bytes), tid * 4, 0, 0));
+    // (W4: one tensor scale, no per-column scales to stage; sw may be null)
+    const float swv = f32_from_bits((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+        make_rsrc(W4 ? (const void*)a.wq : (const void*)(a.sw + t0 * 16), W4 ? 0u : run_bytes), tid * 4, 0, 0));
     const float bv = f32_from_bits((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
         make_rsrc(a.bias ? a.bias + t0 * 16 : a.sw, a.bias ? run_bytes : 0u), tid * 4, 0, 0));
-    auto issue = [&](v4i (&b)[KS], int r) {
+    auto issue = [&](WB (&b)[KS], int r) {
         const bool in_run = r < ntl;
         const __amdgpu_buffer_rsrc_t wr =
-            make_rsrc(a.wq + (int64_t)(t0 + (in_run ? r : 0)) * kt * 1024, in_run ? (uint32_t)kt * 1024u : 0u);
+            make_rsrc(a.wq + (int64_t)(t0 + (in_run ? r : 0)) * kt * kTile, in_run ? (uint32_t)(kt * kTile) : 0u);
 #pragma unroll
-        for (int s = 0; s < KS; ++s) b[s] = buffer_load16_stream(wr, (wave * KS + s) * 1024 + lane * 16);
+        for (int s = 0; s < KS; ++s) {
+            if constexpr (W4)
+                b[s] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                     wr, (wave * KS + s) * 512 + lane * 8, 0, 2));
+            else
+                b[s] = buffer_load16_stream(wr, (wave * KS + s) * 1024 + lane * 16);
+        }
     };
     issue(b0, 0);
     issue(b1, 1);
@@ -595,7 +606,16 @@ __device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, 
         for (int r = 0; r < M; ++r) nonfinite |= (uint32_t)rowmax[r] >= 0x7f800000u;
         if (nonfinite) report_decode_chunks<XR>(a, xv, cbase + lane, 64);
     }
-    // codes into LDS: chunk c = 8 values of row c / cpr at k = 8 (c % cpr)
+    // codes into LDS: chunk c = 8 values of row c / cpr at k = 8 (c % cpr);
+    // W4: in the nibble order of expand_int4 (act_order_int4), and each row's
+    // code sum (zero point, acc - zp * sum_k xq) reduced per row segment
+    int csum = 0, crow = cbase / cpr;
+    auto flush_sum = [&]() {
+        int v = csum;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+        if (lane == 0) atomicAdd(&rowsum[crow], v);
+    };
 #pragma unroll
     for (int j = 0; j < XR; ++j) {
         const int c0 = cbase + j * 64;
@@ -606,10 +626,22 @@ __device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, 
             uint32_t code[2];
             quantize8_bf16(xv[j], sx, rcp, scale_is_pow2(sx), code);
             const int k = (c0 + lane - row * cpr) * 8;
-            *(uint2*)(xs + (((k >> 6) * 4 + ((k >> 4) & 3)) * MM + row) * 16 + (k & 15)) = make_uint2(code[0], code[1]);
+            uint2 st = make_uint2(code[0], code[1]);
+            if constexpr (W4) {
+                if (row != crow) {
+                    flush_sum();
+                    csum = 0;
+                    crow = row;
+                }
+                csum = __builtin_amdgcn_sdot4((int)code[0], 0x01010101, csum, false);
+                csum = __builtin_amdgcn_sdot4((int)code[1], 0x01010101, csum, false);
+                st = act_order_int4(code[0], code[1]);
+            }
+            *(uint2*)(xs + (((k >> 6) * 4 + ((k >> 4) & 3)) * MM + row) * 16 + (k & 15)) = st;
             if (blockIdx.x == 0 && a.xq_out) *(uint2*)(a.xq_out + (int64_t)row * K + k) = make_uint2(code[0], code[1]);
         }
     }
+    if (W4 && cbase < M * cpr) flush_sum();
     if (blockIdx.x == 0 && a.sx_out && tid < M) a.sx_out[tid] = sx_l;
     lds_publish();  // codes and row scales complete
 
@@ -625,13 +657,21 @@ __device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, 
     // the epilogue output of thread tid < 16 MM: row tid / 16, column tid % 16
     const int em = tid >> 4, en = tid & 15;
     const float sxe = srow[em < MM ? em : 0];
+    const int zsum = W4 ? a.w4_zp * rowsum[em < MM ? em : 0] : 0;  // zp * sum_k xq of the row
     uint32_t ymax = 0;  // largest finite |y| of the thread's outputs (f32 bits)
-    auto round = [&](v4i (&b)[KS], int r) {
+    auto round = [&](WB (&b)[KS], int r) {
         const int buf = r & 1;
         wait_vmcnt_le((NB - 1) * KS);  // this round's weights in, the next NB - 1 rounds' in flight
         v4i acc = {0, 0, 0, 0};
 #pragma unroll
-        for (int s = 0; s < KS; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[s], b[s], acc, 0, 0, 0);
+        for (int s = 0; s < KS; ++s) {
+            v4i bw;
+            if constexpr (W4)
+                bw = expand_int4(b[s]);
+            else
+                bw = b[s];
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[s], bw, acc, 0, 0, 0);
+        }
         red[(buf * NW + wave) * 64 + lane] = acc;
         issue(b, r + NB);
         lds_publish();
@@ -644,7 +684,8 @@ __device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, 
 #pragma unroll
                 for (int w = 0; w < NW; ++w) sum += rp[w * 64 * 4];
                 // store_y's steps, keeping y for the row maxima
-                float y = epilogue_w8a8(sum, sxe, swl[r * 16 + en]);
+                // W4: sum_k xq * (code - zp), scaled by the tensor scale
+                float y = W4 ? epilogue_w8a8(sum - zsum, sxe, a.w4_scale) : epilogue_w8a8(sum, sxe, swl[r * 16 + en]);
                 if (a.bias) y = y + bl[r * 16 + en];
                 if (a.relu2) y = relu2(y);
                 store_out(a.out, (int64_t)em * N + n, y, a.out_dtype);
@@ -727,6 +768,17 @@ extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_stream_m8_ke
 extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_stream_m4_kernel(LinearDecodeArgs a) {
     extern __shared__ __align__(16) int8_t lds[];
     linear_decode_stream<4, 2, 4, 2>(a, lds);
+}
+
+// The streaming unit on tiled INT4 weights (W4A8), 3..4 and 5..8 rows.
+extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_stream_w4_m4_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t lds[];
+    linear_decode_stream<4, 2, 4, 2, true>(a, lds);
+}
+
+extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_stream_w4_m8_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t lds[];
+    linear_decode_stream<8, 4, 4, 2, true>(a, lds);
 }
 
 // G2: W8A32 dequant GEMV, y[m][n] = sum_k x[m][k] * q[n][k] * s[n].  The

@@ -94,9 +94,9 @@ bool plan_stream(const nh_context* ctx, size_t m, size_t n, size_t k, DecodePlan
     const size_t tiles = (n + 15) / 16, cu = (size_t)ctx->cu_count;
     const size_t rounds = (tiles + cu - 1) / cu;
     if (rounds > 64) return false;  // a run's scales and bias: at most 1024 LDS floats each
-    // codes [KT][4][8][16], two sets of 16 partial tiles, the run's scales
-    // and bias, row maxima and row scales
-    const size_t lds = (k / 64) * 64 * mm + 2 * 16 * 64 * 16 + 2 * 1024 * 4 + 2 * mm * 4;
+    // codes [KT][4][MM][16], two sets of 16 partial tiles, the run's scales
+    // and bias, row maxima, row scales and (W4) row code sums
+    const size_t lds = (k / 64) * 64 * mm + 2 * 16 * 64 * 16 + 2 * 1024 * 4 + 3 * mm * 4;
     if (lds > ctx->max_shared_per_block) return false;
     *p = DecodePlan{mm == 4 ? K_LINEAR_DECODE_STREAM_M4 : K_LINEAR_DECODE_STREAM_M8, 0, 1024, lds};
     *grid = (unsigned)((tiles + rounds - 1) / rounds);
@@ -417,6 +417,28 @@ nh_status nh_linear_w4a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
     if ((st = bind_device(ctx, err))) return st;
     const int kt = (int)tiled_k_tiles(k), w = gemv_waves(kt);
     const size_t esz = out_dtype == NH_BF16 ? 2 : 4;
+    DecodePlan plan;
+    unsigned grid = 0;
+    if (plan_stream(ctx, m, n, k, &plan, &grid)) {
+        // 3..8 rows: the streaming unit, the INT4 weights streamed once
+        LinearDecodeArgs a{};
+        a.x = x;
+        a.wq = (const int8_t*)w4_tiled;
+        a.bias = bias;
+        a.out = out;
+        a.M = (int)m;
+        a.N = (int)n;
+        a.K = (int)k;
+        a.kt = kt;
+        a.waves = 16;
+        a.x_dtype = x_dtype;
+        a.out_dtype = out_dtype;
+        a.w4_zp = (int)zero_point;
+        a.w4_scale = scale;
+        a.nonfinite = nonfinite;
+        const KernelId kid = m <= 4 ? K_LINEAR_DECODE_STREAM_W4_M4 : K_LINEAR_DECODE_STREAM_W4_M8;
+        return launch(ctx, kid, grid, 1024u, plan.lds, stream, a, err);
+    }
     // groups of up to 4 rows, each a launch that streams the weights once
     for (size_t r0 = 0; r0 < m; r0 += 4) {
         const size_t rows = std::min<size_t>(4, m - r0);
