@@ -770,6 +770,12 @@ extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_stream_m4_ke
     linear_decode_stream<4, 2, 4, 2>(a, lds);
 }
 
+// The same for 9..16 rows (eight activation chunks per thread).
+extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_stream_m16_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t lds[];
+    linear_decode_stream<16, 8, 4, 2>(a, lds);
+}
+
 // The streaming unit on tiled INT4 weights (W4A8), 3..4 and 5..8 rows.
 extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_stream_w4_m4_kernel(LinearDecodeArgs a) {
     extern __shared__ __align__(16) int8_t lds[];

@@ -82,15 +82,15 @@ bool plan_decode(const nh_context* ctx, size_t m, size_t n, size_t k, DecodePlan
     return m <= 4 && row_plan();
 }
 
-// Streaming decode unit (5..8 bf16 rows, K % 512 == 0, K <= 4096, any N):
+// Streaming decode unit (3..16 bf16 rows, K % 512 == 0, K <= 4096, any N):
 // G workgroups of 16 waves, each quantizing the rows once and walking a run
 // of ceil(tiles / G) or one fewer N tiles; G is the CU count or, at the same
 // number of rounds, as few workgroups as that many rounds need.  (At K = 8192
 // each CU would load 128 KiB of activations, as much as its share of a
 // 4096-wide output's weights: 16.4 us against 14.7 in two launches.)
 bool plan_stream(const nh_context* ctx, size_t m, size_t n, size_t k, DecodePlan* p, unsigned* grid) {
-    if (m < 3 || m > 8 || k % 512 != 0 || k > 4096) return false;
-    const size_t mm = m <= 4 ? 4 : 8;
+    if (m < 3 || m > 16 || k % 512 != 0 || k > 4096) return false;
+    const size_t mm = m <= 4 ? 4 : m <= 8 ? 8 : 16;
     const size_t tiles = (n + 15) / 16, cu = (size_t)ctx->cu_count;
     const size_t rounds = (tiles + cu - 1) / cu;
     if (rounds > 64) return false;  // a run's scales and bias: at most 1024 LDS floats each
@@ -98,7 +98,8 @@ bool plan_stream(const nh_context* ctx, size_t m, size_t n, size_t k, DecodePlan
     // and bias, row maxima, row scales and (W4) row code sums
     const size_t lds = (k / 64) * 64 * mm + 2 * 16 * 64 * 16 + 2 * 1024 * 4 + 3 * mm * 4;
     if (lds > ctx->max_shared_per_block) return false;
-    *p = DecodePlan{mm == 4 ? K_LINEAR_DECODE_STREAM_M4 : K_LINEAR_DECODE_STREAM_M8, 0, 1024, lds};
+    *p = DecodePlan{mm == 4 ? K_LINEAR_DECODE_STREAM_M4 : mm == 8 ? K_LINEAR_DECODE_STREAM_M8 : K_LINEAR_DECODE_STREAM_M16,
+                    0, 1024, lds};
     *grid = (unsigned)((tiles + rounds - 1) / rounds);
     return true;
 }
@@ -419,7 +420,7 @@ nh_status nh_linear_w4a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
     const size_t esz = out_dtype == NH_BF16 ? 2 : 4;
     DecodePlan plan;
     unsigned grid = 0;
-    if (plan_stream(ctx, m, n, k, &plan, &grid)) {
+    if (m <= 8 && plan_stream(ctx, m, n, k, &plan, &grid)) {
         // 3..8 rows: the streaming unit, the INT4 weights streamed once
         LinearDecodeArgs a{};
         a.x = x;
@@ -680,8 +681,8 @@ nh_status nh_mlp_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const in
     DecodePlan plan;
     unsigned groups = 0;
     if (x_dtype == NH_BF16 && aligned16(x) && inter % 4 == 0 && plan_stream(ctx, m, inter, hidden, &plan, &groups) &&
-        groups <= kMaxStreamGroups) {
-        // 5..8 rows: the streaming unit leaves each workgroup's row maxima of
+        (size_t)groups * m <= kMaxStreamGroups * 8) {
+        // 3..16 rows: the streaming unit leaves each workgroup's row maxima of
         // h, so h's quantizer needs no reduction pass over the 4 * inter-byte
         // rows and spreads each row over many workgroups (K = 21504: 8.9 us
         // as one workgroup per row)

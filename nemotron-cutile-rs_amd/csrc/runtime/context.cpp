@@ -35,6 +35,7 @@ const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
     "nh_linear_decode_w8a8_m8_kernel",   // K_LINEAR_DECODE_M8
     "nh_linear_decode_stream_m8_kernel",  // K_LINEAR_DECODE_STREAM_M8
     "nh_linear_decode_stream_m4_kernel",  // K_LINEAR_DECODE_STREAM_M4
+    "nh_linear_decode_stream_m16_kernel",  // K_LINEAR_DECODE_STREAM_M16
     "nh_linear_decode_stream_w4_m4_kernel",  // K_LINEAR_DECODE_STREAM_W4_M4
     "nh_linear_decode_stream_w4_m8_kernel",  // K_LINEAR_DECODE_STREAM_W4_M8
     "nh_linear_decode_w8a8_row2_kernel", // K_LINEAR_DECODE_ROW2

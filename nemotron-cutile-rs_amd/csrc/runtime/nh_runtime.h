@@ -37,6 +37,7 @@ enum KernelId : int {
     K_LINEAR_DECODE_M8,  // M <= 8
     K_LINEAR_DECODE_STREAM_M8,  // 5..8 rows, any N, K <= 4096
     K_LINEAR_DECODE_STREAM_M4,  // 3..4 rows
+    K_LINEAR_DECODE_STREAM_M16,  // 9..16 rows
     K_LINEAR_DECODE_STREAM_W4_M4,  // the same on tiled INT4 weights
     K_LINEAR_DECODE_STREAM_W4_M8,
     K_LINEAR_DECODE_ROW2,  // M <= 2, one N tile per workgroup

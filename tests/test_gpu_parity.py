@@ -383,6 +383,7 @@ def mlp_weights(hidden, inter):
                                                   # quantizer: a last K tile partly past inter = 1872, one
                                                   # N tile per workgroup
                                                   (6, 512, 1872, "bf16"), (7, 1024, 4096, "bf16"),
+                                                  (12, 1024, 2048, "bf16"), (4, 4096, 1024, "bf16"),
                                                   # the up projection (bias, ReLU^2, f32 out) on the persistent GEMM
                                                   (1024, 512, 14336, "bf16")])
 def test_mlp_bit_exact(ctx, m, hidden, inter, dtype):
