@@ -53,14 +53,13 @@ constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
 // 128-expert router runs 2 inlined sigmoids per lane instead of fetching the
 // code of 16).
 template <int S>
-__device__ __forceinline__ void route_token(const RouteArgs& a, int token, int lane) {
+__device__ __forceinline__ void route_token(const RouteArgs& a, int token, int lane, const float (&sc)[S]) {
     const int E = a.experts;
-    const float* s = a.scores + (int64_t)token * E;
     int64_t key[S];
 #pragma unroll
     for (int i = 0; i < S; ++i) {
         const int e = lane + 64 * i;
-        key[i] = e < E ? route_key(sigmoid_f32(s[e]), e) : INT64_MIN;
+        key[i] = e < E ? route_key(sigmoid_f32(sc[i]), e) : INT64_MIN;
     }
     float wsel = 0.0f;  // lane j keeps the j-th selected weight (top_k <= 64)
     int esel = 0;
@@ -94,13 +93,17 @@ __device__ __forceinline__ void route_token(const RouteArgs& a, int token, int l
     }
 }
 
-// With x, the same wave first quantizes the token's row (Q2, the wave form
+// With x, the same wave also quantizes the token's row (Q2, the wave form
 // of nh_quantize_rows_i8: same codes and scales), token-major: the up
-// projection gathers its A rows through the permutation.
-extern "C" __global__ __launch_bounds__(256) void nh_moe_route_sigmoid_kernel(RouteArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int token = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (token >= a.tokens) return;
+// projection gathers its A rows through the permutation.  The token's scores
+// are loaded first, so their round trip to memory overlaps the row's (after
+// the quantizer's code stores, the compiler could not have moved them up).
+template <int S>
+__device__ __forceinline__ void route_kernel_body(const RouteArgs& a, int token, int lane) {
+    float sc[S];
+    const float* s = a.scores + (int64_t)token * a.experts;
+#pragma unroll
+    for (int i = 0; i < S; ++i) sc[i] = lane + 64 * i < a.experts ? s[lane + 64 * i] : 0.0f;
     if (a.x) {
         QuantizeRowsArgs q{};
         q.x = a.x;
@@ -116,12 +119,114 @@ extern "C" __global__ __launch_bounds__(256) void nh_moe_route_sigmoid_kernel(Ro
         else
             quantize_row_wave<DT_F32, 8>(q);
     }
+    route_token<S>(a, token, lane, sc);
+}
+
+extern "C" __global__ __launch_bounds__(256) void nh_moe_route_sigmoid_kernel(RouteArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int token = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (token >= a.tokens) return;
     if (a.experts <= 128)
-        route_token<2>(a, token, lane);
+        route_kernel_body<2>(a, token, lane);
     else if (a.experts <= 256)
-        route_token<4>(a, token, lane);
+        route_kernel_body<4>(a, token, lane);
     else
-        route_token<kMaxExpertsPerLane>(a, token, lane);
+        route_kernel_body<kMaxExpertsPerLane>(a, token, lane);
+}
+
+// R2, one workgroup per expert: the same stable counting sort by (expert,
+// route id) as nh_moe_permute_kernel, every expert's slots computed in
+// parallel.  Thread t owns the L consecutive routes [t L, t L + L) (L = the
+// routes over 256 threads, rounded up to whole 16-byte groups), so the route
+// order is the thread order:
+//  1. each thread counts, over its routes, the valid ids below e and the ids
+//     equal to e;
+//  2. one block scan: the ids below e summed over the block are the
+//     expert's offset, and the exclusive prefix of the equal counts is the
+//     thread's first slot within the expert;
+//  3. each thread walks its routes again and places those of expert e.
+// Expert 0's workgroup also marks the routes whose id lies outside [0, E)
+// (pos = -1, not placed); expert E-1's writes offsets[E].  Up to 16 routes
+// per thread (4096 routes) stay in registers between the passes.  (One wave
+// per expert, ballots over 64 routes per step, was a serial chain of 48
+// steps per pass: 6.5 us inside the kernel at 3072 routes.)
+// Needs 16-byte aligned ids.
+extern "C" __global__ __launch_bounds__(256) void nh_moe_permute_expert_kernel(PermuteArgs a) {
+    __shared__ int wave_eq[4], wave_lt[4];
+    const int e = blockIdx.x, E = a.experts, R = a.routes;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int L = ((R + 255) / 256 + 3) & ~3;
+    const int r0 = tid * L;
+    auto ids4 = [&](int r) {  // ids r .. r + 3, -1 past the routes
+        if (r + 3 < R) return *(const v4i*)(a.indices + r);
+        v4i v;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) v[w] = r + w < R ? a.indices[r + w] : -1;
+        return v;
+    };
+    constexpr int kKept = 4;  // 16-byte groups held in registers
+    v4i kept[kKept];
+    const bool in_regs = L <= 4 * kKept;
+#pragma unroll
+    for (int i = 0; i < kKept; ++i) kept[i] = in_regs && 4 * i < L ? ids4(r0 + 4 * i) : v4i{-1, -1, -1, -1};
+    int lt = 0, eq = 0;
+    auto count = [&](const v4i& v) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            lt += v[w] >= 0 && v[w] < e;
+            eq += v[w] == e;
+        }
+    };
+    if (in_regs) {
+#pragma unroll
+        for (int i = 0; i < kKept; ++i) count(kept[i]);
+    } else {
+        for (int c = 0; c < L; c += 4) count(ids4(r0 + c));
+    }
+    // 2. inclusive scan of eq and sum of lt within the wave, then across the 4 waves
+    int incl = eq, lsum = lt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += t;
+        lsum += __shfl_xor(lsum, off, kWave);
+    }
+    if (lane == 63) wave_eq[wave] = incl;
+    if (lane == 0) wave_lt[wave] = lsum;
+    __syncthreads();
+    int before = 0, total = 0, offset = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        before += w < wave ? wave_eq[w] : 0;
+        total += wave_eq[w];
+        offset += wave_lt[w];
+    }
+    if (tid == 0) {
+        a.offsets[e] = offset;
+        if (e == E - 1) a.offsets[E] = offset + total;
+    }
+    if (total == 0 && e != 0) return;  // uniform
+    // 3.
+    int slot = offset + before + incl - eq;
+    const int rend = min(R, r0 + L);  // past this thread's routes (the held groups past L read -1)
+    auto place = [&](const v4i& v, int r) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            if (v[w] == e) {
+                a.perm[slot] = r + w;
+                a.pos[r + w] = slot;
+                ++slot;
+            } else if (e == 0 && r + w < rend && (v[w] < 0 || v[w] >= E)) {
+                a.pos[r + w] = -1;
+            }
+        }
+    };
+    if (in_regs) {
+#pragma unroll
+        for (int i = 0; i < kKept; ++i) place(kept[i], r0 + 4 * i);
+    } else {
+        for (int c = 0; c < L; c += 4) place(ids4(r0 + c), r0 + c);
+    }
 }
 
 // R2: one workgroup of 1024 threads.  Phase 1 histograms the experts (LDS
@@ -129,104 +234,6 @@ extern "C" __global__ __launch_bounds__(256) void nh_moe_route_sigmoid_kernel(Ro
 // phase 3 walks the routes in order in rounds of 1024 and gives every route
 // its stable rank: inside a wave by ballot-matching equal experts, across
 // waves by handing a running per-expert base from wave to wave in order.
-// R2 in four barriers, for routes x experts that fit a table in LDS: the
-// same stable counting sort by (expert, route id) as nh_moe_permute_kernel.
-//  1. every wave matches the experts of its 64 routes (ballots over the
-//     expert's bits: the lanes holding the same expert) and its leaders
-//     write the per-(round, wave) count of each expert into the table;
-//  2. each expert scans its column of the table in (round, wave) order:
-//     the column entries become the slot bases within the expert, and the
-//     totals the expert counts;
-//  3. wave 0 scans the counts into the offsets;
-//  4. every route takes slot = offsets[e] + base[round][wave][e] + its rank
-//     among the earlier lanes of its wave holding the same expert.
-// Routes are visited in id order within each step, so the slots are the
-// stable order of the per-wave serial kernel.  Table: rounds * NW * E ints.
-extern "C" __global__ __launch_bounds__(1024) void nh_moe_permute_table_kernel(PermuteArgs a) {
-    extern __shared__ int sm[];  // table[rounds][NW][E], then offsets[E]
-    const int E = a.experts, R = a.routes;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NW = blockDim.x >> 6;
-    const int rounds = (R + (int)blockDim.x - 1) / (int)blockDim.x;
-    int* table = sm;
-    int* off = sm + rounds * NW * E;
-    for (int i = tid; i < rounds * NW * E; i += blockDim.x) table[i] = 0;
-    __syncthreads();
-    int nbits = 0;
-    while ((1 << nbits) < E) ++nbits;
-    // the lanes of this wave holding expert e (valid routes only), this lane's rank among them
-    auto match = [&](int r, int* e_out, int* rank, int* cnt, bool* leader) {
-        const int ein = r < R ? a.indices[r] : -1;
-        const bool valid = ein >= 0 && ein < E;
-        const int e = valid ? ein : -1;
-        uint64_t mask = __ballot(valid);
-        for (int b = 0; b < nbits; ++b) {
-            const uint64_t bal = __ballot(valid && ((e >> b) & 1));
-            mask &= ((e >> b) & 1) ? bal : ~bal;
-        }
-        const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-        *e_out = e;
-        *rank = __popcll(mask & lt);
-        *cnt = __popcll(mask);
-        *leader = valid && (mask & lt) == 0;
-    };
-    // 1.
-    for (int rd = 0; rd < rounds; ++rd) {
-        int e, rank, cnt;
-        bool leader;
-        match(rd * (int)blockDim.x + tid, &e, &rank, &cnt, &leader);
-        if (leader) table[(rd * NW + wave) * E + e] = cnt;
-    }
-    __syncthreads();
-    // 2.
-    for (int e = tid; e < E; e += blockDim.x) {
-        int run = 0;
-        for (int i = 0; i < rounds * NW; ++i) {
-            const int c = table[i * E + e];
-            table[i * E + e] = run;
-            run += c;
-        }
-        off[e] = run;
-    }
-    __syncthreads();
-    // 3.
-    if (wave == 0) {
-        int carry = 0;
-        for (int base = 0; base < E; base += 64) {
-            const int e = base + lane;
-            const int c = e < E ? off[e] : 0;
-            int v = c;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int t = __shfl_up(v, o, kWave);
-                if (lane >= o) v += t;
-            }
-            if (e < E) {
-                off[e] = carry + v - c;
-                a.offsets[e] = carry + v - c;
-            }
-            carry += __shfl(v, 63, kWave);
-        }
-        if (lane == 0) a.offsets[E] = carry;
-    }
-    __syncthreads();
-    // 4.
-    for (int rd = 0; rd < rounds; ++rd) {
-        const int r = rd * (int)blockDim.x + tid;
-        int e, rank, cnt;
-        bool leader;
-        match(r, &e, &rank, &cnt, &leader);
-        if (r < R) {
-            if (e < 0) {
-                a.pos[r] = -1;  // an expert id outside [0, E) is not placed
-            } else {
-                const int slot = off[e] + table[(rd * NW + wave) * E + e] + rank;
-                a.perm[slot] = r;
-                a.pos[r] = slot;
-            }
-        }
-    }
-}
-
 extern "C" __global__ __launch_bounds__(1024) void nh_moe_permute_kernel(PermuteArgs a) {
     extern __shared__ int sm[];  // counts[E], base[E]
     const int E = a.experts, R = a.routes;
@@ -513,10 +520,8 @@ __device__ __forceinline__ void expert_stream(const ExpertGemmArgs& a, v4i (&b0)
         for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float m = rmax[rb][r];
-#pragma unroll
-                for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
-                if (r16 == 0) atomicMax(&lmax[rb * 16 + 4 * g + r], f32_bits(m));
+                const uint32_t m = row16_max_u32(f32_bits(rmax[rb][r]));  // DPP, within the 16-lane row
+                if (r16 == 0) atomicMax(&lmax[rb * 16 + 4 * g + r], m);
             }
     }
 }

@@ -18,17 +18,13 @@ constexpr int kWave = 64;
 // touching memory.
 constexpr int kOutOfRange = 0x7ffffff0;
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-    return v;
-}
+__device__ __forceinline__ uint32_t wave_max_dpp_u32(uint32_t v);
+__device__ __forceinline__ int wave_min_dpp_i32(int v);
 
-__device__ __forceinline__ int wave_min_i32(int v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = min(v, __shfl_xor(v, off, kWave));
-    return v;
-}
+// Wave maximum of non-negative floats (their bits order like the values).
+__device__ __forceinline__ float wave_max(float v) { return f32_from_bits(wave_max_dpp_u32(f32_bits(v))); }
+
+__device__ __forceinline__ int wave_min_i32(int v) { return wave_min_dpp_i32(v); }
 
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
@@ -74,11 +70,7 @@ __device__ __forceinline__ void store_out(void* p, int64_t i, float v, int dtype
 
 __device__ __forceinline__ bool is_finite_f32(float v) { return (f32_bits(v) & 0x7f800000u) != 0x7f800000u; }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, kWave));
-    return v;
-}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { return wave_max_dpp_u32(v); }
 
 // The same maximum through DPP lane moves (no LDS round trips): within rows
 // of 16 lanes by quad permutes and row rotates, then across rows by the
@@ -93,6 +85,17 @@ __device__ __forceinline__ uint32_t wave_max_dpp_u32(uint32_t v) {
     v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xa, 0xf, false));  // row_bcast 15
     v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xc, 0xf, false));  // row_bcast 31
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// The wave minimum of ints, by the same lane moves.
+__device__ __forceinline__ int wave_min_dpp_i32(int v) {
+    v = min(v, __builtin_amdgcn_update_dpp(v, v, 0xb1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+    v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x4e, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+    v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xf, 0xf, false));  // row_ror 4
+    v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));  // row_ror 8
+    v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xa, 0xf, false));  // row_bcast 15
+    v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xc, 0xf, false));  // row_bcast 31
+    return __builtin_amdgcn_readlane(v, 63);
 }
 
 // Maximum over each row of 16 lanes (every lane of the row gets it).

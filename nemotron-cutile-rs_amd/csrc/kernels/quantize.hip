@@ -255,6 +255,12 @@ extern "C" __global__ __launch_bounds__(1024) void nh_quantize_rows_long_kernel(
 extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_pmax_kernel(QuantizePmaxArgs a) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.y;
+    const int chunks = a.cols >> 2;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    // the chunk first (out of range past the row: zeros, no traffic), so
+    // its round trip overlaps the partial maxima's
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + (int64_t)row * a.cols, (uint32_t)a.cols * 4u);
+    const v4i v = buffer_load16(xr, c < chunks ? c * 16 : kOutOfRange);
     uint32_t m = 0;
     for (int g = lane; g < a.groups; g += 64) m = max(m, a.pmax[(int64_t)g * a.rows + row]);
     m = wave_max_dpp_u32(m);
@@ -262,10 +268,7 @@ extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_pmax_kernel(Q
     if (blockIdx.x == 0 && threadIdx.x == 0) a.scales[row] = s;
     const float rcp = s > 0.0f ? 1.0f / s : 0.0f;
     const bool pow2 = scale_is_pow2(s);
-    const int chunks = a.cols >> 2;
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= chunks) return;
-    const v4i v = __builtin_bit_cast(v4i, *(const int4*)(a.x + (int64_t)row * a.cols + c * 4));
     if (a.nonfinite) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {

@@ -753,11 +753,12 @@ nh_status nh_moe_permute(nh_context* ctx, const int32_t* indices, size_t tokens,
     nh_status st = bind_device(ctx, err);
     if (st) return st;
     PermuteArgs a{indices, offsets, perm, pos, (int)routes, (int)experts};
-    // the table form when rounds x 16 waves x experts fits in 48 KiB of LDS
-    // (3072 routes x 128 experts: 24 KiB), else the per-wave serial form
-    const size_t rounds = (routes + 1023) / 1024;
-    const size_t table = (rounds * 16 * experts + experts) * sizeof(int);
-    if (table <= 48 * 1024) return launch(ctx, K_PERMUTE_TABLE, 1, 1024, table, stream, a, err);
+    // one workgroup per expert while their reads of the ids stay small
+    // (experts x routes <= 4M: 16 MiB of L2 reads; the 512-token top-6 layer
+    // with 128 experts reads 1.5 MiB) and the ids are 16-byte aligned, else
+    // the single-workgroup form
+    if (experts * routes <= ((size_t)1 << 22) && aligned16(indices))
+        return launch(ctx, K_PERMUTE_EXPERT, (unsigned)experts, 256, 0, stream, a, err);
     return launch(ctx, K_PERMUTE, 1, 1024, 2 * experts * sizeof(int), stream, a, err);
 }
 

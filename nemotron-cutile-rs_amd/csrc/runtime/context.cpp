@@ -52,7 +52,7 @@ const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
     "nh_linear_decode_w4a8_m1_kernel",   // K_LINEAR_DECODE_W4_M1
     "nh_linear_decode_w4a8_row2_kernel", // K_LINEAR_DECODE_W4_ROW2
     "nh_linear_decode_w4a8_row4_kernel", // K_LINEAR_DECODE_W4_ROW4
-    "nh_moe_permute_table_kernel",       // K_PERMUTE_TABLE
+    "nh_moe_permute_expert_kernel",      // K_PERMUTE_EXPERT
     "nh_moe_combine4_kernel",            // K_COMBINE4
     "nh_gemm_w8a8_p256x224_kernel",      // K_GEMM_P224
 };

@@ -54,7 +54,7 @@ enum KernelId : int {
     K_LINEAR_DECODE_W4_M1,    // W4A8 decode unit, 1 row
     K_LINEAR_DECODE_W4_ROW2,  // 2 rows
     K_LINEAR_DECODE_W4_ROW4,  // 4 rows
-    K_PERMUTE_TABLE,          // R2 in four barriers
+    K_PERMUTE_EXPERT,         // R2, one workgroup per expert
     K_COMBINE4,               // R4, four columns per thread
     K_GEMM_P224,              // persistent G3, 256 x 224 tiles, tiled A
     K_COUNT

@@ -617,7 +617,9 @@ def test_route_reference_kats_on_device(ctx):
 
 
 @pytest.mark.parametrize("t,k,e", [(512, 6, 128), (1, 1, 1), (1000, 8, 64), (3, 2, 1000), (2000, 6, 128),
-                                   (300, 2, 3)])  # the last: long same-expert runs inside every wave
+                                   (300, 2, 3),  # long same-expert runs inside every wave
+                                   (600, 5, 100), (700, 8, 16),
+                                   (70000, 8, 8)])  # experts x routes past the one-wave-per-expert form
 def test_permute_bit_exact(ctx, t, k, e):
     note(f"permute t={t} k={k} e={e}")
     rng = np.random.default_rng(t + e)
@@ -632,6 +634,33 @@ def test_permute_bit_exact(ctx, t, k, e):
     assert np.array_equal(off.numpy(), ref[0])
     assert np.array_equal(perm.numpy(), ref[1])
     assert np.array_equal(pos.numpy(), ref[2])
+
+
+@pytest.mark.parametrize("t,k,e", [(512, 6, 128), (40, 3, 5)])
+def test_permute_ids_outside_the_experts(ctx, t, k, e):
+    """Expert ids outside [0, E) are not placed (pos = -1) and take no slot;
+    the valid routes keep the stable (expert, route id) order."""
+    note(f"permute invalid ids t={t} k={k} e={e}")
+    rng = np.random.default_rng(7 + e)
+    idx = rng.integers(0, e, size=t * k).astype(np.int32)
+    bad = rng.choice(t * k, size=t * k // 7, replace=False)
+    idx[bad] = rng.choice([-1, -5, e, e + 3], size=bad.size)
+    valid = (idx >= 0) & (idx < e)
+    order = sorted(np.flatnonzero(valid).tolist(), key=lambda r: (idx[r], r))
+    want_off = np.zeros(e + 1, np.int32)
+    np.add.at(want_off, idx[valid] + 1, 1)
+    want_off = np.cumsum(want_off).astype(np.int32)
+    want_pos = np.full(t * k, -1, np.int32)
+    want_pos[order] = np.arange(len(order), dtype=np.int32)
+    di = ctx.upload(idx)
+    off = ctx.empty(e + 1, np.int32)
+    perm = ctx.empty(t * k, np.int32)
+    pos = ctx.empty(t * k, np.int32)
+    NH.call("nh_moe_permute", ctx.handle, di.ptr, t, k, e, off.ptr, perm.ptr, pos.ptr, None)
+    ctx.synchronize()
+    assert np.array_equal(off.numpy(), want_off)
+    assert np.array_equal(perm.numpy()[:len(order)], np.array(order, np.int32))
+    assert np.array_equal(pos.numpy(), want_pos)
 
 
 @pytest.mark.parametrize("tokens,top_k,hidden", [(512, 6, 2688), (7, 3, 37), (5, 2, 8)])
