@@ -522,7 +522,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["moe", "gemm", "stack", "decode", "w8a32", "w4a8"], default=None,
+    ap.add_argument("--only", choices=["moe", "moe_shared", "gemm", "stack", "decode", "w8a32", "w4a8"], default=None,
                     help="run one secondary workload only (for profiling) and print its figures")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (torch's copy kernel), the "
@@ -574,8 +574,8 @@ def main():
     b = Bench()
     if args.only:
         res = {}
-        if args.only == "moe":
-            t, mbytes, mops = b.moe(10, 2)
+        if args.only in ("moe", "moe_shared"):
+            t, mbytes, mops = b.moe(10, 2, shared_inter=3712 if args.only == "moe_shared" else 0)
             res = {"us": round(t * 1e3, 1), "GBps": round(mbytes / (t * 1e-3) / 1e9, 1)}
         elif args.only == "gemm":
             for (mm, nn, kk) in [(2048, 4096, 4096), (2048, 21504, 4096), (2048, 4096, 21504)]:

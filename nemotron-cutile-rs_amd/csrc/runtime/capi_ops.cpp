@@ -232,7 +232,8 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
         return launch(ctx, K_GEMM_P224, grid, 512u, kP224Lds, stream, a, err);
     }
     // Tile choice: 256x128 (8 compute + 8 loader waves) unless that leaves
-    // most CUs idle, then 128x128 (more, smaller tiles).
+    // most CUs idle, then 128x128 (more, smaller tiles), and with tiled A
+    // 64x128 where even 128x128 tiles fill less than half the CUs.
     struct Cfg {
         KernelId id;
         int bm, bn, threads;
@@ -242,9 +243,12 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
     const Cfg small = a_tiled ? Cfg{K_GEMM_TA_128, 128, 128, 512, gemm_lds_bytes(128, 128, 3, 4, 64)}
                               : Cfg{K_GEMM_W8A8_128, 128, 128, 256, gemm_lds_bytes(128, 128, 3, 4, 64)};
     auto tiles = [&](const Cfg& c) { return (int64_t)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn); };
+    const Cfg tiny = {K_GEMM_TA_64, 64, 128, 384, gemm_lds_bytes(64, 128, 3, 4, 64)};
     const Cfg* cfg = nullptr;
     if (tiles(big) >= ctx->cu_count / 4 && big.lds <= ctx->max_shared_per_block)
         cfg = &big;
+    else if (a_tiled && tiles(small) < ctx->cu_count / 2 && tiny.lds <= ctx->max_shared_per_block)
+        cfg = &tiny;
     else if (small.lds <= ctx->max_shared_per_block)
         cfg = &small;
     if (!cfg) {

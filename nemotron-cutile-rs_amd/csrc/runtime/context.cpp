@@ -55,6 +55,7 @@ const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
     "nh_moe_permute_expert_kernel",      // K_PERMUTE_EXPERT
     "nh_moe_combine4_kernel",            // K_COMBINE4
     "nh_gemm_w8a8_p256x224_kernel",      // K_GEMM_P224
+    "nh_gemm_w8a8_ta_64x128_kernel",     // K_GEMM_TA_64
 };
 
 void clear_error(nh_error* err) {

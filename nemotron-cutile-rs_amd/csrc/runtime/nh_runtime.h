@@ -57,6 +57,7 @@ enum KernelId : int {
     K_PERMUTE_EXPERT,         // R2, one workgroup per expert
     K_COMBINE4,               // R4, four columns per thread
     K_GEMM_P224,              // persistent G3, 256 x 224 tiles, tiled A
+    K_GEMM_TA_64,             // G3, 64 x 128 tiles, tiled A
     K_COUNT
 };
 

@@ -385,7 +385,9 @@ def mlp_weights(hidden, inter):
                                                   (6, 512, 1872, "bf16"), (7, 1024, 4096, "bf16"),
                                                   (12, 1024, 2048, "bf16"), (4, 4096, 1024, "bf16"),
                                                   # the up projection (bias, ReLU^2, f32 out) on the persistent GEMM
-                                                  (1024, 512, 14336, "bf16")])
+                                                  (1024, 512, 14336, "bf16"),
+                                                  # the MoE layer's shared expert on 64 x 128 tiles
+                                                  (512, 2688, 3712, "bf16")])
 def test_mlp_bit_exact(ctx, m, hidden, inter, dtype):
     note(f"mlp_w8a8 m={m} hidden={hidden} inter={inter} {dtype}")
     w_up, s_up, w_down, s_down = mlp_weights(hidden, inter)
