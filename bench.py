@@ -582,7 +582,8 @@ def main():
                 t, t_rm = b.gemm(mm, nn, kk, 50, 5)
                 res[f"m{mm}_n{nn}_k{kk}"] = {"us": round(t * 1e3, 1), "row_major_a_us": round(t_rm * 1e3, 1)}
         elif args.only == "w4a8":
-            for (mm, nn, kk) in [(1, 16384, 4096), (4, 16384, 4096), (8, 16384, 4096), (1, 4096, 8192)]:
+            for (mm, nn, kk) in [(1, 16384, 4096), (4, 16384, 4096), (8, 16384, 4096), (16, 16384, 4096),
+                                 (1, 4096, 8192)]:
                 res[f"m{mm}_k{kk}_n{nn}"] = round(b.w4a8(mm, nn, kk, 50, 5) * 1e3, 2)
         elif args.only == "w8a32":
             res = {"us": round(b.w8a32(4096, 4096, 200, 20) * 1e3, 2)}
@@ -616,7 +617,8 @@ def main():
         extra["decode_sweep"] = sweep
         del pool
         w4 = {}
-        for (mm, nn, kk) in [(1, 16384, 4096), (4, 16384, 4096), (8, 16384, 4096), (1, 4096, 8192)]:
+        for (mm, nn, kk) in [(1, 16384, 4096), (4, 16384, 4096), (8, 16384, 4096), (16, 16384, 4096),
+                             (1, 4096, 8192)]:
             log(f"[bench] w4a8 decode m={mm} k={kk} n={nn}")
             t = b.w4a8(mm, nn, kk, max(20, args.steps), 5)
             # int4 codes + bf16 x + bf16 y + f32 token scales (one scale and zero point per tensor)

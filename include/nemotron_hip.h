@@ -377,8 +377,9 @@ nh_status nh_tile_weights_int4_host(const uint8_t *packed, size_t packed_len, si
  * exact) on per-token Q2 codes of x, y = ((float)acc * sx) * scale [+ bias].
  * Two device forms:
  *  * bf16 x with nh_supports_linear_w4a8(m, n, k) (m <= 16, k <= 8192,
- *    k % 16 == 0): the fused decode unit streams the 4-bit weights (groups of
- *    4 rows, each streaming them once); workspace may be NULL;
+ *    k % 16 == 0): the fused decode unit streams the 4-bit weights once (3..16
+ *    rows with k % 512 == 0 and k <= 4096 in one launch, else groups of 4
+ *    rows, each streaming them once); workspace may be NULL;
  *  * otherwise (f32 x, prefill-sized m, longer K; k % 16 == 0 and the W8A8
  *    GEMM envelope): the weights are expanded into int8 tiles of code - zp
  *    in the workspace (nh_linear_w4a8_workspace_size(m, n, k) bytes, 16-byte

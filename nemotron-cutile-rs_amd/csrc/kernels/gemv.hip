@@ -787,6 +787,12 @@ extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_stream_w4_m8
     linear_decode_stream<8, 4, 4, 2, true>(a, lds);
 }
 
+// And for 9..16 rows (the row-group form took one launch per 4 rows).
+extern "C" __global__ __launch_bounds__(1024) void nh_linear_decode_stream_w4_m16_kernel(LinearDecodeArgs a) {
+    extern __shared__ __align__(16) int8_t lds[];
+    linear_decode_stream<16, 8, 4, 2, true>(a, lds);
+}
+
 // G2: W8A32 dequant GEMV, y[m][n] = sum_k x[m][k] * q[n][k] * s[n].  The
 // reference materialises W' = (float)q * s and sums x * W' in f64
 // (linear.rs:126-131, gemm.rs:99-109).  Here each lane sums the 16 products

@@ -424,8 +424,8 @@ nh_status nh_linear_w4a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
     const size_t esz = out_dtype == NH_BF16 ? 2 : 4;
     DecodePlan plan;
     unsigned grid = 0;
-    if (m <= 8 && plan_stream(ctx, m, n, k, &plan, &grid)) {
-        // 3..8 rows: the streaming unit, the INT4 weights streamed once
+    if (plan_stream(ctx, m, n, k, &plan, &grid)) {
+        // 3..16 rows: the streaming unit, the INT4 weights streamed once
         LinearDecodeArgs a{};
         a.x = x;
         a.wq = (const int8_t*)w4_tiled;
@@ -441,7 +441,9 @@ nh_status nh_linear_w4a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
         a.w4_zp = (int)zero_point;
         a.w4_scale = scale;
         a.nonfinite = nonfinite;
-        const KernelId kid = m <= 4 ? K_LINEAR_DECODE_STREAM_W4_M4 : K_LINEAR_DECODE_STREAM_W4_M8;
+        const KernelId kid = m <= 4 ? K_LINEAR_DECODE_STREAM_W4_M4
+                             : m <= 8 ? K_LINEAR_DECODE_STREAM_W4_M8
+                                      : K_LINEAR_DECODE_STREAM_W4_M16;
         return launch(ctx, kid, grid, 1024u, plan.lds, stream, a, err);
     }
     // groups of up to 4 rows, each a launch that streams the weights once

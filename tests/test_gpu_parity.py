@@ -487,11 +487,12 @@ def test_gemv_w8a32_within_tolerance(ctx, m, n, k):
                                             (2, 100, 1040, 15, "bf16"), (3, 4096, 4096, 7, "bf16"),
                                             (4, 33, 64, 8, "bf16"), (7, 4096, 4096, 3, "bf16"),
                                             (16, 1000, 2048, 9, "bf16"),
-                                            # the streaming unit on INT4 tiles (3..8 rows, K % 512 == 0,
+                                            # the streaming unit on INT4 tiles (3..16 rows, K % 512 == 0,
                                             # K <= 4096): bias, fewer N tiles than CUs, a ragged N over
                                             # several rounds, zero points 0 and 15, K = 512
                                             (5, 1000, 512, 4, "bf16"), (8, 16384, 4096, 8, "bf16"),
                                             (6, 100, 2048, 15, "bf16"), (4, 21520, 1024, 0, "bf16"),
+                                            (12, 16384, 4096, 1, "bf16"), (9, 6000, 512, 15, "bf16"),
                                             # the expanded form: f32 rows, K past the fused unit's 8192,
                                             # prefill-sized M on the GEMM (M and N tails)
                                             (3, 1000, 2048, 6, "f32"), (1, 600, 16384, 5, "bf16"),
