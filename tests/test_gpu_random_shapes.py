@@ -1,13 +1,15 @@
-"""Seeded random shapes through the linear, MLP and W4A8 entry points, checked
-against the oracle bit-exactly (the bar of test_gpu_parity.py).
+"""Seeded random shapes through the linear, MLP, W4A8 and MoE entry points,
+checked against the oracle bit-exactly (the bar of test_gpu_parity.py).
 
 The fixed-shape tests pin each kernel at the shapes it was written for; these
 draws cross the dispatch boundaries in combinations nobody picked: rows across
 1..16 (the one-tile, wide and streaming decode units, the two-launch GEMV),
 17..513 (the GEMM on 64 x 128, 128 x 128 and 256 x 128 tiles), K on both sides
 of 512-multiples, 4096 and 8192, ragged N from one tile to several rounds of
-CUs, bf16 and f32 rows, bf16 and f32 outputs, with and without bias.  Each
-case is reproducible from its index (numpy's default_rng(seed)).
+CUs, bf16 and f32 rows, bf16 and f32 outputs, with and without bias; MoE
+layers from 2 to 160 experts, top-1..8, with and without renormalization and
+routed scaling, several passes of rows per expert.  Each case is reproducible
+from its index (numpy's default_rng(seed)).
 """
 import sys
 
@@ -157,4 +159,57 @@ def test_linear_w4a8_random_shapes_bit_exact(ctx, case):
     ctx.synchronize()
     st, ref = O.linear_w4a8(x, packed, n, scale, zp, bias=bias, out_bf16=True)
     assert st == O.OK
+    assert np.array_equal(out.numpy(), ref)
+
+
+def draw_moe(i):
+    rng = np.random.default_rng(10000 + i)
+    while True:
+        experts = int(rng.choice([2, 5, 8, 16, 64, 128, 160]))
+        top_k = int(rng.integers(1, min(8, experts) + 1))
+        tokens = int(rng.integers(1, 600))
+        hidden = int(rng.integers(1, 129)) * 16
+        inter = int(rng.integers(1, 129)) * 16
+        if experts * hidden * inter <= 200_000_000 and tokens * top_k * hidden * inter <= 3_000_000_000:
+            break
+    renorm = int(rng.random() < 0.7)
+    scaling = float(rng.choice([1.0, 2.5]))
+    return tokens, hidden, inter, experts, top_k, renorm, scaling, int(rng.integers(0, 1 << 30))
+
+
+@pytest.mark.parametrize("case", range(10))
+def test_moe_forward_random_shapes_bit_exact(ctx, case):
+    """nh_moe_forward_w8a8 (route, permute, up with ReLU^2, the fused
+    requantization, down, combine) against the oracle's composition."""
+    from exact_int import moe_forward_exact
+    from tiling import tile_experts
+    tokens, hidden, inter, experts, top_k, renorm, scaling, seed = draw_moe(case)
+    note(f"random moe #{case}: t={tokens} h={hidden} i={inter} e={experts} k={top_k} renorm={renorm} "
+         f"scaling={scaling}")
+    rng = np.random.default_rng(seed)
+    x = O.to_bf16(O.normal_f32(seed + 1, tokens * hidden)).reshape(tokens, hidden)
+    logits = O.normal_f32(seed + 2, tokens * experts)
+    up = rng.integers(-127, 128, size=(experts, inter, hidden), dtype=np.int8)
+    down = rng.integers(-127, 128, size=(experts, hidden, inter), dtype=np.int8)
+    su = rng.uniform(1e-4, 1e-3, size=(experts, inter)).astype(np.float32)
+    sd = rng.uniform(1e-4, 1e-3, size=(experts, hidden)).astype(np.float32)
+    ref, idx, w, offsets, perm, pos, _, _ = moe_forward_exact(x, logits, up, su, down, sd, top_k,
+                                                              renormalize=bool(renorm), scaling=scaling)
+    ws_bytes = NH.lib().nh_moe_forward_w8a8_workspace_size(tokens, hidden, inter, experts, top_k)
+    ws = ctx.empty(ws_bytes, np.uint8)
+    ws.fill_bytes(0xa5)
+    dx, dl = ctx.upload(x), ctx.upload(logits)
+    dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
+    out = ctx.empty((tokens, hidden), np.uint16)
+    NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k,
+            renorm, scaling, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, None, None)
+    ctx.synchronize()
+    import ctypes
+    lay = (ctypes.c_size_t * 5)()
+    NH.lib().nh_moe_workspace_layout(tokens, hidden, inter, experts, top_k, lay)
+    wsh = ws.numpy()
+    routes = tokens * top_k
+    assert np.array_equal(wsh[lay[0]:lay[0] + 4 * routes].view(np.int32), idx)
+    assert np.array_equal(wsh[lay[2]:lay[2] + 4 * (experts + 1)].view(np.int32), offsets)
+    assert np.array_equal(wsh[lay[3]:lay[3] + 4 * routes].view(np.int32), perm)
     assert np.array_equal(out.numpy(), ref)
