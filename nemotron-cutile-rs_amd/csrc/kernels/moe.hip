@@ -114,6 +114,8 @@ __device__ __forceinline__ void route_kernel_body(const RouteArgs& a, int token,
         q.x_dtype = a.x_dtype;
         q.nonfinite = a.nonfinite;
         q.nonfinite_stage = 0;
+        q.q_act = a.xq_tiles;
+        q.act_p = 16;
         if (a.x_dtype == DT_BF16)
             quantize_row_wave<DT_BF16, 8>(q);
         else

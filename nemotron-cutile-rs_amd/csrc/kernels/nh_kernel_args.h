@@ -210,6 +210,9 @@ struct RouteArgs {
     uint64_t* nonfinite;
     int32_t x_dtype;
     int32_t hidden;
+    // with x: the same codes also into MFMA A tiles of 16 rows (the layout
+    // of the linear path's quantizer) for a GEMM over all tokens, or null
+    int8_t* xq_tiles;
 };
 
 // R2: counting-sort permutation, one workgroup.

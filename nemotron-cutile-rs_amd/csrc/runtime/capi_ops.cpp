@@ -745,7 +745,7 @@ nh_status nh_moe_route_sigmoid_topk(nh_context* ctx, const float* scores, size_t
     if (st) return st;
     if (tokens == 0) return NH_OK;
     RouteArgs a{scores, indices, weights, (int)tokens, (int)experts, (int)top_k, renormalize ? 1 : 0, scaling, 0,
-                nullptr, nullptr, nullptr, nullptr, 0, 0};
+                nullptr, nullptr, nullptr, nullptr, 0, 0, nullptr};
     return launch(ctx, K_ROUTE_SIGMOID, (unsigned)((tokens + 3) / 4), 256, 0, stream, a, err);
 }
 
@@ -982,25 +982,48 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
     const size_t R = tokens * top_k;
     nh_status st;
     if ((st = check_dtype(x_dtype, err))) return st;
-    if (has_shared &&
-        (st = nh_mlp_w8a8(ctx, x, x_dtype, w_up_sh, s_up_sh, nullptr, w_down_sh, s_down_sh, nullptr, tokens, hidden,
-                          inter_sh, shared, NH_F32, ws + shared_at + shared_bytes, workspace_bytes - shared_at -
-                          shared_bytes, nonfinite, stream, err)))
-        return st;
     const bool fused = expert_fused_ok(ctx, R, experts, hidden, inter, w_up, w_down);
     const size_t esz = x_dtype == NH_BF16 ? 2 : 4;
     // the routing wave of each token also quantizes its row (token-major)
     // when the row fits the wave quantizer; the up projection then gathers
     const bool route_q = fused && aligned16(x) && (hidden * esz) % 16 == 0 && hidden * esz <= 512 * 16 &&
                          experts <= 1024 && top_k <= 64 && tokens <= (size_t)kMaxGrid / 4;
+    // The shared expert (an MLP over every token).  Past the GEMV's 16 rows
+    // its up projection is a GEMM on A tiles of the same codes, so the
+    // routing kernel writes them too (into the tiles of the MLP's workspace)
+    // and the MLP's own quantization of x is skipped (512 tokens: 7.8 us).
+    char* mlp_ws = ws + shared_at + shared_bytes;
+    const size_t mlp_bytes = has_shared ? workspace_bytes - shared_at - shared_bytes : 0;
+    const bool shared_tiles = has_shared && route_q && tokens > kTiledActRows && aligned16(w_up_sh) &&
+                              aligned16(w_down_sh) && check_w8a8_shape(tokens, inter_sh, hidden, nullptr) == NH_OK &&
+                              check_w8a8_shape(tokens, hidden, inter_sh, nullptr) == NH_OK;
+    float* h_sh = (float*)mlp_ws;
+    char* lin_sh = mlp_ws + align256(tokens * inter_sh * sizeof(float)) +
+                   align256(kMaxStreamGroups * 8 * sizeof(uint32_t));  // nh_mlp_w8a8's layout
+    if (has_shared && !shared_tiles &&
+        (st = nh_mlp_w8a8(ctx, x, x_dtype, w_up_sh, s_up_sh, nullptr, w_down_sh, s_down_sh, nullptr, tokens, hidden,
+                          inter_sh, shared, NH_F32, mlp_ws, mlp_bytes, nonfinite, stream, err)))
+        return st;
     if (route_q) {
         if ((st = bind_device(ctx, err))) return st;
         RouteArgs ra{logits, idx, wts, (int)tokens, (int)experts, (int)top_k, renormalize ? 1 : 0, scaling, 0,
-                     x, xq, sx, nonfinite, x_dtype == NH_BF16 ? DT_BF16 : DT_F32, (int)hidden};
+                     x, xq, sx, nonfinite, x_dtype == NH_BF16 ? DT_BF16 : DT_F32, (int)hidden,
+                     shared_tiles ? (int8_t*)lin_sh : nullptr};
         if ((st = launch(ctx, K_ROUTE_SIGMOID, (unsigned)((tokens + 3) / 4), 256, 0, stream, ra, err))) return st;
     } else if ((st = nh_moe_route_sigmoid_topk(ctx, logits, tokens, experts, top_k, renormalize, scaling, idx, wts,
                                                stream, err))) {
         return st;
+    }
+    if (shared_tiles) {
+        // nh_mlp_w8a8's steps from the tiles on: up (ReLU^2, f32 h), then the
+        // linear path on h (its quantization: the layer's intermediate)
+        if ((st = launch_gemm(ctx, (const int8_t*)lin_sh, sx, w_up_sh, s_up_sh, nullptr, (int)tokens, (int)inter_sh,
+                              (int)hidden, h_sh, NH_F32, 1, stream, err, true)))
+            return st;
+        const size_t lin_bytes = mlp_bytes - (size_t)(lin_sh - mlp_ws);
+        if ((st = linear_w8a8(ctx, h_sh, NH_F32, w_down_sh, s_down_sh, nullptr, tokens, hidden, inter_sh, shared,
+                              NH_F32, lin_sh, lin_bytes, nullptr, nullptr, 0, nonfinite, 1, stream, err)))
+            return st;
     }
     if ((st = nh_moe_permute(ctx, idx, tokens, top_k, experts, offsets, perm, pos, stream, err))) return st;
     // otherwise Q2 of each route's token, written in expert order (slot s =
