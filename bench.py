@@ -607,8 +607,10 @@ def main():
     extra = {}
     if not args.quick:
         sweep = {}
-        for (mm, nn, kk) in [(4, 16384, 4096), (8, 16384, 4096), (16, 16384, 4096), (1, 4096, 8192),
-                             (4, 4096, 8192), (8, 4096, 8192), (16, 4096, 8192)]:
+        # (32..128 rows: batched decode on the GEMM's small tiles)
+        for (mm, nn, kk) in [(4, 16384, 4096), (8, 16384, 4096), (16, 16384, 4096), (32, 16384, 4096),
+                             (64, 16384, 4096), (128, 16384, 4096), (1, 4096, 8192), (4, 4096, 8192),
+                             (8, 4096, 8192), (16, 4096, 8192)]:
             log(f"[bench] decode m={mm} k={kk} n={nn}")
             p = pool if (nn, kk) == (n, k) else None
             t, _, _, _ = b.decode(mm, nn, kk, max(20, args.steps), 5, pool=p)

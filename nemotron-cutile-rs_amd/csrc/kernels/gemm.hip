@@ -365,13 +365,23 @@ extern "C" __global__ __launch_bounds__(512) void nh_gemm_w8a8_ta_128x128_kernel
 }
 
 // 64 x 128 tiles, tiled A: 4 compute waves of 32 x 64 + 2 loader waves, for
-// products whose 128 x 128 tiles would leave most CUs idle (M = 512 with
-// N = 2688 or 3712: 84 or 116 tiles on 256 CUs; the MoE layer's shared
-// expert took 338 -> 327 us).  Four compute waves keep every SIMD's MFMA
-// unit busy (two waves of 64 x 64: 337 us).
+// products whose 128 x 128 tiles would leave CUs idle (M = 128 at N = 16384:
+// 256 workgroups; M = 512 with N = 2688 or 3712 took these before the 64 x 64
+// tiles: the MoE layer's shared expert 338 -> 327 us against 128 x 128).
+// Four compute waves keep every SIMD's MFMA unit busy (two waves of 64 x 64:
+// 337 us).
 extern "C" __global__ __launch_bounds__(384) void nh_gemm_w8a8_ta_64x128_kernel(GemmW8A8Args a) {
     extern __shared__ __align__(1024) int8_t smem[];
     gemm_ws<64, 128, 2, 2, 3, 2, true>(a, smem);
+}
+
+// 64 x 64 tiles, tiled A: 4 compute waves of 32 x 32 + 2 loader waves, for
+// products with few rows whose larger tiles leave CUs idle (batched decode
+// past 16 rows: M = 24..64 at 4096 -> 16384 on 256 workgroups, 32.5 -> 23.3 us
+// against 128 workgroups of 64 x 128; the weight stream is the bound there).
+extern "C" __global__ __launch_bounds__(384) void nh_gemm_w8a8_ta_64x64_kernel(GemmW8A8Args a) {
+    extern __shared__ __align__(1024) int8_t smem[];
+    gemm_ws<64, 64, 2, 2, 3, 2, true>(a, smem);
 }
 
 // 128 x 128 tiles, row-major A, 4 waves of 64 x 64, 3 stages (single-role).

@@ -231,9 +231,12 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
         const unsigned grid = (unsigned)std::min<int64_t>(tiles, ctx->cu_count);
         return launch(ctx, K_GEMM_P224, grid, 512u, kP224Lds, stream, a, err);
     }
-    // Tile choice: 256x128 (8 compute + 8 loader waves) unless that leaves
-    // most CUs idle, then 128x128 (more, smaller tiles), and with tiled A
-    // 64x128 where even 128x128 tiles fill less than half the CUs.
+    // Tile choice.  Tiled A: the largest of 256x128 (8 compute + 8 loader
+    // waves), 128x128, 64x128 and 64x64 whose tiles fill every CU, else
+    // 64x64 (the most tiles): M = 128 at 4096 -> 16384 took 34.4 us on 128
+    // workgroups of 256x128 and 28.5 on 256 of 64x128; M = 256 41.0 -> 35.0 on
+    // 128x128.  Row-major A: 256x128 unless that leaves most CUs idle, then
+    // 128x128.
     struct Cfg {
         KernelId id;
         int bm, bn, threads;
@@ -244,13 +247,17 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
                               : Cfg{K_GEMM_W8A8_128, 128, 128, 256, gemm_lds_bytes(128, 128, 3, 4, 64)};
     auto tiles = [&](const Cfg& c) { return (int64_t)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn); };
     const Cfg tiny = {K_GEMM_TA_64, 64, 128, 384, gemm_lds_bytes(64, 128, 3, 4, 64)};
+    const Cfg tiny2 = {K_GEMM_TA_6464, 64, 64, 384, gemm_lds_bytes(64, 64, 3, 4, 32)};
     const Cfg* cfg = nullptr;
-    if (tiles(big) >= ctx->cu_count / 4 && big.lds <= ctx->max_shared_per_block)
+    if (a_tiled) {
+        for (const Cfg* c : {&big, &small, &tiny, &tiny2})
+            if (!cfg && tiles(*c) >= ctx->cu_count && c->lds <= ctx->max_shared_per_block) cfg = c;
+        if (!cfg && tiny2.lds <= ctx->max_shared_per_block) cfg = &tiny2;
+    } else if (tiles(big) >= ctx->cu_count / 4 && big.lds <= ctx->max_shared_per_block) {
         cfg = &big;
-    else if (a_tiled && tiles(small) < ctx->cu_count / 2 && tiny.lds <= ctx->max_shared_per_block)
-        cfg = &tiny;
-    else if (small.lds <= ctx->max_shared_per_block)
+    } else if (small.lds <= ctx->max_shared_per_block) {
         cfg = &small;
+    }
     if (!cfg) {
         if (a_tiled) return set_error(err, NH_UNSUPPORTED, "LDS too small for the GEMM tiles");
         // LDS too small for the MFMA tiles: 16-row GEMV passes (still exact)

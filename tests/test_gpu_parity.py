@@ -322,7 +322,11 @@ def test_linear_decode_unit_bit_exact(ctx, m, n, k):
                                          (8, 21512, 4096, "bf16"), (8, 100, 4096, "bf16"), (5, 4000, 512, "bf16"),
                                          (8, 3000, 6144, "bf16"), (6, 65544, 512, "bf16"),
                                          # the persistent 256 x 224 GEMM with a bias and f32 out
-                                         (1000, 14236, 384, "bf16"), (1024, 14336, 256, "f32")])
+                                         (1000, 14236, 384, "bf16"), (1024, 14336, 256, "f32"),
+                                         # batched decode past 16 rows: 64 x 64 tiles (M = 24, 64),
+                                         # 64 x 128 (M = 128), 128 x 128 (M = 256), ragged N and K
+                                         (24, 16384, 4096, "bf16"), (64, 5000, 1040, "bf16"),
+                                         (128, 16390, 512, "bf16"), (256, 16384, 2048, "f32")])
 def test_linear_small_m_shapes_bit_exact(ctx, m, n, k, dtype):
     """The linear path off the headline shape (and past 16 rows, the GEMM on
     A tiles written by the quantizer, M and K tails included): several K slabs per
