@@ -73,3 +73,107 @@ extern "C" __global__ __launch_bounds__(256) void nh_gemm_f32_kernel(GemmF32Args
         }
     }
 }
+
+// The same product for outputs too few to fill the CUs with 64 x 64 tiles
+// (the MoE router: 512 tokens x 128 experts are 16 such tiles): one output per
+// lane, so every SIMD runs a wave of independent k-ordered chains.  A wave
+// owns one lhs row and 64 consecutive columns, a workgroup four rows.  The
+// row's values are wave-uniform, so they come through scalar loads into SGPRs
+// (no LDS traffic); the rhs block of 64 k x 64 columns is staged in LDS as
+// [column][k], each lane reading four k of its column per 16-byte load, and
+// the next block's global loads are in flight while the current one is
+// consumed.  Per k a lane widens its two operands and issues one fused
+// multiply-add in f64: the arithmetic and order of nh_gemm_f32_kernel, so
+// every output sees exactly K fused multiply-adds, k ascending.
+namespace {
+
+typedef __attribute__((address_space(4))) const float sfloat;
+typedef __attribute__((address_space(4))) const uint32_t suint;
+
+constexpr int kNarrowK = 64;
+
+// The lhs value at column k of the wave's row.  Mode 0: f32 rows (scalar
+// loads).  Mode 1: bf16 rows starting on a 4-byte boundary (scalar loads of
+// pairs).  Mode 2: any other bf16 layout (uniform vector loads).
+template <int kMode>
+__device__ __forceinline__ float lhs_at(const void* row, int64_t k) {
+    if constexpr (kMode == 0) {
+        return ((sfloat*)row)[k];
+    } else if constexpr (kMode == 1) {
+        const uint32_t w = ((suint*)row)[k >> 1];
+        return f32_from_bits((k & 1) ? (w & 0xffff0000u) : (w << 16));
+    } else {
+        return f32_from_bits((uint32_t)((const uint16_t*)row)[k] << 16);
+    }
+}
+
+template <int kMode>
+__device__ __forceinline__ double narrow_chain(const GemmF32Args& a, const void* row, float (*Bt)[kNarrowK + 4],
+                                               float (&rb)[16], int lane, int wave, int64_t n, bool row_ok,
+                                               bool col_ok) {
+    const int64_t K = a.K, N = a.N;
+    // The rhs rows [k0, k0 + 64) as one buffer resource: rows past K and
+    // columns past N read as zeros without a branch per load.  The launch
+    // keeps N below 64 x (CU count), so 64 rows of offsets fit in 31 bits.
+    auto fetch = [&](int64_t k0) {
+        const int64_t rows = K - k0 < kNarrowK ? K - k0 : kNarrowK;
+        const auto rs = make_rsrc(a.rhs + k0 * N, (uint32_t)(rows * N * 4));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int kr = 4 * (wave + 4 * i) + r;
+                const int off = col_ok ? (kr * (int)N + (int)n) * 4 : kOutOfRange;
+                rb[4 * i + r] = f32_from_bits(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+            }
+    };
+    double acc = 0.0;
+    fetch(0);
+    for (int64_t k0 = 0; k0 < K; k0 += kNarrowK) {
+        __syncthreads();  // the previous block's reads are done
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *(float4*)&Bt[lane][4 * (wave + 4 * i)] =
+                make_float4(rb[4 * i], rb[4 * i + 1], rb[4 * i + 2], rb[4 * i + 3]);
+        __syncthreads();
+        if (k0 + kNarrowK < K) fetch(k0 + kNarrowK);  // uniform
+        if (!row_ok) continue;                          // uniform: the wave only stages
+        if (K - k0 >= kNarrowK) {
+#pragma unroll
+            for (int kk = 0; kk < kNarrowK; kk += 4) {
+                const float4 bv = *(const float4*)&Bt[lane][kk];
+                acc = __builtin_fma((double)lhs_at<kMode>(row, k0 + kk), (double)bv.x, acc);
+                acc = __builtin_fma((double)lhs_at<kMode>(row, k0 + kk + 1), (double)bv.y, acc);
+                acc = __builtin_fma((double)lhs_at<kMode>(row, k0 + kk + 2), (double)bv.z, acc);
+                acc = __builtin_fma((double)lhs_at<kMode>(row, k0 + kk + 3), (double)bv.w, acc);
+            }
+        } else {
+            const int kmax = (int)(K - k0);
+            for (int kk = 0; kk < kmax; ++kk)
+                acc = __builtin_fma((double)lhs_at<kMode>(row, k0 + kk), (double)Bt[lane][kk], acc);
+        }
+    }
+    return acc;
+}
+
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void nh_gemm_f32_small_kernel(GemmF32Args a) {
+    __shared__ __align__(16) float Bt[64][kNarrowK + 4];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t m = (int64_t)blockIdx.y * 4 + wave, n = (int64_t)blockIdx.x * 64 + lane;
+    const bool row_ok = m < a.M, col_ok = n < a.N;
+    float rb[16];
+    double acc;
+    if (!a.lhs_bf16) {
+        acc = narrow_chain<0>(a, (const float*)a.lhs + (row_ok ? m : 0) * a.K, Bt, rb, lane, wave, n, row_ok, col_ok);
+    } else {
+        const uint16_t* row = (const uint16_t*)a.lhs + (row_ok ? m : 0) * a.K;
+        if ((((uintptr_t)a.lhs) & 3) == 0 && (a.K & 1) == 0)
+            acc = narrow_chain<1>(a, row, Bt, rb, lane, wave, n, row_ok, col_ok);
+        else
+            acc = narrow_chain<2>(a, row, Bt, rb, lane, wave, n, row_ok, col_ok);
+    }
+    if (row_ok && col_ok) a.out[m * a.N + n] = a.bias ? (float)acc + a.bias[n] : (float)acc;
+}

@@ -517,6 +517,19 @@ int nh_supports_gemm_f32(size_t m, size_t k, size_t n) {
     return m > 0 && k > 0 && n > 0 && m <= INT32_MAX && k <= INT32_MAX && n <= INT32_MAX && (m + 63) / 64 <= 65535;
 }
 
+// The exact f32 product's two tilings: 64 x 64 outputs per workgroup (16 per
+// lane) while those tiles fill every CU, else 4 rows x 64 columns (one output
+// per lane), so a narrow output such as the MoE router's 128 experts still
+// spreads its sequential-k chains over the chip.
+static nh_status launch_gemm_f32(nh_context* ctx, const GemmF32Args& a, nh_stream stream, nh_error* err) {
+    const int64_t big = ((a.M + 63) / 64) * ((a.N + 63) / 64);
+    if (big >= ctx->cu_count)
+        return launch(ctx, K_GEMM_F32, (unsigned)((a.N + 63) / 64), 256, 0, stream, a, err,
+                      (unsigned)((a.M + 63) / 64));
+    return launch(ctx, K_GEMM_F32_SMALL, (unsigned)((a.N + 63) / 64), 256, 0, stream, a, err,
+                  (unsigned)((a.M + 3) / 4));
+}
+
 nh_status nh_gemm_f32(nh_context* ctx, const float* lhs, size_t lhs_len, const float* rhs, size_t rhs_len, size_t m,
                       size_t k, size_t n, float* out, size_t out_len, nh_stream stream, nh_error* err) {
     clear_error(err);
@@ -533,7 +546,7 @@ nh_status nh_gemm_f32(nh_context* ctx, const float* lhs, size_t lhs_len, const f
     nh_status st = bind_device(ctx, err);
     if (st) return st;
     GemmF32Args a{lhs, rhs, out, (int64_t)m, (int64_t)k, (int64_t)n, nullptr, 0, 0};
-    return launch(ctx, K_GEMM_F32, (unsigned)((n + 63) / 64), 256, 0, stream, a, err, (unsigned)((m + 63) / 64));
+    return launch_gemm_f32(ctx, a, stream, err);
 }
 
 nh_status nh_gemm_w8a8(nh_context* ctx, const int8_t* xq, const float* sx, const int8_t* wq, const float* sw,
@@ -1165,9 +1178,7 @@ nh_status nh_moe_layer_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, co
     float* logits = (float*)((char*)workspace + align256(inner));
     GemmF32Args a{x, router_w, logits, (int64_t)tokens, (int64_t)hidden, (int64_t)experts, router_b,
                   x_dtype == NH_BF16 ? 1 : 0, 0};
-    if ((st = launch(ctx, K_GEMM_F32, (unsigned)((experts + 63) / 64), 256, 0, stream, a, err,
-                     (unsigned)((tokens + 63) / 64))))
-        return st;
+    if ((st = launch_gemm_f32(ctx, a, stream, err))) return st;
     return moe_forward(ctx, x, x_dtype, logits, tokens, hidden, inter, experts, top_k, renormalize, scaling, w_up,
                        s_up, w_down, s_down, shared_inter, w_up_shared, s_up_shared, w_down_shared, s_down_shared,
                        out, out_dtype, workspace, align256(inner), nonfinite, stream, err);

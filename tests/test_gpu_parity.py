@@ -222,7 +222,8 @@ _GEMM_KATS = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file_
 
 @pytest.mark.parametrize("case", _GEMM_KATS["gemm"] + [dict(_GEMM_KATS["gemm_pattern"][0], lhs=None)]
                          + [dict(m=m, k=k, n=n, lhs="rand") for (m, k, n) in
-                            [(1, 4096, 4096), (37, 100, 65), (130, 257, 71), (64, 16, 64), (3, 1, 5)]],
+                            [(1, 4096, 4096), (37, 100, 65), (130, 257, 71), (64, 16, 64), (3, 1, 5),
+                             (512, 2688, 128), (5, 130, 200), (1024, 300, 1030)]],
                          ids=lambda c: f"{c['m']}x{c['k']}x{c['n']}")
 def test_gemm_f32_device_bit_exact_with_host_order(ctx, case):
     note(f"gemm_f32 {case['m']}x{case['k']}x{case['n']}")
@@ -941,6 +942,35 @@ def test_moe_layer_with_router_bit_exact(ctx, tokens, hidden, inter, experts, to
     assert np.array_equal(wsh[lay[0]:lay[0] + 4 * tokens * top_k].view(np.int32), idx)
     got = out.numpy()
     assert np.array_equal(got, ref), f"{(got != ref).sum()} of {ref.size} outputs differ"
+
+
+def test_moe_layer_router_reads_bf16_rows_off_a_4_byte_boundary(ctx):
+    """The router GEMM widens bf16 rows that start on a 2-byte boundary (x one
+    element into its allocation) exactly as aligned ones: logits and the
+    layer's output against the oracle."""
+    tokens, hidden, inter, experts, top_k = 13, 64, 32, 8, 3
+    note(f"moe layer + router, x at +2 bytes t={tokens} h={hidden}")
+    x, _, up, su, down, sd = moe_case(tokens, hidden, inter, experts, top_k)
+    rw, rb = router_case(tokens, hidden, experts)
+    logits = router_logits(x, rw, rb)
+    st, ref, idx, *_ = O.moe_forward_w8a8(x, logits, up, su, down, sd, top_k, renormalize=False)
+    assert st == O.OK
+    lib = NH.lib()
+    ws_bytes = lib.nh_moe_layer_w8a8_workspace_size(tokens, hidden, inter, experts, top_k, 0)
+    inner = lib.nh_moe_forward_w8a8_workspace_size(tokens, hidden, inter, experts, top_k)
+    ws = ctx.empty(ws_bytes, np.uint8)
+    dx = ctx.upload(np.concatenate([np.zeros(1, np.uint16), x.ravel()]))
+    drw, drb = ctx.upload(rw), ctx.upload(rb)
+    dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
+    out = ctx.empty((tokens, hidden), np.uint16)
+    NH.call("nh_moe_layer_w8a8", ctx.handle, dx.ptr + 2, NH.BF16, drw.ptr, drb.ptr, tokens, hidden, inter, experts,
+            top_k, 0, 1.0, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, 0, None, None, None, None, out.ptr, NH.BF16, ws.ptr,
+            ws_bytes, None, None)
+    ctx.synchronize()
+    wsh = ws.numpy()
+    at = (inner + 255) // 256 * 256
+    assert np.array_equal(wsh[at:at + 4 * tokens * experts].view(np.uint32), logits.view(np.uint32))
+    assert np.array_equal(out.numpy(), ref)
 
 
 def test_moe_layer_rejects_before_the_device(ctx):
