@@ -218,7 +218,12 @@ class Bench:
 
         return self.time_ms(step, steps, warmup, out=y)
 
-    def moe(self, steps, warmup, tokens=512, hidden=2688, inter=1856, experts=128, top_k=6, shared_inter=0):
+    def moe(self, steps, warmup, tokens=512, hidden=2688, inter=1856, experts=128, top_k=6, shared_inter=0,
+            router=False):
+        """The MoE layer on synthetic expert weights.  With router=True it is
+        nh_moe_layer_w8a8, MoeLayer::forward_into from its input: the dense
+        f32 router (N(0, 0.02) weights, N(0, 0.1) bias) computes the logits
+        on the device first; otherwise the logits are given."""
         L = NH.lib()
         tb_up, tb_down = L.nh_tiled_weights_bytes(inter, hidden), L.nh_tiled_weights_bytes(hidden, inter)
         up_q = self.ctx.empty(experts * tb_up, np.int8)
@@ -259,10 +264,19 @@ class Bench:
                                                                    shared_inter)
         else:
             ws_bytes = L.nh_moe_forward_w8a8_workspace_size(tokens, hidden, inter, experts, top_k)
+        if router:
+            rw = self.ctx.upload(NH.normal_f32(3, hidden * experts, 0.0, 0.02))
+            rb = self.ctx.upload(NH.normal_f32(4, experts, 0.0, 0.1))
+            ws_bytes = L.nh_moe_layer_w8a8_workspace_size(tokens, hidden, inter, experts, top_k, shared_inter)
         ws = self.ctx.empty(ws_bytes, np.uint8)
 
         def step(i):
-            if shared_inter:
+            if router:
+                shp = [q.ptr for q in sh] if shared_inter else [None] * 4
+                st = L.nh_moe_layer_w8a8(h, x.ptr, NH.BF16, rw.ptr, rb.ptr, tokens, hidden, inter, experts, top_k, 1,
+                                         1.0, up_q.ptr, up_s.ptr, down_q.ptr, down_s.ptr, shared_inter, *shp, out.ptr,
+                                         NH.BF16, ws.ptr, ws_bytes, None, self.stream, ctypes.byref(err))
+            elif shared_inter:
                 st = L.nh_moe_forward_shared_w8a8(h, x.ptr, NH.BF16, logits.ptr, tokens, hidden, inter, experts, top_k,
                                                   1, 1.0, up_q.ptr, up_s.ptr, down_q.ptr, down_s.ptr, shared_inter,
                                                   sh[0].ptr, sh[1].ptr, sh[2].ptr, sh[3].ptr, out.ptr, NH.BF16, ws.ptr,
@@ -279,6 +293,7 @@ class Bench:
         wbytes = experts * (inter * hidden + hidden * inter) + experts * 4 * (inter + hidden)
         wbytes += 2 * shared_inter * hidden + 4 * (shared_inter + hidden) if shared_inter else 0
         abytes = tokens * hidden * 2 + tokens * experts * 4 + tokens * hidden * 2
+        wbytes += 4 * (hidden * experts + experts) if router else 0
         return ms, wbytes + abytes, 2.0 * tokens * (top_k * inter + shared_inter) * hidden * 2
 
 
@@ -522,7 +537,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["moe", "moe_shared", "gemm", "stack", "decode", "w8a32", "w4a8"], default=None,
+    ap.add_argument("--only", choices=["moe", "moe_shared", "moe_router", "gemm", "stack", "decode", "w8a32", "w4a8"],
+                    default=None,
                     help="run one secondary workload only (for profiling) and print its figures")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (torch's copy kernel), the "
@@ -574,8 +590,9 @@ def main():
     b = Bench()
     if args.only:
         res = {}
-        if args.only in ("moe", "moe_shared"):
-            t, mbytes, mops = b.moe(10, 2, shared_inter=3712 if args.only == "moe_shared" else 0)
+        if args.only in ("moe", "moe_shared", "moe_router"):
+            t, mbytes, mops = b.moe(10, 2, shared_inter=3712 if args.only == "moe_shared" else 0,
+                                    router=args.only == "moe_router")
             res = {"us": round(t * 1e3, 1), "GBps": round(mbytes / (t * 1e-3) / 1e9, 1)}
         elif args.only == "gemm":
             for (mm, nn, kk) in [(2048, 4096, 4096), (2048, 21504, 4096), (2048, 4096, 21504)]:
@@ -653,6 +670,10 @@ def main():
         extra["moe_512tok_128exp_top6"] = {"us": round(t * 1e3, 1), "GBps": round(mbytes / (t * 1e-3) / 1e9, 1),
                                            "frac_hbm_peak": round(mbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                            "TOPS": round(mops / (t * 1e-3) / 1e12, 2)}
+        log("[bench] moe layer from its input (the dense f32 router on the device)")
+        t, mbytes, mops = b.moe(40, 3, router=True)
+        extra["moe_layer_with_router_512tok"] = {"us": round(t * 1e3, 1), "GBps": round(mbytes / (t * 1e-3) / 1e9, 1),
+                                                 "frac_hbm_peak": round(mbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         log("[bench] moe layer with its 3712-wide shared expert")
         t, mbytes, mops = b.moe(40, 3, shared_inter=3712)
         extra["moe_512tok_128exp_top6_shared3712"] = {

@@ -77,41 +77,51 @@ extern "C" __global__ __launch_bounds__(256) void nh_gemm_f32_kernel(GemmF32Args
 // The same product for outputs too few to fill the CUs with 64 x 64 tiles
 // (the MoE router: 512 tokens x 128 experts are 16 such tiles): one output per
 // lane, so every SIMD runs a wave of independent k-ordered chains.  A wave
-// owns one lhs row and 64 consecutive columns, a workgroup four rows.  The
-// row's values are wave-uniform, so they come through scalar loads into SGPRs
-// (no LDS traffic); the rhs block of 64 k x 64 columns is staged in LDS as
-// [column][k], each lane reading four k of its column per 16-byte load, and
-// the next block's global loads are in flight while the current one is
-// consumed.  Per k a lane widens its two operands and issues one fused
-// multiply-add in f64: the arithmetic and order of nh_gemm_f32_kernel, so
-// every output sees exactly K fused multiply-adds, k ascending.
+// owns one lhs row and 64 consecutive columns, a workgroup four rows.
+//
+// Widening f32 to f64 is a quarter-rate instruction, so neither operand is
+// widened once per use.  The rhs block of 64 k x 64 columns is widened once
+// per workgroup while it is staged and kept in LDS as f64 [column][k] (a lane
+// reads two k of its column per 16-byte load).  The row's values are the same
+// for the whole wave: lane j of every 16-lane row holds the f64 of column
+// k0 + 16 b + j (b = 0..3, one widening per 16 k), and each fused multiply-add
+// takes its lhs operand from a row broadcast (DPP row_newbcast) of lane j.
+// The next block's rhs and lhs loads are in flight while the current one is
+// consumed.  Same arithmetic and order as nh_gemm_f32_kernel: every output
+// sees exactly K fused multiply-adds, k ascending.
 namespace {
-
-typedef __attribute__((address_space(4))) const float sfloat;
-typedef __attribute__((address_space(4))) const uint32_t suint;
 
 constexpr int kNarrowK = 64;
 
-// The lhs value at column k of the wave's row.  Mode 0: f32 rows (scalar
-// loads).  Mode 1: bf16 rows starting on a 4-byte boundary (scalar loads of
-// pairs).  Mode 2: any other bf16 layout (uniform vector loads).
-template <int kMode>
-__device__ __forceinline__ float lhs_at(const void* row, int64_t k) {
-    if constexpr (kMode == 0) {
-        return ((sfloat*)row)[k];
-    } else if constexpr (kMode == 1) {
-        const uint32_t w = ((suint*)row)[k >> 1];
-        return f32_from_bits((k & 1) ? (w & 0xffff0000u) : (w << 16));
-    } else {
+template <int J>
+__device__ __forceinline__ double row_bcast(double v) {
+    return __builtin_amdgcn_mov_dpp(v, 0x150 + J, 0xf, 0xf, true);  // row_newbcast:J
+}
+
+template <bool kBf16>
+__device__ __forceinline__ float lhs_value(const void* row, int64_t k) {
+    if constexpr (kBf16)
         return f32_from_bits((uint32_t)((const uint16_t*)row)[k] << 16);
+    else
+        return ((const float*)row)[k];
+}
+
+// Sixteen k of the block: lhs from lane J of the row, rhs from registers.
+template <int J>
+__device__ __forceinline__ void narrow_16(double& acc, double av, const double2* bv) {
+    if constexpr (J < 16) {
+        acc = __builtin_fma(row_bcast<J>(av), bv[J / 2].x, acc);
+        acc = __builtin_fma(row_bcast<J + 1>(av), bv[J / 2].y, acc);
+        narrow_16<J + 2>(acc, av, bv);
     }
 }
 
-template <int kMode>
-__device__ __forceinline__ double narrow_chain(const GemmF32Args& a, const void* row, float (*Bt)[kNarrowK + 4],
-                                               float (&rb)[16], int lane, int wave, int64_t n, bool row_ok,
-                                               bool col_ok) {
+template <bool kBf16>
+__device__ __forceinline__ double narrow_chain(const GemmF32Args& a, const void* row, double (*Bt)[kNarrowK + 2],
+                                               int lane, int wave, int64_t n, bool row_ok, bool col_ok) {
     const int64_t K = a.K, N = a.N;
+    const int j = lane & 15;
+    float rb[16], ra[4];
     // The rhs rows [k0, k0 + 64) as one buffer resource: rows past K and
     // columns past N read as zeros without a branch per load.  The launch
     // keeps N below 64 x (CU count), so 64 rows of offsets fit in 31 bits.
@@ -126,31 +136,38 @@ __device__ __forceinline__ double narrow_chain(const GemmF32Args& a, const void*
                 const int off = col_ok ? (kr * (int)N + (int)n) * 4 : kOutOfRange;
                 rb[4 * i + r] = f32_from_bits(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
             }
+        if (row_ok && rows == kNarrowK) {  // uniform; a partial block reads its row per k
+#pragma unroll
+            for (int b = 0; b < 4; ++b) ra[b] = lhs_value<kBf16>(row, k0 + 16 * b + j);
+        }
     };
     double acc = 0.0;
     fetch(0);
     for (int64_t k0 = 0; k0 < K; k0 += kNarrowK) {
         __syncthreads();  // the previous block's reads are done
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *(float4*)&Bt[lane][4 * (wave + 4 * i)] =
-                make_float4(rb[4 * i], rb[4 * i + 1], rb[4 * i + 2], rb[4 * i + 3]);
+        for (int i = 0; i < 4; ++i) {
+            double* dst = &Bt[lane][4 * (wave + 4 * i)];
+            *(double2*)dst = make_double2((double)rb[4 * i], (double)rb[4 * i + 1]);
+            *(double2*)(dst + 2) = make_double2((double)rb[4 * i + 2], (double)rb[4 * i + 3]);
+        }
+        double av[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) av[b] = (double)ra[b];
         __syncthreads();
         if (k0 + kNarrowK < K) fetch(k0 + kNarrowK);  // uniform
         if (!row_ok) continue;                          // uniform: the wave only stages
+        const double* bt = Bt[lane];
         if (K - k0 >= kNarrowK) {
+            double2 bv[32];  // the whole block's column: reads issued ahead of the chain
 #pragma unroll
-            for (int kk = 0; kk < kNarrowK; kk += 4) {
-                const float4 bv = *(const float4*)&Bt[lane][kk];
-                acc = __builtin_fma((double)lhs_at<kMode>(row, k0 + kk), (double)bv.x, acc);
-                acc = __builtin_fma((double)lhs_at<kMode>(row, k0 + kk + 1), (double)bv.y, acc);
-                acc = __builtin_fma((double)lhs_at<kMode>(row, k0 + kk + 2), (double)bv.z, acc);
-                acc = __builtin_fma((double)lhs_at<kMode>(row, k0 + kk + 3), (double)bv.w, acc);
-            }
+            for (int i = 0; i < 32; ++i) bv[i] = *(const double2*)(bt + 2 * i);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) narrow_16<0>(acc, av[b], bv + 8 * b);
         } else {
             const int kmax = (int)(K - k0);
             for (int kk = 0; kk < kmax; ++kk)
-                acc = __builtin_fma((double)lhs_at<kMode>(row, k0 + kk), (double)Bt[lane][kk], acc);
+                acc = __builtin_fma((double)lhs_value<kBf16>(row, k0 + kk), bt[kk], acc);
         }
     }
     return acc;
@@ -159,21 +176,15 @@ __device__ __forceinline__ double narrow_chain(const GemmF32Args& a, const void*
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(256) void nh_gemm_f32_small_kernel(GemmF32Args a) {
-    __shared__ __align__(16) float Bt[64][kNarrowK + 4];
+    __shared__ __align__(16) double Bt[64][kNarrowK + 2];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t m = (int64_t)blockIdx.y * 4 + wave, n = (int64_t)blockIdx.x * 64 + lane;
     const bool row_ok = m < a.M, col_ok = n < a.N;
-    float rb[16];
     double acc;
-    if (!a.lhs_bf16) {
-        acc = narrow_chain<0>(a, (const float*)a.lhs + (row_ok ? m : 0) * a.K, Bt, rb, lane, wave, n, row_ok, col_ok);
-    } else {
-        const uint16_t* row = (const uint16_t*)a.lhs + (row_ok ? m : 0) * a.K;
-        if ((((uintptr_t)a.lhs) & 3) == 0 && (a.K & 1) == 0)
-            acc = narrow_chain<1>(a, row, Bt, rb, lane, wave, n, row_ok, col_ok);
-        else
-            acc = narrow_chain<2>(a, row, Bt, rb, lane, wave, n, row_ok, col_ok);
-    }
+    if (a.lhs_bf16)
+        acc = narrow_chain<true>(a, (const uint16_t*)a.lhs + (row_ok ? m : 0) * a.K, Bt, lane, wave, n, row_ok, col_ok);
+    else
+        acc = narrow_chain<false>(a, (const float*)a.lhs + (row_ok ? m : 0) * a.K, Bt, lane, wave, n, row_ok, col_ok);
     if (row_ok && col_ok) a.out[m * a.N + n] = a.bias ? (float)acc + a.bias[n] : (float)acc;
 }
