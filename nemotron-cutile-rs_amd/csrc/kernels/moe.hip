@@ -52,14 +52,35 @@ constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
 // S slots (S = 2, 4 or 16: the body is instantiated per slot count, so a
 // 128-expert router runs 2 inlined sigmoids per lane instead of fetching the
 // code of 16).
+// expf's 2^(i/32) table held across the wave (lane l: entry l % 32, f64
+// bits) and read through the LDS crossbar: no memory load inside the
+// sigmoid, so the routing never waits on the load counter behind the row's
+// loads in flight.
+struct LaneExp2Table {
+    uint32_t lo, hi;
+    __device__ double operator()(uint32_t i) const {
+        const int addr = (int)(i & 31) * 4;
+        const uint32_t l = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)lo);
+        const uint32_t h = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)hi);
+        return f64_from_bits(((uint64_t)h << 32) | l);
+    }
+};
+
+__device__ __forceinline__ LaneExp2Table lane_exp2_table(int lane) {
+    const uint64_t b = f64_bits(exp2_table((uint32_t)lane & 31));
+    return LaneExp2Table{(uint32_t)b, (uint32_t)(b >> 32)};
+}
+
 template <int S>
-__device__ __forceinline__ void route_token(const RouteArgs& a, int token, int lane, const float (&sc)[S]) {
+__device__ __forceinline__ void route_token(const RouteArgs& a, int token, int lane, const float (&sc)[S],
+                                            const LaneExp2Table& tbl) {
     const int E = a.experts;
     int64_t key[S];
 #pragma unroll
     for (int i = 0; i < S; ++i) {
         const int e = lane + 64 * i;
-        key[i] = e < E ? route_key(sigmoid_f32(sc[i]), e) : INT64_MIN;
+        const float w = sigmoid_f32_with(sc[i], tbl);  // every lane: the table reads are cross-lane
+        key[i] = e < E ? route_key(w, e) : INT64_MIN;
     }
     float wsel = 0.0f;  // lane j keeps the j-th selected weight (top_k <= 64)
     int esel = 0;
@@ -96,37 +117,51 @@ __device__ __forceinline__ void route_token(const RouteArgs& a, int token, int l
 // With x, the same wave also quantizes the token's row (Q2, the wave form
 // of nh_quantize_rows_i8: same codes and scales), token-major: the up
 // projection gathers its A rows through the permutation.  The token's scores
-// are loaded first, so their round trip to memory overlaps the row's (after
-// the quantizer's code stores, the compiler could not have moved them up).
+// are loaded first and the row's loads right after them; the routing waits
+// for the scores only, so it runs while the row is in flight, and the
+// quantization follows.
+template <int S, int DT>
+__device__ __forceinline__ void route_quantize(const RouteArgs& a, int token, int lane, const float (&sc)[S],
+                                               const LaneExp2Table& tbl) {
+    QuantizeRowsArgs q{};
+    q.x = a.x;
+    q.q = a.xq;
+    q.scales = a.sx;
+    q.rows = a.tokens;
+    q.cols = a.hidden;
+    q.x_dtype = a.x_dtype;
+    q.nonfinite = a.nonfinite;
+    q.nonfinite_stage = 0;
+    q.q_act = a.xq_tiles;
+    q.act_p = 16;
+    v4i xv[8];
+    const int64_t row = quantize_row_wave_load<DT, 8>(q, xv);  // the token's row (the kernel checked it)
+    route_token<S>(a, token, lane, sc, tbl);
+    quantize_row_wave_finish<DT, 8>(q, xv, row);
+}
+
 template <int S>
 __device__ __forceinline__ void route_kernel_body(const RouteArgs& a, int token, int lane) {
+    const LaneExp2Table tbl = lane_exp2_table(lane);
+    // the token's scores through a buffer resource (experts past E read 0):
+    // every load unconditional, so the wait for them leaves the row's loads
+    // in flight
     float sc[S];
-    const float* s = a.scores + (int64_t)token * a.experts;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.scores + (int64_t)token * a.experts, (uint32_t)a.experts * 4u);
 #pragma unroll
-    for (int i = 0; i < S; ++i) sc[i] = lane + 64 * i < a.experts ? s[lane + 64 * i] : 0.0f;
-    if (a.x) {
-        QuantizeRowsArgs q{};
-        q.x = a.x;
-        q.q = a.xq;
-        q.scales = a.sx;
-        q.rows = a.tokens;
-        q.cols = a.hidden;
-        q.x_dtype = a.x_dtype;
-        q.nonfinite = a.nonfinite;
-        q.nonfinite_stage = 0;
-        q.q_act = a.xq_tiles;
-        q.act_p = 16;
-        if (a.x_dtype == DT_BF16)
-            quantize_row_wave<DT_BF16, 8>(q);
-        else
-            quantize_row_wave<DT_F32, 8>(q);
-    }
-    route_token<S>(a, token, lane, sc);
+    for (int i = 0; i < S; ++i)
+        sc[i] = f32_from_bits(__builtin_amdgcn_raw_buffer_load_b32(rs, (lane + 64 * i) * 4, 0, 0));
+    if (!a.x)
+        route_token<S>(a, token, lane, sc, tbl);
+    else if (a.x_dtype == DT_BF16)
+        route_quantize<S, DT_BF16>(a, token, lane, sc, tbl);
+    else
+        route_quantize<S, DT_F32>(a, token, lane, sc, tbl);
 }
 
 extern "C" __global__ __launch_bounds__(256) void nh_moe_route_sigmoid_kernel(RouteArgs a) {
     const int lane = threadIdx.x & 63;
-    const int token = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int token = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     if (token >= a.tokens) return;
     if (a.experts <= 128)
         route_kernel_body<2>(a, token, lane);

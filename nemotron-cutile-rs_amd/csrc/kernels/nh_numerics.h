@@ -8,8 +8,10 @@
 
 #if defined(__HIPCC__)
 #define NH_HD __host__ __device__ __forceinline__
+#define NH_HD_MEMBER __host__ __device__ __forceinline__
 #else
 #define NH_HD static inline
+#define NH_HD_MEMBER inline
 #endif
 
 namespace nh {
@@ -167,10 +169,12 @@ NH_HD double exp2_table(uint32_t i) {
     return t[i & 31];
 }
 
-NH_HD float expf_rn(float x) {
-    if (x != x) return x + x;
-    if (x > 0x1.62e42ep+6f) return __builtin_inff();  // expf overflows above 88.72283
-    if (x < -0x1.9fe368p+6f) return 0.0f;              // and underflows to +0 below -103.97208
+// The method with the table entry 2^(i/32) supplied by `entry(i)` (i in
+// 0..31), looked up before any input-dependent branch: the device routing
+// kernel reads it from another lane of the wave (a cross-lane read needs every
+// lane active) instead of from memory.
+template <class Entry>
+NH_HD_MEMBER float expf_rn_with(float x, Entry entry) {
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
     const double shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
@@ -181,7 +185,7 @@ NH_HD float expf_rn(float x) {
     uint64_t ki = f64_bits(kd);
     kd -= shift;
     double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    uint64_t t = f64_bits(exp2_table((uint32_t)(ki % 32))) - ((uint64_t)(ki % 32) << 47);
+    uint64_t t = f64_bits(entry((uint32_t)(ki % 32))) - ((uint64_t)(ki % 32) << 47);
     t += ki << 47;
     double s = f64_from_bits(t);
     double z = __builtin_fma(c0, r, c1);
@@ -189,18 +193,27 @@ NH_HD float expf_rn(float x) {
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     y = y * s;
+    if (x != x) return x + x;
+    if (x > 0x1.62e42ep+6f) return __builtin_inff();  // expf overflows above 88.72283
+    if (x < -0x1.9fe368p+6f) return 0.0f;              // and underflows to +0 below -103.97208
     return (float)y;
 }
 
-// Numerically stable sigmoid of activations.rs:73-81, with expf_rn.
-NH_HD float sigmoid_f32(float x) {
-    if (x >= 0.0f) {
-        float z = expf_rn(-x);
-        return 1.0f / (1.0f + z);
-    }
-    float z = expf_rn(x);
-    return z / (1.0f + z);
+struct Exp2Table {
+    NH_HD_MEMBER double operator()(uint32_t i) const { return exp2_table(i); }
+};
+
+NH_HD float expf_rn(float x) { return expf_rn_with(x, Exp2Table{}); }
+
+// Numerically stable sigmoid of activations.rs:73-81, with expf_rn: exp of
+// -|x| (x itself for NaN), then 1 / (1 + z) for x >= 0, z / (1 + z) below.
+template <class Entry>
+NH_HD_MEMBER float sigmoid_f32_with(float x, Entry entry) {
+    const float z = expf_rn_with(x >= 0.0f ? -x : x, entry);
+    return x >= 0.0f ? 1.0f / (1.0f + z) : z / (1.0f + z);
 }
+
+NH_HD float sigmoid_f32(float x) { return sigmoid_f32_with(x, Exp2Table{}); }
 
 // f32::total_cmp ordering key (moe_routing.rs:176-180).
 NH_HD int32_t total_cmp_key(float v) {

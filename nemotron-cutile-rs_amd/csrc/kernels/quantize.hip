@@ -117,23 +117,39 @@ __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, floa
 // code pass, and both reductions are wave reductions: no barrier, and a row
 // costs one round trip to memory.  Same codes and scales as the vector path
 // (max and min are exact in any order).
+// Its two halves, for a caller with other work to do while the row is in
+// flight: the loads (the row this wave owns, or -1 past the last row), then
+// the reductions and the code stores.
 template <int DT, int NCH>
-__device__ __forceinline__ void quantize_row_wave(const QuantizeRowsArgs& a) {
+__device__ __forceinline__ int64_t quantize_row_wave_load(const QuantizeRowsArgs& a, v4i (&xv)[NCH]) {
     constexpr int VPC = DT == DT_BF16 ? 8 : 4;
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= a.rows) return;  // the whole wave
+    // (wave-uniform as the compiler sees it, so the row's buffer resource
+    // sits in SGPRs and each load is one instruction)
+    const int64_t row =
+        (int64_t)blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    if (row >= a.rows) return -1;  // the whole wave
     const int64_t src = a.gather ? a.gather[row] / a.gather_div : row;
     const int cols = (int)a.cols;
     const int chunks = cols / VPC;
     const uint32_t rb = (uint32_t)cols * (DT == DT_BF16 ? 2u : 4u);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc((const char*)a.x + src * (int64_t)rb, rb);
-    v4i xv[NCH];
 #pragma unroll
     for (int r = 0; r < NCH; ++r) {
         const int c = lane + r * 64;
         xv[r] = buffer_load16(xr, c < chunks ? c * 16 : kOutOfRange);
     }
+    return row;
+}
+
+template <int DT, int NCH>
+__device__ __forceinline__ void quantize_row_wave_finish(const QuantizeRowsArgs& a, const v4i (&xv)[NCH],
+                                                         int64_t row) {
+    constexpr int VPC = DT == DT_BF16 ? 8 : 4;
+    const int lane = threadIdx.x & 63;
+    const int64_t src = a.gather ? a.gather[row] / a.gather_div : row;
+    const int cols = (int)a.cols;
+    const int chunks = cols / VPC;
     float amax = 0.0f;
     int bad = 0x7fffffff;
 #pragma unroll
@@ -180,6 +196,13 @@ __device__ __forceinline__ void quantize_row_wave(const QuantizeRowsArgs& a) {
             if (tile) *(uint32_t*)tile = code;
         }
     }
+}
+
+template <int DT, int NCH>
+__device__ __forceinline__ void quantize_row_wave(const QuantizeRowsArgs& a) {
+    v4i xv[NCH];
+    const int64_t row = quantize_row_wave_load<DT, NCH>(a, xv);
+    if (row >= 0) quantize_row_wave_finish<DT, NCH>(a, xv, row);
 }
 
 // Scalar path (any alignment, any column count): pass 1 = absmax + first
