@@ -19,8 +19,10 @@
 using namespace nh;
 
 extern "C" __global__ __launch_bounds__(256) void nh_gemm_f32_kernel(GemmF32Args a) {
-    __shared__ __align__(16) float As[16][64 + 4];
-    __shared__ __align__(16) float Bs[16][64 + 4];
+    // operands widened to f64 once, as they are staged (each value is read by
+    // 16 lanes), so the K loop is loads and fused multiply-adds only
+    __shared__ __align__(16) double As[16][64 + 2];
+    __shared__ __align__(16) double Bs[16][64 + 2];
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
     const int64_t M = a.M, K = a.K, N = a.N;
     const int64_t m0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
@@ -29,7 +31,9 @@ extern "C" __global__ __launch_bounds__(256) void nh_gemm_f32_kernel(GemmF32Args
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
-    for (int64_t k0 = 0; k0 < K; k0 += 16) {
+    // one K step's values of this thread, loaded a step ahead of their use
+    float ra[4], rb[4];
+    auto fetch = [&](int64_t k0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int idx = threadIdx.x + 256 * i;
@@ -39,22 +43,32 @@ extern "C" __global__ __launch_bounds__(256) void nh_gemm_f32_kernel(GemmF32Args
             if (gm < M && gk < K)
                 v = a.lhs_bf16 ? f32_from_bits((uint32_t)((const uint16_t*)a.lhs)[gm * K + gk] << 16)
                                : ((const float*)a.lhs)[gm * K + gk];
-            As[kk][r] = v;
+            ra[i] = v;
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int idx = threadIdx.x + 256 * i;
             const int kk = idx >> 6, c = idx & 63;
             const int64_t gk = k0 + kk, gn = n0 + c;
-            Bs[kk][c] = (gk < K && gn < N) ? a.rhs[gk * N + gn] : 0.0f;
+            rb[i] = (gk < K && gn < N) ? a.rhs[gk * N + gn] : 0.0f;
+        }
+    };
+    fetch(0);
+    for (int64_t k0 = 0; k0 < K; k0 += 16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int idx = threadIdx.x + 256 * i;
+            As[idx & 15][idx >> 4] = (double)ra[i];
+            Bs[idx >> 6][idx & 63] = (double)rb[i];
         }
         __syncthreads();
+        if (k0 + 16 < K) fetch(k0 + 16);  // uniform
         const int kmax = (int)(K - k0 < 16 ? K - k0 : 16);
         for (int kk = 0; kk < kmax; ++kk) {
-            const float4 av = *(const float4*)&As[kk][ty * 4];
-            const float4 bv = *(const float4*)&Bs[kk][tx * 4];
-            const double ad[4] = {av.x, av.y, av.z, av.w};
-            const double bd[4] = {bv.x, bv.y, bv.z, bv.w};
+            const double2 a01 = *(const double2*)&As[kk][ty * 4], a23 = *(const double2*)&As[kk][ty * 4 + 2];
+            const double2 b01 = *(const double2*)&Bs[kk][tx * 4], b23 = *(const double2*)&Bs[kk][tx * 4 + 2];
+            const double ad[4] = {a01.x, a01.y, a23.x, a23.y};
+            const double bd[4] = {b01.x, b01.y, b23.x, b23.y};
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -79,10 +93,9 @@ extern "C" __global__ __launch_bounds__(256) void nh_gemm_f32_kernel(GemmF32Args
 // lane, so every SIMD runs a wave of independent k-ordered chains.  A wave
 // owns one lhs row and 64 consecutive columns, a workgroup four rows.
 //
-// Widening f32 to f64 is a quarter-rate instruction, so neither operand is
-// widened once per use.  The rhs block of 64 k x 64 columns is widened once
-// per workgroup while it is staged and kept in LDS as f64 [column][k] (a lane
-// reads two k of its column per 16-byte load).  The row's values are the same
+// Neither operand is widened to f64 once per use.  The rhs block of 64 k x 64
+// columns is widened once per workgroup while it is staged and kept in LDS as
+// f64 [column][k] (a lane reads two k of its column per 16-byte load).  The row's values are the same
 // for the whole wave: lane j of every 16-lane row holds the f64 of column
 // k0 + 16 b + j (b = 0..3, one widening per 16 k), and each fused multiply-add
 // takes its lhs operand from a row broadcast (DPP row_newbcast) of lane j.
