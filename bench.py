@@ -218,6 +218,31 @@ class Bench:
 
         return self.time_ms(step, steps, warmup, out=y)
 
+    def dequant(self, n, k, steps, warmup):
+        """Q0d and Q3 on an [n][k] matrix: nh_dequantize_int4 (packed codes,
+        one tensor scale and zero point) and nh_dequantize_i8 (row scales), both
+        to f32.  Returns (ms int4, ms int8)."""
+        L, h = NH.lib(), self.ctx.handle
+        err = NH.NhError()
+        rng = np.random.default_rng(5)
+        packed = self.ctx.upload(rng.integers(0, 256, size=n * k // 2, dtype=np.uint8))
+        codes = self.ctx.upload(rng.integers(-127, 128, size=n * k, dtype=np.int8))
+        scales = self.ctx.upload(NH.normal_f32(6, n, 0.01, 0.001))
+        out = self.ctx.empty(n * k, np.float32)
+
+        def step4(i):
+            st = L.nh_dequantize_int4(h, packed.ptr, n * k // 2, n * k, 0.0125, 8, out.ptr, n * k, self.stream,
+                                      ctypes.byref(err))
+            if st:
+                NH.check(st, err)
+
+        def step8(i):
+            st = L.nh_dequantize_i8(h, codes.ptr, scales.ptr, n, k, out.ptr, self.stream, ctypes.byref(err))
+            if st:
+                NH.check(st, err)
+
+        return self.time_ms(step4, steps, warmup, out=out), self.time_ms(step8, steps, warmup, out=out)
+
     def moe(self, steps, warmup, tokens=512, hidden=2688, inter=1856, experts=128, top_k=6, shared_inter=0,
             router=False):
         """The MoE layer on synthetic expert weights.  With router=True it is
@@ -537,7 +562,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["moe", "moe_shared", "moe_router", "gemm", "stack", "decode", "w8a32", "w4a8"],
+    ap.add_argument("--only", choices=["moe", "moe_shared", "moe_router", "gemm", "stack", "decode", "w8a32", "w4a8",
+                                       "dequant"],
                     default=None,
                     help="run one secondary workload only (for profiling) and print its figures")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -604,6 +630,9 @@ def main():
                 res[f"m{mm}_k{kk}_n{nn}"] = round(b.w4a8(mm, nn, kk, 50, 5) * 1e3, 2)
         elif args.only == "w8a32":
             res = {"us": round(b.w8a32(4096, 4096, 200, 20) * 1e3, 2)}
+        elif args.only == "dequant":
+            t4, t8 = b.dequant(4096, 4096, 50, 5)
+            res = {"int4_us": round(t4 * 1e3, 2), "i8_us": round(t8 * 1e3, 2)}
         elif args.only == "stack":
             t, sbytes = b.decode_stack(20, 3)
             res = {"ms": round(t, 4), "GBps": round(sbytes / (t * 1e-3) / 1e9, 1)}
@@ -649,6 +678,12 @@ def main():
         t = b.w8a32(4096, 4096, max(20, args.steps), 5)
         w32_bytes = 4096 * 4096 + 4 * 4096 + 4 * 4096 + 4 * 4096
         extra["w8a32_gemv_k4096_n4096"] = {"us": round(t * 1e3, 2), "GBps": round(w32_bytes / (t * 1e-3) / 1e9, 1)}
+        log("[bench] dequantization to f32, 4096 x 4096 (INT4 and int8 codes)")
+        t4, t8 = b.dequant(4096, 4096, max(20, args.steps // 10), 5)
+        nk = 4096 * 4096
+        extra["dequant_f32_4096x4096"] = {
+            "int4_us": round(t4 * 1e3, 2), "int4_GBps": round((nk // 2 + 4 * nk) / (t4 * 1e-3) / 1e9, 1),
+            "i8_us": round(t8 * 1e3, 2), "i8_GBps": round((nk + 4 * 4096 + 4 * nk) / (t8 * 1e-3) / 1e9, 1)}
         gemms = {}
         for (mm, nn, kk) in [(2048, 4096, 4096), (2048, 21504, 4096), (2048, 4096, 21504)]:
             log(f"[bench] prefill gemm m={mm} n={nn} k={kk}")

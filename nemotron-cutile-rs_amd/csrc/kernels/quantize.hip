@@ -410,10 +410,30 @@ extern "C" __global__ __launch_bounds__(256) void nh_tile_weights_kernel(TileWei
     }
 }
 
+// The dequantizers write four f32 bytes per code byte (or per nibble), so
+// they are bound by their stores.  With 16-byte aligned output (and, for
+// int8, rows of whole 4-code chunks) a thread takes 4 codes: one 4-byte (or
+// 2-byte) load and one 16-byte store, so a wave's store covers 1 KiB of
+// consecutive whole cache lines.  Other layouts take one code per thread.
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 extern "C" __global__ __launch_bounds__(256) void nh_dequantize_i8_kernel(DequantizeI8Args a) {
     const int64_t total = a.rows * a.cols;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    if (a.cols % 4 == 0 && ((((uintptr_t)a.q & 3) | ((uintptr_t)a.out & 15)) == 0)) {
+        const int64_t chunks = total >> 2, cpr = a.cols >> 2;
+        for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += stride) {
+            const int64_t r = c < 0xffffffffll && cpr < 0xffffffffll ? (int64_t)((uint32_t)c / (uint32_t)cpr)
+                                                                   : c / cpr;
+            const float s = a.scales[r];
+            const uint32_t b = *(const uint32_t*)(a.q + (c << 2));
+            const v4f v = {(float)(int8_t)(b & 0xff) * s, (float)(int8_t)((b >> 8) & 0xff) * s,
+                           (float)(int8_t)((b >> 16) & 0xff) * s, (float)(int8_t)(b >> 24) * s};
+            *(v4f*)(a.out + (c << 2)) = v;
+        }
+        return;
+    }
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
         const int64_t r = i / a.cols;
         a.out[i] = (float)a.q[i] * a.scales[r];
     }
@@ -423,8 +443,21 @@ extern "C" __global__ __launch_bounds__(256) void nh_dequantize_i8_kernel(Dequan
 // first, quantize.rs:75-77 and :110-116); the reference unpacked on the host
 // and uploaded one f32 per code (quantize.rs:294-301).
 extern "C" __global__ __launch_bounds__(256) void nh_dequantize_int4_kernel(DequantizeInt4Args a) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.value_count;
-         i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t done = 0;  // codes covered by whole 4-code chunks
+    if ((((uintptr_t)a.packed & 1) | ((uintptr_t)a.out & 15)) == 0) {
+        const int64_t chunks = a.value_count >> 2;
+        for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < chunks; c += stride) {
+            const uint32_t b = *(const uint16_t*)(a.packed + (c << 1));
+            const v4f v = {((float)(b & 0x0F) - a.zero_point) * a.scale,
+                           ((float)((b >> 4) & 0x0F) - a.zero_point) * a.scale,
+                           ((float)((b >> 8) & 0x0F) - a.zero_point) * a.scale,
+                           ((float)((b >> 12) & 0x0F) - a.zero_point) * a.scale};
+            *(v4f*)(a.out + (c << 2)) = v;
+        }
+        done = chunks << 2;
+    }
+    for (int64_t i = done + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.value_count; i += stride) {
         const uint8_t byte = a.packed[i >> 1];
         const uint32_t code = (i & 1) ? ((byte >> 4) & 0x0F) : (byte & 0x0F);
         a.out[i] = ((float)code - a.zero_point) * a.scale;

@@ -490,7 +490,9 @@ nh_status nh_dequantize_i8(nh_context* ctx, const int8_t* q, const float* scales
     if (st) return st;
     if (total == 0) return NH_OK;
     DequantizeI8Args a{q, scales, out, (int64_t)rows, (int64_t)cols};
-    return launch(ctx, K_DEQUANT_I8, grid_for((int64_t)total, 256), 256, 0, stream, a, err);
+    // the kernel's 4-code chunks when the layout allows them (the same test)
+    const bool vec = cols % 4 == 0 && ((uintptr_t)q & 3) == 0 && aligned16(out);
+    return launch(ctx, K_DEQUANT_I8, grid_for((int64_t)(vec ? total / 4 : total), 256), 256, 0, stream, a, err);
 }
 
 nh_status nh_dequantize_int4(nh_context* ctx, const uint8_t* packed, size_t packed_len, size_t value_count,
@@ -508,7 +510,10 @@ nh_status nh_dequantize_int4(nh_context* ctx, const uint8_t* packed, size_t pack
     if (st) return st;
     if (value_count == 0) return NH_OK;
     DequantizeInt4Args a{packed, out, (int64_t)value_count, scale, (float)zero_point};
-    return launch(ctx, K_DEQUANT_INT4, grid_for((int64_t)value_count, 256), 256, 0, stream, a, err);
+    // the kernel's 4-code chunks when the layout allows them (the same test)
+    const bool vec = value_count >= 4 && ((uintptr_t)packed & 1) == 0 && aligned16(out);
+    return launch(ctx, K_DEQUANT_INT4, grid_for((int64_t)(vec ? value_count / 4 : value_count), 256), 256, 0,
+                  stream, a, err);
 }
 
 int nh_supports_gemm_f32(size_t m, size_t k, size_t n) {

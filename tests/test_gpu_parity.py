@@ -163,19 +163,25 @@ def test_quantize_many_rows_bit_exact(ctx, cols, dtype):
     assert np.all(stat[:rows - 1] == -1) and stat[rows - 1] == cols // 2
 
 
-def test_dequantize_i8_bit_exact(ctx):
-    note("dequantize_i8")
-    _, q, s = quantized_weights(256, 1024)
-    dq, ds = ctx.upload(q), ctx.upload(s)
+@pytest.mark.parametrize("rows,cols,shift", [(256, 1024, 0), (37, 100, 0), (7, 30, 0), (5, 48, 1)],
+                         ids=["chunks", "chunks-100", "ragged-cols", "unaligned-codes"])
+def test_dequantize_i8_bit_exact(ctx, rows, cols, shift):
+    """4-code chunks (cols % 4 == 0, codes 4-byte and output 16-byte aligned)
+    and the per-code path (ragged columns, or codes one byte into their
+    allocation)."""
+    note(f"dequantize_i8 {rows}x{cols} shift={shift}")
+    _, q, s = quantized_weights(rows, cols)
+    dq, ds = ctx.upload(np.concatenate([np.zeros(shift, np.int8), q.ravel()])), ctx.upload(s)
     out = ctx.empty(q.shape, np.float32)
-    NH.call("nh_dequantize_i8", ctx.handle, dq.ptr, ds.ptr, q.shape[0], q.shape[1], out.ptr, None)
+    NH.call("nh_dequantize_i8", ctx.handle, dq.ptr + shift, ds.ptr, rows, cols, out.ptr, None)
     ctx.synchronize()
     assert np.array_equal(out.numpy(), O.dequantize_i8(q, s))
 
 
 # ---- Q0d --------------------------------------------------------------------
 @pytest.mark.parametrize("packed,count,scale,zp", [([0x76, 0x98, 0x0A], 5, 0.5, 8), ([0x76, 0x98], 4, 0.5, 8),
-                                                   (None, 1_000_003, 0.037, 3)])
+                                                   (None, 1_000_003, 0.037, 3), (None, 64, 0.25, 0),
+                                                   (None, 33, 1.5, 15), (None, 3, 2.0, 1)])
 def test_dequantize_int4_matches_host_reference(ctx, packed, count, scale, zp):
     note(f"dequantize_int4 n={count}")
     if packed is None:
