@@ -232,7 +232,9 @@ _GEMM_KATS = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file_
                              (512, 2688, 128), (5, 130, 200), (1024, 300, 1030),
                              # one-output-per-lane path: a single whole 64-k block, a whole
                              # block and a 1-k tail, two whole blocks, a tail-only K
-                             (1, 64, 1), (3, 65, 130), (4, 128, 64), (7, 63, 70)]],
+                             (1, 64, 1), (3, 65, 130), (4, 128, 64), (7, 63, 70),
+                             # 64 x 64 tiles filling 256 CUs with a 1-k tail step
+                             (1024, 33, 1024)]],
                          ids=lambda c: f"{c['m']}x{c['k']}x{c['n']}")
 def test_gemm_f32_device_bit_exact_with_host_order(ctx, case):
     note(f"gemm_f32 {case['m']}x{case['k']}x{case['n']}")
