@@ -218,6 +218,23 @@ class Bench:
 
         return self.time_ms(step, steps, warmup, out=y)
 
+    def gemm_f32(self, m, k, n, steps, warmup):
+        """G0d: nh_gemm_f32 (f64 accumulation in k order, bit-identical to the
+        host GEMM) on N(0, 1) operands.  Returns ms per call."""
+        L, h = NH.lib(), self.ctx.handle
+        err = NH.NhError()
+        lhs = self.ctx.upload(NH.normal_f32(7, m * k))
+        rhs = self.ctx.upload(NH.normal_f32(8, k * n))
+        out = self.ctx.empty(m * n, np.float32)
+
+        def step(i):
+            st = L.nh_gemm_f32(h, lhs.ptr, m * k, rhs.ptr, k * n, m, k, n, out.ptr, m * n, self.stream,
+                               ctypes.byref(err))
+            if st:
+                NH.check(st, err)
+
+        return self.time_ms(step, steps, warmup, out=out)
+
     def dequant(self, n, k, steps, warmup):
         """Q0d and Q3 on an [n][k] matrix: nh_dequantize_int4 (packed codes,
         one tensor scale and zero point) and nh_dequantize_i8 (row scales), both
@@ -563,7 +580,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="headline only")
     ap.add_argument("--only", choices=["moe", "moe_shared", "moe_router", "gemm", "stack", "decode", "w8a32", "w4a8",
-                                       "dequant"],
+                                       "dequant", "gemm_f32"],
                     default=None,
                     help="run one secondary workload only (for profiling) and print its figures")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -630,6 +647,9 @@ def main():
                 res[f"m{mm}_k{kk}_n{nn}"] = round(b.w4a8(mm, nn, kk, 50, 5) * 1e3, 2)
         elif args.only == "w8a32":
             res = {"us": round(b.w8a32(4096, 4096, 200, 20) * 1e3, 2)}
+        elif args.only == "gemm_f32":
+            for (mm, kk, nn) in [(512, 2688, 128), (64, 2688, 128), (2048, 4096, 128), (512, 4096, 4096)]:
+                res[f"m{mm}_k{kk}_n{nn}"] = round(b.gemm_f32(mm, kk, nn, 20, 3) * 1e3, 1)
         elif args.only == "dequant":
             t4, t8 = b.dequant(4096, 4096, 50, 5)
             res = {"int4_us": round(t4 * 1e3, 2), "i8_us": round(t8 * 1e3, 2)}
