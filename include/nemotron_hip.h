@@ -180,11 +180,13 @@ nh_status nh_gemm_w8a8_host(const int8_t *xq, const float *sx, const int8_t *wq,
  * intermediate, then the lowest row-major index) and carries on; the codes of
  * such a row, and the outputs that depend on them, are unspecified.
  * nh_take_nonfinite synchronizes `stream`, returns NH_NON_FINITE_INPUT with
- * err->argument "input" (index into x) or "intermediate" (index into the
- * layer's f32 intermediate: the MLP's [m][inter] ReLU^2 output, the MoE's
- * [routes][inter] up output in expert-sorted slot order), err->index and
- * err->value, and clears the word; NH_OK when it is zero.  NULL skips the
- * check at no cost. */
+ * err->argument "input" (index into x), "shared_intermediate" (the MoE
+ * shared expert's f32 [tokens][shared_inter] ReLU^2 output) or
+ * "intermediate" (index into the layer's f32 intermediate: the MLP's
+ * [m][inter] ReLU^2 output, the MoE's [routes][inter] up output in
+ * expert-sorted slot order), err->index and err->value, and clears the word;
+ * NH_OK when it is zero.  The word keeps the first value in that order of
+ * stages, then the lowest index.  NULL skips the check at no cost. */
 nh_status nh_take_nonfinite(nh_context *ctx, uint64_t *nonfinite, nh_stream stream, nh_error *err);
 
 /* Quantized linear layer, the drop-in for LinearProjection::project_into
@@ -202,6 +204,20 @@ nh_status nh_linear_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const
                          const float *bias, size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype,
                          void *workspace, size_t workspace_bytes, int8_t *xq_out, float *sx_out,
                          uint64_t *nonfinite, nh_stream stream, nh_error *err);
+/* Device envelope of nh_linear_w8a8 (supports_shape, gemm.rs:247-254): 1 when
+ * the device entry point runs the shape (k % 16 == 0, k <= 131072, every
+ * dimension and product below 2^31) with a 16-byte aligned wq (and
+ * workspace); otherwise it returns NH_UNSUPPORTED and the caller takes the
+ * host twin (the host-fallback contract, gemm.rs:290-310). */
+int nh_supports_linear_w8a8(size_t m, size_t n, size_t k);
+/* Host twin of nh_linear_w8a8 (LinearProjection::project_into with int8
+ * per-row weights, linear.rs:283-342): the same arguments in host memory (wq
+ * tiled, as on the device), any shape, bit-identical outputs; no workspace.
+ * A non-finite x returns NH_NON_FINITE_INPUT ("input", index, value) before
+ * any output is written.  xq_out/sx_out optional, as on the device. */
+nh_status nh_linear_w8a8_host(const void *x, nh_dtype x_dtype, const int8_t *wq, const float *sw, const float *bias,
+                              size_t m, size_t n, size_t k, void *out, nh_dtype out_dtype, int8_t *xq_out,
+                              float *sx_out, nh_error *err);
 /* nh_linear_w8a8 without a workspace argument and without allocating, for
  * callers that cannot call hipMalloc (code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation).  No counterpart in the
@@ -231,6 +247,15 @@ nh_status nh_mlp_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const in
                       const float *b_up, const int8_t *w_down, const float *s_down, const float *b_down, size_t m,
                       size_t hidden, size_t inter, void *out, nh_dtype out_dtype, void *workspace,
                       size_t workspace_bytes, uint64_t *nonfinite, nh_stream stream, nh_error *err);
+/* Device envelope of nh_mlp_w8a8: both projections inside
+ * nh_supports_linear_w8a8 (16-byte aligned weights and workspace). */
+int nh_supports_mlp_w8a8(size_t m, size_t hidden, size_t inter);
+/* Host twin of nh_mlp_w8a8: same arguments in host memory, bit-identical
+ * outputs, no workspace; NH_NON_FINITE_INPUT "input" or "intermediate" (the
+ * f32 [m][inter] ReLU^2 output) as the device word reports them. */
+nh_status nh_mlp_w8a8_host(const void *x, nh_dtype x_dtype, const int8_t *w_up, const float *s_up, const float *b_up,
+                           const int8_t *w_down, const float *s_down, const float *b_down, size_t m, size_t hidden,
+                           size_t inter, void *out, nh_dtype out_dtype, nh_error *err);
 /* G2: W8A32 dequant GEMV, y = x * ((float)q * s)^T: the value of
  * materialize_dense + gemm_into_host (linear.rs:126-131).  The device sums
  * each 16-code group in f32 and the groups in f64, then scales by s, so
@@ -293,8 +318,21 @@ nh_status nh_moe_combine_shared(nh_context *ctx, const float *slot_out, const in
 nh_status nh_moe_combine_shared_host(const float *slot_out, const int32_t *pos, const float *weights,
                                      const float *shared, size_t tokens, size_t top_k, size_t hidden, void *out,
                                      nh_dtype out_dtype, nh_error *err);
+/* Optional biases of the int8 MoE layer's experts.  The reference's routed
+ * experts and shared expert are MlpLayers whose projections may carry biases
+ * (mlp.rs:79-96, moe.rs:60-65): an up bias is added before ReLU^2, a down
+ * bias to the expert's own output, i.e. before the combine weight
+ * (mlp.rs:201-208).  Each pointer may be NULL (no bias there); a NULL
+ * nh_moe_biases* means no biases at all.  Shared-expert biases without a
+ * shared expert are INVALID_PARAMS. */
+typedef struct nh_moe_biases {
+    const float *up;          /* [experts][inter], expert-major like s_up */
+    const float *down;        /* [experts][hidden], like s_down */
+    const float *shared_up;   /* [shared_inter] */
+    const float *shared_down; /* [hidden] */
+} nh_moe_biases;
 /* Whole int8 MoE layer on the device: Q2(x) -> R1 -> R2 -> up (R3, gather,
- * ReLU^2) -> Q2 -> down (R3) -> R4.  Replaces MoeLayer::forward_into
+ * + bias, ReLU^2) -> Q2 -> down (R3, + bias) -> R4.  Replaces MoeLayer::forward_into
  * (moe.rs:154-249) for routed experts with int8 per-row weights
  * w_up = E tiled [inter][hidden] matrices, w_down = E tiled [hidden][inter]
  * matrices, each expert at a stride of nh_tiled_weights_bytes of its shape.  The routing stages
@@ -309,14 +347,17 @@ void nh_moe_workspace_layout(size_t tokens, size_t hidden, size_t inter, size_t 
 nh_status nh_moe_forward_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, const float *logits,
                               size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
                               int renormalize, float scaling, const int8_t *w_up, const float *s_up,
-                              const int8_t *w_down, const float *s_down, void *out, nh_dtype out_dtype,
-                              void *workspace, size_t workspace_bytes, uint64_t *nonfinite, nh_stream stream,
-                              nh_error *err);
+                              const int8_t *w_down, const float *s_down, const nh_moe_biases *biases, void *out,
+                              nh_dtype out_dtype, void *workspace, size_t workspace_bytes, uint64_t *nonfinite,
+                              nh_stream stream, nh_error *err);
 /* The int8 MoE layer with its shared expert, MoeLayer::forward_into with
  * shared_expert = Some(..) (moe.rs:197-219): the shared expert is an int8
- * MLP over every token (nh_mlp_w8a8 on x, f32, no biases: w_up_shared tiled
- * [shared_inter][hidden], w_down_shared tiled [hidden][shared_inter]), added
- * to each output row before the routed experts (nh_moe_combine_shared).
+ * MLP over every token (nh_mlp_w8a8 on x, f32, with biases->shared_up and
+ * ->shared_down: w_up_shared tiled [shared_inter][hidden], w_down_shared
+ * tiled [hidden][shared_inter]), added to each output row before the routed
+ * experts (nh_moe_combine_shared).  Non-finite values of its intermediate are
+ * reported as "shared_intermediate" (index into [tokens][shared_inter]),
+ * ahead of the routed experts' "intermediate", as the reference meets them.
  * Routing, experts and errors as nh_moe_forward_w8a8; INVALID_PARAMS for a
  * NULL w_up_shared, INVALID_SHAPE for shared_inter == 0 or a missing shared
  * operand.  The workspace (nh_moe_forward_shared_w8a8_workspace_size) starts
@@ -328,9 +369,9 @@ nh_status nh_moe_forward_shared_w8a8(nh_context *ctx, const void *x, nh_dtype x_
                                      int renormalize, float scaling, const int8_t *w_up, const float *s_up,
                                      const int8_t *w_down, const float *s_down, size_t shared_inter,
                                      const int8_t *w_up_shared, const float *s_up_shared,
-                                     const int8_t *w_down_shared, const float *s_down_shared, void *out,
-                                     nh_dtype out_dtype, void *workspace, size_t workspace_bytes,
-                                     uint64_t *nonfinite, nh_stream stream, nh_error *err);
+                                     const int8_t *w_down_shared, const float *s_down_shared,
+                                     const nh_moe_biases *biases, void *out, nh_dtype out_dtype, void *workspace,
+                                     size_t workspace_bytes, uint64_t *nonfinite, nh_stream stream, nh_error *err);
 /* The whole MoeLayer::forward_into (moe.rs:154-249) from its input, router
  * included: logits = x router_w (+ router_b), router_w f32 [hidden][experts]
  * as the reference's dense router LinearProjection stores it (moe.rs:185-188,
@@ -350,8 +391,28 @@ nh_status nh_moe_layer_w8a8(nh_context *ctx, const void *x, nh_dtype x_dtype, co
                             size_t top_k, int renormalize, float scaling, const int8_t *w_up, const float *s_up,
                             const int8_t *w_down, const float *s_down, size_t shared_inter,
                             const int8_t *w_up_shared, const float *s_up_shared, const int8_t *w_down_shared,
-                            const float *s_down_shared, void *out, nh_dtype out_dtype, void *workspace,
-                            size_t workspace_bytes, uint64_t *nonfinite, nh_stream stream, nh_error *err);
+                            const float *s_down_shared, const nh_moe_biases *biases, void *out, nh_dtype out_dtype,
+                            void *workspace, size_t workspace_bytes, uint64_t *nonfinite, nh_stream stream,
+                            nh_error *err);
+/* Host twin of nh_moe_layer_w8a8 (the library's CPU implementation, for the
+ * host-fallback contract, gemm.rs:290-310): the same arguments in host
+ * memory, the same result bit for bit (router logits in f64 with k
+ * ascending, sigmoid top-k, the experts' int8 MLPs in slot order, the
+ * combine), no workspace.  Non-finite values return NH_NON_FINITE_INPUT at
+ * once, in the device word's order: "input", then "shared_intermediate",
+ * then "intermediate" (index in expert-sorted slot order). */
+nh_status nh_moe_layer_w8a8_host(const void *x, nh_dtype x_dtype, const float *router_w, const float *router_b,
+                                 size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
+                                 int renormalize, float scaling, const int8_t *w_up, const float *s_up,
+                                 const int8_t *w_down, const float *s_down, size_t shared_inter,
+                                 const int8_t *w_up_shared, const float *s_up_shared, const int8_t *w_down_shared,
+                                 const float *s_down_shared, const nh_moe_biases *biases, void *out,
+                                 nh_dtype out_dtype, nh_error *err);
+/* Device envelope of nh_moe_layer_w8a8's shape (the router GEMM, routing and
+ * the experts): 1 when the device entry point runs it with 16-byte aligned
+ * weights and workspace, 0 when it returns NH_UNSUPPORTED (take the host twin). */
+int nh_supports_moe_layer_w8a8(size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
+                               size_t shared_inter);
 
 /* ---- INT4 affine weights on the device (W4A8) ---------------------------
  * The reference's INT4 linear weights (Int4LinearWeights, linear.rs:99-131)

@@ -374,14 +374,15 @@ nh_status nh_moe_permute_host(const int32_t* indices, size_t tokens, size_t top_
     return NH_OK;
 }
 
-nh_status nh_moe_grouped_gemm_w8a8_host(const int8_t* aq, const float* sa, int gather, size_t top_k,
-                                        const int32_t* offsets, const int32_t* perm, size_t routes, size_t a_rows,
-                                        size_t experts, const int8_t* w, const float* sw, size_t n, size_t k,
-                                        int relu2_flag, float* out, nh_error* err) {
-    clear_error(err);
-    (void)routes;
-    (void)a_rows;
-    if (experts == 0 || top_k == 0 || n == 0 || k == 0) return set_error(err, NH_INVALID_SHAPE, "invalid shape");
+}  // extern "C"
+
+namespace {
+
+// R3 on the host, with an optional per-expert bias [E][n] added before
+// ReLU^2 (the experts' MlpLayer biases, mlp.rs:201-205).
+void grouped_host(const int8_t* aq, const float* sa, int gather, size_t top_k, const int32_t* offsets,
+                  const int32_t* perm, size_t experts, const int8_t* w, const float* sw, const float* bias, size_t n,
+                  size_t k, int relu2_flag, float* out) {
     std::vector<int8_t> wrow(k);
     for (size_t e = 0; e < experts; ++e) {
         const int8_t* we = w + e * (size_t)tiled_bytes(n, k);
@@ -393,12 +394,205 @@ nh_status nh_moe_grouped_gemm_w8a8_host(const int8_t* aq, const float* sa, int g
                 int32_t acc = 0;
                 for (size_t d = 0; d < k; ++d) acc += (int32_t)a[d] * (int32_t)wrow[d];
                 float y = epilogue_w8a8(acc, sa[row], sw[e * n + c]);
+                if (bias) y = y + bias[e * n + c];
                 if (relu2_flag) y = relu2(y);
                 out[(size_t)slot * n + c] = y;
             }
         }
     }
+}
+
+// Q2 of x then G1/G3 + bias [+ ReLU^2] into out (the order of
+// LinearProjection::project_into, linear.rs:325-339, then mlp.rs:205).  A
+// non-finite x is NonFiniteInput with argument `what`.
+nh_status linear_host(const void* x, nh_dtype x_dtype, const int8_t* wq, const float* sw, const float* bias,
+                      size_t m, size_t n, size_t k, int relu2_flag, void* out, nh_dtype out_dtype, int8_t* xq_out,
+                      float* sx_out, const char* what, nh_error* err) {
+    std::vector<int8_t> xq(m * k);
+    std::vector<float> sx(m);
+    nh_status st = nh_quantize_rows_i8_host(x, x_dtype, m, k, xq.data(), sx.data(), err);
+    if (st) {
+        if (err && st == NH_NON_FINITE_INPUT) err->argument = what;
+        return st;
+    }
+    std::vector<int8_t> row(k);
+    for (size_t c = 0; c < n; ++c) {
+        untile_row(wq, c, k, row.data());
+        for (size_t r = 0; r < m; ++r) {
+            int32_t acc = 0;
+            for (size_t d = 0; d < k; ++d) acc += (int32_t)xq[r * k + d] * (int32_t)row[d];
+            float y = epilogue_w8a8(acc, sx[r], sw[c]);
+            if (bias) y = y + bias[c];
+            if (relu2_flag) y = relu2(y);
+            store_f32(out, r * n + c, y, out_dtype);
+        }
+    }
+    if (xq_out) std::memcpy(xq_out, xq.data(), m * k);
+    if (sx_out) std::memcpy(sx_out, sx.data(), m * sizeof(float));
     return NH_OK;
+}
+
+// The MLP (mlp.rs:157-211) on the host: h = ReLU^2(x W_up^T + b_up) in f32,
+// then h quantized per row (its non-finite values reported as `h_what`) and
+// projected down (+ b_down).
+nh_status mlp_host(const void* x, nh_dtype x_dtype, const int8_t* w_up, const float* s_up, const float* b_up,
+                   const int8_t* w_down, const float* s_down, const float* b_down, size_t m, size_t hidden,
+                   size_t inter, void* out, nh_dtype out_dtype, const char* h_what, nh_error* err) {
+    std::vector<float> h(m * inter);
+    nh_status st = linear_host(x, x_dtype, w_up, s_up, b_up, m, inter, hidden, 1, h.data(), NH_F32, nullptr, nullptr,
+                               "input", err);
+    if (st) return st;
+    return linear_host(h.data(), NH_F32, w_down, s_down, b_down, m, hidden, inter, 0, out, out_dtype, nullptr, nullptr,
+                       h_what, err);
+}
+
+bool dims_ok(size_t a, size_t b, size_t c) {
+    size_t t;
+    return a && b && c && mul_ok(a, b, &t) && mul_ok(b, c, &t) && mul_ok(a, c, &t);
+}
+
+}  // namespace
+
+extern "C" {
+
+nh_status nh_moe_grouped_gemm_w8a8_host(const int8_t* aq, const float* sa, int gather, size_t top_k,
+                                        const int32_t* offsets, const int32_t* perm, size_t routes, size_t a_rows,
+                                        size_t experts, const int8_t* w, const float* sw, size_t n, size_t k,
+                                        int relu2_flag, float* out, nh_error* err) {
+    clear_error(err);
+    (void)routes;
+    (void)a_rows;
+    if (experts == 0 || top_k == 0 || n == 0 || k == 0) return set_error(err, NH_INVALID_SHAPE, "invalid shape");
+    grouped_host(aq, sa, gather, top_k, offsets, perm, experts, w, sw, nullptr, n, k, relu2_flag, out);
+    return NH_OK;
+}
+
+int nh_supports_linear_w8a8(size_t m, size_t n, size_t k) { return dims_ok(m, n, k) && nh_supports_gemm_w8a8(m, n, k); }
+
+int nh_supports_mlp_w8a8(size_t m, size_t hidden, size_t inter) {
+    return nh_supports_linear_w8a8(m, inter, hidden) && nh_supports_linear_w8a8(m, hidden, inter);
+}
+
+nh_status nh_linear_w8a8_host(const void* x, nh_dtype x_dtype, const int8_t* wq, const float* sw, const float* bias,
+                              size_t m, size_t n, size_t k, void* out, nh_dtype out_dtype, int8_t* xq_out,
+                              float* sx_out, nh_error* err) {
+    clear_error(err);
+    // project_into's order (linear.rs:290-311): the layer's shape, then the rows
+    if (n == 0 || k == 0) return set_error(err, NH_INVALID_SHAPE, "invalid linear shape k=%zu n=%zu", k, n);
+    if (m == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
+    if ((x_dtype != NH_F32 && x_dtype != NH_BF16) || (out_dtype != NH_F32 && out_dtype != NH_BF16))
+        return set_error(err, NH_INVALID_PARAMS, "unknown dtype");
+    if (!dims_ok(m, n, k)) return set_error(err, NH_INVALID_SHAPE, "linear shape m=%zu n=%zu k=%zu overflows", m, n, k);
+    return linear_host(x, x_dtype, wq, sw, bias, m, n, k, 0, out, out_dtype, xq_out, sx_out, "input", err);
+}
+
+nh_status nh_mlp_w8a8_host(const void* x, nh_dtype x_dtype, const int8_t* w_up, const float* s_up, const float* b_up,
+                           const int8_t* w_down, const float* s_down, const float* b_down, size_t m, size_t hidden,
+                           size_t inter, void* out, nh_dtype out_dtype, nh_error* err) {
+    clear_error(err);
+    if (hidden == 0 || inter == 0)
+        return set_error(err, NH_INVALID_SHAPE, "mlp shape must be non-zero, got hidden_dim=%zu, intermediate_dim=%zu",
+                         hidden, inter);
+    if (m == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
+    if ((x_dtype != NH_F32 && x_dtype != NH_BF16) || (out_dtype != NH_F32 && out_dtype != NH_BF16))
+        return set_error(err, NH_INVALID_PARAMS, "unknown dtype");
+    if (!dims_ok(m, inter, hidden)) return set_error(err, NH_INVALID_SHAPE, "mlp shape overflows");
+    return mlp_host(x, x_dtype, w_up, s_up, b_up, w_down, s_down, b_down, m, hidden, inter, out, out_dtype,
+                    "intermediate", err);
+}
+
+int nh_supports_moe_layer_w8a8(size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
+                               size_t shared_inter) {
+    size_t routes, t;
+    if (!tokens || !hidden || !inter || !experts || !top_k || top_k > experts) return 0;
+    if (!mul_ok(tokens, top_k, &routes) || routes >= (1ull << 31) || !mul_ok(tokens, hidden, &t)) return 0;
+    // the router GEMM, the routing and the permutation
+    if (!nh_supports_gemm_f32(tokens, hidden, experts) || experts > 1024 || top_k > 64 || tokens > 0x7fffffff / 4)
+        return 0;
+    // the expert GEMMs (the grouped kernel's envelope covers the fused pair)
+    if (!nh_supports_gemm_w8a8(routes, inter, hidden) || !nh_supports_gemm_w8a8(routes, hidden, inter)) return 0;
+    if (hidden > 8192 || inter > 8192 || routes * hidden >= (1ull << 31) || routes * inter >= (1ull << 31)) return 0;
+    return shared_inter == 0 || nh_supports_mlp_w8a8(tokens, hidden, shared_inter);
+}
+
+nh_status nh_moe_layer_w8a8_host(const void* x, nh_dtype x_dtype, const float* router_w, const float* router_b,
+                                 size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
+                                 int renormalize, float scaling, const int8_t* w_up, const float* s_up,
+                                 const int8_t* w_down, const float* s_down, size_t shared_inter,
+                                 const int8_t* w_up_shared, const float* s_up_shared, const int8_t* w_down_shared,
+                                 const float* s_down_shared, const nh_moe_biases* biases, void* out,
+                                 nh_dtype out_dtype, nh_error* err) {
+    clear_error(err);
+    // the device entry point's checks, in its order
+    if (tokens == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
+    if (hidden == 0 || experts == 0 || top_k == 0 || top_k > experts || inter == 0)
+        return set_error(err, NH_INVALID_SHAPE, "invalid MoE shape");
+    if (!router_w) return set_error(err, NH_INVALID_PARAMS, "router_w must not be null");
+    if ((shared_inter != 0) != (w_up_shared != nullptr))
+        return set_error(err, NH_INVALID_SHAPE, "shared_inter and w_up_shared must be given together");
+    if ((x_dtype != NH_F32 && x_dtype != NH_BF16) || (out_dtype != NH_F32 && out_dtype != NH_BF16))
+        return set_error(err, NH_INVALID_PARAMS, "unknown dtype");
+    const bool has_shared = w_up_shared != nullptr;
+    if (has_shared && (!s_up_shared || !w_down_shared || !s_down_shared))
+        return set_error(err, NH_INVALID_SHAPE, "shared expert needs intermediate_dim > 0 and all four operands");
+    const nh_moe_biases nob{nullptr, nullptr, nullptr, nullptr};
+    const nh_moe_biases& b = biases ? *biases : nob;
+    if (!has_shared && (b.shared_up || b.shared_down))
+        return set_error(err, NH_INVALID_PARAMS, "shared expert biases given without a shared expert");
+    size_t routes;
+    if (!mul_ok(tokens, top_k, &routes) || !dims_ok(tokens, hidden, experts) || !dims_ok(routes, inter, hidden) ||
+        routes >= (1ull << 31))
+        return set_error(err, NH_INVALID_SHAPE, "MoE shape overflows");
+    // Q2 of every token (the routed experts' A rows); a non-finite x is the
+    // layer's input error, ahead of everything else
+    std::vector<int8_t> xq(tokens * hidden);
+    std::vector<float> sx(tokens);
+    nh_status st = nh_quantize_rows_i8_host(x, x_dtype, tokens, hidden, xq.data(), sx.data(), err);
+    if (st) {
+        if (err && st == NH_NON_FINITE_INPUT) err->argument = "input";
+        return st;
+    }
+    // router.project (moe.rs:185-188): gemm_into_host (f64, k ascending), then the bias in f32
+    std::vector<float> logits(tokens * experts);
+    for (size_t t = 0; t < tokens; ++t)
+        for (size_t e = 0; e < experts; ++e) {
+            double acc = 0.0;
+            for (size_t d = 0; d < hidden; ++d)
+                acc += (double)load_f32(x, t * hidden + d, x_dtype) * (double)router_w[d * experts + e];
+            float v = (float)acc;
+            if (router_b) v = v + router_b[e];
+            logits[t * experts + e] = v;
+        }
+    std::vector<int32_t> idx(routes), offsets(experts + 1), perm(routes), pos(routes);
+    std::vector<float> wts(routes);
+    if ((st = nh_moe_route_sigmoid_topk_host(logits.data(), logits.size(), tokens, experts, top_k, renormalize,
+                                             scaling, idx.data(), routes, wts.data(), routes, err)))
+        return st;
+    if ((st = nh_moe_permute_host(idx.data(), tokens, top_k, experts, offsets.data(), perm.data(), pos.data(), err)))
+        return st;
+    // the shared expert first (moe.rs:197-219): its intermediate is met before the routed experts'
+    std::vector<float> shared;
+    if (has_shared) {
+        shared.resize(tokens * hidden);
+        if ((st = mlp_host(x, x_dtype, w_up_shared, s_up_shared, b.shared_up, w_down_shared, s_down_shared,
+                           b.shared_down, tokens, hidden, shared_inter, shared.data(), NH_F32, "shared_intermediate",
+                           err)))
+            return st;
+    }
+    // up (+ bias, ReLU^2) per slot, h quantized per row (the layer's intermediate), down (+ bias)
+    std::vector<float> h(routes * inter), d(routes * hidden);
+    grouped_host(xq.data(), sx.data(), 1, top_k, offsets.data(), perm.data(), experts, w_up, s_up, b.up, inter, hidden,
+                 1, h.data());
+    std::vector<int8_t> hq(routes * inter);
+    std::vector<float> sh(routes);
+    if ((st = nh_quantize_rows_i8_host(h.data(), NH_F32, routes, inter, hq.data(), sh.data(), err))) {
+        if (err && st == NH_NON_FINITE_INPUT) err->argument = "intermediate";
+        return st;
+    }
+    grouped_host(hq.data(), sh.data(), 0, top_k, offsets.data(), perm.data(), experts, w_down, s_down, b.down, hidden,
+                 inter, 0, d.data());
+    return nh_moe_combine_shared_host(d.data(), pos.data(), wts.data(), has_shared ? shared.data() : nullptr, tokens,
+                                      top_k, hidden, out, out_dtype, err);
 }
 
 nh_status nh_moe_combine_host(const float* slot_out, const int32_t* pos, const float* weights, size_t tokens,

@@ -57,20 +57,26 @@ __device__ __forceinline__ v4i rsrc_words(const void* base, uint32_t bytes) {
     return v4i{(int)(uint32_t)p, (int)((uint32_t)(p >> 32) & 0xffffu), (int)bytes, 0x00020000};
 }
 
-// 16 bytes per lane from rsrc + voffset into LDS at lds_addr + 16 lane (one
-// wait state between the M0 write and the load that reads it as its LDS base).
+// 16 bytes per lane from rsrc + voffset into LDS at lds_addr + 16 lane.  The
+// load takes its LDS base from M0, a register the compiler reserves: the asm
+// saves M0 in an SGPR of its own, sets it (one wait state before the load
+// reads it), issues the load and puts the saved value back, so M0 holds the
+// same value after the statement as before it and needs no clobber.
 __device__ __forceinline__ void lds_dma16(v4i rsrc, uint32_t voffset, uint32_t lds_addr) {
     // the resource and the LDS address are wave-uniform; say so, so that they are passed in SGPRs
     lds_addr = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_addr);
     rsrc = v4i{__builtin_amdgcn_readfirstlane(rsrc[0]), __builtin_amdgcn_readfirstlane(rsrc[1]),
                __builtin_amdgcn_readfirstlane(rsrc[2]), __builtin_amdgcn_readfirstlane(rsrc[3])};
+    uint32_t saved;
     asm volatile(
-        "s_mov_b32 m0, %0\n\t"
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
         "s_nop 0\n\t"
-        "buffer_load_dwordx4 %1, %2, 0 offen lds"
-        :
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
         : "s"(lds_addr), "v"(voffset), "s"(rsrc)
-        : "memory", "m0");
+        : "memory");
 }
 
 

@@ -72,7 +72,8 @@ __device__ __forceinline__ void store_y(void* out, int out_dtype, int64_t i, int
 
 // The first non-finite activation of rows that hold one (the row maxima
 // said so; a uniform, rare branch), from the workgroup's registers: xv[m][v]
-// holds the 8 values at column (threadIdx.x + v T) 8 of row m.
+// holds the 8 values at column (threadIdx.x + v T) 8 of row m.  The index is
+// reported in the caller's whole input: this launch's rows start at row0.
 template <int MM>
 __device__ __forceinline__ void report_decode_rows(const LinearDecodeArgs& a, const v4i (&xv)[MM][2], int T) {
     __shared__ int red_nf[16];
@@ -87,7 +88,8 @@ __device__ __forceinline__ void report_decode_rows(const LinearDecodeArgs& a, co
         }
     first = block_min_i32(first, red_nf);
     if (threadIdx.x == 0 && first != 0x7fffffff)
-        report_nonfinite(a.nonfinite, 0, first, bf16_to_f32(((const uint16_t*)a.x)[first]));
+        report_nonfinite(a.nonfinite, 0, (int64_t)a.row0 * a.K + first,
+                         bf16_to_f32(((const uint16_t*)a.x)[first]));
 }
 
 // The same for the wide decode units: xv[j] holds chunk c0 + j stride of
@@ -106,7 +108,8 @@ __device__ __forceinline__ void report_decode_chunks(const LinearDecodeArgs& a, 
     }
     first = block_min_i32(first, red_nf);
     if (threadIdx.x == 0 && first != 0x7fffffff)
-        report_nonfinite(a.nonfinite, 0, first, bf16_to_f32(((const uint16_t*)a.x)[first]));
+        report_nonfinite(a.nonfinite, 0, (int64_t)a.row0 * a.K + first,
+                         bf16_to_f32(((const uint16_t*)a.x)[first]));
 }
 
 }  // namespace

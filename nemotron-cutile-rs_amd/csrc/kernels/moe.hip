@@ -378,6 +378,7 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(Gro
     const __amdgpu_buffer_rsrc_t ar = make_rsrc(a.aq, (uint32_t)a.a_rows * (uint32_t)K);
     const int n = tile * 16 + r16;
     const float swn = n < N ? a.sw[(int64_t)e * N + n] : 0.0f;
+    const float bn = a.bias && n < N ? a.bias[(int64_t)e * N + n] : 0.0f;
     // A row of slot s (gathered rows: the public entry point's token-major
     // activations; the MoE layer passes them already in slot order)
     auto a_row = [&](int s) { return a.gather ? a.perm[s] / a.top_k : s; };
@@ -430,6 +431,7 @@ extern "C" __global__ __launch_bounds__(512) void nh_moe_grouped_gemm_kernel(Gro
                 const int srow = m0 + 4 * g + r;
                 if (srow < seg1) {
                     float y = epilogue_w8a8(acc[r], sa_cur[r], swn);
+                    if (a.bias) y = y + bn;
                     if (a.relu2) y = relu2(y);
                     a.out[(int64_t)srow * N + n] = y;
                 }
@@ -473,8 +475,9 @@ constexpr int kExpertPlain = 0, kExpertOmax = 1, kExpertQuantA = 2;
 template <int NRB, int MODE>
 __device__ __forceinline__ void expert_stream(const ExpertGemmArgs& a, v4i (&b0)[kExpertSlab],
                                               v4i (&b1)[kExpertSlab], const int8_t* As, const float* sas,
-                                              const float* sws, const int8_t* wexp, int wave, int lane, int t_begin,
-                                              int nj, int nch, int p0, int seg1, uint32_t* lmax) {
+                                              const float* sws, const float* sbs, const int8_t* wexp, int wave,
+                                              int lane, int t_begin, int nj, int nch, int p0, int seg1,
+                                              uint32_t* lmax) {
     const int N = a.N, kt = a.kt, NW = a.streams;
     const int r16 = lane & 15, g = lane >> 4;
     auto load_chunk = [&](v4i (&b)[kExpertSlab], int j) {
@@ -521,6 +524,7 @@ __device__ __forceinline__ void expert_stream(const ExpertGemmArgs& a, v4i (&b0)
         // workgroup of the expert, so it stores nothing
         if (j < nj && c == nch - 1 && n < N) {
             const float swn = sws[n - t_begin * 16];
+            const float bn = a.bias ? sbs[n - t_begin * 16] : 0.0f;
             // one per-lane base (row p0 + 4 g, column n); rows rb * 16 + r are uniform offsets
             float* ob = a.out + (int64_t)(p0 + 4 * g) * N + n;
             const int rows = seg1 - p0 - 4 * g;  // rows of this lane's group in the pass
@@ -530,6 +534,7 @@ __device__ __forceinline__ void expert_stream(const ExpertGemmArgs& a, v4i (&b0)
                 for (int r = 0; r < 4; ++r)
                     if (rb * 16 + r < rows) {
                         float y = epilogue_w8a8(acc[rb][r], sas[rb * 16 + 4 * g + r], swn);
+                        if (a.bias) y = y + bn;
                         if (a.relu2) y = relu2(y);
                         ob[(rb * 16 + r) * N] = y;
                         if constexpr (MODE == kExpertOmax) {
@@ -605,7 +610,20 @@ __device__ __forceinline__ void expert_gemm(const ExpertGemmArgs& a, int8_t* lds
     float* sas = (float*)(lds + RB * kt * 1024);     // [16 RB] the pass's row scales
     uint32_t* lmax = (uint32_t*)(sas + 16 * RB);     // [64] kExpertOmax: the pass's row maxima
     float* sws = (float*)(lmax + 64);                // [16 tiles_per_wg, rounded up to 64] weight scales
+    float* sbs = sws + (16 * a.tiles_per_wg + 63) / 64 * 64;  // the same for the bias (when a.bias)
     const __amdgpu_buffer_rsrc_t swr = make_rsrc(a.sw + (int64_t)e * N + t_begin * 16, (uint32_t)nw_cols * 4u);
+    const __amdgpu_buffer_rsrc_t sbr =
+        make_rsrc(a.bias ? a.bias + (int64_t)e * N + t_begin * 16 : a.sw, a.bias ? (uint32_t)nw_cols * 4u : 0u);
+    // the workgroup's weight scales (and bias) straight into LDS, 64 floats per wave instruction
+    auto stage_scales = [&]() {
+        for (int i = wave * 64; i < nw_cols; i += NW * 64) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(swr, (lds_void_t*)(sws + i), 4, (uint32_t)(i + lane) * 4u, 0,
+                                                     0, 0);
+            if (a.bias)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(sbr, (lds_void_t*)(sbs + i), 4, (uint32_t)(i + lane) * 4u,
+                                                         0, 0, 0);
+        }
+    };
     const int8_t* wexp = a.w + (int64_t)e * tiled_bytes(N, K);
     v4i b0[kExpertSlab], b1[kExpertSlab];
     auto first = [&](v4i (&b)[kExpertSlab], int j) {
@@ -634,9 +652,7 @@ __device__ __forceinline__ void expert_gemm(const ExpertGemmArgs& a, int8_t* lds
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_void_t*)(As + i * 1024), 16,
                                                              slot < seg1 ? off : (uint32_t)kOutOfRange, 0, 0, 0);
                 }
-                for (int i = wave * 64; i < nw_cols; i += NW * 64)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(swr, (lds_void_t*)(sws + i), 4,
-                                                             (uint32_t)(i + lane) * 4u, 0, 0, 0);
+                stage_scales();
                 if ((int)threadIdx.x < cap && p0 + (int)threadIdx.x < seg1) sav = a.sa[p0 + threadIdx.x];
                 __builtin_amdgcn_sched_barrier(0);
                 first(b0, 0);
@@ -671,9 +687,7 @@ __device__ __forceinline__ void expert_gemm(const ExpertGemmArgs& a, int8_t* lds
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_void_t*)(As + i * 1024), 16,
                                                              tr >= 0 ? off : (uint32_t)kOutOfRange, 0, 0, 0);
                 }
-                for (int i = wave * 64; i < nw_cols; i += NW * 64)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(swr, (lds_void_t*)(sws + i), 4,
-                                                             (uint32_t)(i + lane) * 4u, 0, 0, 0);
+                stage_scales();
                 // thread t < cap holds slot p0 + t: row block t / 16 = g of its wave 0 lane
                 if ((int)threadIdx.x < cap) {
                     const int tr = g == 0 ? tok[0] : g == 1 ? tok[1] : g == 2 ? tok[2] : tok[3];
@@ -740,9 +754,7 @@ __device__ __forceinline__ void expert_gemm(const ExpertGemmArgs& a, int8_t* lds
             issue(1, hv[1]);
             __builtin_amdgcn_sched_barrier(0);
             first(b0, 0);
-            for (int i = wave * 64; i < nw_cols; i += NW * 64)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(swr, (lds_void_t*)(sws + i), 4, (uint32_t)(i + lane) * 4u,
-                                                         0, 0, 0);
+            stage_scales();
             __builtin_amdgcn_sched_barrier(0);
             consume(0, hv[0]);
             issue(2, hv[0]);
@@ -754,14 +766,14 @@ __device__ __forceinline__ void expert_gemm(const ExpertGemmArgs& a, int8_t* lds
             __builtin_amdgcn_sched_barrier(0);
             first(b1, 1);
             __builtin_amdgcn_sched_barrier(0);
-            wait_vmcnt_le(kExpertSlab);  // the weight scales' direct-to-LDS loads in, the second chunk in flight
+            wait_vmcnt_le(kExpertSlab);  // the weight scales' (and bias') direct-to-LDS loads in, the second chunk in flight
         }
         lds_publish();  // every wave's A tiles and the scales
         switch (nrb) {
-        case 1: expert_stream<1, MODE>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1, lmax); break;
-        case 2: expert_stream<2, MODE>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1, lmax); break;
-        case 3: expert_stream<3, MODE>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1, lmax); break;
-        default: expert_stream<4, MODE>(a, b0, b1, As, sas, sws, wexp, wave, lane, t_begin, nj, nch, p0, seg1, lmax); break;
+        case 1: expert_stream<1, MODE>(a, b0, b1, As, sas, sws, sbs, wexp, wave, lane, t_begin, nj, nch, p0, seg1, lmax); break;
+        case 2: expert_stream<2, MODE>(a, b0, b1, As, sas, sws, sbs, wexp, wave, lane, t_begin, nj, nch, p0, seg1, lmax); break;
+        case 3: expert_stream<3, MODE>(a, b0, b1, As, sas, sws, sbs, wexp, wave, lane, t_begin, nj, nch, p0, seg1, lmax); break;
+        default: expert_stream<4, MODE>(a, b0, b1, As, sas, sws, sbs, wexp, wave, lane, t_begin, nj, nch, p0, seg1, lmax); break;
         }
         lds_publish();  // the pass's A and scale reads are done before the next pass restages them
         if constexpr (MODE == kExpertOmax)

@@ -108,14 +108,19 @@ __device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
 }
 
 // NonFiniteInput (quantize.rs:193-195: the first offending element and its
-// value) from the device quantizers.  The key (stage << 63 | flat index << 32
-// | f32 bits of the value) goes into the caller's 64-bit word as its
-// complement through an atomic max, so the word keeps the smallest key (the
-// layer's input before an intermediate, then the lowest row-major index) and
-// a zeroed word means that nothing was found.  Flat indices are < 2^31 (the
-// device envelope).  Vector atomic only.
+// value) from the device quantizers.  The key goes into the caller's 64-bit
+// word as its complement through an atomic max, so the word keeps the
+// smallest key (the lowest NonFiniteStage, then the lowest row-major index)
+// and a zeroed word means that nothing was found:
+//   bits 62..63  the stage (NonFiniteStage)
+//   bits 24..61  the flat index (38 bits: every index the device envelope allows)
+//   bit  23      the value's sign
+//   bits  0..22  the value's mantissa (its exponent is all ones: NaN or infinity)
+// nh_take_nonfinite decodes it.  Vector atomic only.
 __device__ __forceinline__ void report_nonfinite(uint64_t* word, int stage, int64_t index, float value) {
-    const uint64_t key = ((uint64_t)(stage & 1) << 63) | ((uint64_t)(index & 0x7fffffff) << 32) | f32_bits(value);
+    const uint32_t b = f32_bits(value);
+    const uint64_t key = ((uint64_t)(stage & 3) << 62) | (((uint64_t)index & ((1ull << 38) - 1)) << 24) |
+                         (uint64_t)((b >> 8) & 0x800000u) | (uint64_t)(b & 0x7fffffu);
     atomicMax((unsigned long long*)word, (unsigned long long)~key);
 }
 

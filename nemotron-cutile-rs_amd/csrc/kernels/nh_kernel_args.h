@@ -9,6 +9,16 @@ namespace nh {
 
 enum DType : int32_t { DT_F32 = 0, DT_BF16 = 1 };
 
+// Where a non-finite value was found (the stage field of the non-finite key,
+// report_nonfinite in nh_device.h): a smaller stage is reported first, in the
+// order the reference would meet the value (MoeLayer::forward_into runs its
+// shared expert before the routed experts, moe.rs:197-233).
+enum NonFiniteStage : int32_t {
+    kStageInput = 0,               // the layer's input x
+    kStageSharedIntermediate = 1,  // the MoE shared expert's f32 intermediate [tokens][shared_inter]
+    kStageIntermediate = 2,        // the layer's f32 intermediate (MLP [m][inter], MoE [routes][inter])
+};
+
 // Q1/Q2: one workgroup per row.
 struct QuantizeRowsArgs {
     const void* x;        // f32 or bf16 [rows][cols]
@@ -27,7 +37,7 @@ struct QuantizeRowsArgs {
     int32_t gather_div;   // with gather: output row r quantizes input row gather[r] / gather_div
     const int32_t* gather;  // or null (output row r = input row r)
     uint64_t* nonfinite;  // or null: the first non-finite element (report_nonfinite, nh_device.h)
-    int32_t nonfinite_stage;  // 0: x is the caller's input; 1: an intermediate of the layer
+    int32_t nonfinite_stage;  // NonFiniteStage of x
     int32_t pad_;
 };
 
@@ -117,7 +127,8 @@ struct LinearDecodeArgs {
     int32_t relu2;        // ReLU^2 after the bias (the MLP up projection)
     int32_t w4_zp;        // INT4 weights (tiled_int4): the per-tensor zero point
     float w4_scale;       //   and scale, used in place of sw
-    int32_t pad_;
+    int32_t row0;         // first row of x in the caller's whole input (launches over groups of its rows):
+                          // non-finite activations are reported at index (row0 + m) * K + k
     uint64_t* nonfinite;  // or null: the first non-finite activation (report_nonfinite, nh_device.h)
     uint32_t* row_max;    // or null (streaming unit, f32 out): [gridDim.x][M] largest finite |y| of the
                           // workgroup's outputs per row, as f32 bits (each workgroup writes its own slots)
@@ -232,6 +243,7 @@ struct GroupedGemmArgs {
     const int32_t* perm;     // [R]
     const int8_t* w;         // [E] x tiled [N][K], expert stride tiled_bytes(N, K)
     const float* sw;         // [E][N]
+    const float* bias;       // [E][N] or null: added before ReLU^2 (mlp.rs:201-205)
     float* out;              // [R][N]
     int32_t experts, N, K;
     int32_t top_k;
@@ -253,6 +265,7 @@ struct ExpertGemmArgs {
     const int32_t* offsets;  // [E+1]
     const int8_t* w;         // [E] x tiled [N][K], expert stride tiled_bytes(N, K)
     const float* sw;         // [E][N]
+    const float* bias;       // [E][N] or null: added before ReLU^2 (mlp.rs:201-205), staged in LDS with sw
     float* out;              // [R][N]
     int32_t N, K, kt;
     int32_t a_rows;          // R

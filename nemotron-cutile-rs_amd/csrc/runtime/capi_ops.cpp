@@ -473,6 +473,7 @@ nh_status nh_linear_w4a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const
         a.ntw = 1;
         a.w4_zp = (int)zero_point;
         a.w4_scale = scale;
+        a.row0 = (int)r0;  // the group's first row: non-finite inputs are indexed in the whole x
         a.nonfinite = nonfinite;
         const size_t lds = mm * ((size_t)w * 1024 + 16);
         if (lds > ctx->max_shared_per_block) return set_error(err, NH_UNSUPPORTED, "LDS too small");
@@ -685,10 +686,14 @@ size_t nh_mlp_w8a8_workspace_size(size_t m, size_t hidden, size_t inter) {
     return align256(m * inter * sizeof(float)) + align256(kMaxStreamGroups * 8 * sizeof(uint32_t)) + (a > b ? a : b);
 }
 
-nh_status nh_mlp_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* w_up, const float* s_up,
-                      const float* b_up, const int8_t* w_down, const float* s_down, const float* b_down, size_t m,
-                      size_t hidden, size_t inter, void* out, nh_dtype out_dtype, void* workspace,
-                      size_t workspace_bytes, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
+}  // extern "C"
+
+// nh_mlp_w8a8, its f32 intermediate reported at NonFiniteStage h_stage (the
+// MoE layer's shared expert: kStageSharedIntermediate).
+static nh_status mlp_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* w_up, const float* s_up,
+                          const float* b_up, const int8_t* w_down, const float* s_down, const float* b_down, size_t m,
+                          size_t hidden, size_t inter, void* out, nh_dtype out_dtype, void* workspace,
+                          size_t workspace_bytes, uint64_t* nonfinite, int h_stage, nh_stream stream, nh_error* err) {
     clear_error(err);
     if (hidden == 0 || inter == 0)
         return set_error(err, NH_INVALID_SHAPE, "mlp shape must be non-zero, got hidden_dim=%zu, intermediate_dim=%zu",
@@ -718,11 +723,11 @@ nh_status nh_mlp_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const in
         // rows and spreads each row over many workgroups (K = 21504: 8.9 us
         // as one workgroup per row)
         if ((st = linear_w8a8(ctx, x, x_dtype, w_up, s_up, b_up, m, inter, hidden, h, NH_F32, lin_ws, lin_bytes,
-                              nullptr, nullptr, 1, nonfinite, 0, stream, err, hmax)))
+                              nullptr, nullptr, 1, nonfinite, kStageInput, stream, err, hmax)))
             return st;
         int8_t* tiles = (int8_t*)lin_ws;
         float* sh = (float*)((char*)lin_ws + align256(act_tiles_bytes(m, inter)));
-        QuantizePmaxArgs q{h, hmax, tiles, sh, nonfinite, (int)m, (int)inter, (int)groups, 1};
+        QuantizePmaxArgs q{h, hmax, tiles, sh, nonfinite, (int)m, (int)inter, (int)groups, h_stage};
         if ((st = launch(ctx, K_QUANTIZE_ROWS_PMAX, (unsigned)((inter / 4 + 255) / 256), 256, 0, stream, q, err,
                          (unsigned)m)))
             return st;
@@ -730,11 +735,21 @@ nh_status nh_mlp_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const in
                            true, stream, err);
     }
     if ((st = linear_w8a8(ctx, x, x_dtype, w_up, s_up, b_up, m, inter, hidden, h, NH_F32, lin_ws, lin_bytes, nullptr,
-                          nullptr, 1, nonfinite, 0, stream, err)))
+                          nullptr, 1, nonfinite, kStageInput, stream, err)))
         return st;
-    // h: the layer's intermediate (stage 1 of the non-finite report)
+    // h: the layer's intermediate (h_stage of the non-finite report)
     return linear_w8a8(ctx, h, NH_F32, w_down, s_down, b_down, m, hidden, inter, out, out_dtype, lin_ws, lin_bytes,
-                       nullptr, nullptr, 0, nonfinite, 1, stream, err);
+                       nullptr, nullptr, 0, nonfinite, h_stage, stream, err);
+}
+
+extern "C" {
+
+nh_status nh_mlp_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const int8_t* w_up, const float* s_up,
+                      const float* b_up, const int8_t* w_down, const float* s_down, const float* b_down, size_t m,
+                      size_t hidden, size_t inter, void* out, nh_dtype out_dtype, void* workspace,
+                      size_t workspace_bytes, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
+    return mlp_w8a8(ctx, x, x_dtype, w_up, s_up, b_up, w_down, s_down, b_down, m, hidden, inter, out, out_dtype,
+                    workspace, workspace_bytes, nonfinite, kStageIntermediate, stream, err);
 }
 
 nh_status nh_gemv_w8a32(nh_context* ctx, const float* x, const int8_t* wq, const float* sw, size_t m, size_t n,
@@ -811,9 +826,10 @@ static nh_status launch_expert_gemm(nh_context* ctx, KernelId id, ExpertGemmArgs
     // the weight scales arrive by 64-float direct-to-LDS rows (256 bytes
     // each, also past the workgroup's last column), so their region is a
     // whole number of rows
+    // (and as many for the bias, when there is one)
     auto expert_lds = [&](int rb) {
         const size_t sws_floats = ((size_t)tiles_per_wg * 16 + 63) / 64 * 64;
-        return (size_t)rb * kt * 1024 + (size_t)rb * 16 * 4 + 64 * 4 + sws_floats * 4;
+        return (size_t)rb * kt * 1024 + (size_t)rb * 16 * 4 + 64 * 4 + sws_floats * 4 * (e.bias ? 2 : 1);
     };
     int row_blocks = 4;
     while (row_blocks > 1 && expert_lds(row_blocks) > ctx->max_shared_per_block) --row_blocks;
@@ -843,20 +859,20 @@ static bool expert_fused_ok(nh_context* ctx, size_t routes, size_t experts, size
     // the down kernel stages each 16-row block as 4 K tiles per wave (8
     // waves): inter <= 2048
     if (tiled_k_tiles(inter) > 32) return false;
-    auto fits = [&](size_t n, size_t k) {
+    auto fits = [&](size_t n, size_t k) {  // one row block, the weight scales and a bias
         const size_t tiles_per_wg = ((n + 15) / 16 + 1) / 2;
         const size_t sws_floats = (tiles_per_wg * 16 + 63) / 64 * 64;
-        return tiled_k_tiles(k) * 1024 + 16 * 4 + 64 * 4 + sws_floats * 4 <= ctx->max_shared_per_block;
+        return tiled_k_tiles(k) * 1024 + 16 * 4 + 64 * 4 + 2 * sws_floats * 4 <= ctx->max_shared_per_block;
     };
     return fits(inter, hidden) && fits(hidden, inter);
 }
 
-extern "C" {
-
-nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const float* sa, int gather, size_t top_k,
-                                   const int32_t* offsets, const int32_t* perm, size_t routes, size_t a_rows,
-                                   size_t experts, const int8_t* w, const float* sw, size_t n, size_t k, int relu2,
-                                   float* out, nh_stream stream, nh_error* err) {
+// nh_moe_grouped_gemm_w8a8 with an optional per-expert bias [E][n], added
+// before ReLU^2 (the experts' MlpLayer biases, mlp.rs:201-205).
+static nh_status moe_grouped_gemm(nh_context* ctx, const int8_t* aq, const float* sa, int gather, size_t top_k,
+                                  const int32_t* offsets, const int32_t* perm, size_t routes, size_t a_rows,
+                                  size_t experts, const int8_t* w, const float* sw, const float* bias, size_t n,
+                                  size_t k, int relu2, float* out, nh_stream stream, nh_error* err) {
     clear_error(err);
     if (experts == 0 || top_k == 0) return set_error(err, NH_INVALID_SHAPE, "experts and top_k must be non-zero");
     nh_status st;
@@ -873,6 +889,7 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
         e.offsets = offsets;
         e.w = w;
         e.sw = sw;
+        e.bias = bias;
         e.out = out;
         e.a_rows = (int)a_rows;
         e.relu2 = relu2 ? 1 : 0;
@@ -887,6 +904,7 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
     a.perm = perm;
     a.w = w;
     a.sw = sw;
+    a.bias = bias;
     a.out = out;
     a.experts = (int)experts;
     a.N = (int)n;
@@ -899,6 +917,16 @@ nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const floa
     a.kt = (int)tiled_k_tiles(k);
     a.waves = (a.kt + 15) / 16;  // k <= 8192: one 16-tile slab per wave
     return launch(ctx, K_GROUPED_GEMM, (unsigned)a.ntiles, 64u * a.waves, 0, stream, a, err, (unsigned)experts);
+}
+
+extern "C" {
+
+nh_status nh_moe_grouped_gemm_w8a8(nh_context* ctx, const int8_t* aq, const float* sa, int gather, size_t top_k,
+                                   const int32_t* offsets, const int32_t* perm, size_t routes, size_t a_rows,
+                                   size_t experts, const int8_t* w, const float* sw, size_t n, size_t k, int relu2,
+                                   float* out, nh_stream stream, nh_error* err) {
+    return moe_grouped_gemm(ctx, aq, sa, gather, top_k, offsets, perm, routes, a_rows, experts, w, sw, nullptr, n, k,
+                            relu2, out, stream, err);
 }
 
 nh_status nh_moe_combine(nh_context* ctx, const float* slot_out, const int32_t* pos, const float* weights,
@@ -970,12 +998,14 @@ void nh_moe_workspace_layout(size_t tokens, size_t hidden, size_t inter, size_t 
 
 // The routed MoE layer, with the shared expert when w_up_sh is not null:
 // shared = the int8 MLP of x (nh_mlp_w8a8, f32), added first by the combine.
+// biases (optional) are the experts' and the shared expert's MlpLayer biases.
 static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, const float* logits, size_t tokens,
                              size_t hidden, size_t inter, size_t experts, size_t top_k, int renormalize, float scaling,
                              const int8_t* w_up, const float* s_up, const int8_t* w_down, const float* s_down,
                              size_t inter_sh, const int8_t* w_up_sh, const float* s_up_sh, const int8_t* w_down_sh,
-                             const float* s_down_sh, void* out, nh_dtype out_dtype, void* workspace,
-                             size_t workspace_bytes, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
+                             const float* s_down_sh, const nh_moe_biases* biases, void* out, nh_dtype out_dtype,
+                             void* workspace, size_t workspace_bytes, uint64_t* nonfinite, nh_stream stream,
+                             nh_error* err) {
     clear_error(err);
     if (tokens == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
     if (hidden == 0 || experts == 0 || top_k == 0 || top_k > experts || inter == 0)
@@ -983,6 +1013,10 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
     const bool has_shared = w_up_sh != nullptr;
     if (has_shared && (inter_sh == 0 || !s_up_sh || !w_down_sh || !s_down_sh))
         return set_error(err, NH_INVALID_SHAPE, "shared expert needs intermediate_dim > 0 and all four operands");
+    const nh_moe_biases nob{nullptr, nullptr, nullptr, nullptr};
+    const nh_moe_biases& b = biases ? *biases : nob;
+    if (!has_shared && (b.shared_up || b.shared_down))
+        return set_error(err, NH_INVALID_PARAMS, "shared expert biases given without a shared expert");
     size_t off[12];
     moe_layout(tokens, hidden, inter, experts, top_k, off);
     const size_t shared_at = off[11];
@@ -1025,9 +1059,12 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
     float* h_sh = (float*)mlp_ws;
     char* lin_sh = mlp_ws + align256(tokens * inter_sh * sizeof(float)) +
                    align256(kMaxStreamGroups * 8 * sizeof(uint32_t));  // nh_mlp_w8a8's layout
+    // the shared expert's intermediate is reported ahead of the routed
+    // experts' (the reference runs it first, moe.rs:197-219)
     if (has_shared && !shared_tiles &&
-        (st = nh_mlp_w8a8(ctx, x, x_dtype, w_up_sh, s_up_sh, nullptr, w_down_sh, s_down_sh, nullptr, tokens, hidden,
-                          inter_sh, shared, NH_F32, mlp_ws, mlp_bytes, nonfinite, stream, err)))
+        (st = mlp_w8a8(ctx, x, x_dtype, w_up_sh, s_up_sh, b.shared_up, w_down_sh, s_down_sh, b.shared_down, tokens,
+                       hidden, inter_sh, shared, NH_F32, mlp_ws, mlp_bytes, nonfinite, kStageSharedIntermediate, stream,
+                       err)))
         return st;
     if (route_q) {
         if ((st = bind_device(ctx, err))) return st;
@@ -1042,25 +1079,27 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
     if (shared_tiles) {
         // nh_mlp_w8a8's steps from the tiles on: up (ReLU^2, f32 h), then the
         // linear path on h (its quantization: the layer's intermediate)
-        if ((st = launch_gemm(ctx, (const int8_t*)lin_sh, sx, w_up_sh, s_up_sh, nullptr, (int)tokens, (int)inter_sh,
-                              (int)hidden, h_sh, NH_F32, 1, stream, err, true)))
+        if ((st = launch_gemm(ctx, (const int8_t*)lin_sh, sx, w_up_sh, s_up_sh, b.shared_up, (int)tokens,
+                              (int)inter_sh, (int)hidden, h_sh, NH_F32, 1, stream, err, true)))
             return st;
         const size_t lin_bytes = mlp_bytes - (size_t)(lin_sh - mlp_ws);
-        if ((st = linear_w8a8(ctx, h_sh, NH_F32, w_down_sh, s_down_sh, nullptr, tokens, hidden, inter_sh, shared,
-                              NH_F32, lin_sh, lin_bytes, nullptr, nullptr, 0, nonfinite, 1, stream, err)))
+        if ((st = linear_w8a8(ctx, h_sh, NH_F32, w_down_sh, s_down_sh, b.shared_down, tokens, hidden, inter_sh, shared,
+                              NH_F32, lin_sh, lin_bytes, nullptr, nullptr, 0, nonfinite, kStageSharedIntermediate,
+                              stream, err)))
             return st;
     }
     if ((st = nh_moe_permute(ctx, idx, tokens, top_k, experts, offsets, perm, pos, stream, err))) return st;
     // otherwise Q2 of each route's token, written in expert order (slot s =
     // token perm[s] / top_k): the up projection reads its rows contiguously
     if (!route_q && (st = launch_quantize(ctx, x, x_dtype, R, hidden, xq, sx, nullptr, nullptr, stream, err, 0, perm,
-                                          (int)top_k, nonfinite, 0)))
+                                          (int)top_k, nonfinite, kStageInput)))
         return st;
     if (fused) {
-        // up with ReLU^2, h in f32 plus each row's max finite |h| per
-        // workgroup (stage 1 of the non-finite report: h is the layer's
-        // intermediate); the down projection requantizes h per row while it
-        // stages it (the codes and scales of nh_quantize_rows_i8 on h)
+        // up (+ bias) with ReLU^2, h in f32 plus each row's max finite |h|
+        // per workgroup (non-finite h reported at kStageIntermediate: h is
+        // the layer's intermediate); the down projection requantizes h per
+        // row while it stages it (the codes and scales of
+        // nh_quantize_rows_i8 on h), then adds its bias
         uint32_t* hmax = (uint32_t*)(ws + off[8]);  // [R][2]
         ExpertGemmArgs up{};
         up.aq = xq;
@@ -1072,12 +1111,13 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
         up.offsets = offsets;
         up.w = w_up;
         up.sw = s_up;
+        up.bias = b.up;
         up.out = h;
         up.a_rows = route_q ? (int)tokens : (int)R;
         up.relu2 = 1;
         up.omax = hmax;
         up.nonfinite = nonfinite;
-        up.nonfinite_stage = 1;
+        up.nonfinite_stage = kStageIntermediate;
         if ((st = launch_expert_gemm(ctx, K_EXPERT_GEMM_OMAX, up, experts, inter, hidden, stream, err))) return st;
         ExpertGemmArgs down{};
         down.ah = h;
@@ -1085,19 +1125,20 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
         down.offsets = offsets;
         down.w = w_down;
         down.sw = s_down;
+        down.bias = b.down;
         down.out = d;
         down.a_rows = (int)R;
         if ((st = launch_expert_gemm(ctx, K_EXPERT_GEMM_QA, down, experts, hidden, inter, stream, err))) return st;
     } else {
-        if ((st = nh_moe_grouped_gemm_w8a8(ctx, xq, sx, 0, top_k, offsets, perm, R, R, experts, w_up, s_up, inter,
-                                           hidden, 1, h, stream, err)))
+        if ((st = moe_grouped_gemm(ctx, xq, sx, 0, top_k, offsets, perm, R, R, experts, w_up, s_up, b.up, inter,
+                                   hidden, 1, h, stream, err)))
             return st;
-        // the up outputs per slot: the layer's intermediate (stage 1)
+        // the up outputs per slot: the layer's intermediate
         if ((st = launch_quantize(ctx, h, NH_F32, R, inter, hq, sh, nullptr, nullptr, stream, err, 0, nullptr, 1,
-                                  nonfinite, 1)))
+                                  nonfinite, kStageIntermediate)))
             return st;
-        if ((st = nh_moe_grouped_gemm_w8a8(ctx, hq, sh, 0, top_k, offsets, perm, R, R, experts, w_down, s_down,
-                                           hidden, inter, 0, d, stream, err)))
+        if ((st = moe_grouped_gemm(ctx, hq, sh, 0, top_k, offsets, perm, R, R, experts, w_down, s_down, b.down,
+                                   hidden, inter, 0, d, stream, err)))
             return st;
     }
     return nh_moe_combine_shared(ctx, d, pos, wts, shared, tokens, top_k, hidden, out, out_dtype, stream, err);
@@ -1106,10 +1147,11 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
 nh_status nh_moe_forward_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const float* logits, size_t tokens,
                               size_t hidden, size_t inter, size_t experts, size_t top_k, int renormalize,
                               float scaling, const int8_t* w_up, const float* s_up, const int8_t* w_down,
-                              const float* s_down, void* out, nh_dtype out_dtype, void* workspace,
-                              size_t workspace_bytes, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
+                              const float* s_down, const nh_moe_biases* biases, void* out, nh_dtype out_dtype,
+                              void* workspace, size_t workspace_bytes, uint64_t* nonfinite, nh_stream stream,
+                              nh_error* err) {
     return moe_forward(ctx, x, x_dtype, logits, tokens, hidden, inter, experts, top_k, renormalize, scaling, w_up,
-                       s_up, w_down, s_down, 0, nullptr, nullptr, nullptr, nullptr, out, out_dtype, workspace,
+                       s_up, w_down, s_down, 0, nullptr, nullptr, nullptr, nullptr, biases, out, out_dtype, workspace,
                        workspace_bytes, nonfinite, stream, err);
 }
 
@@ -1126,16 +1168,16 @@ nh_status nh_moe_forward_shared_w8a8(nh_context* ctx, const void* x, nh_dtype x_
                                      int renormalize, float scaling, const int8_t* w_up, const float* s_up,
                                      const int8_t* w_down, const float* s_down, size_t shared_inter,
                                      const int8_t* w_up_shared, const float* s_up_shared,
-                                     const int8_t* w_down_shared, const float* s_down_shared, void* out,
-                                     nh_dtype out_dtype, void* workspace, size_t workspace_bytes,
-                                     uint64_t* nonfinite, nh_stream stream, nh_error* err) {
+                                     const int8_t* w_down_shared, const float* s_down_shared,
+                                     const nh_moe_biases* biases, void* out, nh_dtype out_dtype, void* workspace,
+                                     size_t workspace_bytes, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
     if (!w_up_shared) {
         clear_error(err);
         return set_error(err, NH_INVALID_PARAMS, "w_up_shared must not be null (nh_moe_forward_w8a8 has no shared expert)");
     }
     return moe_forward(ctx, x, x_dtype, logits, tokens, hidden, inter, experts, top_k, renormalize, scaling, w_up,
                        s_up, w_down, s_down, shared_inter, w_up_shared, s_up_shared, w_down_shared, s_down_shared,
-                       out, out_dtype, workspace, workspace_bytes, nonfinite, stream, err);
+                       biases, out, out_dtype, workspace, workspace_bytes, nonfinite, stream, err);
 }
 
 size_t nh_moe_layer_w8a8_workspace_size(size_t tokens, size_t hidden, size_t inter, size_t experts, size_t top_k,
@@ -1157,8 +1199,9 @@ nh_status nh_moe_layer_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, co
                             size_t top_k, int renormalize, float scaling, const int8_t* w_up, const float* s_up,
                             const int8_t* w_down, const float* s_down, size_t shared_inter,
                             const int8_t* w_up_shared, const float* s_up_shared, const int8_t* w_down_shared,
-                            const float* s_down_shared, void* out, nh_dtype out_dtype, void* workspace,
-                            size_t workspace_bytes, uint64_t* nonfinite, nh_stream stream, nh_error* err) {
+                            const float* s_down_shared, const nh_moe_biases* biases, void* out, nh_dtype out_dtype,
+                            void* workspace, size_t workspace_bytes, uint64_t* nonfinite, nh_stream stream,
+                            nh_error* err) {
     clear_error(err);
     if (tokens == 0) return set_error(err, NH_INVALID_ROW_COUNT, "row_count must be non-zero, got 0");
     if (hidden == 0 || experts == 0 || top_k == 0 || top_k > experts || inter == 0)
@@ -1186,7 +1229,7 @@ nh_status nh_moe_layer_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, co
     if ((st = launch_gemm_f32(ctx, a, stream, err))) return st;
     return moe_forward(ctx, x, x_dtype, logits, tokens, hidden, inter, experts, top_k, renormalize, scaling, w_up,
                        s_up, w_down, s_down, shared_inter, w_up_shared, s_up_shared, w_down_shared, s_down_shared,
-                       out, out_dtype, workspace, align256(inner), nonfinite, stream, err);
+                       biases, out, out_dtype, workspace, align256(inner), nonfinite, stream, err);
 }
 
 }  // extern "C"
@@ -1222,10 +1265,15 @@ extern "C" nh_status nh_take_nonfinite(nh_context* ctx, uint64_t* nonfinite, nh_
     const uint64_t zero = 0;  // cleared for the next call
     e = hipMemcpy(nonfinite, &zero, sizeof(zero), hipMemcpyHostToDevice);
     if (e != hipSuccess) return device_error(err, e, "hipMemcpy(HtoD)");
+    // the key of report_nonfinite (nh_device.h): stage, 38-bit index, sign and mantissa
     const uint64_t key = ~word;
-    const char* what = (key >> 63) ? "intermediate" : "input";
-    const uint64_t index = (key >> 32) & 0x7fffffffu;
-    const float value = f32_from_bits((uint32_t)key);
+    const uint32_t stage = (uint32_t)(key >> 62);
+    const char* what = stage == kStageInput                ? "input"
+                       : stage == kStageSharedIntermediate ? "shared_intermediate"
+                                                           : "intermediate";
+    const uint64_t index = (key >> 24) & ((1ull << 38) - 1);
+    const float value =
+        f32_from_bits((uint32_t)(((key >> 23) & 1u) << 31) | 0x7f800000u | (uint32_t)(key & 0x7fffffu));
     if (err) {
         err->argument = what;
         err->index = index;

@@ -157,6 +157,14 @@ nh_status nh_context_create(int device, const char* code_object_path, nh_context
             delete ctx;
             return device_error(err, e, kKernelSymbols[i]);
         }
+        e = hipFuncGetAttribute(&ctx->max_threads[i], HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, ctx->fn[i]);
+        if (e == hipSuccess)
+            e = hipFuncGetAttribute(&ctx->static_lds[i], HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, ctx->fn[i]);
+        if (e != hipSuccess) {
+            (void)hipModuleUnload(ctx->module);
+            delete ctx;
+            return device_error(err, e, "hipFuncGetAttribute");
+        }
     }
     *out = ctx;
     return NH_OK;

@@ -76,6 +76,8 @@ struct nh_context {
     int device;
     hipModule_t module;
     hipFunction_t fn[nh::K_COUNT];
+    int max_threads[nh::K_COUNT];   // each kernel's HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK
+    int static_lds[nh::K_COUNT];    // and its static LDS bytes
     int cu_count;
     size_t max_shared_per_block;
     void* scratch;             // this device's address of the static scratch, or null
@@ -95,9 +97,19 @@ nh_status bind_device(nh_context* ctx, nh_error* err);
 // Device address of the static scratch on the current device (scratch.hip).
 nh_status scratch_address(void** out, nh_error* err);
 
+// Launches kernel `id`.  A block larger than the kernel's compiled limit
+// (its __launch_bounds__, read from the code object at context creation) or
+// LDS beyond the device's per-workgroup size is refused before it reaches the
+// GPU: launched, either would run the kernel outside what it was compiled for.
 template <class Args>
 nh_status launch(nh_context* ctx, KernelId id, unsigned gx, unsigned bx, size_t shmem, nh_stream stream,
                  const Args& args, nh_error* err, unsigned gy = 1) {
+    if (bx == 0 || (int)bx > ctx->max_threads[id])
+        return set_error(err, NH_DEVICE_ERROR, "%s: launch of %u x %u blocks of %u threads (kernel limit %d)",
+                         kKernelSymbols[id], gx, gy, bx, ctx->max_threads[id]);
+    if (shmem + (size_t)ctx->static_lds[id] > ctx->max_shared_per_block)
+        return set_error(err, NH_DEVICE_ERROR, "%s: %zu bytes of LDS requested (%zu available)", kKernelSymbols[id],
+                         shmem + (size_t)ctx->static_lds[id], ctx->max_shared_per_block);
     void* params[] = {const_cast<Args*>(&args)};
     hipError_t e = hipModuleLaunchKernel(ctx->fn[id], gx, gy, 1, bx, 1, 1, (unsigned)shmem, (hipStream_t)stream,
                                          params, nullptr);

@@ -40,6 +40,11 @@ F32 = 0
 BF16 = 1
 
 
+class MoeBiases(C.Structure):
+    """nh_moe_biases: optional expert biases (device or host pointers, 0 = none)."""
+    _fields_ = [("up", C.c_void_p), ("down", C.c_void_p), ("shared_up", C.c_void_p), ("shared_down", C.c_void_p)]
+
+
 class NhError(C.Structure):
     _fields_ = [
         ("argument", C.c_char_p),
@@ -68,6 +73,7 @@ P = C.c_void_p
 SZ = C.c_size_t
 ST = C.c_int
 E = C.POINTER(NhError)
+MB = C.POINTER(MoeBiases)
 
 _SIGNATURES = {
     "nh_device_count": (C.c_int, []),
@@ -107,9 +113,13 @@ _SIGNATURES = {
     "nh_linear_w8a8_workspace_size": (SZ, [SZ, SZ]),
     "nh_take_nonfinite": (ST, [P, P, P, E]),
     "nh_linear_w8a8": (ST, [P, P, C.c_int, P, P, P, SZ, SZ, SZ, P, C.c_int, P, SZ, P, P, P, P, E]),
+    "nh_supports_linear_w8a8": (C.c_int, [SZ, SZ, SZ]),
+    "nh_linear_w8a8_host": (ST, [P, C.c_int, P, P, P, SZ, SZ, SZ, P, C.c_int, P, P, E]),
     "nh_linear_w8a8_noalloc": (ST, [P, P, C.c_int, P, P, P, SZ, SZ, SZ, P, C.c_int, P, P, P, P, E]),
     "nh_mlp_w8a8_workspace_size": (SZ, [SZ, SZ, SZ]),
     "nh_mlp_w8a8": (ST, [P, P, C.c_int, P, P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, P, SZ, P, P, E]),
+    "nh_supports_mlp_w8a8": (C.c_int, [SZ, SZ, SZ]),
+    "nh_mlp_w8a8_host": (ST, [P, C.c_int, P, P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, E]),
     "nh_gemv_w8a32": (ST, [P, P, P, P, SZ, SZ, SZ, P, P, E]),
     "nh_gemv_w8a32_host": (ST, [P, P, P, SZ, SZ, SZ, P, E]),
     "nh_sigmoid_f32_host": (C.c_float, [C.c_float]),
@@ -124,16 +134,19 @@ _SIGNATURES = {
     "nh_moe_combine_host": (ST, [P, P, P, SZ, SZ, SZ, P, C.c_int, E]),
     "nh_moe_forward_w8a8_workspace_size": (SZ, [SZ, SZ, SZ, SZ, SZ]),
     "nh_moe_workspace_layout": (None, [SZ, SZ, SZ, SZ, SZ, C.POINTER(SZ)]),
-    "nh_moe_forward_w8a8": (ST, [P, P, C.c_int, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, P,
+    "nh_moe_forward_w8a8": (ST, [P, P, C.c_int, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, MB, P,
                                  C.c_int, P, SZ, P, P, E]),
     "nh_moe_combine_shared": (ST, [P, P, P, P, P, SZ, SZ, SZ, P, C.c_int, P, E]),
     "nh_moe_combine_shared_host": (ST, [P, P, P, P, SZ, SZ, SZ, P, C.c_int, E]),
     "nh_moe_forward_shared_w8a8_workspace_size": (SZ, [SZ, SZ, SZ, SZ, SZ, SZ]),
     "nh_moe_forward_shared_w8a8": (ST, [P, P, C.c_int, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, SZ,
-                                        P, P, P, P, P, C.c_int, P, SZ, P, P, E]),
+                                        P, P, P, P, MB, P, C.c_int, P, SZ, P, P, E]),
     "nh_moe_layer_w8a8_workspace_size": (SZ, [SZ, SZ, SZ, SZ, SZ, SZ]),
     "nh_moe_layer_w8a8": (ST, [P, P, C.c_int, P, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, SZ,
-                               P, P, P, P, P, C.c_int, P, SZ, P, P, E]),
+                               P, P, P, P, MB, P, C.c_int, P, SZ, P, P, E]),
+    "nh_supports_moe_layer_w8a8": (C.c_int, [SZ, SZ, SZ, SZ, SZ, SZ]),
+    "nh_moe_layer_w8a8_host": (ST, [P, C.c_int, P, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, SZ,
+                                    P, P, P, P, MB, P, C.c_int, E]),
     "nh_stream_read": (ST, [P, P, SZ, P, P, E]),
     "nh_tiled_int4_weights_bytes": (SZ, [SZ, SZ]),
     "nh_tile_weights_int4": (ST, [P, P, SZ, SZ, SZ, C.c_uint32, P, SZ, P, E]),

@@ -275,6 +275,22 @@ int or_gemm_f32(const float *lhs, size_t lhs_len, const float *rhs, size_t rhs_l
     return OR_OK;
 }
 
+/* gemm_into_host's loop (gemm.rs:99-109) restricted to the output columns
+ * [col0, col1) of the same [m][n] output, on the whole [k][n] rhs (row stride
+ * n): the per-output arithmetic is identical, so disjoint column ranges run on
+ * several threads write exactly or_gemm_f32's output, on the reference's one
+ * shared matrix.  Used only to time the host path on several cores. */
+void or_gemm_f32_col_range(const float *lhs, const float *rhs, size_t m, size_t k, size_t n, size_t col0,
+                           size_t col1, float *out) {
+    for (size_t row = 0; row < m; ++row) {
+        for (size_t col = col0; col < col1 && col < n; ++col) {
+            double acc = 0.0;
+            for (size_t d = 0; d < k; ++d) acc += (double)lhs[row * k + d] * (double)rhs[d * n + col];
+            out[row * n + col] = (float)acc;
+        }
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* G1/G3 (spec): acc[m,n] = sum_k xq[m,k] * wq[n,k] exactly in int32
  * (|acc| <= K * 127^2 < 2^31 for K <= 133,152). */
@@ -489,14 +505,16 @@ void or_moe_permute(const int32_t *indices, size_t tokens, size_t top_k, size_t 
 /* R3 (spec): per expert e, rows in slots [offsets[e], offsets[e+1]).
  * gather_tokens: the A row of slot i is token perm[i] / top_k (the up
  * projection reads token rows); otherwise A row = slot (the down projection
- * reads the requantised slot rows).  Epilogue as G1, with ReLU^2 for the up
- * projection of the expert MLP (mlp.rs:201-205). */
+ * reads the requantised slot rows).  Epilogue as G1 with the expert's bias
+ * row (bias [E][n] or NULL: the expert MlpLayer's projection bias,
+ * mlp.rs:201-208), then ReLU^2 for the up projection (mlp.rs:205). */
 void or_moe_grouped_w8a8(const int8_t *aq, const float *sa, int gather_tokens, size_t top_k,
                          const int32_t *offsets, const int32_t *perm, size_t experts, const int8_t *w,
-                         const float *sw, size_t n, size_t k, int relu2, float *out) {
+                         const float *sw, const float *bias, size_t n, size_t k, int relu2, float *out) {
     for (size_t e = 0; e < experts; ++e) {
         const int8_t *we = w + e * n * k;
         const float *se = sw + e * n;
+        const float *be = bias ? bias + e * n : NULL;
         for (int32_t slot = offsets[e]; slot < offsets[e + 1]; ++slot) {
             size_t row = gather_tokens ? (size_t)perm[slot] / top_k : (size_t)slot;
             const int8_t *a = aq + row * k;
@@ -504,7 +522,7 @@ void or_moe_grouped_w8a8(const int8_t *aq, const float *sa, int gather_tokens, s
                 const int8_t *b = we + c * k;
                 int32_t acc = 0;
                 for (size_t d = 0; d < k; ++d) acc += (int32_t)a[d] * (int32_t)b[d];
-                out[(size_t)slot * n + c] = epilogue_value(acc, sa[row], se[c], NULL, c, relu2);
+                out[(size_t)slot * n + c] = epilogue_value(acc, sa[row], se[c], be, c, relu2);
             }
         }
     }
@@ -539,10 +557,12 @@ void or_moe_combine_shared(const float *slot_out, const int32_t *pos, const floa
     }
 }
 
-/* int8 MLP of bf16 rows (spec composition, L2 with int8 weights, no biases):
- * Q2(x) -> W8A8 up with ReLU^2 (f32) -> Q2 -> W8A8 down (f32). */
+/* int8 MLP of bf16 rows (spec composition, L2 with int8 weights and
+ * optional biases, mlp.rs:201-208): Q2(x) -> W8A8 up + b_up, ReLU^2 (f32) ->
+ * Q2 -> W8A8 down + b_down (f32). */
 int or_mlp_w8a8(const uint16_t *x_bf16, size_t rows, size_t hidden, size_t inter, const int8_t *w_up,
-                const float *s_up, const int8_t *w_down, const float *s_down, float *out) {
+                const float *s_up, const float *b_up, const int8_t *w_down, const float *s_down,
+                const float *b_down, float *out) {
     int8_t *xq = (int8_t *)malloc(rows * hidden + 1);
     float *sx = (float *)malloc((rows + 1) * sizeof(float));
     int32_t *acc = (int32_t *)malloc((rows * (inter > hidden ? inter : hidden) + 1) * sizeof(int32_t));
@@ -553,12 +573,12 @@ int or_mlp_w8a8(const uint16_t *x_bf16, size_t rows, size_t hidden, size_t inter
     int st = or_quantize_rows_i8_bf16(x_bf16, rows, hidden, xq, sx, &err);
     if (st == OR_OK) {
         or_gemm_i8_i32(xq, w_up, rows, inter, hidden, acc);
-        or_epilogue_w8a8(acc, sx, s_up, NULL, rows, inter, 1, 0, h);
+        or_epilogue_w8a8(acc, sx, s_up, b_up, rows, inter, 1, 0, h);
         st = or_quantize_rows_i8_f32(h, rows, inter, hq, sh, &err);
     }
     if (st == OR_OK) {
         or_gemm_i8_i32(hq, w_down, rows, hidden, inter, acc);
-        or_epilogue_w8a8(acc, sh, s_down, NULL, rows, hidden, 0, 0, out);
+        or_epilogue_w8a8(acc, sh, s_down, b_down, rows, hidden, 0, 0, out);
     }
     free(xq);
     free(sx);
@@ -578,19 +598,23 @@ int or_moe_forward_w8a8(const uint16_t *x_bf16, const float *logits, size_t toke
                         const float *s_down, uint16_t *out_bf16, int32_t *idx_out, float *w_out,
                         int32_t *offsets_out, int32_t *perm_out, int32_t *pos_out) {
     return or_moe_forward_shared_w8a8(x_bf16, logits, tokens, hidden, inter, experts, top_k, renormalize, scaling,
-                                      w_up, s_up, w_down, s_down, 0, NULL, NULL, NULL, NULL, out_bf16, idx_out,
-                                      w_out, offsets_out, perm_out, pos_out);
+                                      w_up, s_up, w_down, s_down, 0, NULL, NULL, NULL, NULL, NULL, out_bf16,
+                                      idx_out, w_out, offsets_out, perm_out, pos_out);
 }
 
 /* The same with a shared expert (w_up_sh not NULL): or_mlp_w8a8 of x, added
- * by the combine ahead of the routes (moe.rs:197-219). */
+ * by the combine ahead of the routes (moe.rs:197-219).  biases (NULL, or 4
+ * pointers each NULL or not): the routed experts' up [E][inter] and down
+ * [E][hidden] biases, the shared expert's up [inter_sh] and down [hidden]. */
 int or_moe_forward_shared_w8a8(const uint16_t *x_bf16, const float *logits, size_t tokens, size_t hidden,
                                size_t inter, size_t experts, size_t top_k, int renormalize, float scaling,
                                const int8_t *w_up, const float *s_up, const int8_t *w_down,
                                const float *s_down, size_t inter_sh, const int8_t *w_up_sh,
                                const float *s_up_sh, const int8_t *w_down_sh, const float *s_down_sh,
-                               uint16_t *out_bf16, int32_t *idx_out, float *w_out, int32_t *offsets_out,
-                               int32_t *perm_out, int32_t *pos_out) {
+                               const float *const *biases, uint16_t *out_bf16, int32_t *idx_out, float *w_out,
+                               int32_t *offsets_out, int32_t *perm_out, int32_t *pos_out) {
+    const float *b_up = biases ? biases[0] : NULL, *b_down = biases ? biases[1] : NULL;
+    const float *b_up_sh = biases ? biases[2] : NULL, *b_down_sh = biases ? biases[3] : NULL;
     size_t routes = tokens * top_k;
     int8_t *xq = (int8_t *)malloc(tokens * hidden + 1);
     float *sx = (float *)malloc((tokens + 1) * sizeof(float));
@@ -605,18 +629,19 @@ int or_moe_forward_shared_w8a8(const uint16_t *x_bf16, const float *logits, size
                                    idx_out, routes, w_out, routes, &err);
     if (st == OR_OK) {
         or_moe_permute(idx_out, tokens, top_k, experts, offsets_out, perm_out, pos_out);
-        or_moe_grouped_w8a8(xq, sx, 1, top_k, offsets_out, perm_out, experts, w_up, s_up, inter, hidden, 1,
-                            h);
+        or_moe_grouped_w8a8(xq, sx, 1, top_k, offsets_out, perm_out, experts, w_up, s_up, b_up, inter, hidden,
+                            1, h);
         st = or_quantize_rows_i8_f32(h, routes, inter, hq, sh, &err);
     }
     float *shared = NULL;
     if (st == OR_OK && w_up_sh) {
         shared = (float *)malloc((tokens * hidden + 1) * sizeof(float));
-        st = or_mlp_w8a8(x_bf16, tokens, hidden, inter_sh, w_up_sh, s_up_sh, w_down_sh, s_down_sh, shared);
+        st = or_mlp_w8a8(x_bf16, tokens, hidden, inter_sh, w_up_sh, s_up_sh, b_up_sh, w_down_sh, s_down_sh,
+                         b_down_sh, shared);
     }
     if (st == OR_OK) {
-        or_moe_grouped_w8a8(hq, sh, 0, top_k, offsets_out, perm_out, experts, w_down, s_down, hidden, inter,
-                            0, d);
+        or_moe_grouped_w8a8(hq, sh, 0, top_k, offsets_out, perm_out, experts, w_down, s_down, b_down, hidden,
+                            inter, 0, d);
         or_moe_combine_shared(d, pos_out, w_out, shared, tokens, top_k, hidden, 1, out_bf16);
     }
     free(shared);
@@ -706,11 +731,15 @@ int or_mlp_forward(const float *input, size_t rows, size_t hidden, size_t inter,
  * top-k without renormalisation, output zeroed, optional shared expert added
  * first, then for every route value += weight * expert(all rows)[token]; an
  * expert's MLP runs over ALL rows the first time it is selected (:226-233).
- * Experts here have no biases. */
+ * Expert e's MlpLayer biases are b_up[e] / b_down[e] (b_up or b_down NULL, or
+ * an entry NULL: no bias), the shared expert's shared_b_up / shared_b_down
+ * (mlp.rs:79-96, 201-208). */
 int or_moe_forward_dense(const float *input, size_t rows, size_t hidden, size_t experts, size_t top_k,
                          const float *router_w, const float *router_b, size_t inter,
-                         const float *const *w_up, const float *const *w_down, size_t shared_inter,
-                         const float *shared_up, const float *shared_down, float *out) {
+                         const float *const *w_up, const float *const *w_down, const float *const *b_up,
+                         const float *const *b_down, size_t shared_inter, const float *shared_up,
+                         const float *shared_down, const float *shared_b_up, const float *shared_b_down,
+                         float *out) {
     if (rows == 0) return OR_INVALID_ROW_COUNT;
     size_t routes = rows * top_k;
     float *scores = (float *)malloc(rows * experts * sizeof(float));
@@ -728,7 +757,8 @@ int or_moe_forward_dense(const float *input, size_t rows, size_t hidden, size_t 
         for (size_t i = 0; i < rows * hidden; ++i) out[i] = 0.0f;
         if (shared_up) {
             shared = (float *)malloc(rows * hidden * sizeof(float));
-            st = or_mlp_forward(input, rows, hidden, shared_inter, shared_up, NULL, shared_down, NULL, shared);
+            st = or_mlp_forward(input, rows, hidden, shared_inter, shared_up, shared_b_up, shared_down,
+                                shared_b_down, shared);
         }
     }
     for (size_t t = 0; st == OR_OK && t < rows; ++t) {
@@ -740,7 +770,8 @@ int or_moe_forward_dense(const float *input, size_t rows, size_t hidden, size_t 
             float wt = w[t * top_k + j];
             if (!expert_out[e]) {
                 expert_out[e] = (float *)malloc(rows * hidden * sizeof(float));
-                st = or_mlp_forward(input, rows, hidden, inter, w_up[e], NULL, w_down[e], NULL, expert_out[e]);
+                st = or_mlp_forward(input, rows, hidden, inter, w_up[e], b_up ? b_up[e] : NULL, w_down[e],
+                                    b_down ? b_down[e] : NULL, expert_out[e]);
             }
             for (size_t h = 0; h < hidden; ++h) orow[h] = orow[h] + wt * expert_out[e][t * hidden + h];
         }

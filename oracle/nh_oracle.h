@@ -75,6 +75,9 @@ void or_dequantize_i8(const int8_t *q, const float *scales, size_t rows, size_t 
 /* ---- G0: reference f32 GEMM, f64 accumulation (gemm.rs:91-147,192-208) ---- */
 int or_gemm_f32(const float *lhs, size_t lhs_len, const float *rhs, size_t rhs_len, size_t m, size_t k,
                 size_t n, float *out, size_t out_len, or_error *err);
+/* the same loop over output columns [col0, col1) only (multi-core timing) */
+void or_gemm_f32_col_range(const float *lhs, const float *rhs, size_t m, size_t k, size_t n, size_t col0,
+                           size_t col1, float *out);
 
 /* ---- G1/G3: W8A8 (spec) --------------------------------------------------- */
 void or_gemm_i8_i32(const int8_t *xq, const int8_t *wq, size_t m, size_t n, size_t k, int32_t *acc);
@@ -104,7 +107,7 @@ void or_moe_permute(const int32_t *indices, size_t tokens, size_t top_k, size_t 
                     int32_t *offsets, int32_t *perm, int32_t *pos);
 void or_moe_grouped_w8a8(const int8_t *aq, const float *sa, int gather_tokens, size_t top_k,
                          const int32_t *offsets, const int32_t *perm, size_t experts, const int8_t *w,
-                         const float *sw, size_t n, size_t k, int relu2, float *out);
+                         const float *sw, const float *bias, size_t n, size_t k, int relu2, float *out);
 void or_moe_combine(const float *slot_out, const int32_t *pos, const float *weights, size_t tokens,
                     size_t top_k, size_t hidden, int out_bf16, void *out);
 int or_moe_forward_w8a8(const uint16_t *x_bf16, const float *logits, size_t tokens, size_t hidden,
@@ -115,14 +118,15 @@ int or_moe_forward_w8a8(const uint16_t *x_bf16, const float *logits, size_t toke
 void or_moe_combine_shared(const float *slot_out, const int32_t *pos, const float *weights, const float *shared,
                            size_t tokens, size_t top_k, size_t hidden, int out_bf16, void *out);
 int or_mlp_w8a8(const uint16_t *x_bf16, size_t rows, size_t hidden, size_t inter, const int8_t *w_up,
-                const float *s_up, const int8_t *w_down, const float *s_down, float *out);
+                const float *s_up, const float *b_up, const int8_t *w_down, const float *s_down,
+                const float *b_down, float *out);
 int or_moe_forward_shared_w8a8(const uint16_t *x_bf16, const float *logits, size_t tokens, size_t hidden,
                                size_t inter, size_t experts, size_t top_k, int renormalize, float scaling,
                                const int8_t *w_up, const float *s_up, const int8_t *w_down,
                                const float *s_down, size_t inter_sh, const int8_t *w_up_sh,
                                const float *s_up_sh, const int8_t *w_down_sh, const float *s_down_sh,
-                               uint16_t *out_bf16, int32_t *idx_out, float *w_out, int32_t *offsets_out,
-                               int32_t *perm_out, int32_t *pos_out);
+                               const float *const *biases, uint16_t *out_bf16, int32_t *idx_out, float *w_out,
+                               int32_t *offsets_out, int32_t *perm_out, int32_t *pos_out);
 
 /* ---- W4A8: the reference's INT4 linear weights with int8 activations ---- */
 int or_linear_w4a8(const uint16_t *x_bf16, size_t m, size_t k, const uint8_t *packed, size_t n, float scale,
@@ -136,8 +140,9 @@ int or_mlp_forward(const float *input, size_t rows, size_t hidden, size_t inter,
                    const float *b_up, const float *w_down, const float *b_down, float *out);
 int or_moe_forward_dense(const float *input, size_t rows, size_t hidden, size_t experts, size_t top_k,
                          const float *router_w, const float *router_b, size_t inter,
-                         const float *const *w_up, const float *const *w_down,
-                         size_t shared_inter, const float *shared_up, const float *shared_down,
+                         const float *const *w_up, const float *const *w_down, const float *const *b_up,
+                         const float *const *b_down, size_t shared_inter, const float *shared_up,
+                         const float *shared_down, const float *shared_b_up, const float *shared_b_down,
                          float *out);
 
 #ifdef __cplusplus

@@ -119,6 +119,35 @@ impl Default for nh_tensor_info {
     }
 }
 
+/// Optional biases of the int8 MoE layer's experts (each pointer may be null; a null
+/// `*const nh_moe_biases` means none): the reference's routed experts and shared expert are
+/// MlpLayers whose projections may carry biases (mlp.rs:79-96, moe.rs:60-65); an up bias is added
+/// before ReLU^2, a down bias to the expert's own output, before the combine weight
+/// (mlp.rs:201-208).
+#[repr(C)]
+#[derive(Clone, Copy, Debug)]
+pub struct nh_moe_biases {
+    /// [experts][inter], expert-major like s_up.
+    pub up: *const f32,
+    /// [experts][hidden], like s_down.
+    pub down: *const f32,
+    /// [shared_inter].
+    pub shared_up: *const f32,
+    /// [hidden].
+    pub shared_down: *const f32,
+}
+
+impl Default for nh_moe_biases {
+    fn default() -> Self {
+        Self {
+            up: core::ptr::null(),
+            down: core::ptr::null(),
+            shared_up: core::ptr::null(),
+            shared_down: core::ptr::null(),
+        }
+    }
+}
+
 /// Opaque device context (immutable once created; safe to share across threads).
 #[repr(C)]
 pub struct nh_context {
@@ -147,6 +176,11 @@ const _: () = {
     assert!(offset_of!(nh_tensor_info, shape) == 24);
     assert!(offset_of!(nh_tensor_info, data_begin) == 88);
     assert!(offset_of!(nh_tensor_info, data_bytes) == 96);
+    assert!(size_of::<nh_moe_biases>() == 32);
+    assert!(offset_of!(nh_moe_biases, up) == 0);
+    assert!(offset_of!(nh_moe_biases, down) == 8);
+    assert!(offset_of!(nh_moe_biases, shared_up) == 16);
+    assert!(offset_of!(nh_moe_biases, shared_down) == 24);
 };
 
 extern "C" {
@@ -505,6 +539,32 @@ extern "C" {
         err: *mut nh_error,
     ) -> nh_status;
 
+    /// Device envelope of nh_linear_w8a8 (supports_shape, gemm.rs:247-254): 1 when the device entry
+    /// point runs the shape (k % 16 == 0, k <= 131072, every dimension and product below 2^31) with a
+    /// 16-byte aligned wq (and workspace); otherwise it returns NH_UNSUPPORTED and the caller takes the
+    /// host twin (the host-fallback contract, gemm.rs:290-310).
+    pub fn nh_supports_linear_w8a8(m: usize, n: usize, k: usize) -> c_int;
+
+    /// Host twin of nh_linear_w8a8 (LinearProjection::project_into with int8 per-row weights,
+    /// linear.rs:283-342): the same arguments in host memory (wq tiled, as on the device), any shape,
+    /// bit-identical outputs; no workspace.  A non-finite x returns NH_NON_FINITE_INPUT ("input",
+    /// index, value) before any output is written.  xq_out/sx_out optional, as on the device.
+    pub fn nh_linear_w8a8_host(
+        x: *const c_void,
+        x_dtype: nh_dtype,
+        wq: *const i8,
+        sw: *const f32,
+        bias: *const f32,
+        m: usize,
+        n: usize,
+        k: usize,
+        out: *mut c_void,
+        out_dtype: nh_dtype,
+        xq_out: *mut i8,
+        sx_out: *mut f32,
+        err: *mut nh_error,
+    ) -> nh_status;
+
     /// nh_linear_w8a8 without a workspace argument and without allocating, for callers that cannot call
     /// hipMalloc (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
     /// No counterpart in the reference.  The workspace is a static device array of 64 MiB (67108864
@@ -560,6 +620,30 @@ extern "C" {
         workspace_bytes: usize,
         nonfinite: *mut u64,
         stream: nh_stream,
+        err: *mut nh_error,
+    ) -> nh_status;
+
+    /// Device envelope of nh_mlp_w8a8: both projections inside nh_supports_linear_w8a8 (16-byte
+    /// aligned weights and workspace).
+    pub fn nh_supports_mlp_w8a8(m: usize, hidden: usize, inter: usize) -> c_int;
+
+    /// Host twin of nh_mlp_w8a8: same arguments in host memory, bit-identical outputs, no workspace;
+    /// NH_NON_FINITE_INPUT "input" or "intermediate" (the f32 [m][inter] ReLU^2 output) as the device
+    /// word reports them.
+    pub fn nh_mlp_w8a8_host(
+        x: *const c_void,
+        x_dtype: nh_dtype,
+        w_up: *const i8,
+        s_up: *const f32,
+        b_up: *const f32,
+        w_down: *const i8,
+        s_down: *const f32,
+        b_down: *const f32,
+        m: usize,
+        hidden: usize,
+        inter: usize,
+        out: *mut c_void,
+        out_dtype: nh_dtype,
         err: *mut nh_error,
     ) -> nh_status;
 
@@ -813,6 +897,7 @@ extern "C" {
         s_up: *const f32,
         w_down: *const i8,
         s_down: *const f32,
+        biases: *const nh_moe_biases,
         out: *mut c_void,
         out_dtype: nh_dtype,
         workspace: *mut c_void,
@@ -823,9 +908,12 @@ extern "C" {
     ) -> nh_status;
 
     /// The int8 MoE layer with its shared expert, MoeLayer::forward_into with shared_expert = Some(..)
-    /// (moe.rs:197-219): the shared expert is an int8 MLP over every token (nh_mlp_w8a8 on x, f32, no
-    /// biases: w_up_shared tiled [shared_inter][hidden], w_down_shared tiled [hidden][shared_inter]),
-    /// added to each output row before the routed experts (nh_moe_combine_shared). Routing, experts and
+    /// (moe.rs:197-219): the shared expert is an int8 MLP over every token (nh_mlp_w8a8 on x, f32, with
+    /// biases->shared_up and ->shared_down: w_up_shared tiled [shared_inter][hidden], w_down_shared
+    /// tiled [hidden][shared_inter]), added to each output row before the routed experts
+    /// (nh_moe_combine_shared).  Non-finite values of its intermediate are reported as
+    /// "shared_intermediate" (index into [tokens][shared_inter]), ahead of the routed experts'
+    /// "intermediate", as the reference meets them.  Routing, experts and
     /// errors as nh_moe_forward_w8a8; INVALID_PARAMS for a NULL w_up_shared, INVALID_SHAPE for
     /// shared_inter == 0 or a missing shared operand.  The workspace
     /// (nh_moe_forward_shared_w8a8_workspace_size) starts with nh_moe_workspace_layout's fields.
@@ -859,6 +947,7 @@ extern "C" {
         s_up_shared: *const f32,
         w_down_shared: *const i8,
         s_down_shared: *const f32,
+        biases: *const nh_moe_biases,
         out: *mut c_void,
         out_dtype: nh_dtype,
         workspace: *mut c_void,
@@ -909,6 +998,7 @@ extern "C" {
         s_up_shared: *const f32,
         w_down_shared: *const i8,
         s_down_shared: *const f32,
+        biases: *const nh_moe_biases,
         out: *mut c_void,
         out_dtype: nh_dtype,
         workspace: *mut c_void,
@@ -917,6 +1007,51 @@ extern "C" {
         stream: nh_stream,
         err: *mut nh_error,
     ) -> nh_status;
+
+    /// Host twin of nh_moe_layer_w8a8 (the library's CPU implementation, for the host-fallback
+    /// contract, gemm.rs:290-310): the same arguments in host memory, the same result bit for bit
+    /// (router logits in f64 with k ascending, sigmoid top-k, the experts' int8 MLPs in slot order, the
+    /// combine), no workspace.  Non-finite values return NH_NON_FINITE_INPUT at once, in the device
+    /// word's order: "input", then "shared_intermediate", then "intermediate" (index in expert-sorted
+    /// slot order).
+    pub fn nh_moe_layer_w8a8_host(
+        x: *const c_void,
+        x_dtype: nh_dtype,
+        router_w: *const f32,
+        router_b: *const f32,
+        tokens: usize,
+        hidden: usize,
+        inter: usize,
+        experts: usize,
+        top_k: usize,
+        renormalize: c_int,
+        scaling: f32,
+        w_up: *const i8,
+        s_up: *const f32,
+        w_down: *const i8,
+        s_down: *const f32,
+        shared_inter: usize,
+        w_up_shared: *const i8,
+        s_up_shared: *const f32,
+        w_down_shared: *const i8,
+        s_down_shared: *const f32,
+        biases: *const nh_moe_biases,
+        out: *mut c_void,
+        out_dtype: nh_dtype,
+        err: *mut nh_error,
+    ) -> nh_status;
+
+    /// Device envelope of nh_moe_layer_w8a8's shape (the router GEMM, routing and the experts): 1 when
+    /// the device entry point runs it with 16-byte aligned weights and workspace, 0 when it returns
+    /// NH_UNSUPPORTED (take the host twin).
+    pub fn nh_supports_moe_layer_w8a8(
+        tokens: usize,
+        hidden: usize,
+        inter: usize,
+        experts: usize,
+        top_k: usize,
+        shared_inter: usize,
+    ) -> c_int;
 
     /// INT4 affine weights on the device (W4A8). The reference's INT4 linear weights
     /// (Int4LinearWeights, linear.rs:99-131) are the [input_dim = K][output_dim = N] matrix of affine

@@ -13,8 +13,9 @@ pub enum HipError {
     LengthMismatch { argument: &'static str, expected: usize, actual: usize },
     /// `QuantizeError::InvalidParams`
     InvalidParams(String),
-    /// `QuantizeError::NonFiniteInput`; `argument` is "input" or, for a layer's
-    /// f32 intermediate, "intermediate".
+    /// `QuantizeError::NonFiniteInput`; `argument` is "input", or for a layer's
+    /// f32 intermediate "intermediate" (the MoE shared expert's:
+    /// "shared_intermediate").
     NonFiniteInput { argument: &'static str, index: usize, value: f32 },
     Int4OutOfRange(u8),
     InvalidRowCount(usize),

@@ -2,6 +2,10 @@
 //! 283-342): codes tiled on the device, one f32 scale per output, optional
 //! bias; `project_into` quantizes each input row on the device (dynamic
 //! per-token scales) and runs the W8A8 GEMV/GEMM with the bias fused.
+//! Outside the device envelope (`nh_supports_linear_w8a8`, e.g. an input
+//! width that is not a multiple of 16) it keeps the reference's
+//! host-fallback contract (gemm.rs:290-310): the weights are copied to the
+//! host once and the library's host twin computes the same result.
 use core::ffi::c_void;
 use std::fmt;
 use std::sync::{Arc, Mutex};
@@ -20,6 +24,22 @@ struct Inner {
     bias: Option<DeviceBuffer<f32>>,
     // per-token quantization workspace of the host-slice entry, grown on demand
     workspace: Mutex<Option<DeviceBuffer<u8>>>,
+    // host copy of the tiled codes, scales and bias for the host twin, made on first use
+    host: Mutex<Option<HostWeights>>,
+}
+
+/// The weights in host memory, in the device layout (tiled codes), for the
+/// library's host twins.
+pub(crate) struct HostWeights {
+    pub(crate) codes: Vec<i8>,
+    pub(crate) scales: Vec<f32>,
+    pub(crate) bias: Option<Vec<f32>>,
+}
+
+impl HostWeights {
+    pub(crate) fn bias_ptr(&self) -> *const f32 {
+        self.bias.as_ref().map_or(core::ptr::null(), |b| b.as_ptr())
+    }
 }
 
 /// `LinearWeights::Int8PerRow`: cloning shares the device copy, and two
@@ -165,6 +185,7 @@ impl Int8PerRowWeights {
                 scales,
                 bias,
                 workspace: Mutex::new(None),
+                host: Mutex::new(None),
             }),
         })
     }
@@ -193,11 +214,70 @@ impl Int8PerRowWeights {
         self.inner.bias.as_ref().map_or(core::ptr::null(), |b| b.as_ptr())
     }
 
+    pub(crate) fn has_bias(&self) -> bool {
+        self.inner.bias.is_some()
+    }
+
+    /// Runs `f` on the host copy of the weights (downloaded on first use:
+    /// the host bridge of gemm.rs:301-310, once per layer instead of per call).
+    pub(crate) fn with_host<R>(&self, f: impl FnOnce(&HostWeights) -> Result<R, HipError>) -> Result<R, HipError> {
+        let mut guard = self.inner.host.lock().unwrap_or_else(|p| p.into_inner());
+        if guard.is_none() {
+            let mut codes = vec![0i8; self.inner.codes.len()];
+            self.inner.codes.copy_to_host(&mut codes)?;
+            let mut scales = vec![0.0f32; self.inner.scales.len()];
+            self.inner.scales.copy_to_host(&mut scales)?;
+            let bias = match self.inner.bias.as_ref() {
+                Some(b) => {
+                    let mut v = vec![0.0f32; b.len()];
+                    b.copy_to_host(&mut v)?;
+                    Some(v)
+                }
+                None => None,
+            };
+            *guard = Some(HostWeights { codes, scales, bias });
+        }
+        f(guard.as_ref().expect("host copy made above"))
+    }
+
+    /// Whether the device entry point runs `row_count` rows of this layer.
+    pub fn device_supports(&self, row_count: usize) -> bool {
+        unsafe { sys::nh_supports_linear_w8a8(row_count, self.inner.output_dim, self.inner.input_dim) != 0 }
+    }
+
+    /// The host twin (`nh_linear_w8a8_host`) on host slices: the same result
+    /// as the device, bit for bit.
+    fn project_host(&self, input: &[f32], row_count: usize, output: &mut [f32]) -> Result<(), HipError> {
+        let (k, n) = (self.inner.input_dim, self.inner.output_dim);
+        self.with_host(|w| {
+            call(|e| unsafe {
+                sys::nh_linear_w8a8_host(
+                    input.as_ptr().cast(),
+                    sys::nh_dtype::F32,
+                    w.codes.as_ptr(),
+                    w.scales.as_ptr(),
+                    w.bias_ptr(),
+                    row_count,
+                    n,
+                    k,
+                    output.as_mut_ptr().cast(),
+                    sys::nh_dtype::F32,
+                    core::ptr::null_mut(),
+                    core::ptr::null_mut(),
+                    e,
+                )
+            })
+        })
+    }
+
     /// The `project_into` arm: `input` f32 `[row_count][input_dim]`, `output`
     /// f32 `[row_count][output_dim]` (host slices, as the reference's), with the
     /// reference's checks in its order (InvalidRowCount, LengthMismatch
     /// "input", LengthMismatch "output").  A NaN or infinity in `input` is
     /// NonFiniteInput { argument: "input", index, value }.  Synchronous.
+    /// Shapes outside the device envelope, and a device call that reports
+    /// Unsupported, take the host twin: the call never fails for a shape the
+    /// reference accepts (gemm.rs:290-310).
     pub fn project_into(&self, input: &[f32], row_count: usize, output: &mut [f32]) -> Result<(), HipError> {
         let (k, n) = (self.inner.input_dim, self.inner.output_dim);
         if row_count == 0 {
@@ -213,6 +293,9 @@ impl Int8PerRowWeights {
                 actual: output.len(),
             });
         }
+        if !self.device_supports(row_count) {
+            return self.project_host(input, row_count, output);
+        }
         let ctx = &self.inner.ctx;
         let x = DeviceBuffer::from_host(ctx, input)?;
         let mut y = DeviceBuffer::<f32>::new(ctx, output.len())?;
@@ -223,7 +306,7 @@ impl Int8PerRowWeights {
             *guard = Some(DeviceBuffer::<u8>::new(ctx, need)?);
         }
         let ws = guard.as_mut().expect("workspace allocated above");
-        self.project_device(
+        match self.project_device(
             x.as_ptr().cast(),
             sys::nh_dtype::F32,
             row_count,
@@ -233,7 +316,13 @@ impl Int8PerRowWeights {
             ws.bytes(),
             word.as_mut_ptr(),
             None,
-        )?;
+        ) {
+            Err(HipError::Unsupported(_)) => {
+                drop(guard);
+                return self.project_host(input, row_count, output);
+            }
+            r => r?,
+        }
         call(|e| unsafe { sys::nh_take_nonfinite(ctx.as_raw(), word.as_mut_ptr(), core::ptr::null_mut(), e) })?;
         y.copy_to_host(output)
     }

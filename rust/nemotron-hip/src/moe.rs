@@ -3,6 +3,9 @@
 //! top-k routing, the routed experts as two grouped GEMMs over an
 //! expert-sorted permutation built on the device, the optional shared expert,
 //! and the weighted combine in the reference's order; one library call.
+//! Expert and shared-expert biases are the MlpLayer biases of the reference
+//! (mlp.rs:79-96, 201-208).  Outside the device envelope the library's host
+//! twin computes the same result (the host-fallback contract, gemm.rs:290-310).
 use std::sync::{Arc, Mutex};
 
 use nemotron_hip_sys as sys;
@@ -38,15 +41,53 @@ pub struct Int8Moe {
     s_up: DeviceBuffer<f32>,
     w_down: DeviceBuffer<i8>, // experts x tiled [hidden][inter]
     s_down: DeviceBuffer<f32>,
+    b_up: Option<DeviceBuffer<f32>>,   // [experts][inter] when any expert has an up bias
+    b_down: Option<DeviceBuffer<f32>>, // [experts][hidden] when any expert has a down bias
     shared: Option<Int8Mlp>,
+    shared_b_up: Option<DeviceBuffer<f32>>,
+    shared_b_down: Option<DeviceBuffer<f32>>,
     workspace: Mutex<Option<DeviceBuffer<u8>>>,
 }
 
 /// One expert's dense f32 weights as the reference's MlpLayer stores them:
-/// `up` `[hidden][inter]`, `down` `[inter][hidden]` (row-major `[in][out]`).
+/// `up` `[hidden][inter]`, `down` `[inter][hidden]` (row-major `[in][out]`),
+/// and its optional projection biases (`[inter]`, `[hidden]`).
 pub struct DenseExpert<'a> {
     pub up: &'a [f32],
     pub down: &'a [f32],
+    pub up_bias: Option<&'a [f32]>,
+    pub down_bias: Option<&'a [f32]>,
+}
+
+/// The experts' biases gathered expert-major, zeros for an expert without
+/// one (adding +0.0 leaves every value but -0.0 unchanged, and the combine
+/// starts from +0.0, so the layer's output is the same); None when no expert
+/// has one.
+fn gather_biases(
+    experts: &[DenseExpert<'_>],
+    width: usize,
+    pick: impl Fn(&DenseExpert<'_>) -> Option<&[f32]>,
+    argument: &'static str,
+) -> Result<Option<Vec<f32>>, HipError> {
+    if experts.iter().all(|e| pick(e).is_none()) {
+        return Ok(None);
+    }
+    let mut all = vec![0.0f32; experts.len() * width];
+    for (i, e) in experts.iter().enumerate() {
+        if let Some(b) = pick(e) {
+            if b.len() != width {
+                return Err(HipError::LengthMismatch { argument, expected: width, actual: b.len() });
+            }
+            all[i * width..(i + 1) * width].copy_from_slice(b);
+        }
+    }
+    Ok(Some(all))
+}
+
+fn download(b: &DeviceBuffer<f32>) -> Result<Vec<f32>, HipError> {
+    let mut v = vec![0.0f32; b.len()];
+    b.copy_to_host(&mut v)?;
+    Ok(v)
 }
 
 fn quantize_tiled(in_dim: usize, out_dim: usize, w: &[f32], argument: &'static str) -> Result<(Vec<i8>, Vec<f32>), HipError> {
@@ -115,6 +156,19 @@ impl Int8Moe {
                 return Err(HipError::InvalidShape("shared expert does not match the layer".into()));
             }
         }
+        let b_up = gather_biases(experts, inter, |e| e.up_bias, "expert_up_bias")?;
+        let b_down = gather_biases(experts, hidden, |e| e.down_bias, "expert_down_bias")?;
+        let upload = |v: Option<Vec<f32>>| -> Result<Option<DeviceBuffer<f32>>, HipError> {
+            v.map(|v| DeviceBuffer::from_host(ctx, &v)).transpose()
+        };
+        // the shared expert's biases, as nh_moe_layer_w8a8 takes them
+        let (shared_b_up, shared_b_down) = match shared.as_ref() {
+            Some(s) => (
+                if s.up().has_bias() { Some(s.up().with_host(|w| Ok(w.bias.clone().unwrap_or_default()))?) } else { None },
+                if s.down().has_bias() { Some(s.down().with_host(|w| Ok(w.bias.clone().unwrap_or_default()))?) } else { None },
+            ),
+            None => (None, None),
+        };
         let (mut up, mut su, mut down, mut sd) = (Vec::new(), Vec::new(), Vec::new(), Vec::new());
         for ex in experts {
             let (t, s) = quantize_tiled(hidden, inter, ex.up, "expert_up")?;
@@ -140,15 +194,95 @@ impl Int8Moe {
             s_up: DeviceBuffer::from_host(ctx, &su)?,
             w_down: DeviceBuffer::from_host(ctx, &down)?,
             s_down: DeviceBuffer::from_host(ctx, &sd)?,
+            b_up: upload(b_up)?,
+            b_down: upload(b_down)?,
             shared,
+            shared_b_up: upload(shared_b_up)?,
+            shared_b_down: upload(shared_b_down)?,
             workspace: Mutex::new(None),
         })
     }
 
+    fn biases(&self) -> sys::nh_moe_biases {
+        let p = |b: &Option<DeviceBuffer<f32>>| b.as_ref().map_or(core::ptr::null(), |b| b.as_ptr());
+        sys::nh_moe_biases {
+            up: p(&self.b_up),
+            down: p(&self.b_down),
+            shared_up: p(&self.shared_b_up),
+            shared_down: p(&self.shared_b_down),
+        }
+    }
+
+    /// Whether the device entry point runs `row_count` rows of this layer.
+    pub fn device_supports(&self, row_count: usize) -> bool {
+        let sh_inter = self.shared.as_ref().map_or(0, |s| s.intermediate_dim());
+        unsafe {
+            sys::nh_supports_moe_layer_w8a8(row_count, self.hidden, self.inter, self.experts, self.top_k, sh_inter) != 0
+        }
+    }
+
+    /// The host twin (`nh_moe_layer_w8a8_host`): every operand copied to the
+    /// host (the bridge of gemm.rs:301-310), the same result bit for bit.
+    fn forward_host(&self, input: &[f32], row_count: usize, output: &mut [f32]) -> Result<(), HipError> {
+        let router_w = download(&self.router_w)?;
+        let router_b = self.router_b.as_ref().map(download).transpose()?;
+        let mut w_up = vec![0i8; self.w_up.len()];
+        self.w_up.copy_to_host(&mut w_up)?;
+        let mut w_down = vec![0i8; self.w_down.len()];
+        self.w_down.copy_to_host(&mut w_down)?;
+        let (s_up, s_down) = (download(&self.s_up)?, download(&self.s_down)?);
+        let b: Vec<Option<Vec<f32>>> = [&self.b_up, &self.b_down, &self.shared_b_up, &self.shared_b_down]
+            .iter()
+            .map(|b| b.as_ref().map(download).transpose())
+            .collect::<Result<_, _>>()?;
+        let p = |v: &Option<Vec<f32>>| v.as_ref().map_or(core::ptr::null(), |v| v.as_ptr());
+        let hb = sys::nh_moe_biases { up: p(&b[0]), down: p(&b[1]), shared_up: p(&b[2]), shared_down: p(&b[3]) };
+        let sh_inter = self.shared.as_ref().map_or(0, |s| s.intermediate_dim());
+        let out_ptr = output.as_mut_ptr();
+        let run = |su_w: *const i8, su_s: *const f32, sd_w: *const i8, sd_s: *const f32| {
+            call(|e| unsafe {
+                sys::nh_moe_layer_w8a8_host(
+                    input.as_ptr().cast(),
+                    sys::nh_dtype::F32,
+                    router_w.as_ptr(),
+                    p(&router_b),
+                    row_count,
+                    self.hidden,
+                    self.inter,
+                    self.experts,
+                    self.top_k,
+                    self.routing.renormalize as core::ffi::c_int,
+                    self.routing.scaling,
+                    w_up.as_ptr(),
+                    s_up.as_ptr(),
+                    w_down.as_ptr(),
+                    s_down.as_ptr(),
+                    sh_inter,
+                    su_w,
+                    su_s,
+                    sd_w,
+                    sd_s,
+                    &hb,
+                    out_ptr.cast(),
+                    sys::nh_dtype::F32,
+                    e,
+                )
+            })
+        };
+        match self.shared.as_ref() {
+            Some(s) => s.up().with_host(|u| {
+                s.down().with_host(|d| run(u.codes.as_ptr(), u.scales.as_ptr(), d.codes.as_ptr(), d.scales.as_ptr()))
+            }),
+            None => run(core::ptr::null(), core::ptr::null(), core::ptr::null(), core::ptr::null()),
+        }
+    }
+
     /// `input`, `output` f32 `[row_count][hidden]`, the reference's checks in
-    /// its order.  NonFiniteInput names "input" or "intermediate" (the
-    /// `[routes][intermediate]` up output in expert-sorted slot order, or the
-    /// shared expert's).  Synchronous.
+    /// its order.  NonFiniteInput names "input", "shared_intermediate" (the
+    /// shared expert's `[row_count][shared_inter]` ReLU^2 output, met first as
+    /// in moe.rs:197-219) or "intermediate" (the `[routes][intermediate]` up
+    /// output in expert-sorted slot order).  Synchronous; outside the device
+    /// envelope (or on an Unsupported device call) the host twin runs.
     pub fn forward_into(&self, input: &[f32], row_count: usize, output: &mut [f32]) -> Result<(), HipError> {
         let h = self.hidden;
         if row_count == 0 {
@@ -164,10 +298,14 @@ impl Int8Moe {
                 actual: output.len(),
             });
         }
+        if !self.device_supports(row_count) {
+            return self.forward_host(input, row_count, output);
+        }
         let ctx = &self.ctx;
         let x = DeviceBuffer::from_host(ctx, input)?;
         let mut y = DeviceBuffer::<f32>::new(ctx, output.len())?;
         let mut word = DeviceBuffer::<u64>::zeroed(ctx, 1)?;
+        let biases = self.biases();
         let sh_inter = self.shared.as_ref().map_or(0, |s| s.intermediate_dim());
         let need = unsafe {
             sys::nh_moe_layer_w8a8_workspace_size(row_count, h, self.inter, self.experts, self.top_k, sh_inter)
@@ -183,7 +321,7 @@ impl Int8Moe {
             Some(s) => (s.up().codes_ptr(), s.up().scales_ptr(), s.down().codes_ptr(), s.down().scales_ptr()),
             None => (null_i8, null_f32, null_i8, null_f32),
         };
-        call(|e| unsafe {
+        let r = call(|e| unsafe {
             sys::nh_moe_layer_w8a8(
                 ctx.as_raw(),
                 x.as_ptr().cast(),
@@ -206,6 +344,7 @@ impl Int8Moe {
                 su_s,
                 sd_w,
                 sd_s,
+                &biases,
                 y.as_mut_ptr().cast(),
                 sys::nh_dtype::F32,
                 ws.as_mut_ptr().cast(),
@@ -214,7 +353,12 @@ impl Int8Moe {
                 core::ptr::null_mut(),
                 e,
             )
-        })?;
+        });
+        if let Err(HipError::Unsupported(_)) = r {
+            drop(guard);
+            return self.forward_host(input, row_count, output);
+        }
+        r?;
         call(|e| unsafe { sys::nh_take_nonfinite(ctx.as_raw(), word.as_mut_ptr(), core::ptr::null_mut(), e) })?;
         y.copy_to_host(output)
     }

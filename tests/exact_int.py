@@ -6,8 +6,8 @@ partial sum of K of them stays below K * 127^2 < 2^53 for K < 5.5e11, so each
 float64 addition BLAS performs, in whatever order and blocking, is exact: the
 float64 result is the integer sum, identical to the oracle's int32 loop
 (or_gemm_i8_i32) whenever that fits in int32, which the device envelope
-guarantees (K <= 131072).  test_oracle_golden.py pins these helpers against the
-oracle on random and extreme inputs; the epilogues and the MoE stages other
+guarantees (K <= 131072).  tests/test_exact_int.py pins these helpers against
+the oracle on random and extreme inputs; the epilogues and the MoE stages other
 than the accumulation are the oracle's own functions.
 """
 import numpy as np

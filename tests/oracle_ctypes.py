@@ -62,6 +62,8 @@ def _declare(L):
     L.or_quantize_rows_i8_bf16.argtypes = [P, SZ, SZ, P, P, C.POINTER(OrError)]
     L.or_dequantize_i8.argtypes = [P, P, SZ, SZ, P]
     L.or_gemm_f32.argtypes = [P, SZ, P, SZ, SZ, SZ, SZ, P, SZ, C.POINTER(OrError)]
+    L.or_gemm_f32_col_range.argtypes = [P, P, SZ, SZ, SZ, SZ, SZ, P]
+    L.or_gemm_f32_col_range.restype = None
     L.or_gemm_i8_i32.argtypes = [P, P, SZ, SZ, SZ, P]
     L.or_epilogue_w8a8.argtypes = [P, P, P, P, SZ, SZ, C.c_int, C.c_int, P]
     L.or_linear_w8a8.argtypes = [P, P, P, P, P, SZ, SZ, SZ, C.c_int, P]
@@ -73,17 +75,17 @@ def _declare(L):
     L.or_route_sigmoid_topk.argtypes = [P, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, SZ, P, SZ, C.POINTER(OrError)]
     L.or_route_softmax_topk.argtypes = [P, SZ, SZ, SZ, SZ, P, SZ, P, SZ, C.POINTER(OrError)]
     L.or_moe_permute.argtypes = [P, SZ, SZ, SZ, P, P, P]
-    L.or_moe_grouped_w8a8.argtypes = [P, P, C.c_int, SZ, P, P, SZ, P, P, SZ, SZ, C.c_int, P]
+    L.or_moe_grouped_w8a8.argtypes = [P, P, C.c_int, SZ, P, P, SZ, P, P, P, SZ, SZ, C.c_int, P]
     L.or_moe_combine.argtypes = [P, P, P, SZ, SZ, SZ, C.c_int, P]
     L.or_moe_forward_w8a8.argtypes = [P, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, P, P, P, P, P, P]
     L.or_linear_project.argtypes = [P, SZ, SZ, P, SZ, SZ, P, P, SZ, C.POINTER(OrError)]
     L.or_mlp_forward.argtypes = [P, SZ, SZ, SZ, P, P, P, P, P]
-    L.or_moe_forward_dense.argtypes = [P, SZ, SZ, SZ, SZ, P, P, SZ, P, P, SZ, P, P, P]
+    L.or_moe_forward_dense.argtypes = [P, SZ, SZ, SZ, SZ, P, P, SZ, P, P, P, P, SZ, P, P, P, P, P]
     L.or_moe_combine_shared.argtypes = [P, P, P, P, SZ, SZ, SZ, C.c_int, P]
     L.or_linear_w4a8.argtypes = [P, SZ, SZ, P, SZ, C.c_float, C.c_uint32, P, C.c_int, P]
-    L.or_mlp_w8a8.argtypes = [P, SZ, SZ, SZ, P, P, P, P, P]
+    L.or_mlp_w8a8.argtypes = [P, SZ, SZ, SZ, P, P, P, P, P, P, P]
     L.or_moe_forward_shared_w8a8.argtypes = [P, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, SZ, P, P, P,
-                                             P, P, P, P, P, P, P]
+                                             P, P, P, P, P, P, P, P]
 
 
 def ptr(a):
@@ -147,6 +149,11 @@ def gemm_f32(lhs, rhs, m, k, n, out_len=None):
     err = OrError()
     st = lib().or_gemm_f32(ptr(lhs), lhs.size, ptr(rhs), rhs.size, m, k, n, ptr(out), out_len, C.byref(err))
     return st, out[:out_len], err
+
+
+def gemm_f32_col_range(lhs, rhs, m, k, n, col0, col1, out):
+    """or_gemm_f32's loop over output columns [col0, col1) of out ([m][n], f32), in place."""
+    lib().or_gemm_f32_col_range(ptr(lhs), ptr(rhs), m, k, n, col0, col1, ptr(out))
 
 
 def gemm_i8_i32(xq, wq):
@@ -220,7 +227,7 @@ def moe_permute(indices, tokens, top_k, experts):
     return offsets, perm[:routes], pos[:routes]
 
 
-def moe_grouped(aq, sa, gather_tokens, top_k, offsets, perm, w, sw, relu2):
+def moe_grouped(aq, sa, gather_tokens, top_k, offsets, perm, w, sw, relu2, bias=None):
     experts, n, k = w.shape
     routes = int(offsets[-1])
     out = np.zeros((max(routes, 1), n), dtype=np.float32)
@@ -230,8 +237,9 @@ def moe_grouped(aq, sa, gather_tokens, top_k, offsets, perm, w, sw, relu2):
     perm = np.ascontiguousarray(perm, dtype=np.int32)
     w = np.ascontiguousarray(w, dtype=np.int8)
     sw = np.ascontiguousarray(sw, dtype=np.float32)
+    bias = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
     lib().or_moe_grouped_w8a8(ptr(aq), ptr(sa), int(gather_tokens), top_k, ptr(offsets), ptr(perm), experts,
-                              ptr(w), ptr(sw), n, k, int(relu2), ptr(out))
+                              ptr(w), ptr(sw), ptr(bias), n, k, int(relu2), ptr(out))
     return out[:routes]
 
 
@@ -276,21 +284,29 @@ def moe_combine_shared(slot_out, pos, weights, shared, tokens, top_k, hidden, ou
     return out
 
 
-def mlp_w8a8(x_bf16, w_up, s_up, w_down, s_down):
-    """int8 MLP of bf16 rows: Q2 -> up (ReLU^2, f32) -> Q2 -> down (f32)."""
+def _f32_or_none(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+def mlp_w8a8(x_bf16, w_up, s_up, w_down, s_down, b_up=None, b_down=None):
+    """int8 MLP of bf16 rows: Q2 -> up (+ b_up, ReLU^2, f32) -> Q2 -> down (+ b_down, f32)."""
     x_bf16 = np.ascontiguousarray(x_bf16, dtype=np.uint16)
     rows, hidden = x_bf16.shape
     inter = w_up.shape[0]
     out = np.zeros((rows, hidden), dtype=np.float32)
+    b_up, b_down = _f32_or_none(b_up), _f32_or_none(b_down)
     st = lib().or_mlp_w8a8(ptr(x_bf16), rows, hidden, inter, ptr(np.ascontiguousarray(w_up, dtype=np.int8)),
-                           ptr(np.ascontiguousarray(s_up, dtype=np.float32)),
+                           ptr(np.ascontiguousarray(s_up, dtype=np.float32)), ptr(b_up),
                            ptr(np.ascontiguousarray(w_down, dtype=np.int8)),
-                           ptr(np.ascontiguousarray(s_down, dtype=np.float32)), ptr(out))
+                           ptr(np.ascontiguousarray(s_down, dtype=np.float32)), ptr(b_down), ptr(out))
     return st, out
 
 
 def moe_forward_shared_w8a8(x_bf16, logits, w_up, s_up, w_down, s_down, top_k, sh_up, sh_su, sh_down, sh_sd,
-                            renormalize=True, scaling=1.0):
+                            renormalize=True, scaling=1.0, biases=None):
+    """The int8 MoE layer with a shared expert (sh_up None: without one);
+    biases = (up [E][inter], down [E][hidden], shared up, shared down), each
+    None or an array."""
     tokens, hidden = x_bf16.shape
     experts, inter, _ = w_up.shape
     routes = tokens * top_k
@@ -300,14 +316,17 @@ def moe_forward_shared_w8a8(x_bf16, logits, w_up, s_up, w_down, s_down, top_k, s
     offsets = np.zeros(experts + 1, dtype=np.int32)
     perm = np.zeros(routes, dtype=np.int32)
     pos = np.zeros(routes, dtype=np.int32)
-    keep = [np.ascontiguousarray(a, dtype=d) for a, d in ((x_bf16, np.uint16), (logits, np.float32), (w_up, np.int8),
-                                                           (s_up, np.float32), (w_down, np.int8), (s_down, np.float32),
-                                                           (sh_up, np.int8), (sh_su, np.float32), (sh_down, np.int8),
-                                                           (sh_sd, np.float32))]
+    keep = [None if a is None else np.ascontiguousarray(a, dtype=d)
+            for a, d in ((x_bf16, np.uint16), (logits, np.float32), (w_up, np.int8), (s_up, np.float32),
+                         (w_down, np.int8), (s_down, np.float32), (sh_up, np.int8), (sh_su, np.float32),
+                         (sh_down, np.int8), (sh_sd, np.float32))]
+    bkeep = [_f32_or_none(b) for b in (biases or (None,) * 4)]
+    bptrs = (C.c_void_p * 4)(*[ptr(b) for b in bkeep]) if biases is not None else None
     st = lib().or_moe_forward_shared_w8a8(ptr(keep[0]), ptr(keep[1]), tokens, hidden, inter, experts, top_k,
                                           int(renormalize), scaling, ptr(keep[2]), ptr(keep[3]), ptr(keep[4]),
-                                          ptr(keep[5]), sh_up.shape[0], ptr(keep[6]), ptr(keep[7]), ptr(keep[8]),
-                                          ptr(keep[9]), ptr(out), ptr(idx), ptr(w), ptr(offsets), ptr(perm), ptr(pos))
+                                          ptr(keep[5]), 0 if sh_up is None else sh_up.shape[0], ptr(keep[6]),
+                                          ptr(keep[7]), ptr(keep[8]), ptr(keep[9]), bptrs, ptr(out), ptr(idx), ptr(w),
+                                          ptr(offsets), ptr(perm), ptr(pos))
     return st, out, idx, w, offsets, perm, pos
 
 

@@ -418,7 +418,7 @@ def test_moe_forward_shared_validation_before_any_launch():
     def call(si, up_sh, ws_bytes, tokens=T):
         dummy = 16
         return NH.call_status("nh_moe_forward_shared_w8a8", None, dummy, NH.BF16, dummy, tokens, H, I, E, K, 1, 1.0,
-                              dummy, dummy, dummy, dummy, si, up_sh, dummy, dummy, dummy, dummy, NH.BF16,
+                              dummy, dummy, dummy, dummy, si, up_sh, dummy, dummy, dummy, None, dummy, NH.BF16,
                               dummy if ws_bytes else None, ws_bytes, None, None)
 
     assert call(SI, None, need)[0] == NH.INVALID_PARAMS
@@ -511,3 +511,192 @@ def test_linear_noalloc_rejects_a_workspace_above_its_scratch_before_the_device(
     # m == 0 and shape errors keep the order of nh_linear_w8a8
     assert NH.call_status("nh_linear_w8a8_noalloc", None, None, NH.BF16, None, None, None, 0, 64, 64, None, NH.BF16,
                           None, None, None, None)[0] == NH.INVALID_ROW_COUNT
+
+
+# ---- layer host twins (the host-fallback contract, gemm.rs:290-310) ----------
+@pytest.mark.parametrize("m,n,k,xdt,odt", [(3, 37, 100, "f32", "f32"),   # k % 16 != 0: outside the device envelope
+                                           (5, 33, 96, "bf16", "bf16"), (1, 20, 1, "bf16", "f32"),
+                                           (17, 9, 200, "f32", "bf16")])
+def test_linear_host_twin_matches_oracle(m, n, k, xdt, odt):
+    """nh_linear_w8a8_host = Q2 + the W8A8 product + bias (the oracle's parts),
+    bit for bit, on shapes the device rejects (k % 16 != 0) and accepts; the
+    device entry point returns Unsupported outside nh_supports_linear_w8a8
+    before touching a device, so a caller takes this twin there."""
+    rng = np.random.default_rng(m * 100 + k)
+    w = O.normal_f32(0, n * k, 0.0, 0.02).reshape(n, k)
+    _, wq, sw, _ = O.quantize_rows_f32(w)
+    bias = rng.standard_normal(n).astype(np.float32)
+    xf = O.normal_f32(1, m * k).reshape(m, k)
+    if xdt == "bf16":
+        x = O.to_bf16(xf)
+        st, xq, sx, _ = O.quantize_rows_bf16(x)
+    else:
+        x = xf
+        st, xq, sx, _ = O.quantize_rows_f32(x)
+    assert st == O.OK
+    bf = odt == "bf16"
+    ref = O.linear_w8a8(xq, sx, wq, sw, bias=bias, out_bf16=bf)
+    out = np.zeros((m, n), dtype=np.uint16 if bf else np.float32)
+    xq_out = np.zeros((m, k), dtype=np.int8)
+    sx_out = np.zeros(m, dtype=np.float32)
+    wt = tile_16x64(wq)
+    NH.call("nh_linear_w8a8_host", x.ctypes.data, NH.BF16 if xdt == "bf16" else NH.F32, wt.ctypes.data,
+            sw.ctypes.data, bias.ctypes.data, m, n, k, out.ctypes.data, NH.BF16 if bf else NH.F32,
+            xq_out.ctypes.data, sx_out.ctypes.data)
+    assert np.array_equal(out, ref)
+    assert np.array_equal(xq_out, xq) and np.array_equal(sx_out.view(np.uint32), sx.view(np.uint32))
+    supported = NH.lib().nh_supports_linear_w8a8(m, n, k)
+    assert supported == (k % 16 == 0)
+    if not supported:
+        st, err = NH.call_status("nh_linear_w8a8", None, 16, NH.F32, 16, 16, None, m, n, k, 16, NH.F32, 16, 1 << 30,
+                                 None, None, None, None)
+        assert st == NH.UNSUPPORTED
+
+
+def test_linear_host_twin_errors_and_nonfinite():
+    k, n = 48, 8
+    x = O.normal_f32(3, 2 * k).reshape(2, k)
+    x[1, 7] = np.nan
+    x[1, 9] = np.inf
+    _, wq, sw, _ = O.quantize_rows_f32(O.normal_f32(0, n * k, 0.0, 0.02).reshape(n, k))
+    wt = tile_16x64(wq)
+    out = np.zeros((2, n), dtype=np.float32)
+    st, err = NH.call_status("nh_linear_w8a8_host", x.ctypes.data, NH.F32, wt.ctypes.data, sw.ctypes.data, None, 2,
+                             n, k, out.ctypes.data, NH.F32, None, None)
+    assert st == NH.NON_FINITE_INPUT and err.argument == b"input" and err.index == k + 7 and math.isnan(err.value)
+    for m_, n_, k_, want in ((0, n, k, NH.INVALID_ROW_COUNT), (2, 0, k, NH.INVALID_SHAPE), (2, n, 0, NH.INVALID_SHAPE)):
+        st, _ = NH.call_status("nh_linear_w8a8_host", x.ctypes.data, NH.F32, wt.ctypes.data, sw.ctypes.data, None, m_,
+                               n_, k_, out.ctypes.data, NH.F32, None, None)
+        assert st == want
+
+
+@pytest.mark.parametrize("m,hidden,inter", [(3, 40, 24), (2, 64, 32), (1, 17, 5)])
+def test_mlp_host_twin_matches_oracle(m, hidden, inter):
+    """nh_mlp_w8a8_host = the oracle's int8 MLP with biases (or_mlp_w8a8),
+    bit for bit, also at hidden / inter not multiples of 16 (no device form);
+    an overflowing intermediate is NonFiniteInput "intermediate" at the
+    oracle's index, a non-finite x "input"."""
+    rng = np.random.default_rng(hidden)
+    x = O.to_bf16(O.normal_f32(7, m * hidden)).reshape(m, hidden)
+    _, wu, su, _ = O.quantize_rows_f32(O.normal_f32(8, inter * hidden, 0, 0.02).reshape(inter, hidden))
+    _, wd, sd, _ = O.quantize_rows_f32(O.normal_f32(9, hidden * inter, 0, 0.02).reshape(hidden, inter))
+    bu = rng.standard_normal(inter).astype(np.float32)
+    bd = rng.standard_normal(hidden).astype(np.float32)
+    st, ref = O.mlp_w8a8(x, wu, su, wd, sd, b_up=bu, b_down=bd)
+    assert st == O.OK
+    wut, wdt = tile_16x64(wu), tile_16x64(wd)
+    out = np.zeros((m, hidden), dtype=np.float32)
+    args = lambda xx, b_up: (xx.ctypes.data, NH.BF16, wut.ctypes.data, su.ctypes.data, b_up.ctypes.data,
+                             wdt.ctypes.data, sd.ctypes.data, bd.ctypes.data, m, hidden, inter, out.ctypes.data, NH.F32)
+    NH.call("nh_mlp_w8a8_host", *args(x, bu))
+    assert np.array_equal(out, ref)
+    assert NH.lib().nh_supports_mlp_w8a8(m, hidden, inter) == (hidden % 16 == 0 and inter % 16 == 0)
+    # the intermediate overflows: ReLU^2 of a 3e38 biased output is +inf
+    big = bu.copy()
+    big[inter - 1] = 3e38
+    _, xq, sx, _ = O.quantize_rows_bf16(x)
+    h = O.epilogue(O.gemm_i8_i32(xq, wu), sx, su, bias=big, relu2=True)
+    ost, _, _, oerr = O.quantize_rows_f32(h)
+    assert ost == O.NON_FINITE_INPUT
+    st, err = NH.call_status("nh_mlp_w8a8_host", *args(x, big))
+    assert st == NH.NON_FINITE_INPUT and err.argument == b"intermediate" and err.index == oerr.index
+    assert np.isinf(err.value)
+    xb = x.copy()
+    xb[m - 1, 2] = 0x7fc0  # bf16 NaN: the input wins over the intermediate
+    st, err = NH.call_status("nh_mlp_w8a8_host", *args(xb, big))
+    assert st == NH.NON_FINITE_INPUT and err.argument == b"input" and err.index == (m - 1) * hidden + 2
+
+
+def _moe_host_case(tokens, hidden, inter, experts, top_k, sh_inter, seed=3):
+    rng = np.random.default_rng(seed)
+    x = O.to_bf16(O.normal_f32(1, tokens * hidden)).reshape(tokens, hidden)
+    rw = O.normal_f32(2, hidden * experts, 0.0, 0.1)
+    rb = rng.standard_normal(experts).astype(np.float32)
+    _, qu, su, _ = O.quantize_rows_f32(O.normal_f32(3, experts * inter * hidden, 0, 0.02).reshape(-1, hidden))
+    _, qd, sd, _ = O.quantize_rows_f32(O.normal_f32(4, experts * hidden * inter, 0, 0.02).reshape(-1, inter))
+    qu, su = qu.reshape(experts, inter, hidden), su.reshape(experts, inter)
+    qd, sd = qd.reshape(experts, hidden, inter), sd.reshape(experts, hidden)
+    sh = None
+    if sh_inter:
+        _, hu, hsu, _ = O.quantize_rows_f32(O.normal_f32(5, sh_inter * hidden, 0, 0.02).reshape(sh_inter, hidden))
+        _, hd, hsd, _ = O.quantize_rows_f32(O.normal_f32(6, hidden * sh_inter, 0, 0.02).reshape(hidden, sh_inter))
+        sh = (hu, hsu, hd, hsd)
+    biases = [rng.standard_normal((experts, inter)).astype(np.float32) * 0.5,
+              rng.standard_normal((experts, hidden)).astype(np.float32),
+              rng.standard_normal(sh_inter).astype(np.float32) * 0.5 if sh_inter else None,
+              rng.standard_normal(hidden).astype(np.float32) if sh_inter else None]
+    return x, rw, rb, qu, su, qd, sd, sh, biases
+
+
+def _moe_host_call(x, xdt, rw, rb, qu, su, qd, sd, sh, biases, top_k, renorm, scaling, out_dtype=NH.BF16):
+    tokens, hidden = x.shape
+    experts, inter, _ = qu.shape
+    sh_inter = sh[0].shape[0] if sh is not None else 0
+    tiles = [tile_experts(qu), tile_experts(qd)] + ([tile_16x64(sh[0]), tile_16x64(sh[2])] if sh is not None else [])
+    shp = [tiles[2].ctypes.data, sh[1].ctypes.data, tiles[3].ctypes.data, sh[3].ctypes.data] if sh is not None \
+        else [None] * 4
+    mb = NH.MoeBiases(*[None if b is None else b.ctypes.data for b in biases]) if biases is not None else None
+    out = np.zeros((tokens, hidden), dtype=np.uint16 if out_dtype == NH.BF16 else np.float32)
+    st, err = NH.call_status("nh_moe_layer_w8a8_host", x.ctypes.data, xdt, rw.ctypes.data, rb.ctypes.data, tokens,
+                             hidden, inter, experts, top_k, renorm, C.c_float(scaling), tiles[0].ctypes.data,
+                             su.ctypes.data, tiles[1].ctypes.data, sd.ctypes.data, sh_inter, *shp, mb,
+                             out.ctypes.data, out_dtype)
+    return st, err, out
+
+
+@pytest.mark.parametrize("tokens,hidden,inter,experts,top_k,sh_inter,renorm,scaling",
+                         [(9, 64, 32, 8, 3, 48, 0, 1.0), (7, 40, 24, 5, 2, 0, 1, 2.5),  # 40 / 24: no device form
+                          (5, 48, 20, 6, 6, 12, 1, 1.0)])
+def test_moe_layer_host_twin_matches_oracle(tokens, hidden, inter, experts, top_k, sh_inter, renorm, scaling):
+    """nh_moe_layer_w8a8_host = router.project (gemm_into_host then the bias,
+    linear.rs:325-339: or_linear_project) + the oracle's int8 MoE with its
+    shared expert and all four biases, bit for bit; with f32 x of bf16 values
+    the same output."""
+    x, rw, rb, qu, su, qd, sd, sh, b = _moe_host_case(tokens, hidden, inter, experts, top_k, sh_inter)
+    logits = np.zeros(tokens * experts, dtype=np.float32)
+    xf = O.bf16_to_f32(x)
+    err = O.OrError()
+    assert O.lib().or_linear_project(O.ptr(xf), xf.size, tokens, O.ptr(rw), hidden, experts, O.ptr(rb),
+                                     O.ptr(logits), logits.size, C.byref(err)) == O.OK
+    shargs = sh if sh is not None else (None, None, None, None)
+    st, ref, *_ = O.moe_forward_shared_w8a8(x, logits, qu, su, qd, sd, top_k, *shargs, renormalize=bool(renorm),
+                                            scaling=scaling, biases=tuple(b))
+    assert st == O.OK
+    st, e, out = _moe_host_call(x, NH.BF16, rw, rb, qu, su, qd, sd, sh, b, top_k, renorm, scaling)
+    assert st == NH.OK, e.message
+    assert np.array_equal(out, ref)
+    st, e, out_f = _moe_host_call(np.ascontiguousarray(xf), NH.F32, rw, rb, qu, su, qd, sd, sh, b, top_k, renorm,
+                                  scaling)
+    assert st == NH.OK and np.array_equal(out_f, ref)
+    supported = NH.lib().nh_supports_moe_layer_w8a8(tokens, hidden, inter, experts, top_k, sh_inter)
+    assert supported == (hidden % 16 == 0 and inter % 16 == 0 and (sh_inter % 16 == 0))
+
+
+def test_moe_layer_host_twin_nonfinite_order_and_errors():
+    """Input first, then the shared expert's intermediate, then the routed
+    experts' (the order MoeLayer::forward_into meets them, moe.rs:197-233, and
+    the device word's stages)."""
+    tokens, hidden, inter, experts, top_k, sh_inter = 6, 32, 16, 4, 2, 16
+    x, rw, rb, qu, su, qd, sd, sh, b = _moe_host_case(tokens, hidden, inter, experts, top_k, sh_inter)
+    b_sh_big = list(b)
+    b_sh_big[2] = b[2].copy()
+    b_sh_big[2][3] = 3e38
+    st, e, _ = _moe_host_call(x, NH.BF16, rw, rb, qu, su, qd, sd, sh, b_sh_big, top_k, 0, 1.0)
+    assert st == NH.NON_FINITE_INPUT and e.argument == b"shared_intermediate" and np.isinf(e.value)
+    assert e.index % sh_inter == 3
+    b_all_big = list(b_sh_big)
+    b_all_big[0] = b[0].copy()
+    b_all_big[0][:, 5] = 3e38
+    st, e, _ = _moe_host_call(x, NH.BF16, rw, rb, qu, su, qd, sd, sh, b_all_big, top_k, 0, 1.0)
+    assert st == NH.NON_FINITE_INPUT and e.argument == b"shared_intermediate"
+    st, e, _ = _moe_host_call(x, NH.BF16, rw, rb, qu, su, qd, sd, sh, [b_all_big[0], b[1], b[2], b[3]], top_k, 0, 1.0)
+    assert st == NH.NON_FINITE_INPUT and e.argument == b"intermediate" and e.index == 5  # slot 0, column 5
+    xb = x.copy()
+    xb[2, 4] = 0xff80  # -inf
+    st, e, _ = _moe_host_call(xb, NH.BF16, rw, rb, qu, su, qd, sd, sh, b_all_big, top_k, 0, 1.0)
+    assert st == NH.NON_FINITE_INPUT and e.argument == b"input" and e.index == 2 * hidden + 4 and e.value < 0
+    # shared biases without a shared expert
+    st, e, _ = _moe_host_call(x, NH.BF16, rw, rb, qu, su, qd, sd, None, [None, None, b[2], None], top_k, 0, 1.0)
+    assert st == NH.INVALID_PARAMS
+    st, e, _ = _moe_host_call(x[:0], NH.BF16, rw, rb, qu, su, qd, sd, sh, b, top_k, 0, 1.0)
+    assert st == NH.INVALID_ROW_COUNT

@@ -375,6 +375,38 @@ def test_linear_small_m_shapes_bit_exact(ctx, m, n, k, dtype):
     assert np.array_equal(out.numpy().view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 4096)], ids=["qkv", "o"])
+@pytest.mark.parametrize("out_dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_linear_decode_stack_attention_shapes(ctx, n, k, out_dtype, with_bias):
+    """The decode stack's attention projections at its batch of 8 rows (QKV
+    4096 -> 6144 and O 4096 -> 4096): the streaming decode unit's runs over
+    384 and 256 N tiles.  bf16 rows in; bf16 and f32 out, with and without a
+    bias, against LinearProjection::project_into's order (linear.rs:325-339:
+    GEMM, then the bias)."""
+    m = 8
+    note(f"linear_w8a8 attention m={m} n={n} k={k} out={out_dtype} bias={with_bias}")
+    _, wq, sw = quantized_weights(n, k, seed=7)
+    bias = O.normal_f32(9, n, 0.0, 0.1) if with_bias else None
+    x = activations_bf16(m, k, seed=60)
+    _, xq_ref, sx_ref, _ = O.quantize_rows_bf16(x)
+    ref = linear_w8a8_exact(xq_ref, sx_ref, wq, sw, bias=bias, out_bf16=out_dtype == "bf16")
+    dx, dw, ds = ctx.upload(x), ctx.upload(tile_16x64(wq)), ctx.upload(sw)
+    db = ctx.upload(bias) if with_bias else None
+    ws_bytes = NH.lib().nh_linear_w8a8_workspace_size(m, k)
+    ws = ctx.empty(max(ws_bytes, 1), np.uint8)
+    odt = NH.BF16 if out_dtype == "bf16" else NH.F32
+    out = ctx.empty((m, n), np.uint16 if out_dtype == "bf16" else np.float32)
+    NH.call("nh_linear_w8a8", ctx.handle, dx.ptr, NH.BF16, dw.ptr, ds.ptr, db.ptr if db else None, m, n, k, out.ptr,
+            odt, ws.ptr, ws_bytes, None, None, None, None)
+    ctx.synchronize()
+    got = out.numpy()
+    if out_dtype == "bf16":
+        assert np.array_equal(got, ref)
+    else:
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 # ---- L2: int8 MLP layer (MlpLayer::forward_into, mlp.rs:157-211) -----------------
 def mlp_oracle(x, xdt, w_up, s_up, b_up, w_down, s_down, b_down, out_bf16):
     """Per-token Q2, up projection + bias, ReLU^2 (mlp.rs:205) in f32, Q2 of
@@ -809,7 +841,7 @@ def test_moe_forward_shared_expert_bit_exact(ctx, tokens, hidden, inter, experts
     dhu, dhsu, dhd, dhsd = ctx.upload(tile_16x64(hu)), ctx.upload(hsu), ctx.upload(tile_16x64(hd)), ctx.upload(hsd)
     out = ctx.empty((tokens, hidden), np.uint16)
     NH.call("nh_moe_forward_shared_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k,
-            1, 1.0, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, sh_inter, dhu.ptr, dhsu.ptr, dhd.ptr, dhsd.ptr, out.ptr,
+            1, 1.0, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, sh_inter, dhu.ptr, dhsu.ptr, dhd.ptr, dhsd.ptr, None, out.ptr,
             NH.BF16, ws.ptr, ws_bytes, None, None)
     ctx.synchronize()
     assert np.array_equal(out.numpy(), ref)
@@ -829,7 +861,7 @@ def test_moe_forward_bit_exact(ctx, tokens, hidden, inter, experts, top_k):
     dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
     out = ctx.empty((tokens, hidden), np.uint16)
     NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
-            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, None, None)
+            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, None, out.ptr, NH.BF16, ws.ptr, ws_bytes, None, None)
     ctx.synchronize()
     lay = (ctypes.c_size_t * 5)()
     NH.lib().nh_moe_workspace_layout(tokens, hidden, inter, experts, top_k, lay)
@@ -871,7 +903,7 @@ def test_moe_forward_config3_bit_exact(ctx):
     dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
     out = ctx.empty((tokens, hidden), np.uint16)
     NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
-            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, None, None)
+            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, None, out.ptr, NH.BF16, ws.ptr, ws_bytes, None, None)
     ctx.synchronize()
     lay = (ctypes.c_size_t * 5)()
     NH.lib().nh_moe_workspace_layout(tokens, hidden, inter, experts, top_k, lay)
@@ -942,7 +974,7 @@ def test_moe_layer_with_router_bit_exact(ctx, tokens, hidden, inter, experts, to
         sh = [dhu.ptr, dhsu.ptr, dhd.ptr, dhsd.ptr]
     out = ctx.empty((tokens, hidden), np.uint16)
     NH.call("nh_moe_layer_w8a8", ctx.handle, dx.ptr, NH.BF16, drw.ptr, drb.ptr, tokens, hidden, inter, experts,
-            top_k, 0, 1.0, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, sh_inter, *sh, out.ptr, NH.BF16, ws.ptr, ws_bytes,
+            top_k, 0, 1.0, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, sh_inter, *sh, None, out.ptr, NH.BF16, ws.ptr, ws_bytes,
             None, None)
     ctx.synchronize()
     wsh = ws.numpy()
@@ -953,6 +985,101 @@ def test_moe_layer_with_router_bit_exact(ctx, tokens, hidden, inter, experts, to
     assert np.array_equal(wsh[lay[0]:lay[0] + 4 * tokens * top_k].view(np.int32), idx)
     got = out.numpy()
     assert np.array_equal(got, ref), f"{(got != ref).sum()} of {ref.size} outputs differ"
+
+
+def moe_biases_case(experts, inter, hidden, sh_inter, seed=50):
+    """Expert and shared-expert biases (the reference's MlpLayer biases,
+    mlp.rs:79-96), N(0, 0.5) up and N(0, 1) down."""
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((experts, inter)).astype(np.float32) * 0.5,
+            rng.standard_normal((experts, hidden)).astype(np.float32),
+            rng.standard_normal(sh_inter).astype(np.float32) * 0.5 if sh_inter else None,
+            rng.standard_normal(hidden).astype(np.float32) if sh_inter else None)
+
+
+@pytest.mark.parametrize("tokens,hidden,inter,experts,top_k,sh_inter", [(13, 64, 32, 8, 3, 16), (64, 2688, 1856, 128, 6, 3712),
+                                                                         (40, 2688, 1856, 128, 6, 0),
+                                                                         (7, 64, 2112, 4, 2, 0)])  # unfused: inter > 2048
+def test_moe_layer_with_biases_bit_exact(ctx, tokens, hidden, inter, experts, top_k, sh_inter):
+    """nh_moe_layer_w8a8 with the routed experts' up and down biases and the
+    shared expert's (the up bias before ReLU^2, the down bias on the expert's
+    output before the combine weight, mlp.rs:201-208) against the oracle's
+    int8 layer with the same biases, every output; and against the host twin."""
+    note(f"moe layer + biases t={tokens} h={hidden} i={inter} e={experts} k={top_k} si={sh_inter}")
+    x, _, up, su, down, sd = moe_case(tokens, hidden, inter, experts, top_k)
+    rw, rb = router_case(tokens, hidden, experts)
+    logits = router_logits(x, rw, rb)
+    b = moe_biases_case(experts, inter, hidden, sh_inter)
+    shw = (None, None, None, None)
+    if sh_inter:
+        _, hu, hsu = quantized_weights(sh_inter, hidden, seed=30)
+        _, hd, hsd = quantized_weights(hidden, sh_inter, seed=31)
+        shw = (hu, hsu, hd, hsd)
+    st, ref, idx, *_ = O.moe_forward_shared_w8a8(x, logits, up, su, down, sd, top_k, *shw, renormalize=False,
+                                                 biases=b)
+    assert st == O.OK
+    lib = NH.lib()
+    ws_bytes = lib.nh_moe_layer_w8a8_workspace_size(tokens, hidden, inter, experts, top_k, sh_inter)
+    ws = ctx.empty(ws_bytes, np.uint8)
+    ws.fill_bytes(0x5a)
+    dx, drw, drb = ctx.upload(x), ctx.upload(rw), ctx.upload(rb)
+    dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
+    dbs = [ctx.upload(v) if v is not None else None for v in b]
+    mb = NH.MoeBiases(*[d.ptr if d is not None else None for d in dbs])
+    sh = [None] * 4
+    if sh_inter:
+        dsh = [ctx.upload(tile_16x64(hu)), ctx.upload(hsu), ctx.upload(tile_16x64(hd)), ctx.upload(hsd)]
+        sh = [d.ptr for d in dsh]
+    out = ctx.empty((tokens, hidden), np.uint16)
+    NH.call("nh_moe_layer_w8a8", ctx.handle, dx.ptr, NH.BF16, drw.ptr, drb.ptr, tokens, hidden, inter, experts,
+            top_k, 0, 1.0, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, sh_inter, *sh, mb, out.ptr, NH.BF16, ws.ptr,
+            ws_bytes, None, None)
+    ctx.synchronize()
+    got = out.numpy()
+    assert np.array_equal(got, ref), f"{(got != ref).sum()} of {ref.size} outputs differ"
+    if tokens <= 13:  # the host twin on the same operands (the fallback path), bit for bit
+        tiles = [tile_experts(up), tile_experts(down)] + ([tile_16x64(hu), tile_16x64(hd)] if sh_inter else [])
+        hsh = [tiles[2].ctypes.data, hsu.ctypes.data, tiles[3].ctypes.data, hsd.ctypes.data] if sh_inter else [None] * 4
+        hb = NH.MoeBiases(*[v.ctypes.data if v is not None else None for v in b])
+        hout = np.zeros((tokens, hidden), np.uint16)
+        NH.call("nh_moe_layer_w8a8_host", x.ctypes.data, NH.BF16, rw.ctypes.data, rb.ctypes.data, tokens, hidden,
+                inter, experts, top_k, 0, ctypes.c_float(1.0), tiles[0].ctypes.data, su.ctypes.data,
+                tiles[1].ctypes.data, sd.ctypes.data, sh_inter, *hsh, hb, hout.ctypes.data, NH.BF16)
+        assert np.array_equal(hout, got)
+
+
+def test_moe_shared_intermediate_reported_ahead_of_the_routed_experts(ctx):
+    """The shared expert's overflowing intermediate is reported as
+    "shared_intermediate" (its own [tokens][shared_inter] index), ahead of an
+    overflow in the routed experts' intermediate, as MoeLayer::forward_into
+    meets the shared expert first (moe.rs:197-219); a routed overflow alone is
+    "intermediate"."""
+    tokens, hidden, inter, experts, top_k, sh_inter = 64, 2688, 1856, 128, 6, 3712
+    note(f"moe shared-intermediate non-finite t={tokens} si={sh_inter}")
+    x, logits, up, su, down, sd = moe_case(tokens, hidden, inter, experts, top_k)
+    _, hu, hsu = quantized_weights(sh_inter, hidden, seed=30)
+    _, hd, hsd = quantized_weights(hidden, sh_inter, seed=31)
+    b_up = np.zeros((experts, inter), np.float32)
+    b_up[:, 7] = 3e38  # every routed row overflows at column 7
+    b_sh = np.zeros(sh_inter, np.float32)
+    b_sh[100] = 3e38   # every shared row overflows at column 100
+    lib = NH.lib()
+    ws_bytes = lib.nh_moe_forward_shared_w8a8_workspace_size(tokens, hidden, inter, experts, top_k, sh_inter)
+    ws = ctx.empty(ws_bytes, np.uint8)
+    dx, dl = ctx.upload(x), ctx.upload(logits)
+    dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
+    dsh = [ctx.upload(tile_16x64(hu)), ctx.upload(hsu), ctx.upload(tile_16x64(hd)), ctx.upload(hsd)]
+    dbu, dbs = ctx.upload(b_up), ctx.upload(b_sh)
+    word = ctx.upload(np.zeros(1, dtype=np.uint64))
+    out = ctx.empty((tokens, hidden), np.uint16)
+    for mb, want, index in ((NH.MoeBiases(dbu.ptr, None, dbs.ptr, None), b"shared_intermediate", 100),
+                            (NH.MoeBiases(dbu.ptr, None, None, None), b"intermediate", 7)):
+        NH.call("nh_moe_forward_shared_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts,
+                top_k, 1, 1.0, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, sh_inter, *[d.ptr for d in dsh], mb, out.ptr,
+                NH.BF16, ws.ptr, ws_bytes, word.ptr, None)
+        st, err = take_nonfinite(ctx, word)
+        assert st == NH.NON_FINITE_INPUT and err.argument == want and err.index == index
+        assert np.isinf(err.value) and err.value > 0
 
 
 def test_moe_layer_router_reads_bf16_rows_off_a_4_byte_boundary(ctx):
@@ -975,7 +1102,7 @@ def test_moe_layer_router_reads_bf16_rows_off_a_4_byte_boundary(ctx):
     dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
     out = ctx.empty((tokens, hidden), np.uint16)
     NH.call("nh_moe_layer_w8a8", ctx.handle, dx.ptr + 2, NH.BF16, drw.ptr, drb.ptr, tokens, hidden, inter, experts,
-            top_k, 0, 1.0, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, 0, None, None, None, None, out.ptr, NH.BF16, ws.ptr,
+            top_k, 0, 1.0, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, 0, None, None, None, None, None, out.ptr, NH.BF16, ws.ptr,
             ws_bytes, None, None)
     ctx.synchronize()
     wsh = ws.numpy()
@@ -988,14 +1115,14 @@ def test_moe_layer_rejects_before_the_device(ctx):
     err = NH.NhError()
     L = NH.lib()
     st = L.nh_moe_layer_w8a8(ctx.handle, None, NH.BF16, None, None, 0, 64, 32, 8, 3, 0, 1.0, None, None, None, None,
-                             0, None, None, None, None, None, NH.BF16, None, 0, None, None, ctypes.byref(err))
+                             0, None, None, None, None, None, None, NH.BF16, None, 0, None, None, ctypes.byref(err))
     assert st == NH.INVALID_ROW_COUNT
     st = L.nh_moe_layer_w8a8(ctx.handle, None, NH.BF16, None, None, 4, 64, 32, 8, 3, 0, 1.0, None, None, None, None,
-                             0, None, None, None, None, None, NH.BF16, None, 0, None, None, ctypes.byref(err))
+                             0, None, None, None, None, None, None, NH.BF16, None, 0, None, None, ctypes.byref(err))
     assert st == NH.INVALID_PARAMS
     ws_need = L.nh_moe_layer_w8a8_workspace_size(4, 64, 32, 8, 3, 0)
     st = L.nh_moe_layer_w8a8(ctx.handle, None, NH.BF16, ctypes.c_void_p(16), None, 4, 64, 32, 8, 3, 0, 1.0, None,
-                             None, None, None, 0, None, None, None, None, None, NH.BF16, None, 0, None, None,
+                             None, None, None, 0, None, None, None, None, None, None, NH.BF16, None, 0, None, None,
                              ctypes.byref(err))
     assert st == NH.LENGTH_MISMATCH and err.argument == b"workspace" and err.expected == ws_need
 
@@ -1081,6 +1208,41 @@ def test_linear_nonfinite_input_reported(ctx, m, n, k, dtype):
     assert np.array_equal(word.numpy(), np.zeros(1, dtype=np.uint64))
 
 
+@pytest.mark.parametrize("m,n,k,bad", [(8, 1024, 8192, [(5, 7)]),            # groups of 4 rows: row 5 is group 2
+                                       (8, 1024, 8192, [(6, 3), (2, 100)]),  # the earlier group's index wins
+                                       (6, 1024, 4096, [(4, 9)])])          # the streaming unit (one launch)
+def test_linear_w4a8_nonfinite_input_reported(ctx, m, n, k, bad):
+    """nh_linear_w4a8 reports a non-finite activation at its index in the
+    whole input, also where it runs the rows in groups of 4 launches
+    (K = 8192): a NaN in row 5 is reported as 5 K + c, not as its index inside
+    the second group."""
+    note(f"linear_w4a8 nonfinite m={m} n={n} k={k} bad={bad}")
+    zp, scale = 8, 0.01
+    packed = np.random.default_rng(m).integers(0, 256, size=(k * n + 1) // 2, dtype=np.uint8)
+    xf = O.normal_f32(70 + m, m * k).reshape(m, k)
+    for r, c in bad:
+        xf[r, c] = np.nan
+    x = O.to_bf16(xf)
+    first = int(np.flatnonzero(~np.isfinite(O.bf16_to_f32(x)))[0])
+    assert first == min(r * k + c for r, c in bad)
+    tiled_len = NH.lib().nh_tiled_int4_weights_bytes(n, k)
+    dpk = ctx.upload(packed)
+    dt4 = ctx.empty(tiled_len, np.uint8)
+    NH.call("nh_tile_weights_int4", ctx.handle, dpk.ptr, packed.size, k, n, zp, dt4.ptr, tiled_len, None)
+    dx = ctx.upload(x)
+    word = ctx.upload(np.zeros(1, dtype=np.uint64))
+    ws_bytes = NH.lib().nh_linear_w4a8_workspace_size(m, n, k)
+    ws = ctx.empty(max(ws_bytes, 1), np.uint8)
+    out = ctx.empty((m, n), np.uint16)
+    NH.call("nh_linear_w4a8", ctx.handle, dx.ptr, NH.BF16, dt4.ptr, ctypes.c_float(scale), zp, None, m, n, k,
+            out.ptr, NH.BF16, ws.ptr, ws_bytes, word.ptr, None)
+    st, err = take_nonfinite(ctx, word)
+    assert st == NH.NON_FINITE_INPUT
+    assert err.argument == b"input" and err.index == first
+    assert np.isnan(err.value)
+    assert take_nonfinite(ctx, word)[0] == NH.OK  # cleared
+
+
 @pytest.mark.parametrize("m", [2, 6])
 def test_mlp_nonfinite_intermediate_and_input_reported(ctx, m):
     """The MLP's f32 intermediate overflows (ReLU^2 of a 3e38 biased output is
@@ -1151,14 +1313,14 @@ def test_moe_nonfinite_intermediate_reported(ctx):
     out = ctx.empty((tokens, hidden), np.uint16)
     word = ctx.upload(np.zeros(1, dtype=np.uint64))
     NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
-            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, word.ptr, None)
+            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, None, out.ptr, NH.BF16, ws.ptr, ws_bytes, word.ptr, None)
     st, err = take_nonfinite(ctx, word)
     assert st == NH.NON_FINITE_INPUT and err.argument == b"intermediate" and err.index == bad[0]
     assert np.isinf(err.value) and err.value > 0
     # the word was cleared: a clean call reports nothing
     dsu_clean = ctx.upload(su)
     NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
-            dup.ptr, dsu_clean.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, word.ptr, None)
+            dup.ptr, dsu_clean.ptr, ddown.ptr, dsd.ptr, None, out.ptr, NH.BF16, ws.ptr, ws_bytes, word.ptr, None)
     st, _ = take_nonfinite(ctx, word)
     assert st == NH.OK
 
@@ -1176,7 +1338,7 @@ def test_moe_nonfinite_input_reported(ctx):
     out = ctx.empty((tokens, hidden), np.uint16)
     word = ctx.upload(np.zeros(1, dtype=np.uint64))
     NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k, 1, 1.0,
-            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, word.ptr, None)
+            dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, None, out.ptr, NH.BF16, ws.ptr, ws_bytes, word.ptr, None)
     st, err = take_nonfinite(ctx, word)
     assert st == NH.NON_FINITE_INPUT and err.argument == b"input" and err.index == 5 * hidden + 10
     assert np.isinf(err.value) and err.value < 0

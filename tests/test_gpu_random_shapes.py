@@ -202,7 +202,7 @@ def test_moe_forward_random_shapes_bit_exact(ctx, case):
     dup, dsu, ddown, dsd = ctx.upload(tile_experts(up)), ctx.upload(su), ctx.upload(tile_experts(down)), ctx.upload(sd)
     out = ctx.empty((tokens, hidden), np.uint16)
     NH.call("nh_moe_forward_w8a8", ctx.handle, dx.ptr, NH.BF16, dl.ptr, tokens, hidden, inter, experts, top_k,
-            renorm, scaling, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, out.ptr, NH.BF16, ws.ptr, ws_bytes, None, None)
+            renorm, scaling, dup.ptr, dsu.ptr, ddown.ptr, dsd.ptr, None, out.ptr, NH.BF16, ws.ptr, ws_bytes, None, None)
     ctx.synchronize()
     import ctypes
     lay = (ctypes.c_size_t * 5)()

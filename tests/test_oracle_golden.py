@@ -176,6 +176,27 @@ def test_gemm_random_matches_float64_reference_rounded_once():
     assert not np.allclose(out.reshape(m, n), lhs.reshape(m, k) @ rhs.reshape(n, k).T, rtol=1e-3)
 
 
+def test_gemm_col_range_pieces_equal_the_whole_gemm():
+    """The multi-core CPU baseline's column ranges: disjoint ranges over the
+    one shared [K][N] matrix write exactly or_gemm_f32's output (every bit),
+    and a range writes nothing outside itself."""
+    rng = np.random.default_rng(11)
+    m, k, n = 3, 53, 41
+    lhs = rng.standard_normal(m * k).astype(np.float32)
+    rhs = rng.standard_normal(k * n).astype(np.float32)
+    st, whole, _ = O.gemm_f32(lhs, rhs, m, k, n)
+    assert st == O.OK
+    out = np.full(m * n, np.nan, dtype=np.float32)
+    for c0, c1 in ((0, 7), (7, 8), (8, 30), (30, 41)):
+        O.gemm_f32_col_range(lhs, rhs, m, k, n, c0, c1, out)
+    assert np.array_equal(out.view(np.uint32), whole.view(np.uint32))
+    part = np.full(m * n, np.nan, dtype=np.float32)
+    O.gemm_f32_col_range(lhs, rhs, m, k, n, 8, 30, part)
+    p = part.reshape(m, n)
+    assert np.all(np.isnan(p[:, :8])) and np.all(np.isnan(p[:, 30:]))
+    assert np.array_equal(p[:, 8:30].view(np.uint32), whole.reshape(m, n)[:, 8:30].view(np.uint32))
+
+
 # --------------------------------------------------------------------------
 # bf16 and the synthetic generator
 def test_bf16_round_to_nearest_even():
@@ -548,7 +569,8 @@ def test_moe_layer_reference_kats(kat):
     rb = np.array(kat["router_b"], dtype=np.float32)
     out = np.full(kat["rows"] * kat["hidden"], -1.0, dtype=np.float32)
     st = O.lib().or_moe_forward_dense(O.ptr(inp), kat["rows"], kat["hidden"], E, kat["top_k"], O.ptr(rw), O.ptr(rb),
-                                      1, up_ptrs, down_ptrs, 1, O.ptr(shared_up), O.ptr(shared_down), O.ptr(out))
+                                      1, up_ptrs, down_ptrs, None, None, 1, O.ptr(shared_up), O.ptr(shared_down),
+                                      None, None, O.ptr(out))
     assert st == O.OK
     assert_close(out, kat["out"], kat["tol"])
 
@@ -680,6 +702,150 @@ def test_moe_forward_shared_composes_its_parts():
     _, shared = O.mlp_w8a8(x, hu, hsu, hd, hsd)
     assert np.array_equal(out, O.moe_combine_shared(d, pos, w, shared, tokens, top_k, hidden, out_bf16=True))
     assert not np.array_equal(out, out0)  # the shared expert contributes
+
+
+# --------------------------------------------------------------------------
+# Expert biases.  The reference's experts and shared expert are MlpLayers
+# with optional biases (mlp.rs:79-96, moe.rs:60-65): up bias before ReLU^2,
+# down bias on the expert's own output, i.e. before the combine weight
+# (mlp.rs:201-208).  or_mlp_forward's bias handling is pinned by the
+# mlp.rs:347-363 KAT above.
+def _mlp_dense(x, wu, bu, wd, bd):
+    rows, hidden = x.shape
+    inter = wu.shape[1]
+    out = np.zeros(rows * hidden, dtype=np.float32)
+    st = O.lib().or_mlp_forward(O.ptr(np.ascontiguousarray(x)), rows, hidden, inter, O.ptr(wu), O.ptr(bu),
+                                O.ptr(wd), O.ptr(bd), O.ptr(out))
+    assert st == O.OK
+    return out.reshape(rows, hidden)
+
+
+def test_moe_dense_reference_with_biases_composes_its_biased_mlps():
+    """or_moe_forward_dense with expert and shared biases: output 0, + the
+    shared expert's biased MLP, + w * the selected expert's biased MLP in route
+    order (moe.rs:195-244), each MLP the KAT-pinned or_mlp_forward."""
+    rng = np.random.default_rng(21)
+    rows, hidden, inter, E, top_k, sh_inter = 3, 5, 4, 4, 2, 3
+    x = rng.standard_normal((rows, hidden)).astype(np.float32)
+    rw = rng.standard_normal((hidden, E)).astype(np.float32)
+    rb = rng.standard_normal(E).astype(np.float32)
+    wu = [rng.standard_normal((hidden, inter)).astype(np.float32) for _ in range(E)]
+    wd = [rng.standard_normal((inter, hidden)).astype(np.float32) for _ in range(E)]
+    bu = [rng.standard_normal(inter).astype(np.float32) for _ in range(E)]
+    bd = [rng.standard_normal(hidden).astype(np.float32) for _ in range(E)]
+    shu, shd = rng.standard_normal((hidden, sh_inter)).astype(np.float32), rng.standard_normal((sh_inter, hidden)).astype(np.float32)
+    shbu, shbd = rng.standard_normal(sh_inter).astype(np.float32), rng.standard_normal(hidden).astype(np.float32)
+    arr = lambda lst: (C.c_void_p * E)(*[O.ptr(a) for a in lst])
+    out = np.full(rows * hidden, -1.0, dtype=np.float32)
+    st = O.lib().or_moe_forward_dense(O.ptr(x), rows, hidden, E, top_k, O.ptr(rw), O.ptr(rb), inter, arr(wu), arr(wd),
+                                      arr(bu), arr(bd), sh_inter, O.ptr(shu), O.ptr(shd), O.ptr(shbu), O.ptr(shbd),
+                                      O.ptr(out))
+    assert st == O.OK
+    scores = np.zeros(rows * E, dtype=np.float32)
+    err = O.OrError()
+    assert O.lib().or_linear_project(O.ptr(x), x.size, rows, O.ptr(rw), hidden, E, O.ptr(rb), O.ptr(scores),
+                                     scores.size, C.byref(err)) == O.OK
+    st, idx, w, _ = O.route_sigmoid(scores, rows, E, top_k)
+    shared = _mlp_dense(x, shu, shbu, shd, shbd)
+    experts = [_mlp_dense(x, wu[e], bu[e], wd[e], bd[e]) for e in range(E)]
+    want = np.zeros((rows, hidden), dtype=np.float32)
+    for t in range(rows):
+        v = np.float32(0.0) + shared[t]
+        for j in range(top_k):
+            v = v + np.float32(w[t * top_k + j]) * experts[idx[t * top_k + j]][t]
+        want[t] = v
+    assert np.array_equal(out.reshape(rows, hidden), want)
+    # the biases matter: without them the layer differs
+    out0 = np.full(rows * hidden, -1.0, dtype=np.float32)
+    O.lib().or_moe_forward_dense(O.ptr(x), rows, hidden, E, top_k, O.ptr(rw), O.ptr(rb), inter, arr(wu), arr(wd),
+                                 None, None, sh_inter, O.ptr(shu), O.ptr(shd), None, None, O.ptr(out0))
+    assert not np.allclose(out0, out, atol=1e-3)
+
+
+def _biased_moe_case(seed=31):
+    tokens, hidden, inter, experts, top_k, sh_inter = 12, 64, 32, 8, 3, 48
+    rng = np.random.default_rng(seed)
+    x = O.to_bf16(O.normal_f32(1, tokens * hidden)).reshape(tokens, hidden)
+    logits = O.normal_f32(2, tokens * experts)
+    _, qu, su, _ = O.quantize_rows_f32(O.normal_f32(3, experts * inter * hidden, 0, 0.02).reshape(-1, hidden))
+    _, qd, sd, _ = O.quantize_rows_f32(O.normal_f32(4, experts * hidden * inter, 0, 0.02).reshape(-1, inter))
+    _, hu, hsu, _ = O.quantize_rows_f32(O.normal_f32(5, sh_inter * hidden, 0, 0.02).reshape(sh_inter, hidden))
+    _, hd, hsd, _ = O.quantize_rows_f32(O.normal_f32(6, hidden * sh_inter, 0, 0.02).reshape(hidden, sh_inter))
+    qu, su = qu.reshape(experts, inter, hidden), su.reshape(experts, inter)
+    qd, sd = qd.reshape(experts, hidden, inter), sd.reshape(experts, hidden)
+    biases = (rng.standard_normal((experts, inter)).astype(np.float32) * 0.5,
+              rng.standard_normal((experts, hidden)).astype(np.float32),
+              rng.standard_normal(sh_inter).astype(np.float32) * 0.5,
+              rng.standard_normal(hidden).astype(np.float32))
+    return tokens, hidden, top_k, x, logits, qu, su, qd, sd, hu, hsu, hd, hsd, biases
+
+
+def test_moe_int8_biases_compose_their_parts():
+    """or_moe_forward_shared_w8a8 with all four biases = R3 with the up bias
+    (before ReLU^2), Q2, R3 with the down bias, the biased shared MLP, the
+    combine; each bias changes the output."""
+    tokens, hidden, top_k, x, logits, qu, su, qd, sd, hu, hsu, hd, hsd, b = _biased_moe_case()
+    st, out, idx, w, offsets, perm, pos = O.moe_forward_shared_w8a8(x, logits, qu, su, qd, sd, top_k, hu, hsu, hd,
+                                                                    hsd, biases=b)
+    assert st == O.OK
+    _, xq, sx, _ = O.quantize_rows_bf16(x)
+    h = O.moe_grouped(xq, sx, True, top_k, offsets, perm, qu, su, relu2=True, bias=b[0])
+    _, hq, sh, _ = O.quantize_rows_f32(h)
+    d = O.moe_grouped(hq, sh, False, top_k, offsets, perm, qd, sd, relu2=False, bias=b[1])
+    _, shared = O.mlp_w8a8(x, hu, hsu, hd, hsd, b_up=b[2], b_down=b[3])
+    assert np.array_equal(out, O.moe_combine_shared(d, pos, w, shared, tokens, top_k, hidden, out_bf16=True))
+    for i in range(4):
+        partial = tuple(v if j != i else None for j, v in enumerate(b))
+        _, o2, *_ = O.moe_forward_shared_w8a8(x, logits, qu, su, qd, sd, top_k, hu, hsu, hd, hsd, biases=partial)
+        assert not np.array_equal(o2, out), f"bias {i} has no effect"
+
+
+def test_moe_int8_down_bias_is_weighted_by_the_route():
+    """Down bias on the expert's own output, before the combine weight
+    (mlp.rs:208 inside the expert, moe.rs:239-244 after it): with raw
+    (un-renormalised) sigmoid weights and a different constant bias per
+    expert, the layer moves by sum_j w_j b[e_j], not by the unweighted sum."""
+    tokens, hidden, top_k, x, logits, qu, su, qd, sd, hu, hsu, hd, hsd, _ = _biased_moe_case()
+    experts = qu.shape[0]
+    bd = np.repeat(np.arange(1, experts + 1, dtype=np.float32)[:, None] * 4.0, hidden, axis=1)
+    none = (None, None, None, None)
+    st, o0, idx, w, *_ = O.moe_forward_shared_w8a8(x, logits, qu, su, qd, sd, top_k, None, None, None, None,
+                                                   renormalize=False, biases=none)
+    st1, o1, *_ = O.moe_forward_shared_w8a8(x, logits, qu, su, qd, sd, top_k, None, None, None, None,
+                                           renormalize=False, biases=(None, bd, None, None))
+    assert st == st1 == O.OK
+    shift = O.bf16_to_f32(o1).astype(np.float64) - O.bf16_to_f32(o0).astype(np.float64)
+    want = np.array([sum(w[t * top_k + j] * bd[idx[t * top_k + j], 0] for j in range(top_k)) for t in range(tokens)])
+    unweighted = np.array([sum(bd[idx[t * top_k + j], 0] for j in range(top_k)) for t in range(tokens)])
+    tol = 2.0 ** -7 * (np.abs(O.bf16_to_f32(o1)).max() + 1.0)  # two bf16 roundings
+    assert np.all(np.abs(shift - want[:, None]) <= tol)
+    assert np.all(np.abs(shift - unweighted[:, None]).max(axis=1) > tol)
+
+
+def test_moe_int8_up_bias_lossless_equals_dense_reference():
+    """On lossless inputs (integer rows with absmax 127, scale 1) the up
+    projection with an integer bias is exactly relu2(x W_e^T + b_e) of the
+    reference's expert (mlp.rs:201-205): the bias before ReLU^2, per expert."""
+    rng = np.random.default_rng(5)
+    tokens, hidden, inter, experts, top_k = 4, 8, 4, 4, 2
+    x = rng.integers(-3, 4, size=(tokens, hidden)).astype(np.float32)
+    x[:, 0] = 127.0
+    wu = rng.integers(-2, 3, size=(experts, inter, hidden)).astype(np.float32)
+    wu[:, :, 1] = 127.0
+    bu = rng.integers(-300, 301, size=(experts, inter)).astype(np.float32)
+    logits = O.normal_f32(5, tokens * experts)
+    _, qu, su, _ = O.quantize_rows_f32(wu.reshape(-1, hidden))
+    _, xq, sx, _ = O.quantize_rows_bf16(O.to_bf16(x))
+    assert np.all(su == 1.0) and np.all(sx == 1.0)
+    st, idx, w, _ = O.route_sigmoid(logits, tokens, experts, top_k)
+    offsets, perm, pos = O.moe_permute(idx, tokens, top_k, experts)
+    h = O.moe_grouped(xq, sx, True, top_k, offsets, perm, qu.reshape(experts, inter, hidden),
+                      su.reshape(experts, inter), relu2=True, bias=bu)
+    for r in range(tokens * top_k):
+        t, e = r // top_k, idx[r]
+        dense = np.maximum(x[t] @ wu[e].T + bu[e], 0) ** 2
+        assert np.array_equal(h[pos[r]], dense.astype(np.float32))
+    assert np.any(h == 0.0)  # some biased outputs went negative before ReLU^2
 
 
 # --------------------------------------------------------------------------

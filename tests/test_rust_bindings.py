@@ -20,7 +20,8 @@ SYS_RS = os.path.join(ROOT, "rust", "nemotron-hip-sys", "src", "lib.rs")
 C_TO_RUST = {"size_t": "usize", "int": "c_int", "float": "f32", "uint32_t": "u32", "uint64_t": "u64",
              "int32_t": "i32", "int8_t": "i8", "uint8_t": "u8", "char": "c_char", "void": "c_void",
              "nh_context": "nh_context", "nh_stream": "nh_stream", "nh_dtype": "nh_dtype",
-             "nh_status": "nh_status", "nh_error": "nh_error", "nh_tensor_info": "nh_tensor_info"}
+             "nh_status": "nh_status", "nh_error": "nh_error", "nh_tensor_info": "nh_tensor_info",
+             "nh_moe_biases": "nh_moe_biases"}
 
 
 def c_source():
@@ -114,7 +115,7 @@ def test_status_and_dtype_constants_match_header_enums():
 
 
 RUST_CTYPES = {"u64": ctypes.c_uint64, "u32": ctypes.c_uint32, "f32": ctypes.c_float, "c_int": ctypes.c_int,
-               "c_char": ctypes.c_char, "*const c_char": ctypes.c_void_p}
+               "c_char": ctypes.c_char, "*const c_char": ctypes.c_void_p, "*const f32": ctypes.c_void_p}
 
 
 def rust_struct(name):
@@ -151,7 +152,7 @@ def gcc_layout(tmp_path, struct, fields):
     return vals[0], dict(zip([n for n, _ in fields], vals[1:]))
 
 
-@pytest.mark.parametrize("struct", ["nh_error", "nh_tensor_info"])
+@pytest.mark.parametrize("struct", ["nh_error", "nh_tensor_info", "nh_moe_biases"])
 def test_struct_layout_matches_c(tmp_path, struct):
     fields = rust_struct(struct)
     src = c_source()
