@@ -6,7 +6,8 @@ token and multiplied by int8 per-row weights, bf16 out, in ONE fused gfx950
 kernel.  value = algorithmic bytes of the unit / time per unit, in GB/s.
 Weights rotate through a >512 MiB pool so the 256 MiB Infinity Cache never
 serves them.  The same JSON line also reports the prefill GEMM (M=2048, TOPS
-vs the int8 MFMA peak), the other decode shapes, the W8A32 GEMV
+vs the int8 MFMA peak) and the M=2048 linear layer around it (per-token
+quantization of bf16 rows + the GEMM), the other decode shapes, the W8A32 GEMV
 the MoE layer and the 52-layer decode stack at batch 8, plus
 the reference's CPU path timed on this host.
 
@@ -640,7 +641,9 @@ def main():
         elif args.only == "gemm":
             for (mm, nn, kk) in [(2048, 4096, 4096), (2048, 21504, 4096), (2048, 4096, 21504)]:
                 t, t_rm = b.gemm(mm, nn, kk, 50, 5)
-                res[f"m{mm}_n{nn}_k{kk}"] = {"us": round(t * 1e3, 1), "row_major_a_us": round(t_rm * 1e3, 1)}
+                t_lin, _, _, _ = b.decode(mm, nn, kk, 50, 5)
+                res[f"m{mm}_n{nn}_k{kk}"] = {"us": round(t * 1e3, 1), "row_major_a_us": round(t_rm * 1e3, 1),
+                                             "linear_bf16_us": round(t_lin * 1e3, 1)}
         elif args.only == "w4a8":
             for (mm, nn, kk) in [(1, 16384, 4096), (4, 16384, 4096), (8, 16384, 4096), (16, 16384, 4096),
                                  (1, 4096, 8192)]:
@@ -715,6 +718,14 @@ def main():
                                           "row_major_a_us": round(t_rm * 1e3, 1),
                                           "row_major_a_TOPS": round(ops / (t_rm * 1e-3) / 1e12, 1)}
         extra["prefill_gemm"] = gemms
+        lins = {}
+        for (mm, nn, kk) in [(2048, 4096, 4096), (2048, 21504, 4096), (2048, 4096, 21504)]:
+            log(f"[bench] prefill linear layer m={mm} n={nn} k={kk} (bf16 rows quantized per token, then the GEMM)")
+            t, _, _, _ = b.decode(mm, nn, kk, 50, 5)
+            ops = 2.0 * mm * nn * kk
+            lins[f"m{mm}_n{nn}_k{kk}"] = {"us": round(t * 1e3, 1), "TOPS": round(ops / (t * 1e-3) / 1e12, 1),
+                                         "frac_int8_peak": round(ops / (t * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
+        extra["prefill_linear_bf16"] = lins
         log("[bench] decode stack, 52 layers, m=8")
         t, sbytes = b.decode_stack(20, 3)
         extra["decode_stack_52l_m8"] = {"ms": round(t, 4), "GBps": round(sbytes / (t * 1e-3) / 1e9, 1),

@@ -22,9 +22,11 @@
 //  * B: one 1 KiB tile of the tiled weights per instruction, already in the
 //    MFMA operand order (fragment reads are linear ds_read_b128).
 //
-// Epilogue: the per-token and per-channel scales (+bias, +ReLU^2) are applied
-// in registers, the tile is staged through LDS and every lane stores 16
-// contiguous bytes of an output row (f32 or bf16).
+// Epilogue: the MFMAs take the weight fragment first, so each lane's four
+// accumulators are four consecutive columns of one output row; the per-token
+// and per-channel scales (+bias, +ReLU^2) are applied in registers and the
+// lane stores the four results as one 8-byte (bf16) or 16-byte (f32) write,
+// with no LDS staging and no barrier after the main loop.
 //
 // blockIdx -> tile mapping is XCD-aware: workgroups are dealt round-robin to
 // the 8 XCDs, so consecutive ids are re-packed to make each XCD own a
@@ -36,64 +38,147 @@ using namespace nh;
 
 namespace {
 
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
-// Epilogue of a wave's WM x WN accumulator tile (16x16 fragments, lane l
-// holding D[4 (l / 16) + r][l % 16]): y = ((float)acc * sx[m]) * sw[n]
-// [+ bias][ReLU^2], staged through this wave's LDS area (64 rows at a time,
-// rows padded by 16 bytes) so that every lane stores 16 contiguous bytes of
-// an output row.  `et` holds 64 * (WN * 4 + 16) bytes.
-template <int WM, int WN, int FM, int FN>
-__device__ __forceinline__ void store_tile_through_lds(const GemmW8A8Args& a, const v4i (&acc)[FM][FN],
-                                                       const float (&sxv)[FM][4], const float (&swv)[FN], int8_t* et,
-                                                       int gm0, int gn0, int lane) {
+
+// The tile's per-token scales (BM floats), per-channel scales (BN) and, when
+// given, bias (BN) into LDS at `sc`, in that order: direct-to-LDS dword loads,
+// 64 values per instruction, issued by one wave ahead of its stage loads (so
+// its first stage wait covers them and the first barrier publishes them).
+// Rows and columns past the matrix read zeros (their results are not stored).
+template <int BM, int BN>
+__device__ __forceinline__ void issue_scale_loads(const GemmW8A8Args& a, int m0, int n0, int8_t* sc, int lane) {
+    const uint32_t l4 = (uint32_t)lane * 4u;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.sx + m0, (uint32_t)(a.M - m0) * 4u);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.sw + n0, (uint32_t)(a.N - n0) * 4u);
+#pragma unroll
+    for (int q = 0; q < BM / 64; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(sc + q * 256), 4, q * 256 + l4, 0, 0, 0);
+#pragma unroll
+    for (int q = 0; q < BN / 64; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t*)(sc + BM * 4 + q * 256), 4, q * 256 + l4, 0, 0, 0);
+    if (a.bias) {
+        const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.bias + n0, (uint32_t)(a.N - n0) * 4u);
+#pragma unroll
+        for (int q = 0; q < BN / 64; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(sc + (BM + BN) * 4 + q * 256), 4, q * 256 + l4,
+                                                     0, 0, 0);
+    }
+}
+
+// Epilogue of a wave's tile at local offset (lm0, ln0) of the workgroup tile
+// (global m0 + lm0, n0 + ln0), straight from the accumulators.  The MFMAs take
+// the weight fragment first, so lane l holds C[16 i + l % 16][16 j + 4 (l / 16)
+// + r] of the wave tile in register r of acc[i][j]: four consecutive columns
+// of one row.  y = ((float)acc * sx[m]) * sw[n] [+ bias][ReLU^2] (the numerics
+// spec's two RN multiplies), with the scales and bias read from the LDS copy
+// `sc` (issue_scale_loads); each lane stores its four results as 8 bytes
+// (bf16, two v_cvt_pk_bf16_f32) or 16 (f32).
+//
+// The epilogue is VALU-bound (a wave64 VALU instruction takes 4 cycles, and
+// all 256 x 128 results of a workgroup pass through the CU's four SIMDs at
+// once at the end of a single-round launch), so the usual case, a wave tile
+// inside the matrix with aligned rows, is straight code with no per-element
+// or per-fragment check; bias and ReLU^2 are uniform branches.  Wave tiles at
+// the matrix edge or with unaligned rows take a compact general loop that
+// stores element by element where four columns do not fit.
+template <int BM, int BN, int FM, int FN>
+__device__ __forceinline__ void store_tile(const GemmW8A8Args& a, v4i (&acc)[FM][FN], const int8_t* sc, int m0,
+                                           int n0, int lm0, int ln0, int lane) {
     const int M = a.M, N = a.N;
-    const int esz = a.out_dtype == DT_BF16 ? 2 : 4;
-    const int pitch = WN * esz + 16;
-    const int lpr = WN * esz / 16;           // lanes per output row
-    const int rows_per_pass = 64 / lpr;
-    const int rl = lane / lpr, cl = (lane % lpr) * 16;
     const int64_t ldo = a.ldo;
-    const bool full_n = gn0 + WN <= N && ((ldo * esz) & 15) == 0;
-    constexpr int kPassFrags = 4;            // 64 rows = 4 fragment rows per pass
-    float bnv[FN];
+    const int c4 = 4 * (lane >> 4);
+    const bool bf = a.out_dtype == DT_BF16;
+    const bool has_bias = a.bias != nullptr, has_relu2 = a.relu2 != 0;
+    const int esz = bf ? 2 : 4;
+    const bool aligned = ((((uint64_t)a.out) | ((uint64_t)ldo * esz)) & (uint64_t)(4 * esz - 1)) == 0;
+    const float* sx = (const float*)sc;
+    const float* sw = sx + BM;
+    const float* sb = sw + BN;
+    if (aligned && n0 + ln0 + FN * 16 <= N && m0 + lm0 + FM * 16 <= M) {
+        int8_t* base = (int8_t*)a.out + ((int64_t)(m0 + lm0 + (lane & 15)) * ldo + n0 + ln0 + c4) * esz;
 #pragma unroll
-    for (int j = 0; j < FN; ++j) bnv[j] = a.bias ? a.bias[min(gn0 + j * 16 + (lane & 15), N - 1)] : 0.0f;
+        for (int i = 0; i < FM; ++i) {
+            const float sxm = sx[lm0 + i * 16 + (lane & 15)];
+            int8_t* row = base + (int64_t)i * 16 * ldo * esz;
 #pragma unroll
-    for (int i0 = 0; i0 < FM; i0 += kPassFrags) {
+            for (int j = 0; j < FN; ++j) {
+                const int ln = ln0 + j * 16 + c4;
+                const v4f w = *(const v4f*)(sw + ln);
+                float y[4];
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int nl = j * 16 + (lane & 15);
+                for (int r = 0; r < 4; ++r) y[r] = epilogue_w8a8(acc[i][j][r], sxm, w[r]);
+                if (has_bias) {
+                    const v4f b = *(const v4f*)(sb + ln);
 #pragma unroll
-            for (int i = i0; i < i0 + kPassFrags && i < FM; ++i)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float y = epilogue_w8a8(acc[i][j][r], sxv[i][r], swv[j]);
-                    if (a.bias) y = y + bnv[j];
-                    if (a.relu2) y = relu2(y);
-                    const int ml = (i - i0) * 16 + 4 * (lane >> 4) + r;
-                    if (esz == 2)
-                        *(uint16_t*)(et + ml * pitch + nl * 2) = f32_to_bf16(y);
-                    else
-                        *(float*)(et + ml * pitch + nl * 4) = y;
+                    for (int r = 0; r < 4; ++r) y[r] = y[r] + b[r];
                 }
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
-        const int prow = min(WM - i0 * 16, 64);
-        for (int ml = rl; ml < prow; ml += rows_per_pass) {
-            const int m = gm0 + i0 * 16 + ml;
-            if (m >= M) break;
-            const v4i v = *(const v4i*)(et + ml * pitch + cl);
-            int8_t* dst = (int8_t*)a.out + ((int64_t)m * ldo + gn0) * esz + cl;
-            if (full_n) {
-                *(v4i*)dst = v;
-            } else {
-                const int valid = (N - gn0) * esz - cl;
+                if (has_relu2) {
 #pragma unroll
-                for (int e = 0; e < 16; ++e)
-                    if (e < valid) dst[e] = (int8_t)(v[e >> 2] >> (8 * (e & 3)));
+                    for (int r = 0; r < 4; ++r) y[r] = relu2(y[r]);
+                }
+                if (bf)
+                    *(v2u*)(row + j * 32) = v2u{f32x2_to_bf16x2(y[0], y[1]), f32x2_to_bf16x2(y[2], y[3])};
+                else
+                    *(v4f*)(row + j * 64) = v4f{y[0], y[1], y[2], y[3]};
             }
         }
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next pass overwrites
+        return;
+    }
+    // General form: fragments through loops that are not unrolled, each
+    // iteration taking the first fragment and shifting the others up.
+#pragma unroll 1
+    for (int i = 0; i < FM; ++i) {
+        v4i cur[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) cur[j] = acc[0][j];
+#pragma unroll
+        for (int k = 0; k + 1 < FM; ++k)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[k][j] = acc[k + 1][j];
+        const int lm = lm0 + i * 16 + (lane & 15);
+        const int m = m0 + lm;
+        if (m >= M) break;  // rows grow with i
+        const float sxm = sx[lm];
+        int8_t* row = (int8_t*)a.out + (int64_t)m * ldo * esz;
+#pragma unroll 1
+        for (int j = 0; j < FN; ++j) {
+            const v4i q = cur[0];
+#pragma unroll
+            for (int k = 0; k + 1 < FN; ++k) cur[k] = cur[k + 1];
+            const int ln = ln0 + j * 16 + c4;
+            const int c = n0 + ln;
+            const v4f w = *(const v4f*)(sw + ln);
+            const v4f b = has_bias ? *(const v4f*)(sb + ln) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            float y[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = epilogue_w8a8(q[r], sxm, w[r]);
+                if (has_bias) v = v + b[r];
+                y[r] = has_relu2 ? relu2(v) : v;
+            }
+            if (aligned && c + 3 < N) {
+                if (bf)
+                    *(v2u*)(row + (int64_t)c * 2) = v2u{f32x2_to_bf16x2(y[0], y[1]), f32x2_to_bf16x2(y[2], y[3])};
+                else
+                    *(v4f*)(row + (int64_t)c * 4) = v4f{y[0], y[1], y[2], y[3]};
+            } else {
+                float y0 = y[0], y1 = y[1], y2 = y[2], y3 = y[3];
+#pragma unroll 1
+                for (int r = 0; r < 4; ++r) {
+                    if (c + r < N) {
+                        if (bf)
+                            ((uint16_t*)row)[c + r] = f32_to_bf16(y0);
+                        else
+                            ((float*)row)[c + r] = y0;
+                    }
+                    y0 = y1;
+                    y1 = y2;
+                    y2 = y3;
+                }
+            }
+        }
     }
 }
 
@@ -128,13 +213,6 @@ __device__ __forceinline__ void gemm_tile(const GemmW8A8Args& a, int8_t* smem) {
     const __amdgpu_buffer_rsrc_t rb =
         make_rsrc(a.wq + (int64_t)nt0 * KT * 1024, (uint32_t)min(TB, ntiles - nt0) * (uint32_t)KT * 1024u);
 
-    float swv[FN], sxv[FM][4];
-#pragma unroll
-    for (int j = 0; j < FN; ++j) swv[j] = a.sw[min(n0 + wn * WN + j * 16 + (lane & 15), N - 1)];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sxv[i][r] = a.sx[min(m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r, M - 1)];
 
     // A: instruction q covers local rows 8q .. 8q + 7; lane l -> row 8q + l / 8,
     // LDS slot l % 8, global chunk c = slot ^ (row % 8) ^ ((row / 8) % 2)
@@ -178,6 +256,7 @@ __device__ __forceinline__ void gemm_tile(const GemmW8A8Args& a, int8_t* smem) {
         for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
     const int ns = (KT + 1) / 2;
+    if (wave == 0) issue_scale_loads<BM, BN>(a, m0, n0, smem + S * kStage, lane);
 #pragma unroll
     for (int s0 = 0; s0 < S - 1; ++s0)
         if (s0 < ns) issue(s0, s0);
@@ -197,13 +276,11 @@ __device__ __forceinline__ void gemm_tile(const GemmW8A8Args& a, int8_t* smem) {
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
         }
     }
 
-    lds_barrier();
-    store_tile_through_lds<WM, WN, FM, FN>(a, acc, sxv, swv, smem + wave * (64 * (WN * 4 + 16)), m0 + wm * WM,
-                                            n0 + wn * WN, lane);
+    store_tile<BM, BN, FM, FN>(a, acc, smem + S * kStage, m0, n0, wm * WM, wn * WN, lane);
 }
 
 
@@ -223,17 +300,18 @@ __device__ __forceinline__ void gemm_tile(const GemmW8A8Args& a, int8_t* smem) {
 // by the row quantizer), every A load one contiguous KiB; otherwise
 // row-major A through the swizzled 8-row x 128-byte loads of gemm_tile.
 // Tiled A measured 1.66 vs 1.40 POPS at (2048, 21504, 4096).
-template <int BM, int BN, int WGM, int WGN, int S, int NL, bool ATILED>
+template <int BM, int BN, int WGM, int WGN, int S, int NL, bool ATILED, int KS = 2>
 __device__ __forceinline__ void gemm_ws(const GemmW8A8Args& a, int8_t* smem) {
+    static_assert(KS == 2 || (KS == 1 && ATILED), "row-major A loads cover 128 bytes of K per stage");
     constexpr int NC = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int FM = WM / 16, FN = WN / 16;
     constexpr int TA = BM / 16, TB = BN / 16;
-    constexpr int IA = ATILED ? 2 * TA : BM / 8;  // A load instructions per 128-byte stage
-    constexpr int IB = 2 * TB;
+    constexpr int IA = ATILED ? KS * TA : BM / 8;  // A load instructions per stage of KS K tiles
+    constexpr int IB = KS * TB;
     constexpr int LPW = (IA + IB) / NL;
     static_assert((IA + IB) % NL == 0, "stage loads must split evenly over the loader waves");
-    constexpr int kA = BM * 128;
+    constexpr int kA = BM * 64 * KS;
     constexpr int kStage = kA + IB * 1024;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -243,7 +321,7 @@ __device__ __forceinline__ void gemm_ws(const GemmW8A8Args& a, int8_t* smem) {
     if ((nblk & 7) == 0) b = (b & 7) * (nblk >> 3) + (b >> 3);
     const int tm_idx = b % a.tiles_m, tn_idx = b / a.tiles_m;
     const int m0 = tm_idx * BM, n0 = tn_idx * BN;
-    const int ns = (KT + 1) / 2;
+    const int ns = (KT + KS - 1) / KS;
 
     if (wave >= NC) {  // ---- loader wave
         const int mt0 = m0 / 16, mtiles = (M + 15) / 16;
@@ -256,6 +334,7 @@ __device__ __forceinline__ void gemm_ws(const GemmW8A8Args& a, int8_t* smem) {
         const uint32_t l16 = (uint32_t)lane * 16u;
         const int a_r = lane >> 3, a_s = lane & 7;
         const int lw = wave - NC;
+        if (lw == 0) issue_scale_loads<BM, BN>(a, m0, n0, smem + S * kStage, lane);
         auto issue = [&](int st, int slot) {
 #pragma unroll
             for (int i = 0; i < LPW; ++i) {
@@ -263,7 +342,7 @@ __device__ __forceinline__ void gemm_ws(const GemmW8A8Args& a, int8_t* smem) {
                 lds_void_t* dst = (lds_void_t*)(smem + slot * kStage + q * 1024);
                 if (q < IA) {
                     if constexpr (ATILED) {  // K tile q / TA of the stage, M tile q % TA
-                        const int kt = st * 2 + q / TA;
+                        const int kt = st * KS + q / TA;
                         const uint32_t off = (uint32_t)((q % TA) * KT + kt) * 1024u + l16;
                         __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, dst, 16, kt < KT ? off : (uint32_t)kOutOfRange,
                                                                  0, 0, 0);
@@ -276,7 +355,7 @@ __device__ __forceinline__ void gemm_ws(const GemmW8A8Args& a, int8_t* smem) {
                     }
                 } else {  // K tile u / TB of the stage, N tile u % TB
                     const int u = q - IA;
-                    const int kt = st * 2 + u / TB;
+                    const int kt = st * KS + u / TB;
                     const uint32_t off = (uint32_t)((u % TB) * KT + kt) * 1024u + l16;
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, dst, 16, kt < KT ? off : (uint32_t)kOutOfRange, 0, 0,
                                                              2);
@@ -291,25 +370,17 @@ __device__ __forceinline__ void gemm_ws(const GemmW8A8Args& a, int8_t* smem) {
             lds_barrier();
             if (st + S - 1 < ns) issue(st + S - 1, (st + S - 1) % S);
         }
-        lds_barrier();  // the compute waves' last reads are done before the epilogue reuses the LDS
         return;
     }
 
     // ---- compute wave
     const int wm = wave / WGN, wn = wave % WGN;
-    float swv[FN], sxv[FM][4];
-#pragma unroll
-    for (int j = 0; j < FN; ++j) swv[j] = a.sw[min(n0 + wn * WN + j * 16 + (lane & 15), N - 1)];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sxv[i][r] = a.sx[min(m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r, M - 1)];
     // A fragment (M fragment i, K step w) read offsets within a stage
-    int a_off[FM][2];
+    int a_off[FM][KS];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int w = 0; w < 2; ++w) {
+        for (int w = 0; w < KS; ++w) {
             if constexpr (ATILED) {
                 a_off[i][w] = (w * TA + wm * FM + i) * 1024 + lane * 16;
             } else {
@@ -326,7 +397,7 @@ __device__ __forceinline__ void gemm_ws(const GemmW8A8Args& a, int8_t* smem) {
         lds_barrier();
         const int8_t* sb = smem + (st % S) * kStage;
 #pragma unroll
-        for (int w = 0; w < 2; ++w) {
+        for (int w = 0; w < KS; ++w) {
             v4i af[FM], bf[FN];
 #pragma unroll
             for (int i = 0; i < FM; ++i) af[i] = *(const v4i*)(sb + a_off[i][w]);
@@ -336,12 +407,10 @@ __device__ __forceinline__ void gemm_ws(const GemmW8A8Args& a, int8_t* smem) {
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
         }
     }
-    lds_barrier();
-    store_tile_through_lds<WM, WN, FM, FN>(a, acc, sxv, swv, smem + wave * (64 * (WN * 4 + 16)), m0 + wm * WM,
-                                            n0 + wn * WN, lane);
+    store_tile<BM, BN, FM, FN>(a, acc, smem + S * kStage, m0, n0, wm * WM, wn * WN, lane);
 }
 
 }  // namespace

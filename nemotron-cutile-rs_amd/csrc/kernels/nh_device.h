@@ -126,6 +126,17 @@ __device__ __forceinline__ void report_nonfinite(uint64_t* word, int stage, int6
 
 typedef unsigned short nh_u16x2 __attribute__((ext_vector_type(2)));
 
+// Two f32 values to bf16 in one v_cvt_pk_bf16_f32 (gfx950), lo in the low
+// half.  Bit-identical to f32_to_bf16 (round to nearest even, a NaN kept
+// with its quiet bit set) on all 2^32 inputs, checked exhaustively on the
+// device.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+    typedef __bf16 nh_bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float nh_f32x2 __attribute__((ext_vector_type(2)));
+    const nh_f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, nh_bf16x2));
+}
+
 // Largest bf16 magnitude of the 8 values of one 16-byte load, as its 15-bit
 // pattern (sign cleared).  Magnitude bit patterns order like the values, and
 // infinities and NaNs (0x7f80 and above) order above every finite value, so

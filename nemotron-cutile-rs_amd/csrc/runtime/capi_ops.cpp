@@ -104,14 +104,12 @@ bool plan_stream(const nh_context* ctx, size_t m, size_t n, size_t k, DecodePlan
     return true;
 }
 
-// Dynamic LDS of the GEMM kernels: a ring of `stages` stages (BM rows x 128
-// bytes of A plus 2 * BN/16 weight tiles of 1 KiB), or the epilogue staging
-// of `waves` waves (64 rows x (wave tile width * 4 + 16) bytes each),
-// whichever is larger.
-size_t gemm_lds_bytes(int bm, int bn, int stages, int waves, int wave_n) {
-    const size_t ring = (size_t)stages * ((size_t)bm * 128 + 2 * (size_t)(bn / 16) * 1024);
-    const size_t epi = (size_t)waves * 64 * ((size_t)wave_n * 4 + 16);
-    return ring > epi ? ring : epi;
+// Dynamic LDS of the GEMM kernels: a ring of `stages` stages of `ks` K tiles
+// (BM rows x 64 ks bytes of A plus ks * BN/16 weight tiles of 1 KiB), then
+// the tile's scales and bias (BM + 2 BN floats) for the epilogue.
+size_t gemm_lds_bytes(int bm, int bn, int stages, int ks = 2) {
+    const size_t ring = (size_t)stages * ((size_t)bm * 64 * ks + (size_t)ks * (size_t)(bn / 16) * 1024);
+    return ring + (size_t)(bm + 2 * bn) * 4;
 }
 
 nh_status check_dtype(nh_dtype d, nh_error* err) {
@@ -240,14 +238,14 @@ nh_status launch_gemm(nh_context* ctx, const int8_t* xq, const float* sx, const 
     struct Cfg {
         KernelId id;
         int bm, bn, threads;
-        size_t lds;  // max(ring of stages, epilogue staging of the compute waves)
+        size_t lds;  // ring of stages + the tile's scales and bias
     };
-    const Cfg big = {a_tiled ? K_GEMM_TA_256 : K_GEMM_W8A8, 256, 128, 1024, gemm_lds_bytes(256, 128, 3, 8, 64)};
-    const Cfg small = a_tiled ? Cfg{K_GEMM_TA_128, 128, 128, 512, gemm_lds_bytes(128, 128, 3, 4, 64)}
-                              : Cfg{K_GEMM_W8A8_128, 128, 128, 256, gemm_lds_bytes(128, 128, 3, 4, 64)};
+    const Cfg big = {a_tiled ? K_GEMM_TA_256 : K_GEMM_W8A8, 256, 128, 1024, gemm_lds_bytes(256, 128, 3)};
+    const Cfg small = a_tiled ? Cfg{K_GEMM_TA_128, 128, 128, 512, gemm_lds_bytes(128, 128, 3)}
+                              : Cfg{K_GEMM_W8A8_128, 128, 128, 256, gemm_lds_bytes(128, 128, 3)};
     auto tiles = [&](const Cfg& c) { return (int64_t)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn); };
-    const Cfg tiny = {K_GEMM_TA_64, 64, 128, 384, gemm_lds_bytes(64, 128, 3, 4, 64)};
-    const Cfg tiny2 = {K_GEMM_TA_6464, 64, 64, 384, gemm_lds_bytes(64, 64, 3, 4, 32)};
+    const Cfg tiny = {K_GEMM_TA_64, 64, 128, 384, gemm_lds_bytes(64, 128, 3)};
+    const Cfg tiny2 = {K_GEMM_TA_6464, 64, 64, 384, gemm_lds_bytes(64, 64, 3)};
     const Cfg* cfg = nullptr;
     if (a_tiled) {
         for (const Cfg* c : {&big, &small, &tiny, &tiny2})
