@@ -521,17 +521,29 @@ int nh_supports_gemm_f32(size_t m, size_t k, size_t n) {
     return m > 0 && k > 0 && n > 0 && m <= INT32_MAX && k <= INT32_MAX && n <= INT32_MAX && (m + 63) / 64 <= 65535;
 }
 
-// The exact f32 product's two tilings: 64 x 64 outputs per workgroup (16 per
-// lane) while those tiles fill every CU, else 4 rows x 64 columns (one output
-// per lane), so a narrow output such as the MoE router's 128 experts still
-// spreads its sequential-k chains over the chip.
+// The exact f32 product's two kernels: 64 x 64 outputs per workgroup (16 per
+// lane, f64 FMAs) while those tiles fill every CU, else 16 x 16 outputs per
+// workgroup on the f64 matrix cores (v_mfma_f64_4x4x4f64 chains), so a narrow
+// output such as the MoE router's 128 experts still spreads its k-ordered
+// chains over the chip (512 x 2688 x 128: 24.1 us against 52.3 us for one
+// output per lane on f64 FMAs; 2048 x 4096 x 128: 80 against 180 us;
+// 512 x 4096 x 4096 stays on the 64 x 64 tiles: 531 us against 628 on the
+// matrix cores).
 static nh_status launch_gemm_f32(nh_context* ctx, const GemmF32Args& a, nh_stream stream, nh_error* err) {
     const int64_t big = ((a.M + 63) / 64) * ((a.N + 63) / 64);
     if (big >= ctx->cu_count)
         return launch(ctx, K_GEMM_F32, (unsigned)((a.N + 63) / 64), 256, 0, stream, a, err,
                       (unsigned)((a.M + 63) / 64));
-    return launch(ctx, K_GEMM_F32_SMALL, (unsigned)((a.N + 63) / 64), 256, 0, stream, a, err,
-                  (unsigned)((a.M + 3) / 4));
+    // fewer than cu_count 64 x 64 tiles: at most 16 x cu_count 16 x 16 tiles;
+    // its buffer loads take 32-bit byte offsets into either operand
+    const uint64_t lhs_bytes = (uint64_t)a.M * (uint64_t)a.K * (a.lhs_bf16 ? 2u : 4u);
+    const uint64_t rhs_bytes = (uint64_t)a.K * (uint64_t)a.N * 4u;
+    if (lhs_bytes >= 0x7ffffff0u || rhs_bytes >= 0x7ffffff0u)  // the kernels' out-of-range offset
+        return launch(ctx, K_GEMM_F32, (unsigned)((a.N + 63) / 64), 256, 0, stream, a, err,
+                      (unsigned)((a.M + 63) / 64));
+    const bool vec = aligned16(a.lhs) && aligned16(a.rhs) && a.K % (a.lhs_bf16 ? 8 : 4) == 0 && a.N % 4 == 0;
+    const KernelId id = !vec ? K_GEMM_F32_MFMA_ANY : a.lhs_bf16 ? K_GEMM_F32_MFMA_BF16 : K_GEMM_F32_MFMA;
+    return launch(ctx, id, (unsigned)(((a.M + 15) / 16) * ((a.N + 15) / 16)), 256, 0, stream, a, err);
 }
 
 nh_status nh_gemm_f32(nh_context* ctx, const float* lhs, size_t lhs_len, const float* rhs, size_t rhs_len, size_t m,

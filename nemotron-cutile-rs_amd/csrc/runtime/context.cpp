@@ -58,7 +58,9 @@ const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
     "nh_gemm_w8a8_ta_64x128_kernel",     // K_GEMM_TA_64
     "nh_linear_decode_stream_w4_m16_kernel",  // K_LINEAR_DECODE_STREAM_W4_M16
     "nh_gemm_w8a8_ta_64x64_kernel",      // K_GEMM_TA_6464
-    "nh_gemm_f32_small_kernel",          // K_GEMM_F32_SMALL
+    "nh_gemm_f32_mfma_kernel",           // K_GEMM_F32_MFMA
+    "nh_gemm_f32_mfma_bf16_kernel",      // K_GEMM_F32_MFMA_BF16
+    "nh_gemm_f32_mfma_any_kernel",       // K_GEMM_F32_MFMA_ANY
 };
 
 void clear_error(nh_error* err) {

@@ -60,7 +60,9 @@ enum KernelId : int {
     K_GEMM_TA_64,             // G3, 64 x 128 tiles, tiled A
     K_LINEAR_DECODE_STREAM_W4_M16,  // W4A8 streaming decode unit, 9..16 rows
     K_GEMM_TA_6464,           // G3, 64 x 64 tiles, tiled A
-    K_GEMM_F32_SMALL,         // G0d, 16 x 16 outputs per workgroup
+    K_GEMM_F32_MFMA,          // G0d on the f64 matrix cores, 16 x 16 outputs per workgroup, f32 lhs
+    K_GEMM_F32_MFMA_BF16,     // ... bf16 lhs
+    K_GEMM_F32_MFMA_ANY,      // ... any alignment, K and N
     K_COUNT
 };
 

@@ -230,9 +230,11 @@ _GEMM_KATS = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file_
                          + [dict(m=m, k=k, n=n, lhs="rand") for (m, k, n) in
                             [(1, 4096, 4096), (37, 100, 65), (130, 257, 71), (64, 16, 64), (3, 1, 5),
                              (512, 2688, 128), (5, 130, 200), (1024, 300, 1030),
-                             # one-output-per-lane path: a single whole 64-k block, a whole
-                             # block and a 1-k tail, two whole blocks, a tail-only K
-                             (1, 64, 1), (3, 65, 130), (4, 128, 64), (7, 63, 70),
+                             # the f64 matrix-core path (16 x 16 tiles, 128-k chunks): one
+                             # partial chunk, a chunk and a 1-k tail, whole chunks, K below
+                             # one 4-k step, partial tiles both ways, two chunks and a tail
+                             (1, 64, 1), (3, 65, 130), (4, 128, 64), (7, 63, 70), (17, 3, 17),
+                             (33, 257, 31), (2, 384, 3),
                              # 64 x 64 tiles filling 256 CUs with a 1-k tail step
                              (1024, 33, 1024)]],
                          ids=lambda c: f"{c['m']}x{c['k']}x{c['n']}")
