@@ -135,7 +135,7 @@ __device__ __forceinline__ void route_quantize(const RouteArgs& a, int token, in
     q.q_act = a.xq_tiles;
     q.act_p = 16;
     v4i xv[8];
-    const int64_t row = quantize_row_wave_load<DT, 8>(q, xv);  // the token's row (the kernel checked it)
+    const int64_t row = quantize_row_wave_load<DT, 8>(q, xv, token);  // the token's row (the kernel checked it)
     route_token<S>(a, token, lane, sc, tbl);
     quantize_row_wave_finish<DT, 8>(q, xv, row);
 }
@@ -161,7 +161,10 @@ __device__ __forceinline__ void route_kernel_body(const RouteArgs& a, int token,
 
 extern "C" __global__ __launch_bounds__(256) void nh_moe_route_sigmoid_kernel(RouteArgs a) {
     const int lane = threadIdx.x & 63;
-    const int token = blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    // with the token codes going to A tiles, a tile line's 8 tokens to one XCD (xcd_line_order)
+    const int per = (int)(blockDim.x >> 6);
+    const int blk = a.x && a.xq_tiles ? (int)xcd_line_order(blockIdx.x, (a.tokens + per - 1) / per, per) : (int)blockIdx.x;
+    const int token = blk * per + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     if (token >= a.tokens) return;
     if (a.experts <= 128)
         route_kernel_body<2>(a, token, lane);
