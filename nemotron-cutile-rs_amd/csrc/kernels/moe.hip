@@ -54,8 +54,7 @@ constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
 // code of 16).
 // expf's 2^(i/32) table held across the wave (lane l: entry l % 32, f64
 // bits) and read through the LDS crossbar: no memory load inside the
-// sigmoid, so the routing never waits on the load counter behind the row's
-// loads in flight.
+// sigmoid.
 struct LaneExp2Table {
     uint32_t lo, hi;
     __device__ double operator()(uint32_t i) const {
@@ -114,15 +113,23 @@ __device__ __forceinline__ void route_token(const RouteArgs& a, int token, int l
     }
 }
 
-// With x, the same wave also quantizes the token's row (Q2, the wave form
-// of nh_quantize_rows_i8: same codes and scales), token-major: the up
-// projection gathers its A rows through the permutation.  The token's scores
-// are loaded first and the row's loads right after them; the routing waits
-// for the scores only, so it runs while the row is in flight, and the
-// quantization follows.
-template <int S, int DT>
-__device__ __forceinline__ void route_quantize(const RouteArgs& a, int token, int lane, const float (&sc)[S],
-                                               const LaneExp2Table& tbl) {
+template <int S>
+__device__ __forceinline__ void route_kernel_body(const RouteArgs& a, int token, int lane) {
+    const LaneExp2Table tbl = lane_exp2_table(lane);
+    // the token's scores through a buffer resource (experts past E read 0)
+    float sc[S];
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.scores + (int64_t)token * a.experts, (uint32_t)a.experts * 4u);
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+        sc[i] = f32_from_bits(__builtin_amdgcn_raw_buffer_load_b32(rs, (lane + 64 * i) * 4, 0, 0));
+    route_token<S>(a, token, lane, sc, tbl);
+}
+
+// The quantization half of a token when another wave routes it: Q2 of the
+// token's row, token-major (and into the A tiles when given): the codes and
+// scales of nh_quantize_rows_i8.
+template <int DT>
+__device__ __forceinline__ void quantize_token(const RouteArgs& a, int token) {
     QuantizeRowsArgs q{};
     q.x = a.x;
     q.q = a.xq;
@@ -135,37 +142,30 @@ __device__ __forceinline__ void route_quantize(const RouteArgs& a, int token, in
     q.q_act = a.xq_tiles;
     q.act_p = 16;
     v4i xv[8];
-    const int64_t row = quantize_row_wave_load<DT, 8>(q, xv, token);  // the token's row (the kernel checked it)
-    route_token<S>(a, token, lane, sc, tbl);
+    const int64_t row = quantize_row_wave_load<DT, 8>(q, xv, token);
     quantize_row_wave_finish<DT, 8>(q, xv, row);
 }
 
-template <int S>
-__device__ __forceinline__ void route_kernel_body(const RouteArgs& a, int token, int lane) {
-    const LaneExp2Table tbl = lane_exp2_table(lane);
-    // the token's scores through a buffer resource (experts past E read 0):
-    // every load unconditional, so the wait for them leaves the row's loads
-    // in flight
-    float sc[S];
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.scores + (int64_t)token * a.experts, (uint32_t)a.experts * 4u);
-#pragma unroll
-    for (int i = 0; i < S; ++i)
-        sc[i] = f32_from_bits(__builtin_amdgcn_raw_buffer_load_b32(rs, (lane + 64 * i) * 4, 0, 0));
-    if (!a.x)
-        route_token<S>(a, token, lane, sc, tbl);
-    else if (a.x_dtype == DT_BF16)
-        route_quantize<S, DT_BF16>(a, token, lane, sc, tbl);
-    else
-        route_quantize<S, DT_F32>(a, token, lane, sc, tbl);
-}
-
+// Without x: one wave per token routes it (4 tokens per workgroup).  With x
+// (the MoE layer): 2 tokens per workgroup, waves 0 and 1 route them while
+// waves 2 and 3 quantize their rows, so the two chains run side by side
+// instead of one after the other in one wave (the 512-token MoE layer:
+// 272.1-272.4 against 273.2-273.3 us).
 extern "C" __global__ __launch_bounds__(256) void nh_moe_route_sigmoid_kernel(RouteArgs a) {
     const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int per = a.x ? 2 : 4;  // tokens per workgroup
     // with the token codes going to A tiles, a tile line's 8 tokens to one XCD (xcd_line_order)
-    const int per = (int)(blockDim.x >> 6);
     const int blk = a.x && a.xq_tiles ? (int)xcd_line_order(blockIdx.x, (a.tokens + per - 1) / per, per) : (int)blockIdx.x;
-    const int token = blk * per + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int token = blk * per + (wave & (per - 1));
     if (token >= a.tokens) return;
+    if (a.x && wave >= 2) {
+        if (a.x_dtype == DT_BF16)
+            quantize_token<DT_BF16>(a, token);
+        else
+            quantize_token<DT_F32>(a, token);
+        return;
+    }
     if (a.experts <= 128)
         route_kernel_body<2>(a, token, lane);
     else if (a.experts <= 256)

@@ -1081,7 +1081,8 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
         RouteArgs ra{logits, idx, wts, (int)tokens, (int)experts, (int)top_k, renormalize ? 1 : 0, scaling, 0,
                      x, xq, sx, nonfinite, x_dtype == NH_BF16 ? DT_BF16 : DT_F32, (int)hidden,
                      shared_tiles ? (int8_t*)lin_sh : nullptr};
-        if ((st = launch(ctx, K_ROUTE_SIGMOID, (unsigned)((tokens + 3) / 4), 256, 0, stream, ra, err))) return st;
+        // two tokens per workgroup: two waves route, two quantize
+        if ((st = launch(ctx, K_ROUTE_SIGMOID, (unsigned)((tokens + 1) / 2), 256, 0, stream, ra, err))) return st;
     } else if ((st = nh_moe_route_sigmoid_topk(ctx, logits, tokens, experts, top_k, renormalize, scaling, idx, wts,
                                                stream, err))) {
         return st;
