@@ -528,8 +528,11 @@ __device__ __forceinline__ void expert_stream(const ExpertGemmArgs& a, v4i (&b0)
         if (j < nj && c == nch - 1 && n < N) {
             const float swn = sws[n - t_begin * 16];
             const float bn = a.bias ? sbs[n - t_begin * 16] : 0.0f;
-            // one per-lane base (row p0 + 4 g, column n); rows rb * 16 + r are uniform offsets
-            float* ob = a.out + (int64_t)(p0 + 4 * g) * N + n;
+            // one per-lane base (row p0 + 4 g, column n); rows rb * 16 + r are
+            // uniform offsets (row-major, or 16 floats apart in column-tile order)
+            float* ob = a.out_tcol ? a.out + ((int64_t)(n >> 4) * a.out_rows + p0 + 4 * g) * 16 + (n & 15)
+                                   : a.out + (int64_t)(p0 + 4 * g) * N + n;
+            const int rs = a.out_tcol ? 16 : N;
             const int rows = seg1 - p0 - 4 * g;  // rows of this lane's group in the pass
 #pragma unroll
             for (int rb = 0; rb < NRB; ++rb)
@@ -539,7 +542,7 @@ __device__ __forceinline__ void expert_stream(const ExpertGemmArgs& a, v4i (&b0)
                         float y = epilogue_w8a8(acc[rb][r], sas[rb * 16 + 4 * g + r], swn);
                         if (a.bias) y = y + bn;
                         if (a.relu2) y = relu2(y);
-                        ob[(rb * 16 + r) * N] = y;
+                        ob[(rb * 16 + r) * rs] = y;
                         if constexpr (MODE == kExpertOmax) {
                             if (is_finite_f32(y))
                                 rmax[rb][r] = fmaxf(rmax[rb][r], fabsf(y));
@@ -716,16 +719,20 @@ __device__ __forceinline__ void expert_gemm(const ExpertGemmArgs& a, int8_t* lds
                 hm[rb][1] = ok ? a.ahmax[row * 2 + 1] : 0u;
             }
             v4i hv[2][4][4];
+            // the lane's 16 values of a K tile: 64 contiguous bytes in either order
+            auto piece = [&](int row, int t) -> uint32_t {
+                return a.ah_tcol ? ((uint32_t)(t * 4 + g) * (uint32_t)a.a_rows + (uint32_t)row) * 64u
+                                 : ((uint32_t)row * (uint32_t)K + (uint32_t)(t * 64 + g * 16)) * 4u;
+            };
             auto issue = [&](int rb, v4i (&buf)[4][4]) {
                 const int row = p0 + rb * 16 + r16;
                 const bool ok = rb < nrb && row < seg1;
-                const uint32_t rowoff = (uint32_t)row * (uint32_t)K * 4u;
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const int t = wave + u * NW;
-                        const uint32_t off = rowoff + (uint32_t)((t * 64 + g * 16 + 4 * q) * 4);
+                        const uint32_t off = piece(row, t) + (uint32_t)(16 * q);
                         buf[u][q] = buffer_load16(hr, ok && t < kt ? (int)off : kOutOfRange);
                     }
             };

@@ -282,6 +282,14 @@ struct ExpertGemmArgs {
     int32_t nonfinite_stage;
     int32_t gather_div;      // with perm: A row (and sa entry) of slot s = perm[s] / gather_div
     const int32_t* perm;     // [R] or null (A rows in slot order)
+    // Column-tile order of the MoE layer's f32 intermediate h (the up
+    // projection's output, the down projection's A): element (row, col) of
+    // an [R][C] matrix at ((col / 16) * R + row) * 16 + col % 16 (C % 16 ==
+    // 0), so a 16-row block of one 16-column tile is one contiguous KiB and
+    // the four stores of a lane's rows fill whole lines back to back.
+    int32_t out_tcol;        // out in column-tile order with out_rows rows
+    int32_t out_rows;
+    int32_t ah_tcol;         // ah in column-tile order with a_rows rows
 };
 
 // R4: scatter-combine.

@@ -985,7 +985,7 @@ static void moe_layout(size_t T, size_t H, size_t I, size_t E, size_t k, size_t 
     off[4] = take(R * 4);        // pos
     off[5] = take(R * H);        // xq, one row per route in expert order
     off[6] = take(R * 4);        // sx
-    off[7] = take(R * I * 4);    // up output (f32, ReLU^2 applied)
+    off[7] = take(R * I * 4);    // up output (f32, ReLU^2 applied; column-tile order on the fused path)
     off[8] = take(R * I);        // requantized up output
     off[9] = take(R * 4);        // its scales
     off[10] = take(R * H * 4);   // down output per slot (f32)
@@ -1124,6 +1124,8 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
         up.sw = s_up;
         up.bias = b.up;
         up.out = h;
+        up.out_tcol = 1;  // h in column-tile order: 270.4-270.8 us per layer against 271.9-272.4 row-major
+        up.out_rows = (int)R;
         up.a_rows = route_q ? (int)tokens : (int)R;
         up.relu2 = 1;
         up.omax = hmax;
@@ -1132,6 +1134,7 @@ static nh_status moe_forward(nh_context* ctx, const void* x, nh_dtype x_dtype, c
         if ((st = launch_expert_gemm(ctx, K_EXPERT_GEMM_OMAX, up, experts, inter, hidden, stream, err))) return st;
         ExpertGemmArgs down{};
         down.ah = h;
+        down.ah_tcol = 1;
         down.ahmax = hmax;
         down.offsets = offsets;
         down.w = w_down;
