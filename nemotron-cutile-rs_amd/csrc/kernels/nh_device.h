@@ -56,6 +56,17 @@ __device__ __forceinline__ int block_min_i32(int v, int* red) {
     return r;
 }
 
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, int* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = wave_max_dpp_u32(v);
+    if (lane == 0) red[wave] = (int)v;
+    __syncthreads();
+    uint32_t r = (uint32_t)red[0];
+    for (int i = 1; i < nw; ++i) r = max(r, (uint32_t)red[i]);
+    __syncthreads();
+    return r;
+}
+
 __device__ __forceinline__ float load_as_f32(const void* p, int64_t i, int dtype) {
     if (dtype == DT_BF16) return bf16_to_f32(((const uint16_t*)p)[i]);
     return ((const float*)p)[i];
@@ -148,6 +159,30 @@ __device__ __forceinline__ uint32_t bf16x8_absmax_bits(v4i xv) {
     for (int j = 1; j < 4; ++j)
         m = __builtin_elementwise_max(m, __builtin_bit_cast(nh_u16x2, (uint32_t)xv[j] & 0x7fff7fffu));
     return max((uint32_t)m.x, (uint32_t)m.y);
+}
+
+// The row quantizers' absmax scan on bit patterns (as above): one integer
+// maximum per value (per bf16 pair) gives a row's absmax, or says that the
+// row holds a non-finite value, and only then does a quantizer run the exact
+// scan that finds the first one.
+constexpr uint32_t kInfBits = 0x7f800000u;
+
+// m: two running maxima of bf16 patterns; the pair updated with 8 values.
+__device__ __forceinline__ uint32_t absbits_bf16x8(v4i v, uint32_t m) {
+    nh_u16x2 acc = __builtin_bit_cast(nh_u16x2, m);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        acc = __builtin_elementwise_max(acc, __builtin_bit_cast(nh_u16x2, (uint32_t)v[j] & 0x7fff7fffu));
+    return __builtin_bit_cast(uint32_t, acc);
+}
+
+// The f32 pattern of the larger bf16 pattern of a pair.
+__device__ __forceinline__ uint32_t absbits_pair_f32(uint32_t m) { return max(m & 0xffffu, m >> 16) << 16; }
+
+__device__ __forceinline__ uint32_t absbits_f32x4(v4i v, uint32_t m) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = max(m, (uint32_t)v[j] & 0x7fffffffu);
+    return m;
 }
 
 // Index (0..7) of the first non-finite value of a 16-byte bf16 load, or 8.

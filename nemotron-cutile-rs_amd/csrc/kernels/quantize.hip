@@ -84,17 +84,29 @@ __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, floa
             else amax = fmaxf(amax, fabsf(f[j]));
         }
     };
+    // the row: registers, then the tail 4 loads at a time (past the row: zeros)
+    auto walk = [&](auto&& f) {
 #pragma unroll
-    for (int r = 0; r < kRegChunks; ++r) scan(xv[r], threadIdx.x + r * T);  // chunks past the row read zeros
-    for (int c0 = threadIdx.x + kRegChunks * T; c0 < chunks; c0 += 4 * T) {  // the tail, 4 loads at a time
-        v4i t[4];
+        for (int r = 0; r < kRegChunks; ++r) f(xv[r], threadIdx.x + r * T);
+        for (int c0 = threadIdx.x + kRegChunks * T; c0 < chunks; c0 += 4 * T) {
+            v4i t[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) t[j] = buffer_load16(xr, c0 + j * T < chunks ? (c0 + j * T) * 16 : kOutOfRange);
+            for (int j = 0; j < 4; ++j)
+                t[j] = buffer_load16(xr, c0 + j * T < chunks ? (c0 + j * T) * 16 : kOutOfRange);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) scan(t[j], c0 + j * T);  // past the row: zeros
+            for (int j = 0; j < 4; ++j) f(t[j], c0 + j * T);
+        }
+    };
+    uint32_t m = 0;
+    walk([&](v4i v, int) { m = DT == DT_BF16 ? absbits_bf16x8(v, m) : absbits_f32x4(v, m); });
+    m = block_max_u32(DT == DT_BF16 ? absbits_pair_f32(m) : m, redi);
+    if (m < kInfBits) {
+        amax = f32_from_bits(m);
+    } else {  // a non-finite value: the exact scan names the first one
+        walk(scan);
+        amax = block_max(amax, redf);
+        bad = block_min_i32(bad, redi);
     }
-    amax = block_max(amax, redf);
-    bad = block_min_i32(bad, redi);
     const float s = scale_from_amax(amax);
     if (threadIdx.x == 0) {
         a.scales[row] = s;
@@ -133,6 +145,44 @@ __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, floa
     }
 }
 
+// A wave's row of up to 64 * NCH chunks held in registers (chunks past the
+// row read zeros): its finite absmax and first non-finite column (INT_MAX if
+// none), wave-uniform.  The bit-pattern scan first; the exact scan only for a
+// row with a non-finite value.
+template <int DT, int NCH>
+__device__ __forceinline__ void row_absmax(const v4i (&xv)[NCH], float& amax, int& bad) {
+    constexpr int VPC = DT == DT_BF16 ? 8 : 4;
+    const int lane = threadIdx.x & 63;
+    uint32_t m = 0;
+#pragma unroll
+    for (int r = 0; r < NCH; ++r) m = DT == DT_BF16 ? absbits_bf16x8(xv[r], m) : absbits_f32x4(xv[r], m);
+    m = wave_max_u32(DT == DT_BF16 ? absbits_pair_f32(m) : m);
+    bad = 0x7fffffff;
+    if (m < kInfBits) {
+        amax = f32_from_bits(m);
+        return;
+    }
+    amax = 0.0f;
+#pragma unroll
+    for (int r = 0; r < NCH; ++r) {
+        float f[VPC];
+        if constexpr (DT == DT_BF16) {
+            unpack_bf16x8(xv[r], f);
+        } else {
+#pragma unroll
+            for (int j = 0; j < VPC; ++j) f[j] = f32_from_bits((uint32_t)xv[r][j]);
+        }
+        const int c = lane + r * 64;
+#pragma unroll
+        for (int j = 0; j < VPC; ++j) {
+            if (!is_finite_f32(f[j])) bad = min(bad, c * VPC + j);
+            else amax = fmaxf(amax, fabsf(f[j]));
+        }
+    }
+    amax = wave_max(amax);
+    bad = wave_min_i32(bad);
+}
+
 // Wave path: one wave per row, 4 rows per 256-thread workgroup.  A row of up
 // to 64 * NCH 16-byte chunks stays in registers between the absmax and the
 // code pass, and both reductions are wave reductions: no barrier, and a row
@@ -167,26 +217,9 @@ __device__ __forceinline__ void quantize_row_wave_finish(const QuantizeRowsArgs&
     const int64_t src = a.gather ? a.gather[row] / a.gather_div : row;
     const int cols = (int)a.cols;
     const int chunks = cols / VPC;
-    float amax = 0.0f;
-    int bad = 0x7fffffff;
-#pragma unroll
-    for (int r = 0; r < NCH; ++r) {
-        float f[VPC];
-        if constexpr (DT == DT_BF16) {
-            unpack_bf16x8(xv[r], f);
-        } else {
-#pragma unroll
-            for (int j = 0; j < VPC; ++j) f[j] = f32_from_bits((uint32_t)xv[r][j]);
-        }
-        const int c = lane + r * 64;  // chunks past the row read zeros
-#pragma unroll
-        for (int j = 0; j < VPC; ++j) {
-            if (!is_finite_f32(f[j])) bad = min(bad, c * VPC + j);
-            else amax = fmaxf(amax, fabsf(f[j]));
-        }
-    }
-    amax = wave_max(amax);
-    bad = wave_min_i32(bad);
+    float amax;
+    int bad;
+    row_absmax<DT, NCH>(xv, amax, bad);
     const float s = scale_from_amax(amax);
     if (lane == 0) {
         a.scales[row] = s;
@@ -225,6 +258,70 @@ __device__ __forceinline__ void quantize_row_wave(const QuantizeRowsArgs& a) {
     const int64_t row = quantize_row_wave_load<DT, NCH>(
         a, xv, (int64_t)blockIdx.x * (blockDim.x >> 6) + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)));
     if (row >= 0) quantize_row_wave_finish<DT, NCH>(a, xv, row);
+}
+
+// Rows into the GEMM's A tiles (act_p = 16) for many rows: 8 rows per
+// workgroup, one wave per row.  A tile's 128-byte line holds 16 codes of each
+// of 8 consecutive rows, so the workgroup owns whole lines: every wave
+// quantizes its row into an LDS image of the 8 rows' lines, then the
+// workgroup writes the lines with 16-byte stores, 8 lanes per line and 8
+// lines per wave instruction (a wave storing its own row's 8-byte pieces puts
+// 32 lines' pieces in every store instruction).  The row (up to 64 * NCH
+// 16-byte chunks) stays in registers between the absmax and the code pass.
+// Same codes, scales and non-finite reports as the vector path.
+template <int DT, int NCH>
+__device__ __forceinline__ void quantize_tiles(const QuantizeRowsArgs& a, int8_t* lds) {
+    constexpr int VPC = DT == DT_BF16 ? 8 : 4;  // values (and codes) per 16-byte chunk
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t r0 = (int64_t)blockIdx.x * 8;
+    const int64_t row = r0 + w;
+    const int cols = (int)a.cols, chunks = cols / VPC;
+    const int kt = (cols + 63) / 64;
+    if (row < a.rows) {  // wave-uniform; a row past the matrix leaves its LDS slots to padding rows
+        const uint32_t rbytes = (uint32_t)cols * (DT == DT_BF16 ? 2u : 4u);
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc((const char*)a.x + row * (int64_t)rbytes, rbytes);
+        v4i xv[NCH];
+#pragma unroll
+        for (int r = 0; r < NCH; ++r) {
+            const int c = lane + r * 64;
+            xv[r] = buffer_load16(xr, c < chunks ? c * 16 : kOutOfRange);
+        }
+        float amax;
+        int bad;
+        row_absmax<DT, NCH>(xv, amax, bad);
+        const float s = scale_from_amax(amax);
+        if (lane == 0) {
+            a.scales[row] = s;
+            if (a.row_status) a.row_status[row] = bad == 0x7fffffff ? -1 : bad;
+            report_row(a, row, bad);
+        }
+        const float rcp = s > 0.0f ? 1.0f / s : 0.0f;
+        const bool pow2 = scale_is_pow2(s);
+#pragma unroll
+        for (int r = 0; r < NCH; ++r) {
+            const int c = lane + r * 64;
+            if (c >= chunks) break;
+            const int k = c * VPC;
+            const int off = (((k >> 6) * 4 + ((k >> 4) & 3)) * 8 + w) * 16 + (k & 15);  // line (K tile, group)
+            if constexpr (DT == DT_BF16) {
+                uint32_t code[2];
+                quantize8_bf16(xv[r], s, rcp, pow2, code);
+                *(uint2*)(lds + off) = make_uint2(code[0], code[1]);
+                if (a.q) *(uint2*)(a.q + row * cols + k) = make_uint2(code[0], code[1]);
+            } else {
+                const uint32_t code = quantize4_f32(xv[r], s, rcp, pow2);
+                *(uint32_t*)(lds + off) = code;
+                if (a.q) *(uint32_t*)(a.q + row * cols + k) = code;
+            }
+        }
+    }
+    __syncthreads();
+    // line (K tile t, group g) of this 8-row half of a 16-row block
+    int8_t* dst = a.q_act + (r0 >> 4) * (int64_t)kt * 1024 + ((r0 >> 3) & 1) * 128;
+    const int p = (int)(threadIdx.x & 7) * 16;
+    for (int l = (int)(threadIdx.x >> 3); l < kt * 4; l += (int)(blockDim.x >> 3))
+        *(v4i*)(dst + (int64_t)(l >> 2) * 1024 + (l & 3) * 256 + p) = *(const v4i*)(lds + l * 128 + p);
 }
 
 // Scalar path (any alignment, any column count): pass 1 = absmax + first
@@ -359,6 +456,17 @@ extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_wave_kernel(Q
         quantize_row_wave<DT_BF16, 8>(a);
     else
         quantize_row_wave<DT_F32, 8>(a);
+}
+
+// Q2 into the GEMM's A tiles (act_p = 16, no gather) for rows of up to
+// 8 * 64 chunks (bf16 K <= 4096, f32 K <= 2048): grid = ceil(rows / 8), 512
+// threads, dynamic LDS 8 * 64 * KT bytes.
+extern "C" __global__ __launch_bounds__(512) void nh_quantize_tiles_kernel(QuantizeRowsArgs a) {
+    extern __shared__ __align__(16) int8_t lds[];
+    if (a.x_dtype == DT_BF16)
+        quantize_tiles<DT_BF16, 8>(a, lds);
+    else
+        quantize_tiles<DT_F32, 8>(a, lds);
 }
 
 // Diagnostic: one read of [src, src + bytes) in 16-byte non-temporal loads,

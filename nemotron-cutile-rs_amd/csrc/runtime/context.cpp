@@ -45,6 +45,7 @@ const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
     "nh_moe_expert_gemm_qa_kernel",      // K_EXPERT_GEMM_QA
     "nh_stream_read_kernel",             // K_STREAM_READ
     "nh_quantize_rows_wave_kernel",      // K_QUANTIZE_ROWS_WAVE
+    "nh_quantize_tiles_kernel",          // K_QUANTIZE_TILES
     "nh_quantize_rows_long_kernel",      // K_QUANTIZE_ROWS_LONG
     "nh_quantize_rows_pmax_kernel",      // K_QUANTIZE_ROWS_PMAX
     "nh_expand_int4_tiles_kernel",       // K_EXPAND_INT4

@@ -47,6 +47,7 @@ enum KernelId : int {
     K_EXPERT_GEMM_QA,      // ... quantizing f32 A rows while staging them (MoE down projection)
     K_STREAM_READ,         // diagnostic read stream
     K_QUANTIZE_ROWS_WAVE,  // row quantizer, one wave per row
+    K_QUANTIZE_TILES,      // row quantizer into GEMM A tiles, 8 rows per workgroup
     K_QUANTIZE_ROWS_LONG,  // row quantizer, 1024 threads per row
     K_QUANTIZE_ROWS_PMAX,  // f32 rows with producer-reduced maxima, many workgroups per row
     K_EXPAND_INT4,         // tiled INT4 -> tiled int8 code - zp

@@ -1173,7 +1173,10 @@ def take_nonfinite(ctx, word):
                                          (8, 4096, 8192, "bf16"),    # streaming unit, 8 K tiles per wave
                                          (12, 1024, 4096, "bf16"),   # quantizer into activation tiles + GEMV
                                          (2, 1024, 4096, "f32"),     # f32 rows: the row quantizer
-                                         (40, 512, 1024, "bf16")])   # quantizer into A tiles + GEMM
+                                         (40, 512, 1024, "bf16"),    # quantizer into A tiles + GEMM
+                                         (41, 512, 1024, "f32"),     # the same, f32 rows, a partial 8-row group
+                                         (300, 256, 21504, "bf16"),  # long rows: a workgroup per row, re-read tail
+                                         (20, 256, 21504, "f32")])   # long rows: 1024 threads per row
 def test_linear_nonfinite_input_reported(ctx, m, n, k, dtype):
     """A NaN or infinity in x: nh_take_nonfinite returns NonFiniteInput with
     the oracle's first non-finite index (row-major) and value, then the word is
