@@ -193,8 +193,12 @@ nh_status nh_take_nonfinite(nh_context *ctx, uint64_t *nonfinite, nh_stream stre
  * with int8 per-row weights (linear.rs:283-342): dynamic per-token
  * quantization of x (f32 or bf16) then G1/G3 + bias.  For bf16 x with
  * k <= 8192 and m <= 4 (m <= 8 when k % 512 == 0) the quantization is fused
- * into the GEMV (one launch; the workspace is not touched); otherwise it
- * runs as its own launch into a workspace of
+ * into the GEMV (one launch; the workspace is not touched); other bf16 x
+ * with m <= 16 and k <= 8192 is one launch whose quantizer workgroups hand
+ * the codes to its GEMV workgroups through the workspace and a counter slot
+ * of the context (kHandoffSlots = 256 slots taken in turn: at most 256 such
+ * launches may be in flight at once on one context); otherwise the
+ * quantization runs as its own launch into a workspace of
  * nh_linear_w8a8_workspace_size(m, k) bytes, 16-byte aligned (for m <= 16
  * it holds the codes in the GEMV's operand order).  Pass that workspace on
  * every call.  xq_out/sx_out (optional) receive the quantized activations
@@ -499,6 +503,14 @@ nh_status nh_load_linear_i8(nh_context *ctx, const char *path, const char *codes
  * counterpart in the reference. */
 nh_status nh_stream_read(nh_context *ctx, const void *src, size_t bytes, int32_t *sink, nh_stream stream,
                          nh_error *err);
+
+/* The in-launch handoff of nh_linear_w8a8 at up to 16 bf16 rows (the row
+ * quantizer's workgroups hand the codes to the GEMV's workgroups inside one
+ * launch, through a counter slot of the context): synchronizes the device,
+ * then counts the slots whose wait ran out of polls (*timeouts) and the slots
+ * not back at zero (*busy).  Both are 0 unless a handoff launch misbehaved.
+ * No counterpart in the reference. */
+nh_status nh_handoff_status(nh_context *ctx, uint32_t *timeouts, uint32_t *busy, nh_error *err);
 
 /* ---- synthetic inputs (build-defined seeded generator; the reference has
  *      no RNG): splitmix64 -> Box-Muller (f64) -> f32 ------------------- */

@@ -178,6 +178,103 @@ __device__ __forceinline__ void gemv_w8a8(const GemvW8A8Args& a, v4i* red) {
     }
 }
 
+// The linear layer at M <= 16 bf16 rows as ONE launch (LinearHandoffArgs):
+// the row quantizer and the tiled-A GEMV of the two-launch path, with the
+// dependency between them kept inside the launch instead of at a kernel
+// boundary.  The GEMV workgroups issue their weight slab first (it does not
+// depend on the activations), then wait for the quantized rows, so the
+// weight stream overlaps the quantization and the second launch's start-up.
+// The handoff crosses XCDs, whose L2 caches are not coherent with each
+// other: the producers store the codes and scales with agent-scope (sc1)
+// writes and wait for them to complete before adding to the counter; the
+// consumers read the counter, the codes and the scales with agent-scope
+// (sc1) loads, which do not return stale L2 lines.  One lane of an extra
+// wave polls (s_sleep between polls, a bounded number of polls), so the
+// waves holding the weight slab never wait behind a poll; a bare s_barrier
+// then releases them.  Same codes, scales and outputs as the two launches.
+constexpr uint32_t kHandoffPolls = 1u << 22;
+
+__device__ __forceinline__ void handoff_consume(const LinearHandoffArgs& h, v4i* red) {
+    const GemvW8A8Args& a = h.g;
+    const int lane = threadIdx.x & 63, W = a.waves;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int M = a.M, N = a.N, kt = a.kt;
+    const int tile = (int)blockIdx.x - h.q.rows;
+    const int n = tile * 16 + r16;
+    v4i b[kSlab];
+    float swn = 0.0f, bn = 0.0f;
+    if (wave < W) {
+        const __amdgpu_buffer_rsrc_t wr = row_tile_rsrc(a.wq, tile, kt);
+        swn = n < N ? a.sw[n] : 0.0f;
+        bn = (a.bias && n < N) ? a.bias[n] : 0.0f;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < kSlab; ++s) b[s] = buffer_load16_stream(wr, (wave + s * W) * 1024 + lane * 16);
+        __builtin_amdgcn_sched_barrier(0);
+    } else if (lane == 0) {
+        uint32_t polls = 0;
+        bool ready;
+        while (!(ready = __hip_atomic_load(&h.slot[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= (uint32_t)M) &&
+               ++polls < kHandoffPolls)
+            __builtin_amdgcn_s_sleep(2);
+        if (!ready) __hip_atomic_store(&h.slot[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__hip_atomic_fetch_add(&h.slot[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            (uint32_t)h.consumers - 1) {  // the last workgroup past the wait: every row is in, reset the slot
+            __hip_atomic_store(&h.slot[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&h.slot[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    lds_barrier();  // the rows are in
+    v4i acc = {0, 0, 0, 0};
+    float sxl[4];
+    if (wave < W) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            sxl[r] = 4 * g + r < M ? f32_from_bits(__hip_atomic_load((const uint32_t*)&a.sx[4 * g + r], __ATOMIC_RELAXED,
+                                                                     __HIP_MEMORY_SCOPE_AGENT))
+                                   : 0.0f;
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xq, (uint32_t)M * (uint32_t)kt * 64u);
+        const bool xrow = r16 < M;
+        const int xlane = (g * M + r16) * 16;
+        v4i x[kSlab];
+#pragma unroll
+        for (int s = 0; s < kSlab; ++s) {
+            const int t = wave + s * W;
+            x[s] = __builtin_amdgcn_raw_buffer_load_b128(xr, (xrow && t < kt) ? xlane + t * 64 * M : kOutOfRange, 0,
+                                                         16 /* sc1 */);
+        }
+#pragma unroll
+        for (int s = 0; s < kSlab; ++s) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[s], b[s], acc, 0, 0, 0);
+        red[wave * 64 + lane] = acc;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        for (int w = 1; w < W; ++w) acc += red[w * 64 + lane];
+        if (n < N) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (4 * g + r < M)
+                    store_y(a.out, a.out_dtype, (int64_t)(4 * g + r) * N + n, acc[r], sxl[r], swn, a.bias, bn,
+                            a.relu2);
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(576) void nh_linear_handoff_kernel(LinearHandoffArgs h) {
+    __shared__ v4i red[8 * 64];
+    __shared__ float redf[16];
+    __shared__ int redi[16];
+    if ((int64_t)blockIdx.x < h.q.rows) {  // a quantizer workgroup: one row, then publish it
+        quantize_row_vec<DT_BF16, 2, true>(h.q, redf, redi);
+        wait_vmcnt_le(0);  // this wave's codes and scale have completed
+        lds_barrier();
+        if (threadIdx.x == 0) __hip_atomic_fetch_add(&h.slot[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    handoff_consume(h, red);
+}
+
 extern "C" __global__ __launch_bounds__(512) void nh_gemv_w8a8_kernel(GemvW8A8Args a) {
     __shared__ v4i red[8 * 64];
     gemv_w8a8<false>(a, red);

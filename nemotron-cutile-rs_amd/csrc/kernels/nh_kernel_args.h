@@ -106,6 +106,23 @@ struct GemvW8A8Args {
     int32_t relu2;        // ReLU^2 after the bias (the MLP up projection)
 };
 
+// Linear layer at M <= 16 rows in one launch with an in-launch handoff
+// (nh_linear_handoff_kernel): workgroups 0 .. M-1 quantize one bf16 row each
+// (q: act_p = M activation tiles, agent-scope stores), the other
+// ceil(N / 16) run the tiled-A GEMV (g: one slab per wave, K <= 8192) with
+// one extra wave that waits for the M rows.  `slot` is a zeroed counter
+// block of the context's ring: [0] rows published, [1] GEMV workgroups past
+// the wait (the last one zeroes [0] and [1] again), [2] set when a wait ran
+// out of polls (never expected: the quantizer workgroups are dispatched
+// first and wait for nothing).
+struct LinearHandoffArgs {
+    QuantizeRowsArgs q;
+    GemvW8A8Args g;
+    uint32_t* slot;
+    int32_t consumers;
+    int32_t pad_;
+};
+
 // Decode unit (M <= 16, K <= 8192, K % 512 == 0): per-token quantization
 // (Q2) of bf16 rows fused in front of G1.  A workgroup owns ntw 16-row N
 // tiles with `waves` waves each: blockDim = 64 * waves * ntw <= 1024 and

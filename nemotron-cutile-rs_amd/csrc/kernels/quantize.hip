@@ -52,7 +52,10 @@ __device__ __forceinline__ void report_row(const QuantizeRowsArgs& a, int64_t sr
 // Codes go to the row-major matrix and/or the A-operand tiles (act_p rows
 // per tile: the compact [KT][4][rows][16] of the M <= 16 GEMV, or 16, the
 // weights' tiled layout read by the GEMM).
-template <int DT, int kRegChunks>
+// COH: the scale and the activation-tile codes are stored as agent-scope
+// (sc1) writes, visible to other workgroups of the same launch once the
+// stores have completed (the producer half of nh_linear_handoff_kernel).
+template <int DT, int kRegChunks, bool COH = false>
 __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, float* redf, int* redi) {
     constexpr int VPC = DT == DT_BF16 ? 8 : 4;  // values per 16-byte chunk
     const int64_t row = tile_line_order(a, blockIdx.x, a.rows, 1);
@@ -109,7 +112,10 @@ __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, floa
     }
     const float s = scale_from_amax(amax);
     if (threadIdx.x == 0) {
-        a.scales[row] = s;
+        if constexpr (COH)
+            __hip_atomic_store((uint32_t*)&a.scales[row], f32_bits(s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            a.scales[row] = s;
         if (a.row_status) a.row_status[row] = bad == 0x7fffffff ? -1 : bad;
         report_row(a, src, bad);
     }
@@ -123,7 +129,13 @@ __device__ __forceinline__ void quantize_row_vec(const QuantizeRowsArgs& a, floa
             uint32_t code[2];
             quantize8_bf16(v, s, rcp, pow2, code);
             if (a.q) *(uint2*)(a.q + row * cols + k) = make_uint2(code[0], code[1]);
-            if (tile) *(uint2*)tile = make_uint2(code[0], code[1]);
+            if constexpr (COH) {
+                if (tile)
+                    __hip_atomic_store((uint64_t*)tile, ((uint64_t)code[1] << 32) | code[0], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            } else if (tile) {
+                *(uint2*)tile = make_uint2(code[0], code[1]);
+            }
         } else {
             const uint32_t code = quantize4_f32(v, s, rcp, pow2);
             if (a.q) *(uint32_t*)(a.q + row * cols + k) = code;

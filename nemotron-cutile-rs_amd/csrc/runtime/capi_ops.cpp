@@ -4,6 +4,7 @@
 #include <cstdint>
 #include <cmath>
 #include <cstring>
+#include <vector>
 
 #include "nh_runtime.h"
 
@@ -653,6 +654,32 @@ nh_status linear_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, const in
         if (!aligned16(workspace)) return set_error(err, NH_UNSUPPORTED, "workspace must be 16-byte aligned");
         int8_t* tiles = (int8_t*)workspace;
         float* sx = sx_out ? sx_out : (float*)((char*)workspace + align256(act_tiles_bytes(m, k)));
+        if (x_dtype == NH_BF16 && aligned16(x) && k % 8 == 0 && k <= 8192 && ((uintptr_t)xq_out & 7u) == 0) {
+            // one launch: the quantizer workgroups hand the rows to the GEMV
+            // workgroups inside it (M = 8, 8192 -> 4096: 13.57 against 13.96
+            // us in two launches; the 52-layer stack 1.733 against 1.760 ms)
+            LinearHandoffArgs h{};
+            h.q = QuantizeRowsArgs{x, xq_out, sx, nullptr, tiles, (int64_t)m, (int64_t)k, x_dtype, 1, (int)m, 1,
+                                   nullptr, nonfinite, nonfinite_stage, 0};
+            GemvW8A8Args& g = h.g;
+            g.xq = tiles;
+            g.sx = sx;
+            g.wq = wq;
+            g.sw = sw;
+            g.bias = bias;
+            g.out = out;
+            g.M = (int)m;
+            g.N = (int)n;
+            g.K = (int)k;
+            g.kt = (int)tiled_k_tiles(k);
+            g.waves = gemv_waves(g.kt);
+            g.out_dtype = out_dtype;
+            g.x_tiled = 1;
+            g.relu2 = relu2;
+            h.consumers = (int)((n + 15) / 16);
+            h.slot = ctx->handoff + (size_t)(ctx->handoff_next.fetch_add(1) % kHandoffSlots) * 16;
+            return launch(ctx, K_LINEAR_HANDOFF, (unsigned)(m + h.consumers), 64u * (g.waves + 1), 0, stream, h, err);
+        }
         if ((st = launch_quantize(ctx, x, x_dtype, m, k, xq_out, sx, nullptr, tiles, stream, err, 0, nullptr, 1,
                                   nonfinite, nonfinite_stage)))
             return st;
@@ -1258,6 +1285,23 @@ nh_status nh_moe_layer_w8a8(nh_context* ctx, const void* x, nh_dtype x_dtype, co
 // One read of bytes from src (device memory, 16-byte aligned, a multiple of
 // 16, < 2^31): 1024 workgroups of 256 threads, four 16-byte loads per thread
 // in flight.  sink: 256 device ints, normally never written.
+extern "C" nh_status nh_handoff_status(nh_context* ctx, uint32_t* timeouts, uint32_t* busy, nh_error* err) {
+    clear_error(err);
+    if (!timeouts || !busy) return set_error(err, NH_INVALID_PARAMS, "null output pointer");
+    nh_status st = bind_device(ctx, err);
+    if (st) return st;
+    std::vector<uint32_t> ring((size_t)kHandoffSlots * 16);
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(ring.data(), ctx->handoff, ring.size() * 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return device_error(err, e, "nh_handoff_status");
+    *timeouts = *busy = 0;
+    for (uint32_t i = 0; i < kHandoffSlots; ++i) {
+        *timeouts += ring[i * 16 + 2] != 0;
+        *busy += ring[i * 16] != 0 || ring[i * 16 + 1] != 0;
+    }
+    return NH_OK;
+}
+
 extern "C" nh_status nh_stream_read(nh_context* ctx, const void* src, size_t bytes, int32_t* sink, nh_stream stream,
                                     nh_error* err) {
     clear_error(err);

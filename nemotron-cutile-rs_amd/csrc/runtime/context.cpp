@@ -46,6 +46,7 @@ const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
     "nh_stream_read_kernel",             // K_STREAM_READ
     "nh_quantize_rows_wave_kernel",      // K_QUANTIZE_ROWS_WAVE
     "nh_quantize_tiles_kernel",          // K_QUANTIZE_TILES
+    "nh_linear_handoff_kernel",          // K_LINEAR_HANDOFF
     "nh_quantize_rows_long_kernel",      // K_QUANTIZE_ROWS_LONG
     "nh_quantize_rows_pmax_kernel",      // K_QUANTIZE_ROWS_PMAX
     "nh_expand_int4_tiles_kernel",       // K_EXPAND_INT4
@@ -169,6 +170,19 @@ nh_status nh_context_create(int device, const char* code_object_path, nh_context
             return device_error(err, e, "hipFuncGetAttribute");
         }
     }
+    // the handoff ring, zeroed before any launch can use it
+    void* ring = nullptr;
+    e = hipMalloc(&ring, (size_t)kHandoffSlots * 64);
+    if (e == hipSuccess) e = hipMemset(ring, 0, (size_t)kHandoffSlots * 64);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        if (ring) (void)hipFree(ring);
+        (void)hipModuleUnload(ctx->module);
+        delete ctx;
+        return device_error(err, e, "handoff counters");
+    }
+    ctx->handoff = (uint32_t*)ring;
+    ctx->handoff_next.store(0);
     *out = ctx;
     return NH_OK;
 }
@@ -178,6 +192,7 @@ void nh_context_destroy(nh_context* ctx) {
     int cur = -1;
     if (hipGetDevice(&cur) != hipSuccess) cur = -1;
     (void)hipSetDevice(ctx->device);
+    if (ctx->handoff) (void)hipFree(ctx->handoff);
     (void)hipModuleUnload(ctx->module);
     if (cur >= 0) (void)hipSetDevice(cur);
     delete ctx;

@@ -3,6 +3,7 @@
 #pragma once
 #include <hip/hip_runtime_api.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstddef>
 #include <cstdint>
@@ -48,6 +49,7 @@ enum KernelId : int {
     K_STREAM_READ,         // diagnostic read stream
     K_QUANTIZE_ROWS_WAVE,  // row quantizer, one wave per row
     K_QUANTIZE_TILES,      // row quantizer into GEMM A tiles, 8 rows per workgroup
+    K_LINEAR_HANDOFF,      // row quantizer + tiled-A GEMV in one launch (M <= 16)
     K_QUANTIZE_ROWS_LONG,  // row quantizer, 1024 threads per row
     K_QUANTIZE_ROWS_PMAX,  // f32 rows with producer-reduced maxima, many workgroups per row
     K_EXPAND_INT4,         // tiled INT4 -> tiled int8 code - zp
@@ -73,6 +75,11 @@ extern const char* const kKernelSymbols[K_COUNT];
 // uses as its workspace.
 constexpr size_t kScratchBytes = 64ull << 20;
 
+// Counter slots of the in-launch handoff ring (64 bytes each): two calls
+// that share a slot must not run at the same time, i.e. at most
+// kHandoffSlots handoff launches may be in flight at once on one context.
+constexpr uint32_t kHandoffSlots = 256;
+
 }  // namespace nh
 
 struct nh_context {
@@ -85,6 +92,11 @@ struct nh_context {
     size_t max_shared_per_block;
     void* scratch;             // this device's address of the static scratch, or null
     char scratch_error[128];   // why it is null
+    // counter slots of the in-launch handoff (nh_linear_handoff_kernel):
+    // kHandoffSlots blocks of 64 bytes, zeroed at creation; every launch
+    // leaves its slot zeroed again.  Calls take the slots in turn.
+    uint32_t* handoff;
+    std::atomic<uint32_t> handoff_next;
 };
 
 namespace nh {

@@ -148,6 +148,7 @@ _SIGNATURES = {
     "nh_moe_layer_w8a8_host": (ST, [P, C.c_int, P, P, SZ, SZ, SZ, SZ, SZ, C.c_int, C.c_float, P, P, P, P, SZ,
                                     P, P, P, P, MB, P, C.c_int, E]),
     "nh_stream_read": (ST, [P, P, SZ, P, P, E]),
+    "nh_handoff_status": (ST, [P, P, P, E]),
     "nh_tiled_int4_weights_bytes": (SZ, [SZ, SZ]),
     "nh_tile_weights_int4": (ST, [P, P, SZ, SZ, SZ, C.c_uint32, P, SZ, P, E]),
     "nh_tile_weights_int4_host": (ST, [P, SZ, SZ, SZ, C.c_uint32, P, SZ, E]),

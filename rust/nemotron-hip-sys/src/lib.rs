@@ -1191,6 +1191,18 @@ extern "C" {
         err: *mut nh_error,
     ) -> nh_status;
 
+    /// The in-launch handoff of `nh_linear_w8a8` at up to 16 bf16 rows (the row quantizer's
+    /// workgroups hand the codes to the GEMV's workgroups inside one launch, through a counter
+    /// slot of the context): synchronizes the device, then counts the slots whose wait ran out of
+    /// polls (`*timeouts`) and the slots not back at zero (`*busy`).  Both are 0 unless a handoff
+    /// launch misbehaved.  No counterpart in the reference.
+    pub fn nh_handoff_status(
+        ctx: *mut nh_context,
+        timeouts: *mut u32,
+        busy: *mut u32,
+        err: *mut nh_error,
+    ) -> nh_status;
+
     /// synthetic inputs (build-defined seeded generator; the reference has no RNG): splitmix64 ->
     /// Box-Muller (f64) -> f32
     pub fn nh_fill_normal_f32_host(seed: u64, mean: f32, stddev: f32, out: *mut f32, n: usize);

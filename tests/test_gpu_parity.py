@@ -409,6 +409,106 @@ def test_linear_decode_stack_attention_shapes(ctx, n, k, out_dtype, with_bias):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+# ---- the in-launch handoff (quantizer + tiled-A GEMV as one launch, M <= 16) ------
+def handoff_status(ctx):
+    timeouts, busy = ctypes.c_uint32(0), ctypes.c_uint32(0)
+    NH.call("nh_handoff_status", ctx.handle, ctypes.addressof(timeouts), ctypes.addressof(busy))
+    return timeouts.value, busy.value
+
+
+@pytest.mark.parametrize("m,n,k,out_dtype,with_bias", [(5, 100, 16, "f32", True), (9, 1000, 80, "bf16", False),
+                                                       (13, 4096, 528, "f32", False), (16, 4100, 8192, "bf16", True),
+                                                       (11, 16, 4112, "bf16", True), (8, 4096, 8192, "f32", True),
+                                                       (6, 2000, 4160, "bf16", False), (16, 300, 6144, "f32", True)])
+def test_linear_handoff_bit_exact(ctx, m, n, k, out_dtype, with_bias):
+    """5..16 bf16 rows that no fused decode unit takes (K % 512 != 0, K past
+    4096, or 9..16 rows at K past 4096): the quantizer's workgroups hand the
+    rows to the GEMV's workgroups inside one launch.  Codes, scales and
+    outputs bit-exact against Q2 and linear.rs:325-339's order; the context's
+    handoff slots all back at zero, no wait out of polls."""
+    note(f"linear_w8a8 handoff m={m} n={n} k={k} out={out_dtype} bias={with_bias}")
+    _, wq, sw = quantized_weights(n, k, seed=11)
+    bias = O.normal_f32(13, n, 0.0, 0.1) if with_bias else None
+    x = activations_bf16(m, k, seed=80 + m)
+    _, xq_ref, sx_ref, _ = O.quantize_rows_bf16(x)
+    ref = linear_w8a8_exact(xq_ref, sx_ref, wq, sw, bias=bias, out_bf16=out_dtype == "bf16")
+    dx, dw, ds = ctx.upload(x), ctx.upload(tile_16x64(wq)), ctx.upload(sw)
+    db = ctx.upload(bias) if with_bias else None
+    ws_bytes = NH.lib().nh_linear_w8a8_workspace_size(m, k)
+    ws = ctx.empty(max(ws_bytes, 1), np.uint8)
+    ws.fill_bytes(0x5a)
+    odt = NH.BF16 if out_dtype == "bf16" else NH.F32
+    out = ctx.empty((m, n), np.uint16 if out_dtype == "bf16" else np.float32)
+    xq, sx = ctx.empty((m, k), np.int8), ctx.empty(m, np.float32)
+    NH.call("nh_linear_w8a8", ctx.handle, dx.ptr, NH.BF16, dw.ptr, ds.ptr, db.ptr if db else None, m, n, k, out.ptr,
+            odt, ws.ptr, ws_bytes, xq.ptr, sx.ptr, None, None)
+    ctx.synchronize()
+    assert np.array_equal(xq.numpy(), xq_ref)
+    assert np.array_equal(sx.numpy().view(np.uint32), sx_ref.view(np.uint32))
+    got = out.numpy()
+    assert np.array_equal(got if out_dtype == "bf16" else got.view(np.uint32),
+                          ref if out_dtype == "bf16" else ref.view(np.uint32))
+    assert handoff_status(ctx) == (0, 0)
+
+
+def test_linear_handoff_slots_wrap_and_graph_replays(ctx):
+    """More handoff launches than the context has counter slots (each slot
+    must come back to zero for its next user), each against its own oracle
+    result; then three calls captured in a HIP graph, replayed four times with
+    eager calls and synchronizations between the replays, every replay
+    checked."""
+    m, n, k = 8, 512, 1040
+    note(f"linear_w8a8 handoff ring m={m} n={n} k={k}")
+    _, wq, sw = quantized_weights(n, k, seed=12)
+    dw, ds = ctx.upload(tile_16x64(wq)), ctx.upload(sw)
+    ws_bytes = NH.lib().nh_linear_w8a8_workspace_size(m, k)
+    ws = ctx.empty(ws_bytes, np.uint8)
+    xs = [activations_bf16(m, k, seed=500 + i) for i in range(6)]
+    refs = []
+    for x in xs:
+        _, xq_ref, sx_ref, _ = O.quantize_rows_bf16(x)
+        refs.append(linear_w8a8_exact(xq_ref, sx_ref, wq, sw, out_bf16=True))
+    dxs = [ctx.upload(x) for x in xs]
+    out = ctx.empty((m, n), np.uint16)
+
+    def run(i, stream=None):
+        NH.call("nh_linear_w8a8", ctx.handle, dxs[i].ptr, NH.BF16, dw.ptr, ds.ptr, None, m, n, k, out.ptr, NH.BF16,
+                ws.ptr, ws_bytes, None, None, None, stream)
+
+    for c in range(300):
+        run(c % 6)
+        ctx.synchronize()
+        assert np.array_equal(out.numpy(), refs[c % 6]), f"call {c}"
+    assert handoff_status(ctx) == (0, 0)
+    stream = ctypes.c_void_p()
+    NH.call("nh_stream_create", ctx.handle, ctypes.byref(stream))
+    graphs = NH.HipGraphs()
+    outs = [ctx.empty((m, n), np.uint16) for _ in range(3)]
+
+    def issue():
+        for j in range(3):
+            NH.call("nh_linear_w8a8", ctx.handle, dxs[j].ptr, NH.BF16, dw.ptr, ds.ptr, None, m, n, k, outs[j].ptr,
+                    NH.BF16, ws.ptr, ws_bytes, None, None, None, stream)
+
+    g, ex = graphs.capture(stream, issue)
+    try:
+        for rep in range(4):
+            for o in outs:
+                o.fill_bytes(0)
+            ctx.synchronize()
+            graphs.launch(ex, stream)
+            ctx.synchronize(stream)
+            for j in range(3):
+                assert np.array_equal(outs[j].numpy(), refs[j]), f"replay {rep}, call {j}"
+            run(3 + rep % 3)
+            ctx.synchronize()
+            assert np.array_equal(out.numpy(), refs[3 + rep % 3])
+    finally:
+        graphs.destroy(g, ex)
+        NH.call("nh_stream_destroy", ctx.handle, stream)
+    assert handoff_status(ctx) == (0, 0)
+
+
 # ---- L2: int8 MLP layer (MlpLayer::forward_into, mlp.rs:157-211) -----------------
 def mlp_oracle(x, xdt, w_up, s_up, b_up, w_down, s_down, b_down, out_bf16):
     """Per-token Q2, up projection + bias, ReLU^2 (mlp.rs:205) in f32, Q2 of
