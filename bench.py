@@ -132,7 +132,10 @@ class Bench:
         return pool
 
     # ---- decode unit ---------------------------------------------------------
-    def decode(self, m, n, k, steps, warmup, pool=None):
+    def decode(self, m, n, k, steps, warmup, pool=None, eager_only=False):
+        """nh_linear_w8a8 on bf16 rows (bf16 out) over a pool of tiled weights.
+        Returns (ms per call, pool, x, out); eager_only times eager calls
+        (no graph capture: the profiling runs of the K = 8192 shapes)."""
         copies = max(2, -(-POOL_BYTES // (n * k)))
         pool = pool or self.quantized_pool(n, k, copies)
         x = self.ctx.upload(NH_bf16(NH.normal_f32(1, m * k)).reshape(m, k))
@@ -149,7 +152,7 @@ class Bench:
             if st:
                 NH.check(st, err)
 
-        ms = self.time_ms(step, steps, warmup, out=out)
+        ms = self.time_eager_ms(step, steps, warmup) if eager_only else self.time_ms(step, steps, warmup, out=out)
         self.last_step = step
         return ms, pool, x, out
 
@@ -580,8 +583,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="headline only")
-    ap.add_argument("--only", choices=["moe", "moe_shared", "moe_router", "gemm", "stack", "decode", "w8a32", "w4a8",
-                                       "dequant", "gemm_f32"],
+    ap.add_argument("--only", choices=["moe", "moe_shared", "moe_router", "gemm", "stack", "decode", "decode_eager",
+                                       "w8a32", "w4a8", "dequant", "gemm_f32"],
                     default=None,
                     help="run one secondary workload only (for profiling) and print its figures")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -656,6 +659,11 @@ def main():
         elif args.only == "dequant":
             t4, t8 = b.dequant(4096, 4096, 50, 5)
             res = {"int4_us": round(t4 * 1e3, 2), "i8_us": round(t8 * 1e3, 2)}
+        elif args.only == "decode_eager":
+            # M = 16 and 8 at 8192 -> 4096 (out_proj), eager calls only: 110 each
+            for mm in (16, 8):
+                t, _, _, _ = b.decode(mm, 4096, 8192, 100, 10, eager_only=True)
+                res[f"m{mm}_k8192_n4096_eager"] = round(t * 1e3, 2)
         elif args.only == "stack":
             t, sbytes = b.decode_stack(20, 3)
             res = {"ms": round(t, 4), "GBps": round(sbytes / (t * 1e-3) / 1e9, 1)}
