@@ -636,7 +636,7 @@ __device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, 
     const int cbase = wave * XR * 64;  // the wave's first chunk
     v4i xv[XR];
     using WB = std::conditional_t<W4, uint2, v4i>;  // one lane's share of a weight tile
-    WB b0[KS], b1[KS], b2[KS];
+    WB b0[KS], b1[KS], b2[KS], b3[KS];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < XR; ++j) {
@@ -662,10 +662,30 @@ __device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, 
                 b[s] = buffer_load16_stream(wr, (wave * KS + s) * 1024 + lane * 16);
         }
     };
-    issue(b0, 0);
-    issue(b1, 1);
-    if (NB > 2) issue(b2, 2);
+    // Where the weight rounds go relative to the activations (same-box A/B,
+    // the 52-layer stack at 8 rows and M = 16 at 4096 -> 16384): at 5..8
+    // rows they are issued once this wave's activations have landed (stack
+    // 1.727-1.729 against 1.734-1.738 ms: the activation loads otherwise
+    // queue behind the whole chip's weight misses); at 9..16 rows every
+    // wave's activation loads go out before any weight load (a barrier:
+    // 18.51-18.73 against 19.03-19.14 us); at 3..4 rows neither helped.
+    constexpr bool kLateWeights = MM == 8, kActFirst = MM == 16;
+    if constexpr (kActFirst) lds_barrier();
+    if constexpr (!kLateWeights) {
+        issue(b0, 0);
+        issue(b1, 1);
+        if (NB > 2) issue(b2, 2);
+        if (NB > 3) issue(b3, 3);
+    }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kLateWeights) {
+        wait_vmcnt_le(2);  // the activations (the weight scale and bias loads may still fly)
+        issue(b0, 0);
+        issue(b1, 1);
+        if (NB > 2) issue(b2, 2);
+        if (NB > 3) issue(b3, 3);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     // 2. activations in (weights in flight): row absmax, one reduction per
     //    row the wave holds (rows change only where a 64-chunk group starts)
@@ -799,6 +819,7 @@ __device__ __forceinline__ void linear_decode_stream(const LinearDecodeArgs& a, 
         round(b0, r);
         round(b1, r + 1);
         if (NB > 2) round(b2, r + 2);
+        if (NB > 3) round(b3, r + 3);
     }
     // the workgroup's row maxima: the 16 threads of a row are one DPP row
     if (a.row_max && tid < 16 * MM) {
