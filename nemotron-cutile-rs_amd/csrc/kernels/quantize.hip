@@ -415,8 +415,20 @@ extern "C" __global__ __launch_bounds__(256) void nh_quantize_rows_pmax_kernel(Q
     // its round trip overlaps the partial maxima's
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + (int64_t)row * a.cols, (uint32_t)a.cols * 4u);
     const v4i v = buffer_load16(xr, c < chunks ? c * 16 : kOutOfRange);
+    // the partial maxima, 4 per lane in flight at once (up to 256 groups
+    // in one round trip; a loop of dependent loads took one per 64 groups)
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.pmax, (uint32_t)a.groups * (uint32_t)a.rows * 4u);
     uint32_t m = 0;
-    for (int g = lane; g < a.groups; g += 64) m = max(m, a.pmax[(int64_t)g * a.rows + row]);
+    for (int g0 = 0; g0 < a.groups; g0 += 256) {
+        uint32_t pm[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int g = g0 + lane + 64 * i;
+            pm[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                pr, g < a.groups ? (g * a.rows + row) * 4 : kOutOfRange, 0, 0);
+        }
+        m = max(m, max(max(pm[0], pm[1]), max(pm[2], pm[3])));
+    }
     m = wave_max_dpp_u32(m);
     const float s = scale_from_amax(f32_from_bits(m));
     if (blockIdx.x == 0 && threadIdx.x == 0) a.scales[row] = s;
