@@ -192,7 +192,7 @@ __device__ __forceinline__ void gemv_w8a8(const GemvW8A8Args& a, v4i* red) {
 // wave polls (s_sleep between polls, a bounded number of polls), so the
 // waves holding the weight slab never wait behind a poll; a bare s_barrier
 // then releases them.  Same codes, scales and outputs as the two launches.
-constexpr uint32_t kHandoffPolls = 1u << 22;
+constexpr uint32_t kHandoffPolls = 1u << 18;  // ~0.5 s of polls: the rows take microseconds
 
 __device__ __forceinline__ void handoff_consume(const LinearHandoffArgs& h, v4i* red) {
     const GemvW8A8Args& a = h.g;

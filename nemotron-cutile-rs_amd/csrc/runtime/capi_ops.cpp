@@ -26,11 +26,12 @@ unsigned grid_for(int64_t items, int per_block) {
 int gemv_waves(int kt) { return std::max(1, std::min(8, (kt + 15) / 16)); }
 
 // The linear entry point's M ranges: the fused decode unit (quantizer inside
-// the GEMV, one launch) for up to 4 bf16 rows (K <= 8192) and for 5..8 bf16
-// rows (K <= 8192, K % 512 == 0); otherwise quantization into activation tiles +
-// the tiled-A GEMV up to 16 rows, and the MFMA GEMM beyond.  A dependent
-// second launch costs ~4 us; at 16 rows the two launches win (19.5 vs
-// 21.6 us fused, K = 4096, N = 16384).
+// the GEMV, one launch) for up to 4 bf16 rows (K <= 8192) and for 3..16 bf16
+// rows (K <= 4096, K % 512 == 0, the streaming form); other bf16 rows up to
+// 16 (K <= 8192) as the handoff launch (quantizer workgroups feeding the
+// tiled-A GEMV's workgroups inside one launch); otherwise quantization into
+// activation tiles + the tiled-A GEMV up to 16 rows (f32 rows, K > 8192),
+// and the MFMA GEMM beyond.
 constexpr size_t kTiledActRows = 16;
 
 // Fused decode unit: kernel, N tiles per workgroup, block size, LDS bytes.
