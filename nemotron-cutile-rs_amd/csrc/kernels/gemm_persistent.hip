@@ -9,6 +9,11 @@
 //    the MFMA rate (the 64 x 64 tiles of gemm.hip: 128), and the tile needs
 //    34 B/clk from L2 per CU instead of 48;
 //  * stages of two K tiles (128 bytes of K), one barrier per two MFMA K steps;
+//  * the weights one stage further ahead than the activations (an A ring of
+//    two slots, a B ring of three): with the weights cold in HBM, as a
+//    model's layers read them, rather than in the MALL, as one matrix timed
+//    over and over is, (2048, 21504, 4096) takes 181.7-184.9 us against
+//    193.6-196.4 us for one common ring of two stages (170-173 us warm either way);
 //  * the first K step of stage g is read into one register set right after
 //    the barrier while the MFMAs of the second K step of stage g - 1 run from
 //    the other, so every barrier is followed by MFMA work already in registers;
@@ -30,8 +35,8 @@
 // number it issued after stage g's loads -- never more than are actually
 // outstanding after them -- and the barrier then publishes every wave's part
 // of the stage.  The per-tile scales (sx for BM rows, sw and bias for BN
-// columns) arrive the same way, with the tile's first stage, into one of
-// S + 1 LDS buffers.
+// columns) arrive the same way, with the tile's first A stage, into one of
+// three LDS buffers.
 //
 // Operand layouts: A and B both in the tiled layout (nh_numerics.h), so each
 // 1 KiB tile is one MFMA operand.  The MFMA takes the weight fragment as its
@@ -85,29 +90,31 @@ __device__ __forceinline__ void lds_dma16(v4i rsrc, uint32_t voffset, uint32_t l
 
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
 
-// The same with stages of two K tiles (128 bytes of K): one barrier per two
-// MFMA K steps.  Register set X holds a stage's first K step, Y its second.
-// Step of stage g: barrier; X <- K step 0 of stage g; MFMAs of Y (K step 1
-// of stage g - 1) -- at a tile's first stage followed by the previous tile's
-// epilogue; the loads of stage g + S - 1; Y <- K step 1 of stage g (after the
-// MFMAs that read Y issued); MFMAs of X.  Every barrier is followed at once
-// by MFMA work whose operands are already in registers.
-template <int BM, int BN, int WGM, int WGN, int S>
+// Stages of two K tiles (128 bytes of K): one barrier per two MFMA K steps.
+// The weight operand (B) runs one stage further ahead than the activations
+// (A): a 2-slot A ring and a 3-slot B ring, each slot holding only its own
+// operand's tiles (so the three B slots still fit the LDS), and a weight
+// stage has two stages of MFMA time to arrive instead of one.  Register set X
+// holds a stage's first K step, Y its second.  Step of stage g: barrier;
+// X <- K step 0 of stage g; MFMAs of Y (K step 1 of stage g - 1) -- at a
+// tile's first stage followed by the previous tile's epilogue; the A loads of
+// stage g + 1 (with its tile's scales) and the B loads of stage g + 2;
+// Y <- K step 1 of stage g (after the MFMAs that read Y issued); MFMAs of X.
+// Every barrier is followed at once by MFMA work whose operands are already
+// in registers.  Before the barrier of stage g + 1 a wave waits for all but
+// its B loads of stage g + 2, the last it issued.
+template <int BM, int BN, int WGM, int WGN>
 __device__ __forceinline__ void gemm_persistent(const GemmW8A8Args& a, int8_t* smem) {
     constexpr int NW = WGM * WGN;
-    constexpr int TA = BM / 16, TB = BN / 16, TQ = TA + TB;
-    constexpr int LPW = (2 * TQ + NW - 1) / NW;  // operand loads per wave per stage
-    constexpr int kStage = NW * LPW * 1024;      // two K tiles; slots past 2 TQ take zeros
-    constexpr int C = LPW + 1;                   // loads per wave per stage: operands + one scale load
+    constexpr int TA = BM / 16, TB = BN / 16;
+    constexpr int LPWA = (2 * TA + NW - 1) / NW, LPWB = (2 * TB + NW - 1) / NW;
+    constexpr int kA = NW * LPWA * 1024;  // an A slot: [K half][TA tiles] (+ padding slots)
+    constexpr int kB = 2 * TB * 1024;     // a B slot: [K half][TB tiles]; padding loads go to the spare KiB
     constexpr int FM = BM / WGM / 16, FN = BN / WGN / 16;
     static_assert(BM % (16 * WGM) == 0 && BN % (16 * WGN) == 0, "wave tiles of whole fragments");
     static_assert(BM <= 256 && BN <= 256, "one 16-byte load per lane holds a tile's scales");
-    static_assert(S >= 2, "");
-    constexpr int NSB = S + 1;
+    constexpr int NSB = 3;
     constexpr int kScales = 3 * 1024;
-    constexpr int NSTORE = FM * FN;
-    constexpr int kAllow0 = (S - 2) * C;
-    constexpr int kAllow1 = kAllow0 + NSTORE < 63 ? kAllow0 + NSTORE : 63;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
@@ -120,50 +127,82 @@ __device__ __forceinline__ void gemm_persistent(const GemmW8A8Args& a, int8_t* s
     const int nst = my_tiles * KT2;
     if (nst == 0) return;
     typedef __attribute__((address_space(3))) int8_t lds_i8;
-    const uint32_t ring0 = (uint32_t)(uintptr_t)(lds_i8*)smem;
-    const uint32_t scal0 = ring0 + (uint32_t)(S * kStage);
+    const uint32_t ringa = (uint32_t)(uintptr_t)(lds_i8*)smem;
+    const uint32_t ringb = ringa + (uint32_t)(2 * kA);
+    const uint32_t scal0 = ringb + (uint32_t)(3 * kB);
     const uint32_t dummy = scal0 + (uint32_t)(NSB * kScales);
-    const float* scales = (const float*)(smem + S * kStage);
+    const float* scales = (const float*)(smem + 2 * kA + 3 * kB);
     const int esz = a.out_dtype == DT_BF16 ? 2 : 4;
     const v4i out_r = rsrc_words(a.out, (uint32_t)M * (uint32_t)a.ldo * (uint32_t)esz);
     const v4i null_r = rsrc_words(a.out, 0u);
 
-    int it_i = 0, kt_i = 0, s_i = 0, sb_i = 0;  // next stage to issue: tile, stage within it, slot, scale buffer
+    // A stream (with the tile's scales) and B stream: next stage to issue
+    int ia_t = 0, ia_k = 0, sa_i = 0, sb_i = 0;
+    int ib_t = 0, ib_k = 0, sbb_i = 0;
     v4i ra, rb, rsc;
     uint32_t sc_dst;
-    auto set_issue_tile = [&]() {
-        const int p = it_i * G + pos;
+    auto set_a_tile = [&]() {
+        const int p = ia_t * G + pos;
         const int m0 = (p % a.tiles_m) * BM, n0 = (p / a.tiles_m) * BN;
-        const int mt0 = m0 >> 4, nt0 = n0 >> 4;
+        const int mt0 = m0 >> 4;
         ra = rsrc_words(a.xq + (int64_t)mt0 * KT * 1024, (uint32_t)min(TA, mtiles - mt0) * (uint32_t)KT * 1024u);
-        rb = rsrc_words(a.wq + (int64_t)nt0 * KT * 1024, (uint32_t)min(TB, ntiles - nt0) * (uint32_t)KT * 1024u);
         rsc = wave == 0   ? rsrc_words(a.sx + m0, (uint32_t)(M - m0) * 4u)
               : wave == 1 ? rsrc_words(a.sw + n0, (uint32_t)(N - n0) * 4u)
               : (wave == 2 && a.bias) ? rsrc_words(a.bias + n0, (uint32_t)(N - n0) * 4u) : null_r;
         const uint32_t sb = scal0 + (uint32_t)(sb_i * kScales);
         sc_dst = wave == 0 ? sb : wave == 1 ? sb + 1024 : wave == 2 ? sb + 2048 : dummy;
     };
-    set_issue_tile();
-    // slot layout of a stage: [K step][A tiles, B tiles] of 1 KiB; q = h TQ + t
-    auto issue = [&]() {
-        const uint32_t st = ring0 + (uint32_t)(s_i * kStage);
-        const int kt0 = 2 * kt_i;
+    auto set_b_tile = [&]() {
+        const int p = ib_t * G + pos;
+        const int nt0 = ((p / a.tiles_m) * BN) >> 4;
+        rb = rsrc_words(a.wq + (int64_t)nt0 * KT * 1024, (uint32_t)min(TB, ntiles - nt0) * (uint32_t)KT * 1024u);
+    };
+    set_a_tile();
+    set_b_tile();
+    auto issue_a = [&]() {
+        const uint32_t st = ringa + (uint32_t)(sa_i * kA);
+        const int kt0 = 2 * ia_k;
 #pragma unroll
-        for (int i = 0; i < LPW; ++i) {
+        for (int i = 0; i < LPWA; ++i) {
             const int q = wave + i * NW;  // uniform
-            const int h = q >= TQ ? 1 : 0, t = q - h * TQ;
-            const bool isa = t < TA;
-            const int row = isa ? t : t - TA;
-            const uint32_t off = q < 2 * TQ ? (uint32_t)((row * KT + kt0 + h) * 1024 + lane * 16) : (uint32_t)kOutOfRange;
-            lds_dma16(isa ? ra : rb, off, st + (uint32_t)(q * 1024));
+            const int h = q >= TA ? 1 : 0, t = q - h * TA;
+            const uint32_t off = q < 2 * TA ? (uint32_t)((t * KT + kt0 + h) * 1024 + lane * 16) : (uint32_t)kOutOfRange;
+            lds_dma16(ra, off, st + (uint32_t)(q * 1024));
         }
-        lds_dma16(kt_i == 0 ? rsc : null_r, (uint32_t)lane * 16u, kt_i == 0 ? sc_dst : dummy);
-        s_i = s_i + 1 == S ? 0 : s_i + 1;
-        if (++kt_i == KT2) {
-            kt_i = 0;
-            ++it_i;
+        lds_dma16(ia_k == 0 ? rsc : null_r, (uint32_t)lane * 16u, ia_k == 0 ? sc_dst : dummy);
+        sa_i ^= 1;
+        if (++ia_k == KT2) {
+            ia_k = 0;
+            ++ia_t;
             sb_i = sb_i + 1 == NSB ? 0 : sb_i + 1;
-            if (it_i < my_tiles) set_issue_tile();
+            if (ia_t < my_tiles) set_a_tile();
+        }
+    };
+    // the B loads of the next B stage (past the last stage: loads of zeros
+    // from an empty resource into a slot no stage reads any more).  Wave w
+    // issues the slots w, w + NW, ... below 2 TB: LPWB loads for the first
+    // (2 TB) % NW waves, LPWB - 1 for the others, no padding loads.
+    constexpr int kBFull = (2 * TB) % NW == 0 ? NW : (2 * TB) % NW;  // waves with LPWB B loads
+    auto issue_b = [&]() {
+        const bool live = ib_t < my_tiles;  // uniform
+        const v4i rbx = live ? rb : null_r;
+        const uint32_t st = ringb + (uint32_t)(sbb_i * kB);
+        const int kt0 = 2 * ib_k;
+#pragma unroll
+        for (int i = 0; i < LPWB; ++i) {
+            const int q = wave + i * NW;  // uniform
+            if (i + 1 < LPWB || wave < kBFull) {
+                const int h = q >= TB ? 1 : 0, t = q - h * TB;
+                lds_dma16(rbx, (uint32_t)((t * KT + kt0 + h) * 1024 + lane * 16), st + (uint32_t)(q * 1024));
+            }
+        }
+        if (live) {
+            sbb_i = sbb_i + 1 == 3 ? 0 : sbb_i + 1;
+            if (++ib_k == KT2) {
+                ib_k = 0;
+                ++ib_t;
+                if (ib_t < my_tiles) set_b_tile();
+            }
         }
     };
 
@@ -173,12 +212,14 @@ __device__ __forceinline__ void gemm_persistent(const GemmW8A8Args& a, int8_t* s
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
     v4i xa[FM], xb[FN], ya[FM], yb[FN];
-    auto read = [&](v4i (&fa)[FM], v4i (&fb)[FN], int slot, int h) {
-        const int8_t* st = smem + slot * kStage + h * TQ * 1024 + lane * 16;
+    int rda = 0, rdb = 0;  // read slots of the A and B rings
+    auto read = [&](v4i (&fa)[FM], v4i (&fb)[FN], int h) {
+        const int8_t* sta = smem + rda * kA + h * TA * 1024 + lane * 16;
+        const int8_t* stb = smem + 2 * kA + rdb * kB + h * TB * 1024 + lane * 16;
 #pragma unroll
-        for (int i = 0; i < FM; ++i) fa[i] = *(const v4i*)(st + (wm * FM + i) * 1024);
+        for (int i = 0; i < FM; ++i) fa[i] = *(const v4i*)(sta + (wm * FM + i) * 1024);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) fb[j] = *(const v4i*)(st + (TA + wn * FN + j) * 1024);
+        for (int j = 0; j < FN; ++j) fb[j] = *(const v4i*)(stb + (wn * FN + j) * 1024);
     };
     auto mma = [&](const v4i (&fa)[FM], const v4i (&fb)[FN]) {
 #pragma unroll
@@ -228,31 +269,34 @@ __device__ __forceinline__ void gemm_persistent(const GemmW8A8Args& a, int8_t* s
         sb_e = sb_e + 1 == NSB ? 0 : sb_e + 1;
     };
 
-#pragma unroll
-    for (int s = 0; s < S - 1; ++s)
-        if (s < nst) issue();
-    int s_r = 0, last_epi = -S;
-    // the stores of an epilogue come before the loads of its step, so they
-    // follow stage g's loads when the epilogue ran in steps g - S + 2 .. g - 1
-    const bool exact = KT2 >= S - 2;
+    // prologue: B of stage 0, A of stage 0 (and its scales), B of stage 1
+    issue_b();
+    issue_a();
+    issue_b();
+    // before the barrier of stage g: every operation but the B loads of stage
+    // g + 1 (issued last) has completed
     auto sync = [&](int g) {
         wait_lgkm0();
-        if (!exact || g + S - 2 >= nst) NH_WAIT_VMCNT(0);
-        else if (g - last_epi < S - 1) NH_WAIT_VMCNT(kAllow1);
-        else NH_WAIT_VMCNT(kAllow0);
+        if (g + 1 >= nst) NH_WAIT_VMCNT(0);
+        else if (wave < kBFull) NH_WAIT_VMCNT(LPWB);
+        else NH_WAIT_VMCNT(LPWB - 1);
         lds_barrier();
     };
     auto second_half = [&](int g) {
-        if (g + S - 1 < nst) issue();
-        read(ya, yb, s_r, 1);
-        s_r = s_r + 1 == S ? 0 : s_r + 1;
+        if (g + 1 < nst) {
+            issue_a();
+            issue_b();
+        }
+        read(ya, yb, 1);
+        rda ^= 1;
+        rdb = rdb + 1 == 3 ? 0 : rdb + 1;
         __builtin_amdgcn_sched_barrier(0);
         mma(xa, xb);
     };
     auto rest_of_tile = [&](int& g) {
         for (int k2 = 1; k2 < KT2; ++k2, ++g) {
             sync(g);
-            read(xa, xb, s_r, 0);
+            read(xa, xb, 0);
             __builtin_amdgcn_sched_barrier(0);
             mma(ya, yb);
             second_half(g);
@@ -260,17 +304,16 @@ __device__ __forceinline__ void gemm_persistent(const GemmW8A8Args& a, int8_t* s
     };
     int g = 0;
     sync(0);
-    read(xa, xb, s_r, 0);
+    read(xa, xb, 0);
     second_half(0);
     g = 1;
     rest_of_tile(g);
     for (int t = 1; t < my_tiles; ++t, ++g) {
         sync(g);
-        read(xa, xb, s_r, 0);
+        read(xa, xb, 0);
         __builtin_amdgcn_sched_barrier(0);
         mma(ya, yb);
         epilogue();
-        last_epi = g;
         second_half(g);
         ++g;
         rest_of_tile(g);
@@ -285,13 +328,13 @@ __device__ __forceinline__ void gemm_persistent(const GemmW8A8Args& a, int8_t* s
 
 }  // namespace
 
-// LDS of gemm_persistent: the ring (two K tiles per stage), S + 1 scale buffers, one spare KiB.
-#define NH_GEMM_P_LDS(BM, BN, NW, S) \
-    ((S) * (NW) * ((2 * ((BM) + (BN)) / 16 + (NW) - 1) / (NW)) * 1024 + ((S) + 1) * 3 * 1024 + 1024)
+// LDS of gemm_persistent: two A slots (whole loads per wave), three B slots, three scale buffers, one spare KiB.
+#define NH_GEMM_P_LDS(BM, BN, NW)                                                                      \
+    (2 * (NW) * ((2 * (BM) / 16 + (NW) - 1) / (NW)) * 1024 + 3 * (2 * (BN) / 16) * 1024 + 3 * 3 * 1024 + 1024)
 
-// 256 x 224 tiles, 8 waves of 64 x 112, 2 stages: the 21504-wide projection at
-// M = 2048 is 768 tiles, three per CU.
+// 256 x 224 tiles, 8 waves of 64 x 112: the 21504-wide projection at M = 2048
+// is 768 tiles, three per CU.
 extern "C" __global__ __launch_bounds__(512) void nh_gemm_w8a8_p256x224_kernel(GemmW8A8Args a) {
     extern __shared__ __align__(1024) int8_t smem[];
-    gemm_persistent<256, 224, 4, 2, 2>(a, smem);
+    gemm_persistent<256, 224, 4, 2>(a, smem);
 }

@@ -195,9 +195,9 @@ nh_status launch_gemv(nh_context* ctx, const int8_t* xq, const float* sx, const 
 // loader-wave kernel's 256 x 128 tiles: rounds x tile area (the 21504-wide
 // up projection at M = 2048: 3 rounds of 256 x 224 against 5.5 of 256 x 128;
 // measured 201-203 against 231-236 us).
-constexpr int kP224Stages = 2;
-constexpr size_t kP224Lds = (size_t)kP224Stages * 8 * ((2 * (256 + 224) / 16 + 7) / 8) * 1024 + (kP224Stages + 1) * 3 * 1024 +
-                            1024;
+// Its LDS: two A slots of 2 x 16 tiles, three B slots of 2 x 14 tiles (the
+// weights run a stage further ahead), three scale buffers, a spare KiB.
+constexpr size_t kP224Lds = 2 * 8 * ((2 * 256 / 16 + 7) / 8) * 1024 + 3 * (2 * 224 / 16) * 1024 + 3 * 3 * 1024 + 1024;
 
 bool use_persistent_224(const nh_context* ctx, const void* xq, const float* sx, const float* sw, const float* bias,
                         int M, int N, int kt, const void* out, nh_dtype out_dtype) {
