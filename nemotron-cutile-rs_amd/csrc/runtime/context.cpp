@@ -63,6 +63,7 @@ const char* const kKernelSymbols[K_COUNT] = {  // in KernelId order
     "nh_gemm_f32_mfma_kernel",           // K_GEMM_F32_MFMA
     "nh_gemm_f32_mfma_bf16_kernel",      // K_GEMM_F32_MFMA_BF16
     "nh_gemm_f32_mfma_any_kernel",       // K_GEMM_F32_MFMA_ANY
+    "nh_quantize_rows_r11_kernel",       // K_QUANTIZE_ROWS_R11
 };
 
 void clear_error(nh_error* err) {

@@ -66,6 +66,7 @@ enum KernelId : int {
     K_GEMM_F32_MFMA,          // G0d on the f64 matrix cores, 16 x 16 outputs per workgroup, f32 lhs
     K_GEMM_F32_MFMA_BF16,     // ... bf16 lhs
     K_GEMM_F32_MFMA_ANY,      // ... any alignment, K and N
+    K_QUANTIZE_ROWS_R11,      // row quantizer, 256 threads per row, up to 2816 chunks in registers
     K_COUNT
 };
 

@@ -128,11 +128,14 @@ def test_quantize_rows_special_rows(ctx):
 
 
 @pytest.mark.parametrize("cols,dtype", [(2688, "bf16"), (1856, "f32"), (4096, "bf16"), (2048, "f32"), (8, "bf16"),
-                                        (4, "f32")])
+                                        (4, "f32"),
+                                        # whole rows of 1025..2816 chunks in a workgroup's registers
+                                        (21504, "bf16"), (8200, "bf16"), (22528, "bf16"), (11264, "f32")])
 def test_quantize_many_rows_bit_exact(ctx, cols, dtype):
     """1100 rows: the one-wave-per-row quantizer (rows of up to 512 16-byte
-    chunks, 1024 rows or more), with tie, tiny, subnormal and non-finite rows
-    among them."""
+    chunks, 1024 rows or more) and the whole-row workgroup quantizer (rows of
+    1025..2816 chunks), with tie, tiny, subnormal and non-finite rows among
+    them."""
     rows = 1100
     note(f"quantize_rows many {rows}x{cols} {dtype}")
     x = O.normal_f32(11, rows * cols, 0.0, 0.02 if dtype == "f32" else 1.0).reshape(rows, cols)
