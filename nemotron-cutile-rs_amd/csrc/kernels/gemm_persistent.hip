@@ -29,7 +29,8 @@
 // follow, would otherwise wait for every load in flight (vmcnt(0)) before
 // each fragment read.  The ring's synchronization is explicit instead: each
 // wave issues a fixed number of vector-memory operations per stage (operand
-// loads, one scale load or a load of zeros into a spare KiB, and per tile a
+// loads, past the last stage loads of zeros from an empty resource; one
+// scale load or a load of zeros into a spare KiB; and per tile a
 // fixed number of unconditional buffer stores; counts complete in issue
 // order), so before the barrier of stage g it waits with vmcnt equal to the
 // number it issued after stage g's loads -- never more than are actually
