@@ -58,8 +58,11 @@ def run_pair(ctx, m, n, k, dtype, seed):
 def test_noalloc_equals_workspace_entry_two_calls_second_smaller(ctx):
     # first call: 300 rows through the GEMM on A tiles in the scratch (2.4 MB
     # of it); second, smaller: 12 rows through the activation tiles + GEMV
-    # (the scratch keeps the first call's bytes past what the second writes)
-    for (m, n, k, dtype, seed) in [(300, 2048, 8192, "bf16", 80), (12, 1024, 4096, "f32", 90)]:
+    # (the scratch keeps the first call's bytes past what the second writes);
+    # third: 12 bf16 rows at K = 8192, the one-launch handoff whose quantizer
+    # workgroups write the activation tiles into the scratch
+    for (m, n, k, dtype, seed) in [(300, 2048, 8192, "bf16", 80), (12, 1024, 4096, "f32", 90),
+                                   (12, 1024, 8192, "bf16", 100)]:
         (a, b), (ref, xq_ref, sx_ref) = run_pair(ctx, m, n, k, dtype, seed)
         assert np.array_equal(b[0], a[0]), f"{(b[0] != a[0]).sum()} outputs differ"
         assert np.array_equal(b[1], a[1]) and np.array_equal(b[2].view(np.uint32), a[2].view(np.uint32))
