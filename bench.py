@@ -156,10 +156,11 @@ class Bench:
         self.last_step = step
         return ms, pool, x, out
 
-    def w4a8(self, m, n, k, steps, warmup):
+    def w4a8(self, m, n, k, steps, warmup, eager_only=False):
         """The W4A8 decode unit (nh_linear_w4a8): bf16 rows quantized per token
         in the GEMV over tiled INT4 weights (per-tensor scale 0.01, zero point
-        8), rotating through a > 512 MiB pool of random codes."""
+        8), rotating through a > 512 MiB pool of random codes; eager_only
+        times eager calls (for tracing)."""
         copies = max(2, -(-POOL_BYTES // (n * k // 2)))
         L, h = NH.lib(), self.ctx.handle
         packed = np.random.default_rng(7).integers(0, 256, size=(k * n + 1) // 2, dtype=np.uint8)
@@ -182,6 +183,8 @@ class Bench:
             if st:
                 NH.check(st, err)
 
+        if eager_only:
+            return self.time_eager_ms(step, steps, warmup)
         return self.time_ms(step, steps, warmup, out=out)
 
     def gemm(self, m, n, k, steps, warmup):
@@ -584,7 +587,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--quick", action="store_true", help="headline only")
     ap.add_argument("--only", choices=["moe", "moe_shared", "moe_router", "gemm", "stack", "decode", "decode_eager",
-                                       "w8a32", "w4a8", "dequant", "gemm_f32"],
+                                       "w8a32", "w4a8", "w4a8_eager", "dequant", "gemm_f32"],
                     default=None,
                     help="run one secondary workload only (for profiling) and print its figures")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -660,10 +663,16 @@ def main():
             t4, t8 = b.dequant(4096, 4096, 50, 5)
             res = {"int4_us": round(t4 * 1e3, 2), "i8_us": round(t8 * 1e3, 2)}
         elif args.only == "decode_eager":
-            # M = 16 and 8 at 8192 -> 4096 (out_proj), eager calls only: 110 each
-            for mm in (16, 8):
-                t, _, _, _ = b.decode(mm, 4096, 8192, 100, 10, eager_only=True)
-                res[f"m{mm}_k8192_n4096_eager"] = round(t * 1e3, 2)
+            # M = 16 and 8 at 8192 -> 4096 (out_proj), then M = 4, 8 and 16 at
+            # 4096 -> 16384 (the streaming unit), eager calls only: 110 each
+            for (mm, nn, kk) in [(16, 4096, 8192), (8, 4096, 8192), (4, 16384, 4096), (8, 16384, 4096),
+                                 (16, 16384, 4096)]:
+                t, _, _, _ = b.decode(mm, nn, kk, 100, 10, eager_only=True)
+                res[f"m{mm}_k{kk}_n{nn}_eager"] = round(t * 1e3, 2)
+        elif args.only == "w4a8_eager":
+            # the W4A8 decode units at 4096 -> 16384, M = 1, 4, 8, 16: eager calls only, 110 each
+            for mm in (1, 4, 8, 16):
+                res[f"m{mm}_k4096_n16384_eager"] = round(b.w4a8(mm, 16384, 4096, 100, 10, eager_only=True) * 1e3, 2)
         elif args.only == "stack":
             t, sbytes = b.decode_stack(20, 3)
             res = {"ms": round(t, 4), "GBps": round(sbytes / (t * 1e-3) / 1e9, 1)}
